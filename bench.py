@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""Benchmark of the jointkv hard residual-quantization hot path on one MI355X.
+
+Headline line: GSRQ-2 encode of a Mistral-7B-shaped
+cache, 32 layers x {K,V} x [1,8,8192,128] fp16 with 4 outlier channels per
+head, 16 groups x 8 dims x 2 residual stages x 256 fp16 codewords per
+(head, group) (stage 1 N(0,1), stage 2 N(0,0.25)), codes + fp16
+reconstruction written.  One step = the 64 encodes of the whole cache.
+
+Extra measurements in the same JSON line:
+  decode   config 4: fused packed-code GQA decode (32q/8kv, B16, 4096 window,
+           G2 codes), one new token per step over 32 layers (encode + append +
+           attention per layer), us/step
+  vstep    config 5: V-only STE calibration step over 32 layers at
+           [4,8,2048,128] (encode fwd, scatter bwd, global clip, SGD), steps/s
+  cq2      config 3: reference cq2 grouped-CQ encode ([8,32,256,4]) of
+           32 layers x {K,V} x [4,8,2048,128], tokens/s
+  roofline of the encode kernel (MFMA, algorithmic flops) and cpu_baseline
+  (the oracle's eager-PyTorch restatement of the reference on a bounded
+  sample, timed on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "tac-vq-kv-cache_amd"))
+sys.path.insert(0, str(ROOT))
+
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+
+LAYERS = 32
+HEADS = 8
+HEAD_DIM = 128
+GROUPS = 16
+GROUP_DIM = 8
+STAGES = 2
+CLUSTERS = 256
+FLOP_PER_VEC_G2 = STAGES * GROUPS * CLUSTERS * GROUP_DIM * 2  # 131072
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_states(gen, batch, heads, tokens, device):
+    import torch
+
+    x = torch.randn(batch, heads, tokens, HEAD_DIM, generator=gen, device=device)
+    for h in range(heads):
+        ch = torch.randperm(HEAD_DIM, generator=gen, device=device)[:4]
+        x[:, h, :, ch] *= 8.0
+    return x.half()
+
+
+def make_tables(gen, shape, sigmas, stage_axis, device):
+    import torch
+
+    t = torch.randn(*shape, generator=gen, device=device)
+    for s, sg in enumerate(sigmas):
+        idx = [slice(None)] * len(shape)
+        idx[stage_axis] = s
+        t[tuple(idx)] *= sg
+    return t.half().float().contiguous()
+
+
+def timed(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per step
+
+
+def encode_workload(args, device):
+    import torch
+    from jointkv_amd import _ops
+
+    gen = torch.Generator(device=device).manual_seed(8601)
+    layers = []
+    for _layer in range(LAYERS):
+        for _kind in range(2):
+            states = make_states(gen, 1, HEADS, args.tokens, device)
+            tables = make_tables(gen, (HEADS * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), 1, device)
+            layers.append((states, tables))
+    log(f"encode inputs ready: {len(layers)} tensors of {tuple(layers[0][0].shape)}")
+
+    def step():
+        for states, tables in layers:
+            _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+
+    ms = timed(step, args.steps, args.warmup)
+    # per-launch kernel time with events bracketing each launch
+    durations = []
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in layers]
+    for (a, b), (states, tables) in zip(ev, layers):
+        a.record()
+        _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+        b.record()
+    torch.cuda.synchronize()
+    durations = [a.elapsed_time(b) for a, b in ev]
+    avg_launch_ms = sum(durations) / len(durations)
+    vecs_per_launch = HEADS * args.tokens
+    flops_per_launch = vecs_per_launch * FLOP_PER_VEC_G2
+    bytes_per_launch = vecs_per_launch * (HEAD_DIM * 2 + GROUPS * STAGES + HEAD_DIM * 2) + HEADS * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 4
+    return {
+        "ms_per_step": ms,
+        "tokens_per_s": args.tokens / (ms / 1e3),
+        "vecs_per_s": 2 * LAYERS * HEADS * args.tokens / (ms / 1e3),
+        "avg_launch_ms": avg_launch_ms,
+        "flops_per_launch": flops_per_launch,
+        "bytes_per_launch": bytes_per_launch,
+        "launches_per_step": len(layers),
+    }
+
+
+def cq2_workload(args, device):
+    import torch
+    from jointkv_amd import _ops
+
+    gen = torch.Generator(device=device).manual_seed(8601)
+    tensors = []
+    for _ in range(LAYERS * 2):
+        states = make_states(gen, 4, HEADS, 2048, device)
+        books = make_tables(gen, (HEADS * 32, 1, CLUSTERS, 4), (1.0,), 1, device)
+        tensors.append((states, books))
+
+    def step():
+        for states, books in tensors:
+            _ops.rvq_encode(states, books, groups=32, group_dim=4, exits=(1,))
+
+    ms = timed(step, max(1, args.steps // 2), 1)
+    return {"ms_per_step": ms, "tokens_per_s": 4 * 2048 / (ms / 1e3)}
+
+
+def decode_workload(args, device):
+    import torch
+    import jointkv_amd as jkv
+    from jointkv_amd import _ops
+
+    batch, qh, kvh, window = 16, 32, 8, 4096
+    gen = torch.Generator(device=device).manual_seed(8601)
+    caches, tabs = [], []
+    for _ in range(LAYERS):
+        kt = make_tables(gen, (kvh * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), 1, device)
+        vt = make_tables(gen, (kvh * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), 1, device)
+        cache = jkv.PackedCodeCache(batch, kvh, GROUPS, STAGES, capacity=window, device=device)
+        codes = torch.randint(0, 256, (batch, kvh, window - 1, GROUPS, STAGES), generator=gen, device=device,
+                              dtype=torch.uint8)
+        cache.append(codes, codes.roll(1, dims=2))
+        caches.append(cache)
+        tabs.append((kt, vt, _ops.f32_to_f16(kt), _ops.f32_to_f16(vt)))
+    q = torch.randn(batch, qh, HEAD_DIM, generator=gen, device=device).half()
+    knew = make_states(gen, batch, kvh, 1, device)
+    vnew = make_states(gen, batch, kvh, 1, device)
+    lengths = torch.full((batch,), window, dtype=torch.int32, device=device)
+    slot = (window - 1) % window
+
+    def step():
+        for cache, (kt, vt, kt16, vt16) in zip(caches, tabs):
+            _r, kc = _ops.rvq_encode(knew, kt, groups=GROUPS, group_dim=GROUP_DIM, exits=())
+            _r, vc = _ops.rvq_encode(vnew, vt, groups=GROUPS, group_dim=GROUP_DIM, exits=())
+            cache.key[:, :, slot] = kc[:, :, 0]
+            cache.value[:, :, slot] = vc[:, :, 0]
+            _ops.decode_attention(q, cache.key, cache.value, kt16, vt16, lengths, window=window,
+                                  rope_theta=10000.0)
+
+    ms = timed(step, args.steps, args.warmup)
+    # attention kernels alone
+    def attn_only():
+        for cache, (_kt, _vt, kt16, vt16) in zip(caches, tabs):
+            _ops.decode_attention(q, cache.key, cache.value, kt16, vt16, lengths, window=window,
+                                  rope_theta=10000.0)
+
+    attn_ms = timed(attn_only, args.steps, 1)
+    bytes_per_layer = 2 * batch * kvh * window * GROUPS * STAGES + 2 * kvh * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 2 + 2 * batch * qh * HEAD_DIM * 2
+    return {
+        "us_per_step": ms * 1e3,
+        "attention_us_per_step": attn_ms * 1e3,
+        "hbm_bytes_per_step": bytes_per_layer * LAYERS,
+        "hbm_frac": bytes_per_layer * LAYERS / (attn_ms / 1e3) / (HBM_PEAK_GBS * 1e9),
+    }
+
+
+def vstep_workload(args, device):
+    import torch
+    from jointkv_amd import _ops
+    import jointkv_amd as jkv
+
+    gen = torch.Generator(device=device).manual_seed(8601)
+    values = [make_states(gen, 4, HEADS, 2048, device) for _ in range(LAYERS)]
+    masters = [torch.nn.Parameter(make_tables(gen, (HEADS * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), 1, device))
+               for _ in range(LAYERS)]
+    upstream = [(torch.randn(4, HEADS, 2048, HEAD_DIM, generator=gen, device=device) * 1e-3 ** 0.5).half()
+                for _ in range(LAYERS)]
+
+    class Codec:
+        key_tables = []
+        value_tables = masters
+
+    def step():
+        for p in masters:
+            p.grad = None
+        for x, p, g in zip(values, masters, upstream):
+            recon, codes = _ops.rvq_encode(x, p.detach(), groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+            grad = torch.zeros_like(p)
+            _ops.rvq_scatter_grad([g], [STAGES], codes, grad, group_dim=GROUP_DIM)
+            p.grad = grad
+        jkv.clip_codebook_gradients(Codec, maximum_norm=1.0, mode="global")
+        jkv.sgd_step(masters, lr=0.001)
+
+    ms = timed(step, max(1, args.steps // 2), 1)
+    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms}
+
+
+def cpu_baseline(args):
+    """The oracle (eager PyTorch restatement of the reference) on one layer's K
+    over a bounded token sample, timed on this host; scaled to tokens/s of the
+    full 32-layer x {K,V} workload."""
+
+    import torch
+    from oracle import jointkv_oracle as ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(8601)
+    tokens = args.cpu_tokens
+    states = ref.synthetic_states(gen, 1, HEADS, tokens)
+    tables = ref.synthetic_tables(gen, (HEADS, GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), stage_axis=2)
+    ref.grouped_residual_vq(states[:, :, :64], tables, prefixes=(2,))  # warm-up
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            ref.grouped_residual_vq(states, tables, prefixes=(2,))
+        runs.append(time.perf_counter() - t0)
+    sec = sorted(runs)[1]
+    # one (layer, K) tensor of `tokens` tokens took `sec`; a full token needs 64 such
+    per_token = sec / tokens * (2 * LAYERS)
+    return {
+        "value": 1.0 / per_token,
+        "unit": "tokens/s",
+        "cores": int(torch.get_num_threads()),
+        "kind": "port",
+        "sample": f"oracle grouped_residual_vq (reference op sequence, token_chunk_size=1024) on one "
+                  f"(layer,K) tensor [1,8,{tokens},128], median of 3, scaled x64 tensors per token",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=2)
+    parser.add_argument("--tokens", type=int, default=8192)
+    parser.add_argument("--cpu-tokens", type=int, default=2048)
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,vstep,cq2,cpu")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the hot path has no multi-GPU leg "
+              "(per-head sharding needs no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+    import torch
+
+    skip = set(filter(None, args.skip.split(",")))
+    device = torch.device("cuda:0")
+    log("encode workload (config 2)")
+    enc = encode_workload(args, device)
+    log(f"encode: {enc['ms_per_step']:.3f} ms/step")
+    extras = {}
+    if "cq2" not in skip:
+        log("cq2 workload (config 3)")
+        extras["cq2_encode"] = cq2_workload(args, device)
+    if "decode" not in skip:
+        log("decode workload (config 4)")
+        extras["decode"] = decode_workload(args, device)
+    if "vstep" not in skip:
+        log("V-only step workload (config 5)")
+        extras["v_only_step"] = vstep_workload(args, device)
+    cpu = None
+    if "cpu" not in skip:
+        log("cpu baseline")
+        cpu = cpu_baseline(args)
+    achieved = enc["flops_per_launch"] / (enc["avg_launch_ms"] / 1e3) / 1e12
+    record = {
+        "metric": "GSRQ-2 encode tokens/s (32 layers x {K,V} x [1,8,8192,128], G2 16x8x2x256)",
+        "value": enc["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": enc["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic: seeded N(0,1) states with 4 x8 outlier channels per head; seeded codebooks",
+        "config": {
+            "workload": "BASELINE config 2: GSRQ-2 grouped residual encode + fp16 reconstruction",
+            "layers": LAYERS, "kv_heads": HEADS, "tokens": args.tokens, "batch": 1,
+            "groups": GROUPS, "group_dim": GROUP_DIM, "stages": STAGES, "codewords": CLUSTERS,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": MFMA_FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
+            "traffic": None,
+            "kernel": "rvq_encode_mfma<8,2>",
+            "avg_launch_us": enc["avg_launch_ms"] * 1e3,
+            "algorithmic_flop_per_launch": enc["flops_per_launch"],
+            "algorithmic_bytes_per_launch": enc["bytes_per_launch"],
+            "hbm_frac_at_algorithmic_bytes": enc["bytes_per_launch"] / (enc["avg_launch_ms"] / 1e3) / (HBM_PEAK_GBS * 1e9),
+        },
+        "cpu_baseline": cpu,
+        "extra": extras,
+        "vecs_per_s": enc["vecs_per_s"],
+    }
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

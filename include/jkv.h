@@ -1,0 +1,173 @@
+/*
+ * jkv.h — C ABI of the MI355X (gfx950) hard residual-quantization hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, element
+ * counts and strides, enqueues its work on the caller's HIP stream and never
+ * synchronises the host.  The caller owns every device buffer (outputs and
+ * workspaces included); the library keeps no device state between calls.
+ * Return value: JKV_OK (0) or a negative JKV_E* code; jkv_last_error() then
+ * returns a thread-local message.
+ *
+ * Layout conventions (identical to the reference operator API):
+ *   states  [B,H,T,G*d]  fp16/bf16/fp32, last axis contiguous, strides in
+ *                        elements for the B, H and T axes
+ *   tables  [H*G,S,K,d]  fp32 masters (the kernels search and decode with
+ *                        their fp16 round trip, as the reference does)
+ *   codes   [B,H,T,G,S]  uint8, the (G,S) block contiguous, byte strides for
+ *                        the B, H and T axes
+ * Residual VQ over full head vectors is G=1, d=D; grouped CQ is S=1.
+ */
+#ifndef JKV_H
+#define JKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* jkv_stream_t; /* == hipStream_t */
+
+enum {
+  JKV_OK = 0,
+  JKV_EINVAL = -1,   /* invalid geometry or argument            */
+  JKV_EHIP = -2,     /* HIP runtime / launch error              */
+  JKV_ENOTSUP = -3,  /* geometry outside what the kernels cover */
+};
+
+enum { JKV_F16 = 0, JKV_BF16 = 1, JKV_F32 = 2 };
+
+#define JKV_MAX_EXITS 8
+
+/* Library version (major*10000 + minor*100 + patch). */
+int jkv_version(void);
+
+/* Thread-local text of the last error raised by this thread. */
+const char* jkv_last_error(void);
+
+/* Bytes of device workspace jkv_rvq_encode needs for this geometry. */
+int64_t jkv_rvq_encode_workspace_bytes(int64_t H, int64_t G, int64_t S,
+                                       int64_t K, int64_t d,
+                                       int32_t has_whitener);
+
+/*
+ * Hard greedy residual-VQ / grouped-CQ encode with fp16-deployed codewords.
+ * Replaces the stage loop of hard_residual_vq_exits
+ * (src/jointkv/closed_loop_vq.py:235-410, nearest search :52-76) and the
+ * search/gather of hard_grouped_cq (src/jointkv/cq_tac.py:33-114).
+ *   whiteners  [H*G,d,d] fp32 or NULL: search runs in W·x coordinates with
+ *              W·c tables (closed_loop_vq.py:312-330,384-390; cq_tac.py:80-85)
+ *   recon[e]   [B,H,T,G*d] contiguous in the states dtype, written with
+ *              fp16/bf16/fp32( sum_{s<exit_depths[e]} fp32(fp16(c_s)) )
+ *              (closed_loop_vq.py:381,396-402); NULL entries are skipped.
+ * Ties resolve to the lowest codeword index (torch.argmin).
+ */
+int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B,
+                   int64_t H, int64_t T, int64_t G, int64_t d,
+                   int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                   const float* tables, int64_t S, int64_t K,
+                   const float* whiteners, uint8_t* codes,
+                   int64_t code_stride_b, int64_t code_stride_h,
+                   int64_t code_stride_t, int32_t n_exits,
+                   const int32_t* exit_depths, void* const* recon,
+                   void* workspace, int64_t workspace_bytes,
+                   jkv_stream_t stream);
+
+/*
+ * Codes-to-vector reconstruction with given (frozen) codes:
+ * out = dtype( sum_{s<depth} fp32(fp16(tables[h*G+g, s, code])) ).
+ * Replaces frozen_assignment_u16_reconstruction
+ * (experiments/train_pure_uniform16_closed_loop_vq.py:395-442) and the
+ * decoded workspace of LayerCache.append
+ * (experiments_followup_mistral/evaluate_mistral_longbench.py:44-60).
+ */
+int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b,
+                   int64_t code_stride_h, int64_t code_stride_t, int64_t B,
+                   int64_t H, int64_t T, int64_t G, int64_t d,
+                   const float* tables, int64_t S, int64_t K, int32_t depth,
+                   void* out, int32_t out_dtype, jkv_stream_t stream);
+
+/* Bytes of device workspace jkv_rvq_scatter_grad needs. */
+int64_t jkv_rvq_scatter_workspace_bytes(int64_t B, int64_t H, int64_t T,
+                                        int64_t G, int64_t d, int64_t S,
+                                        int64_t K, int32_t deterministic);
+
+/*
+ * Straight-through codebook gradient: for every stage s,
+ *   grad_tables[h*G+g, s, k, :] += sum over rows with codes[..,g,s]==k of
+ *       sum over exits e with exit_depths[e] > s of fp32(grads[e][.., g*d:(g+1)*d])
+ * Replaces the autograd backward of torch.gather at
+ * closed_loop_vq.py:376-381 (via the deploy STE :298) and cq_tac.py:98-99.
+ * grads[e] are [B,H,T,G*d] contiguous in grad_dtype.  deterministic != 0
+ * selects a fixed summation order (per 256-row chunk an in-order sum per
+ * codeword, then the chunk partials summed in chunk order; needs
+ * jkv_rvq_scatter_workspace_bytes() of workspace); otherwise LDS-privatised
+ * bins are flushed with global fp32 atomics.
+ */
+int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads,
+                         int32_t grad_dtype, const int32_t* exit_depths,
+                         const uint8_t* codes, int64_t code_stride_b,
+                         int64_t code_stride_h, int64_t code_stride_t,
+                         int64_t B, int64_t H, int64_t T, int64_t G, int64_t d,
+                         int64_t S, int64_t K, float* grad_tables,
+                         int32_t deterministic, void* workspace,
+                         int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
+ * Squared L2 norm of each of n fp32 buffers, accumulated in fp64, written to
+ * out_sumsq[n] (device).  Replaces the per-table torch.linalg.vector_norm of
+ * clip_codebook_gradients
+ * (experiments/train_pure_uniform16_closed_loop_vq.py:1151-1304).
+ */
+int jkv_sumsq(int32_t n, const float* const* buffers, const int64_t* numels,
+              double* out_sumsq, jkv_stream_t stream);
+
+/*
+ * In-place grad[i] *= scales[i] (the clip_grad_norm_ multiply) and, when
+ * lr != 0, the plain SGD update param[i] -= lr * grad[i]
+ * (train_mistral_v_only.py:128,153: SGD, no momentum, no weight decay).
+ * params may be NULL when lr == 0.  scales is a host array.
+ */
+int jkv_scale_sgd(int32_t n, float* const* params, float* const* grads,
+                  const int64_t* numels, const float* scales, float lr,
+                  jkv_stream_t stream);
+
+/*
+ * Fused decode attention over a packed uint8 code cache (one new query token
+ * per sequence).  Replaces the decode branch of attention_forward
+ * (evaluate_mistral_longbench.py:112-122): decoded K̂/V̂ window
+ * (LayerCache.visible :62-70), RoPE of q at its position and of K̂ at the
+ * absolute key positions (:114-118), repeat_kv (:119-120) and SDPA without
+ * mask (:121-122), in one pass that never writes K̂ or V̂.
+ *   q        [B,QH,D] fp16 (pre-RoPE), row stride q_stride_b / q_stride_h
+ *   k_codes, v_codes  [B,KVH,cap,G,S] uint8 (byte strides b, h; token
+ *            stride G*S); key position p lives in slot p % cap
+ *   k_tables, v_tables  fp16 deployed codebooks [KVH*G,S,K,d]
+ *   lengths  [B] int32 device: tokens in the cache including the new one;
+ *            query position = lengths[b]-1; visible keys are the last
+ *            min(window, lengths[b]) positions
+ *   out      [B,QH,D] fp16 contiguous
+ *   workspace  jkv_decode_workspace_bytes() bytes (split-KV partials)
+ */
+int64_t jkv_decode_workspace_bytes(int64_t B, int64_t QH, int64_t D,
+                                   int64_t window);
+int jkv_decode_attention(const void* q, int64_t q_stride_b,
+                         int64_t q_stride_h, const uint8_t* k_codes,
+                         const uint8_t* v_codes, int64_t code_stride_b,
+                         int64_t code_stride_h, int64_t cap,
+                         const void* k_tables, const void* v_tables, int64_t B,
+                         int64_t QH, int64_t KVH, int64_t G, int64_t d,
+                         int64_t S, int64_t K, const int32_t* lengths,
+                         int64_t window, float rope_theta, void* out,
+                         void* workspace, int64_t workspace_bytes,
+                         jkv_stream_t stream);
+
+/* fp32 -> fp16 copy (the deploy round trip tables.half()), n elements. */
+int jkv_f32_to_f16(const float* src, void* dst, int64_t n, jkv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JKV_H */

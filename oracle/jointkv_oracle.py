@@ -1,0 +1,450 @@
+"""CPU oracle for the jointkv hard residual-quantization hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this module, and only as the
+checker or as the timed CPU baseline.  The product (``jointkv_amd``) never
+calls it.
+
+Each function restates, with eager PyTorch ops on the CPU, the arithmetic of
+the reference operator it names (same fp32 distance formula, same argmin tie
+rule, same fp16 deploy round trip, same stage order, same autograd graph), so
+its outputs are what the reference computes on the same inputs.  The
+reference itself is pure Python/PyTorch; it was read, not run.
+
+Pins (see tests/test_oracle_*.py):
+  * nearest search and greedy residual stages: fp64 exhaustive brute force
+    in ``oracle/c/vq_bruteforce.c`` (codes equal wherever the fp64 margin
+    clears fp32 noise), plus the reference's own relational tests
+    (exits equal the decode of the codes; fp16-persistent codewords).
+  * straight-through gradient: the closed form
+    grad[h,s,k] = sum_{n: code[n,s]=k} dL/dX̂[n] checked by brute force in C,
+    and the reference's 1-D known answer (table [0,1,10,20], state 0.1:
+    gradient exactly 1.0 on word 0, zero elsewhere).
+  * clip: the reference's exact numeric expectations
+    (tests/test_pure_uniform16_closed_loop_vq.py:53-138).
+  * decode/prefill attention: fp64 textbook softmax attention with the
+    rotate-half RoPE; HF transformers' fp16 rotary arithmetic itself is
+    third-party (transformers 4.45.1, not vendored) and is restated from its
+    published definition.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+
+import torch
+import torch.nn.functional as F
+
+
+# ---------------------------------------------------------------------------
+# Nearest search and residual VQ
+
+
+def nearest_indices(states: torch.Tensor, table: torch.Tensor, *, token_chunk_size: int) -> torch.Tensor:
+    """argmin_k |r|^2 + |c_k|^2 - 2 r.c_k in fp32, chunked over rows.
+
+    Follows src/jointkv/closed_loop_vq.py:52-76 (first index on ties).
+    states [H,N,D], table [H,K,D] -> int64 [H,N].
+    """
+
+    norms = table.square().sum(dim=-1)
+    out = []
+    for start in range(0, states.shape[1], token_chunk_size):
+        rows = states[:, start : start + token_chunk_size]
+        dist = rows.square().sum(dim=-1, keepdim=True) + norms[:, None, :] - 2.0 * torch.bmm(
+            rows, table.transpose(-1, -2)
+        )
+        out.append(dist.argmin(dim=-1))
+    return torch.cat(out, dim=1)
+
+
+def distances_top2(states: torch.Tensor, table: torch.Tensor, *, token_chunk_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Best and second-best fp32 distances with the same formula (for margins)."""
+
+    norms = table.square().sum(dim=-1)
+    best, second = [], []
+    for start in range(0, states.shape[1], token_chunk_size):
+        rows = states[:, start : start + token_chunk_size]
+        dist = rows.square().sum(dim=-1, keepdim=True) + norms[:, None, :] - 2.0 * torch.bmm(
+            rows, table.transpose(-1, -2)
+        )
+        k = min(2, dist.shape[-1])
+        vals = dist.topk(k, dim=-1, largest=False).values
+        best.append(vals[..., 0])
+        second.append(vals[..., -1] if k == 2 else torch.full_like(vals[..., 0], float("inf")))
+    return torch.cat(best, dim=1), torch.cat(second, dim=1)
+
+
+def hard_residual_vq_exits(
+    states: torch.Tensor,
+    tables: torch.Tensor,
+    *,
+    prefixes: Sequence[int],
+    assignment_whiteners: torch.Tensor | None = None,
+    token_chunk_size: int = 1024,
+    straight_through_states: bool = True,
+    return_margins: bool = False,
+):
+    """Greedy residual VQ exactly as src/jointkv/closed_loop_vq.py:235-410.
+
+    states [B,H,T,D], tables [H,S,K,D] (fp32 masters).  The search and the
+    reconstruction use ``tables.half().float()`` (:298); with a whitener the
+    search runs on W x and W c and subtracts whitened codewords (:312-330,
+    :384-390).  ``decoded`` accumulates fp32 codewords in stage order (:381)
+    and each exit is cast once to states.dtype (:396-402), plus the identity
+    straight-through edge (:408).  Autograd reaches the fp32 masters through
+    ``torch.gather`` (:376-381).  With ``return_margins`` also returns the
+    best and second-best fp32 search distances per (B,H,T,S).
+    """
+
+    batch, heads, tokens, dim = map(int, states.shape)
+    stages = int(tables.shape[1])
+    requested = tuple(sorted(set(int(p) for p in prefixes)))
+    x = states.detach().float()
+    raw = x.permute(1, 0, 2, 3).reshape(heads, batch * tokens, dim).contiguous().clone()
+    deployed = tables + (tables.half().float() - tables).detach()
+    frozen = deployed.detach().float()
+    search_rows = raw
+    search_tables = frozen
+    if assignment_whiteners is not None:
+        w = assignment_whiteners.detach().float()
+        search_rows = (
+            torch.einsum("hde,bhte->bhtd", w, x).permute(1, 0, 2, 3).reshape(heads, batch * tokens, dim).contiguous()
+        )
+        search_tables = torch.einsum("hrke,hde->hrkd", frozen, w)
+    decoded = torch.zeros((heads, batch * tokens, dim), dtype=torch.float32)
+    codes = torch.empty((batch, heads, tokens, stages), dtype=torch.uint8)
+    d1 = torch.empty((batch, heads, tokens, stages), dtype=torch.float32)
+    d2 = torch.empty_like(d1)
+    outputs = {}
+    for s in range(stages):
+        table_s = search_tables[:, s]
+        with torch.no_grad():
+            idx = nearest_indices(search_rows, table_s, token_chunk_size=token_chunk_size)
+            if return_margins:
+                b1, b2 = distances_top2(search_rows, table_s, token_chunk_size=token_chunk_size)
+                d1[..., s] = b1.reshape(heads, batch, tokens).permute(1, 0, 2)
+                d2[..., s] = b2.reshape(heads, batch, tokens).permute(1, 0, 2)
+        chosen = torch.gather(deployed[:, s].float(), 1, idx[..., None].expand(-1, -1, dim))
+        decoded = decoded + chosen
+        with torch.no_grad():
+            raw.sub_(chosen.detach())
+            if assignment_whiteners is not None:
+                search_rows.sub_(torch.gather(table_s, 1, idx[..., None].expand(-1, -1, dim)))
+            codes[..., s] = idx.reshape(heads, batch, tokens).permute(1, 0, 2).to(torch.uint8)
+        if s + 1 in requested:
+            out = decoded.reshape(heads, batch, tokens, dim).permute(1, 0, 2, 3).contiguous().to(states.dtype)
+            if straight_through_states:
+                out = out + (states - states.detach())
+            outputs[s + 1] = out
+    if return_margins:
+        return outputs, codes, d1, d2
+    return outputs, codes
+
+
+def grouped_residual_vq(
+    states: torch.Tensor,
+    tables: torch.Tensor,
+    *,
+    prefixes: Sequence[int],
+    token_chunk_size: int = 1024,
+    straight_through_states: bool = True,
+    return_margins: bool = False,
+):
+    """Grouped residual VQ via the reference's own call on folded heads.
+
+    states [B,H,T,G*d], tables [H,G,S,K,d]: fold (head, group) into the head
+    axis, call :func:`hard_residual_vq_exits` (the reference operator), and
+    unfold: codes [B,H,T,G,S], exits [B,H,T,G*d].
+    """
+
+    batch, heads, tokens, dim = map(int, states.shape)
+    _h, groups, stages, clusters, d = map(int, tables.shape)
+    folded = states.reshape(batch, heads, tokens, groups, d).permute(0, 1, 3, 2, 4).reshape(
+        batch, heads * groups, tokens, d
+    )
+    res = hard_residual_vq_exits(
+        folded,
+        tables.reshape(heads * groups, stages, clusters, d),
+        prefixes=prefixes,
+        token_chunk_size=token_chunk_size,
+        straight_through_states=straight_through_states,
+        return_margins=return_margins,
+    )
+    outputs, codes = res[0], res[1]
+
+    def unfold_rows(t):
+        return t.reshape(batch, heads, groups, tokens, -1).permute(0, 1, 3, 2, 4)
+
+    out = {k: unfold_rows(v).reshape(batch, heads, tokens, dim) for k, v in outputs.items()}
+    codes_u = unfold_rows(codes).contiguous()
+    if return_margins:
+        return out, codes_u, unfold_rows(res[2]).contiguous(), unfold_rows(res[3]).contiguous()
+    return out, codes_u
+
+
+def hard_grouped_cq(
+    states: torch.Tensor,
+    codebooks: torch.Tensor,
+    *,
+    selector_whiteners: torch.Tensor | None = None,
+    token_chunk_size: int = 64,
+    straight_through_states: bool = True,
+    return_margins: bool = False,
+):
+    """Grouped CQ exactly as src/jointkv/cq_tac.py:33-114.
+
+    states [B,H,T,D], codebooks [H,G,K,S] -> (recon [B,H,T,D], codes [B,H,T,G]).
+    """
+
+    batch, heads, tokens, dim = map(int, states.shape)
+    _h, groups, clusters, sub = map(int, codebooks.shape)
+    problems, rows_n = heads * groups, batch * tokens
+    raw = (
+        states.detach().float().permute(1, 0, 2, 3).reshape(heads, rows_n, groups, sub)
+        .permute(0, 2, 1, 3).reshape(problems, rows_n, sub).contiguous()
+    )
+    deployed = codebooks + (codebooks.half().float() - codebooks).detach()
+    search_tables = deployed.detach().float().reshape(problems, clusters, sub)
+    search_rows = raw
+    if selector_whiteners is not None:
+        f = selector_whiteners.detach().float().reshape(problems, sub, sub)
+        search_rows = torch.bmm(raw, f.transpose(1, 2))
+        search_tables = torch.bmm(search_tables, f.transpose(1, 2))
+    norms = search_tables.square().sum(-1).unsqueeze(1)
+    idx = torch.empty(problems, rows_n, dtype=torch.long)
+    b1 = torch.empty(problems, rows_n)
+    b2 = torch.empty(problems, rows_n)
+    for start in range(0, rows_n, token_chunk_size):
+        stop = min(start + token_chunk_size, rows_n)
+        cur = search_rows[:, start:stop]
+        dist = cur.square().sum(-1, keepdim=True) + norms - 2.0 * torch.bmm(cur, search_tables.transpose(1, 2))
+        idx[:, start:stop] = dist.argmin(-1)
+        if return_margins:
+            k = min(2, clusters)
+            vals = dist.topk(k, dim=-1, largest=False).values
+            b1[:, start:stop] = vals[..., 0]
+            b2[:, start:stop] = vals[..., -1] if k == 2 else float("inf")
+    live = deployed.reshape(problems, clusters, sub)
+    chosen = torch.gather(live, 1, idx[..., None].expand(-1, -1, sub))
+    out = (
+        chosen.reshape(heads, groups, batch, tokens, sub).permute(2, 0, 3, 1, 4)
+        .reshape(batch, heads, tokens, dim).to(states.dtype)
+    )
+    if straight_through_states:
+        out = out + (states - states.detach())
+
+    def shape_rows(t):
+        return t.reshape(heads, groups, batch, tokens).permute(2, 0, 3, 1).contiguous()
+
+    codes = shape_rows(idx).to(torch.uint8)
+    if return_margins:
+        return out, codes, shape_rows(b1), shape_rows(b2)
+    return out, codes
+
+
+def frozen_decode(codes: torch.Tensor, tables: torch.Tensor, depth: int, dtype: torch.dtype) -> torch.Tensor:
+    """fp16-deployed decode of given codes: codes [B,H,T,G,S], tables [H*G,S,K,d].
+
+    Same arithmetic as frozen_assignment_u16_reconstruction
+    (experiments/train_pure_uniform16_closed_loop_vq.py:395-442): fp32 sum of
+    fp16 round-tripped words in stage order, one cast at the end.
+    """
+
+    batch, heads, tokens, groups, stages = map(int, codes.shape)
+    problems, _s, clusters, d = map(int, tables.shape)
+    deployed = tables.detach().half().float()
+    flat = codes.long().permute(1, 3, 0, 2, 4).reshape(heads * groups, batch * tokens, stages)
+    acc = torch.zeros(problems, batch * tokens, d)
+    for s in range(depth):
+        acc = acc + torch.gather(deployed[:, s], 1, flat[..., s, None].expand(-1, -1, d))
+    return acc.reshape(heads, groups, batch, tokens, d).permute(2, 0, 3, 1, 4).reshape(
+        batch, heads, tokens, groups * d
+    ).to(dtype)
+
+
+def table_gradient(grads: Sequence[torch.Tensor], exits: Sequence[int], codes: torch.Tensor, table_shape) -> torch.Tensor:
+    """Closed form of the gather backward: codes [B,H,T,G,S], grads [B,H,T,G*d].
+
+    grad[p,s,k,:] = sum over rows with code[.., g, s] = k of
+    sum_{exits e: depth_e > s} fp32(grads_e[.., g*d:(g+1)*d]).
+    This is what autograd computes for closed_loop_vq.py:376-381 / cq_tac.py:98-99.
+    """
+
+    batch, heads, tokens, groups, stages = map(int, codes.shape)
+    problems, _s, clusters, d = map(int, table_shape)
+    out = torch.zeros(table_shape, dtype=torch.float32)
+    flat_codes = codes.long().permute(1, 3, 0, 2, 4).reshape(problems, batch * tokens, stages)
+    for s in range(stages):
+        g = None
+        for grad, depth in zip(grads, exits):
+            if depth > s:
+                gf = grad.float().reshape(batch, heads, tokens, groups, d).permute(1, 3, 0, 2, 4).reshape(
+                    problems, batch * tokens, d
+                )
+                g = gf if g is None else g + gf
+        if g is None:
+            continue
+        out[:, s].scatter_add_(1, flat_codes[..., s, None].expand(-1, -1, d), g)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Gradient clipping (experiments/train_pure_uniform16_closed_loop_vq.py:1151-1304)
+
+
+def clip_codebook_gradients(key_tables, value_tables, *, maximum_norm: float, mode: str) -> dict:
+    """Restatement with torch.nn.utils.clip_grad_norm_ on CPU parameters."""
+
+    if not math.isfinite(maximum_norm) or maximum_norm <= 0:
+        raise ValueError("gradient cap must be finite and positive")
+    groups = [(layer, kind, p) for kind, tabs in (("key", key_tables), ("value", value_tables)) for layer, p in enumerate(tabs)]
+
+    def norm(p):
+        return 0.0 if p.grad is None else float(torch.linalg.vector_norm(p.grad.detach().float()))
+
+    if mode == "global":
+        params = [p for _l, _k, p in groups if p.requires_grad]
+        if not params:
+            raise RuntimeError("gradient clipping received no trainable codebooks")
+        before = float(torch.nn.utils.clip_grad_norm_(params, maximum_norm))
+        return {
+            "mode": mode,
+            "group_count": len(groups),
+            "trainable_group_count": len(params),
+            "total_norm_before_clip": before,
+            "total_norm_after_clip": min(before, maximum_norm),
+            "global_scale": min(1.0, maximum_norm / (before + 1e-12)),
+            "per_group": None,
+        }
+    if mode not in {"per_layer_kv", "key_global_value_per_layer"}:
+        raise ValueError(f"unknown gradient clip mode: {mode}")
+    rows = []
+    if mode == "key_global_value_per_layer":
+        keys = [g for g in groups if g[1] == "key"]
+        key_before = {layer: norm(p) for layer, _k, p in keys}
+        key_total = math.sqrt(sum(v * v for v in key_before.values()))
+        key_params = [p for _l, _k, p in keys if p.requires_grad]
+        if key_params:
+            torch.nn.utils.clip_grad_norm_(key_params, maximum_norm)
+        for layer, kind, p in keys:
+            b, a = key_before[layer], norm(p)
+            rows.append({"layer": layer, "kind": kind, "norm_before_clip": b, "norm_after_clip": a,
+                         "scale": 1.0 if b == 0.0 else a / b, "clip_activated": key_total > maximum_norm})
+        rest = [g for g in groups if g[1] == "value"]
+    else:
+        rest = groups
+        key_total = None
+    for layer, kind, p in rest:
+        if p.grad is None:
+            b = a = 0.0
+        else:
+            b = norm(p)
+            torch.nn.utils.clip_grad_norm_([p], maximum_norm)
+            a = norm(p)
+        rows.append({"layer": layer, "kind": kind, "norm_before_clip": b, "norm_after_clip": a,
+                     "scale": 1.0 if b == 0.0 else a / b, "clip_activated": b > maximum_norm})
+    out = {
+        "mode": mode,
+        "total_norm_before_clip": math.sqrt(sum(r["norm_before_clip"] ** 2 for r in rows)),
+        "total_norm_after_clip": math.sqrt(sum(r["norm_after_clip"] ** 2 for r in rows)),
+        "per_group": rows,
+    }
+    if key_total is not None:
+        out["key_global_norm_before_clip"] = key_total
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Attention consumers
+
+
+def rotary_cos_sin(positions: torch.Tensor, head_dim: int, theta: float, dtype=torch.float16):
+    """Rotary tables as the HF Mistral/Llama rotary module builds them.
+
+    inv_freq = 1/theta^(arange(0,D,2)/D) in fp32; angle = position*inv_freq
+    in fp32; emb = cat(freqs, freqs); cos/sin in fp32 cast to ``dtype``
+    (transformers 4.45.1, third-party: restated from its published code).
+    """
+
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    freqs = positions.float()[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """(x * cos) + (rotate_half(x) * sin) in x.dtype (HF apply_rotary_pos_emb)."""
+
+    return (x * cos) + (rotate_half(x) * sin)
+
+
+def decode_attention(
+    q: torch.Tensor,
+    key_hat: torch.Tensor,
+    value_hat: torch.Tensor,
+    query_position: int,
+    key_positions: torch.Tensor,
+    *,
+    theta: float = 10000.0,
+) -> torch.Tensor:
+    """One decode step as evaluate_mistral_longbench.py:112-122.
+
+    q [B,QH,1,D] fp16 pre-RoPE; key_hat/value_hat [B,KVH,Tvis,D] fp16
+    (decoded, pre-RoPE); RoPE(q) at query_position, RoPE(K̂) at
+    key_positions, repeat_kv, SDPA without mask.  Returns [B,QH,1,D] fp16.
+    """
+
+    head_dim = q.shape[-1]
+    qc, qs = rotary_cos_sin(torch.tensor([query_position]), head_dim, theta)
+    kc, ks = rotary_cos_sin(key_positions, head_dim, theta)
+    qr = apply_rotary(q, qc[None, None], qs[None, None])
+    kr = apply_rotary(key_hat, kc[None, None], ks[None, None])
+    groups = q.shape[1] // key_hat.shape[1]
+    kr = kr.repeat_interleave(groups, dim=1)
+    vr = value_hat.repeat_interleave(groups, dim=1)
+    # fp32 math on the fp16-rounded operands; output rounded to fp16
+    out = F.scaled_dot_product_attention(qr.float(), kr.float(), vr.float(), attn_mask=None, dropout_p=0.0)
+    return out.to(torch.float16)
+
+
+def attention_fp64(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
+    """Textbook softmax(q k^T / sqrt(D)) v in fp64 (pin for the SDPA leg)."""
+
+    q64, k64, v64 = q_rot.double(), k_rot.double(), v.double()
+    scores = q64 @ k64.transpose(-1, -2) / math.sqrt(q64.shape[-1])
+    if mask is not None:
+        scores = scores.masked_fill(~mask, float("-inf"))
+    return torch.softmax(scores, dim=-1) @ v64
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs (fixed generator draw order)
+
+
+def synthetic_states(generator: torch.Generator, batch: int, heads: int, tokens: int, dim: int = 128,
+                     outliers: int = 4, outlier_scale: float = 8.0) -> torch.Tensor:
+    """N(0,1) states with ``outliers`` random channels per head scaled, as fp16."""
+
+    x = torch.randn(batch, heads, tokens, dim, generator=generator)
+    for h in range(heads):
+        channels = torch.randperm(dim, generator=generator)[:outliers]
+        x[:, h, :, channels] *= outlier_scale
+    return x.half()
+
+
+def synthetic_tables(generator: torch.Generator, shape, stage_sigmas: Sequence[float], stage_axis: int) -> torch.Tensor:
+    """fp16-valued fp32 codebooks; stage s drawn N(0, sigma_s^2)."""
+
+    t = torch.randn(*shape, generator=generator)
+    for s, sigma in enumerate(stage_sigmas):
+        index = [slice(None)] * len(shape)
+        index[stage_axis] = s
+        t[tuple(index)] *= sigma
+    return t.half().float()

@@ -1,0 +1,86 @@
+"""Build libjkv.so (the gfx950 HIP kernels behind include/jkv.h) in-tree.
+
+Usage: python tac-vq-kv-cache_amd/build_lib.py [--jobs N]
+
+Every ``csrc/*.hip`` file is compiled with hipcc for gfx950 only and linked
+into ``jointkv_amd/libjkv.so``.  Packed-fp32 VALU instructions are disabled
+for all device code.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent
+REPO_ROOT = PKG_ROOT.parent
+CSRC = PKG_ROOT / "csrc"
+INCLUDE = REPO_ROOT / "include"
+OUT = PKG_ROOT / "jointkv_amd" / "libjkv.so"
+BUILD_DIR = PKG_ROOT / "_build"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+CXXFLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-munsafe-fp-atomics",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-result",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    cmd = [HIPCC, *CXXFLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    return obj
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every kernel source and link ``libjkv.so``; returns its path."""
+
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    BUILD_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError("no HIP sources found")
+    workers = jobs or min(8, len(sources))
+    with cf.ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(_compile, sources))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT} from {len(sources)} sources", flush=True)
+    return OUT
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--jobs", type=int, default=None)
+    args = parser.parse_args()
+    build(args.jobs, verbose=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,58 @@
+"""jointkv_amd — MI355X (gfx950) hard residual-quantization hot path.
+
+Drop-in operator API of wrb1371/tac-vq-kv-cache's ``jointkv`` hot path
+(hard residual VQ / grouped CQ encode with straight-through gradients, the
+codec modules, codebook-gradient clipping, the rate ledger) plus fused decode
+attention over packed code caches.  All device work runs in the hand-written
+HIP kernels of ``libjkv.so``; there is no CPU fallback.
+"""
+
+from . import _lib
+from .attention import PackedCodeCache, decode_attention, deploy_tables
+from .budget import (
+    CacheGeometry,
+    StorageLedger,
+    dynamic_bpa,
+    paired_prefix_rates,
+    prefix_index_bits,
+    residual_vq_ledger,
+    validate_stage_bits,
+)
+from .calibration import clip_codebook_gradients, sgd_step
+from .closed_loop_vq import (
+    QuantizedKV,
+    frozen_assignment_reconstruction,
+    hard_grouped_residual_vq,
+    hard_residual_vq_exits,
+)
+from .cq_tac import ClosedLoopGroupedCQ, hard_grouped_cq
+from .packed_nested import pack_fixed_width, unpack_fixed_width
+from .uniform_depth_tac import ClosedLoopUniformResidualVQ
+
+__all__ = [
+    "CacheGeometry",
+    "ClosedLoopGroupedCQ",
+    "ClosedLoopUniformResidualVQ",
+    "PackedCodeCache",
+    "QuantizedKV",
+    "StorageLedger",
+    "clip_codebook_gradients",
+    "decode_attention",
+    "deploy_tables",
+    "dynamic_bpa",
+    "frozen_assignment_reconstruction",
+    "hard_grouped_cq",
+    "hard_grouped_residual_vq",
+    "hard_residual_vq_exits",
+    "pack_fixed_width",
+    "paired_prefix_rates",
+    "prefix_index_bits",
+    "residual_vq_ledger",
+    "sgd_step",
+    "unpack_fixed_width",
+    "validate_stage_bits",
+]
+
+
+def library_version() -> int:
+    return int(_lib.load().jkv_version())

@@ -1,0 +1,248 @@
+"""Thin tensor-level wrappers over the libjkv C ABI.
+
+Each function validates shapes and devices on the host, allocates outputs and
+workspaces with the PyTorch caching allocator, and enqueues one library call
+on the current HIP stream.  Nothing here computes on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+
+def _encode_states_strides(states: torch.Tensor) -> tuple[torch.Tensor, tuple[int, int, int]]:
+    if states.stride(-1) != 1:
+        states = states.contiguous()
+    return states, (states.stride(0), states.stride(1), states.stride(2))
+
+
+def rvq_encode(
+    states: torch.Tensor,
+    tables: torch.Tensor,
+    *,
+    groups: int,
+    group_dim: int,
+    exits: Sequence[int],
+    whiteners: torch.Tensor | None = None,
+) -> tuple[list[torch.Tensor], torch.Tensor]:
+    """Encode ``states[B,H,T,G*d]`` with fp32 masters ``tables[H*G,S,K,d]``.
+
+    Returns (reconstructions at each requested exit depth in ``exits`` order,
+    codes ``[B,H,T,G,S]`` uint8).
+    """
+
+    device = _lib.require_device(states, tables, whiteners)
+    batch, heads, tokens, dim = map(int, states.shape)
+    problems, stages, clusters, d = map(int, tables.shape)
+    if dim != groups * group_dim or d != group_dim or problems != heads * groups:
+        raise ValueError("state and table geometry differs")
+    if tables.dtype != torch.float32 or not tables.is_contiguous():
+        raise ValueError("encode tables must be contiguous fp32 masters")
+    if len(exits) > _lib.MAX_EXITS:
+        raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
+    lib = _lib.load()
+    states, (sb, sh, st) = _encode_states_strides(states)
+    codes = torch.empty((batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device)
+    recon = [torch.empty((batch, heads, tokens, dim), dtype=states.dtype, device=device) for _ in exits]
+    if whiteners is not None:
+        whiteners = whiteners.detach().float().contiguous()
+        if tuple(whiteners.shape) != (problems, d, d):
+            raise ValueError("assignment whitener has invalid geometry")
+    ws_bytes = int(lib.jkv_rvq_encode_workspace_bytes(heads, groups, stages, clusters, d, int(whiteners is not None)))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
+    depth_arr = _lib.ptr_array(ctypes.c_int32, [int(e) for e in exits])
+    recon_arr = _lib.ptr_array(ctypes.c_void_p, [r.data_ptr() for r in recon])
+    code = lib.jkv_rvq_encode(
+        states.data_ptr(), _lib.dtype_code(states.dtype), batch, heads, tokens, groups, d,
+        sb, sh, st, tables.data_ptr(), stages, clusters,
+        _lib.ptr(whiteners), codes.data_ptr(),
+        codes.stride(0), codes.stride(1), codes.stride(2),
+        len(exits), depth_arr, recon_arr,
+        _lib.ptr(workspace), ws_bytes, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return recon, codes
+
+
+def rvq_decode(
+    codes: torch.Tensor,
+    tables: torch.Tensor,
+    *,
+    depth: int,
+    dtype: torch.dtype,
+) -> torch.Tensor:
+    """``codes[B,H,T,G,S]`` + fp32 masters ``tables[H*G,S,K,d]`` -> ``[B,H,T,G*d]``."""
+
+    device = _lib.require_device(codes, tables)
+    batch, heads, tokens, groups, stages = map(int, codes.shape)
+    problems, t_stages, clusters, d = map(int, tables.shape)
+    if problems != heads * groups or t_stages != stages:
+        raise ValueError("code and table geometry differs")
+    if codes.dtype != torch.uint8 or codes.stride(-1) != 1 or codes.stride(-2) != stages:
+        raise ValueError("codes must be uint8 with a contiguous (G,S) block")
+    tables = tables.detach()
+    if tables.dtype != torch.float32 or not tables.is_contiguous():
+        tables = tables.float().contiguous()
+    out = torch.empty((batch, heads, tokens, groups * d), dtype=dtype, device=device)
+    code = _lib.load().jkv_rvq_decode(
+        codes.data_ptr(), codes.stride(0), codes.stride(1), codes.stride(2),
+        batch, heads, tokens, groups, d, tables.data_ptr(), stages, clusters, int(depth),
+        out.data_ptr(), _lib.dtype_code(dtype), _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return out
+
+
+def rvq_scatter_grad(
+    grads: Sequence[torch.Tensor],
+    exits: Sequence[int],
+    codes: torch.Tensor,
+    grad_tables: torch.Tensor,
+    *,
+    group_dim: int,
+    deterministic: bool = False,
+) -> None:
+    """Accumulate the straight-through codebook gradient into ``grad_tables``."""
+
+    device = _lib.require_device(codes, grad_tables, *grads)
+    batch, heads, tokens, groups, stages = map(int, codes.shape)
+    problems, t_stages, clusters, d = map(int, grad_tables.shape)
+    if problems != heads * groups or t_stages != stages or d != group_dim:
+        raise ValueError("code and gradient-table geometry differs")
+    if grad_tables.dtype != torch.float32 or not grad_tables.is_contiguous():
+        raise ValueError("gradient tables must be contiguous fp32")
+    dtype = grads[0].dtype
+    grads = [g.to(dtype).contiguous() for g in grads]
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_rvq_scatter_workspace_bytes(batch, heads, tokens, groups, d, stages, clusters, int(deterministic)))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    code = lib.jkv_rvq_scatter_grad(
+        len(grads), _lib.ptr_array(ctypes.c_void_p, [g.data_ptr() for g in grads]),
+        _lib.dtype_code(dtype), _lib.ptr_array(ctypes.c_int32, [int(e) for e in exits]),
+        codes.data_ptr(), codes.stride(0), codes.stride(1), codes.stride(2),
+        batch, heads, tokens, groups, d, stages, clusters, grad_tables.data_ptr(),
+        int(deterministic), _lib.ptr(workspace), ws_bytes, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+
+
+def sumsq(tensors: Sequence[torch.Tensor]) -> torch.Tensor:
+    """fp64 squared L2 norms of fp32 device tensors, as one device tensor."""
+
+    device = _lib.require_device(*tensors)
+    flat = [t.detach() for t in tensors]
+    for t in flat:
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("norm inputs must be contiguous fp32")
+    out = torch.empty(len(flat), dtype=torch.float64, device=device)
+    code = _lib.load().jkv_sumsq(
+        len(flat), _lib.ptr_array(ctypes.c_void_p, [t.data_ptr() for t in flat]),
+        _lib.ptr_array(ctypes.c_int64, [t.numel() for t in flat]),
+        out.data_ptr(), _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return out
+
+
+def scale_sgd(
+    grads: Sequence[torch.Tensor],
+    scales: Sequence[float],
+    *,
+    params: Sequence[torch.Tensor] | None = None,
+    lr: float = 0.0,
+) -> None:
+    """``grad *= scale`` in place and, when ``lr`` is non-zero, ``param -= lr*grad``."""
+
+    device = _lib.require_device(*grads)
+    if params is not None and len(params) != len(grads):
+        raise ValueError("parameter and gradient lists differ")
+    for g in grads:
+        if g.dtype != torch.float32 or not g.is_contiguous():
+            raise ValueError("gradients must be contiguous fp32")
+    if params is not None:
+        for p, g in zip(params, grads):
+            if p.dtype != torch.float32 or not p.is_contiguous() or p.shape != g.shape:
+                raise ValueError("parameters must be contiguous fp32 matching their gradients")
+    code = _lib.load().jkv_scale_sgd(
+        len(grads),
+        None if params is None else _lib.ptr_array(ctypes.c_void_p, [p.data_ptr() for p in params]),
+        _lib.ptr_array(ctypes.c_void_p, [g.data_ptr() for g in grads]),
+        _lib.ptr_array(ctypes.c_int64, [g.numel() for g in grads]),
+        _lib.ptr_array(ctypes.c_float, [float(s) for s in scales]),
+        float(lr), _lib.stream_handle(device),
+    )
+    _lib.check(code)
+
+
+def f32_to_f16(tensor: torch.Tensor) -> torch.Tensor:
+    """The deploy round trip ``tensor.half()`` through the library."""
+
+    device = _lib.require_device(tensor)
+    src = tensor.detach()
+    if src.dtype != torch.float32 or not src.is_contiguous():
+        src = src.float().contiguous()
+    out = torch.empty(src.shape, dtype=torch.float16, device=device)
+    _lib.check(_lib.load().jkv_f32_to_f16(src.data_ptr(), out.data_ptr(), src.numel(), _lib.stream_handle(device)))
+    return out
+
+
+def decode_attention(
+    q: torch.Tensor,
+    key_codes: torch.Tensor,
+    value_codes: torch.Tensor,
+    key_tables16: torch.Tensor,
+    value_tables16: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    window: int,
+    rope_theta: float,
+) -> torch.Tensor:
+    """One decode step of GQA attention straight from the packed code cache.
+
+    ``q[B,QH,D]`` fp16 (pre-RoPE), codes ``[B,KVH,cap,G,S]`` uint8, fp16
+    deployed tables ``[KVH*G,S,K,d]``, ``lengths[B]`` int32 (cache length
+    including the new token).  Returns ``[B,QH,D]`` fp16.
+    """
+
+    device = _lib.require_device(q, key_codes, value_codes, key_tables16, value_tables16, lengths)
+    if q.dtype != torch.float16 or q.ndim != 3 or q.stride(-1) != 1:
+        raise ValueError("decode queries must be fp16 [B,QH,D] with a contiguous last axis")
+    batch, qheads, dim = map(int, q.shape)
+    if key_codes.shape != value_codes.shape or key_codes.dtype != torch.uint8:
+        raise ValueError("key/value code caches differ")
+    kb, kvheads, cap, groups, stages = map(int, key_codes.shape)
+    if kb != batch:
+        raise ValueError("query and cache batch differ")
+    for c in (key_codes, value_codes):
+        if c.stride(-1) != 1 or c.stride(-2) != stages or c.stride(-3) != groups * stages:
+            raise ValueError("code caches need contiguous [cap,G,S] blocks")
+    if key_codes.stride() != value_codes.stride():
+        raise ValueError("key/value code caches need identical strides")
+    problems, t_stages, clusters, d = map(int, key_tables16.shape)
+    if key_tables16.shape != value_tables16.shape or problems != kvheads * groups or t_stages != stages:
+        raise ValueError("code-cache and codebook geometry differs")
+    if key_tables16.dtype != torch.float16 or value_tables16.dtype != torch.float16:
+        raise ValueError("decode codebooks must be fp16 deployed tables")
+    key_tables16 = key_tables16.contiguous()
+    value_tables16 = value_tables16.contiguous()
+    if lengths.dtype != torch.int32 or lengths.shape != (batch,):
+        raise ValueError("lengths must be int32 [B]")
+    lengths = lengths.contiguous()
+    lib = _lib.load()
+    out = torch.empty((batch, qheads, dim), dtype=torch.float16, device=device)
+    ws_bytes = int(lib.jkv_decode_workspace_bytes(batch, qheads, dim, int(window)))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    code = lib.jkv_decode_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), key_codes.data_ptr(), value_codes.data_ptr(),
+        key_codes.stride(0), key_codes.stride(1), cap, key_tables16.data_ptr(),
+        value_tables16.data_ptr(), batch, qheads, kvheads, groups, d, stages, clusters,
+        lengths.data_ptr(), int(window), float(rope_theta), out.data_ptr(),
+        workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return out

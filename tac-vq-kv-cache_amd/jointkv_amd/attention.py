@@ -1,0 +1,134 @@
+"""Decode attention straight from a packed uint8 code cache.
+
+The reference's LongBench decode loop (experiments_followup_mistral/
+evaluate_mistral_longbench.py:29-124) keeps uint8 codes *and* a decoded fp16
+4096-token workspace, re-applies RoPE to all visible keys every step, repeats
+K/V across the GQA group and calls SDPA.  Here the cache holds only codes
+(a ring buffer of ``capacity`` slots per (batch, kv head)), and one fused
+kernel rebuilds K̂/V̂ from fp16 codewords, rotates K̂ at its absolute
+position, and runs split-KV softmax attention for every query head of the
+group.  The fp16 workspace, the RoPE pass over the window, ``repeat_kv`` and
+the O(T) ``torch.cat`` appends disappear.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _ops
+
+MISTRAL_WINDOW = 4096
+MISTRAL_ROPE_THETA = 10000.0
+
+
+def deploy_tables(tables: torch.Tensor, groups: int | None = None) -> torch.Tensor:
+    """fp16 deployed codebooks ``[KVH*G,S,K,d]`` from fp32 masters.
+
+    Accepts ``[H,S,K,D]`` (residual VQ, G=1), ``[H,G,S,K,d]`` (grouped
+    residual) or ``[H,G,K,d]`` with ``groups`` given (grouped CQ, S=1).
+    """
+
+    if tables.ndim == 5:
+        h, g, s, k, d = tables.shape
+        flat = tables.reshape(h * g, s, k, d)
+    elif tables.ndim == 4 and groups is not None:
+        h, g, k, d = tables.shape
+        flat = tables.reshape(h * g, 1, k, d)
+    elif tables.ndim == 4:
+        flat = tables
+    else:
+        raise ValueError("unsupported codebook geometry")
+    return _ops.f32_to_f16(flat.contiguous())
+
+
+def decode_attention(
+    query: torch.Tensor,
+    key_codes: torch.Tensor,
+    value_codes: torch.Tensor,
+    key_tables16: torch.Tensor,
+    value_tables16: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    window: int = MISTRAL_WINDOW,
+    rope_theta: float = MISTRAL_ROPE_THETA,
+) -> torch.Tensor:
+    """Attention output for one new token per sequence.
+
+    ``query``: pre-RoPE ``[B,QH,1,D]`` or ``[B,QH,D]`` fp16.  ``key_codes``,
+    ``value_codes``: ``[B,KVH,cap,G,S]`` (or ``[B,KVH,cap,G*S]``) uint8 with
+    position p in slot ``p % cap``.  ``lengths[b]`` counts the cached tokens
+    including the new one, so the query sits at position ``lengths[b]-1``
+    and sees the last ``min(window, lengths[b])`` positions (the reference's
+    ``LayerCache.visible``).  Returns ``[B,QH,1,D]`` (or ``[B,QH,D]``) fp16.
+    """
+
+    squeeze = query.ndim == 3
+    q = query if squeeze else query.reshape(query.shape[0], query.shape[1], query.shape[-1])
+    if key_codes.ndim == 4:
+        groups = key_tables16.shape[0] // key_codes.shape[1]
+        stages = key_codes.shape[-1] // groups
+        key_codes = key_codes.unflatten(-1, (groups, stages))
+        value_codes = value_codes.unflatten(-1, (groups, stages))
+    out = _ops.decode_attention(
+        q, key_codes, value_codes, key_tables16, value_tables16, lengths,
+        window=window, rope_theta=rope_theta,
+    )
+    return out if squeeze else out.unsqueeze(2)
+
+
+class PackedCodeCache:
+    """Per-layer uint8 code cache for batched decode (ring buffer).
+
+    Replaces ``LayerCache`` (evaluate_mistral_longbench.py:29-78) for the
+    quantized path: it stores K and V codes only, appends in O(new tokens)
+    into slot ``position % capacity``, and tracks per-sequence lengths.
+    """
+
+    def __init__(
+        self,
+        batch: int,
+        kv_heads: int,
+        groups: int,
+        stages: int,
+        *,
+        capacity: int = MISTRAL_WINDOW,
+        device: torch.device | str = "cuda",
+    ) -> None:
+        if min(batch, kv_heads, groups, stages, capacity) <= 0:
+            raise ValueError("invalid code-cache geometry")
+        shape = (batch, kv_heads, capacity, groups, stages)
+        self.key = torch.zeros(shape, dtype=torch.uint8, device=device)
+        self.value = torch.zeros(shape, dtype=torch.uint8, device=device)
+        self.lengths = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.capacity = capacity
+        self._host_length = 0
+
+    @property
+    def length(self) -> int:
+        return self._host_length
+
+    def append(self, key_codes: torch.Tensor, value_codes: torch.Tensor) -> None:
+        """Append ``[B,KVH,T,G,S]`` codes for T new positions (all sequences)."""
+
+        if key_codes.shape != value_codes.shape or key_codes.dtype != torch.uint8:
+            raise ValueError("key/value codes differ")
+        new = int(key_codes.shape[2])
+        if new > self.capacity:
+            key_codes = key_codes[:, :, -self.capacity :]
+            value_codes = value_codes[:, :, -self.capacity :]
+            self._host_length += new - self.capacity
+            new = self.capacity
+        start = self._host_length % self.capacity
+        first = min(new, self.capacity - start)
+        self.key[:, :, start : start + first] = key_codes[:, :, :first]
+        self.value[:, :, start : start + first] = value_codes[:, :, :first]
+        if first < new:
+            self.key[:, :, : new - first] = key_codes[:, :, first:]
+            self.value[:, :, : new - first] = value_codes[:, :, first:]
+        self._host_length += new
+        self.lengths.fill_(self._host_length)
+
+    def payload_bytes(self) -> int:
+        visible = min(self._host_length, self.capacity)
+        per_slot = self.key.shape[3] * self.key.shape[4]
+        return 2 * self.key.shape[0] * self.key.shape[1] * visible * per_slot

@@ -1,0 +1,88 @@
+"""C ABI checks that need no GPU: exports, signatures, argument validation."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from jointkv_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "jkv.h"
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(jkv_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert "jkv_rvq_encode" in declared and "jkv_decode_attention" in declared
+    for name in declared:
+        assert hasattr(lib, name), f"libjkv.so does not export {name}"
+    assert declared == set(_lib.SIGNATURES), "ctypes signatures out of sync with include/jkv.h"
+
+
+def test_version_and_error_text():
+    lib = _lib.load()
+    assert lib.jkv_version() >= 100
+    assert isinstance(lib.jkv_last_error(), bytes)
+
+
+def _encode_call(**overrides):
+    lib = _lib.load()
+    args = dict(states=1, dtype=0, B=1, H=1, T=4, G=1, d=8, sb=32, sh=32, st=8, tables=1, S=1, K=256,
+                whiteners=None, codes=1, cb=4, ch=4, ct=1, n_exits=0, exits=None, recon=None,
+                ws=None, ws_bytes=0, stream=None)
+    args.update(overrides)
+    return lib.jkv_rvq_encode(*args.values())
+
+
+def test_encode_rejects_invalid_geometry_before_touching_the_device():
+    # These return before any HIP call, so they run without a GPU.
+    assert _encode_call(K=300) == _lib.JKV_EINVAL
+    assert b"256" in _lib.load().jkv_last_error()
+    assert _encode_call(d=0) == _lib.JKV_EINVAL
+    assert _encode_call(dtype=7) == _lib.JKV_EINVAL
+    assert _encode_call(d=200) == _lib.JKV_EINVAL
+    depths = (ctypes.c_int32 * 1)(5)
+    assert _encode_call(n_exits=1, exits=depths, S=2) == _lib.JKV_EINVAL
+    assert b"ladder" in _lib.load().jkv_last_error()
+    # an empty problem is a successful no-op
+    assert _encode_call(T=0) == _lib.JKV_OK
+
+
+def test_workspace_queries():
+    lib = _lib.load()
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 0) == 0
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 1) == 8 * 16 * 2 * 256 * 8 * 4
+    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, 0) == 0
+    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, 1) == 2 * 8 * 16 * 2 * 256 * 8 * 4
+    assert lib.jkv_decode_workspace_bytes(16, 32, 128, 4096) == 16 * 32 * 16 * 130 * 4
+
+
+def test_decode_rejects_unsupported_geometry():
+    # Only argument combinations that fail validation: a valid geometry with
+    # placeholder pointers would launch a kernel.
+    lib = _lib.load()
+    rc = lib.jkv_decode_attention(1, 0, 0, 1, 1, 0, 0, 4096, 1, 1, 1, 32, 8, 8, 8, 2, 256, 1,
+                                  4096, 10000.0, 1, 1, 1 << 30, None)
+    assert rc == _lib.JKV_EINVAL and b"head_dim" in lib.jkv_last_error()
+    rc = lib.jkv_decode_attention(1, 0, 0, 1, 1, 0, 0, 100, 1, 1, 1, 32, 8, 16, 8, 2, 256, 1,
+                                  4096, 10000.0, 1, 1, 1 << 30, None)
+    assert rc == _lib.JKV_EINVAL and b"capacity" in lib.jkv_last_error()
+
+
+def test_product_rejects_host_tensors_loudly():
+    import jointkv_amd as jkv
+
+    states = torch.randn(1, 2, 4, 8)
+    tables = torch.randn(2, 1, 256, 8)
+    with pytest.raises(ValueError, match="HIP"):
+        jkv.hard_residual_vq_exits(states, tables, prefixes=(1,))

@@ -1,0 +1,74 @@
+"""Fused decode attention over packed code caches vs the oracle's
+decode -> RoPE -> repeat_kv -> SDPA sequence (2e-3 max abs)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import jointkv_amd as jkv
+from oracle import jointkv_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _case(seed, batch, qh, kvh, groups, stages, d, length, cap):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, qh, 1, 128, generator=gen).half()
+    kc = torch.randint(0, 256, (batch, kvh, cap, groups, stages), generator=gen, dtype=torch.uint8)
+    vc = torch.randint(0, 256, (batch, kvh, cap, groups, stages), generator=gen, dtype=torch.uint8)
+    sig = (1.0, 0.5, 0.25, 0.125)[:stages]
+    kt = ref.synthetic_tables(gen, (kvh * groups, stages, 256, d), sig, stage_axis=1)
+    vt = ref.synthetic_tables(gen, (kvh * groups, stages, 256, d), sig, stage_axis=1)
+    return q, kc, vc, kt, vt
+
+
+def _expect(q, kc, vc, kt, vt, length, window, cap):
+    start = max(0, length - window)
+    pos = torch.arange(start, length)
+    slots = pos % cap
+    khat = ref.frozen_decode(kc[:, :, slots].contiguous(), kt, kt.shape[1], torch.float16)
+    vhat = ref.frozen_decode(vc[:, :, slots].contiguous(), vt, vt.shape[1], torch.float16)
+    return ref.decode_attention(q, khat, vhat, length - 1, pos)
+
+
+@pytest.mark.parametrize("batch,qh,kvh,groups,stages,d,length,window,cap", [
+    (2, 32, 8, 16, 2, 8, 4096, 4096, 4096),   # config 4 geometry, full window
+    (1, 8, 2, 16, 2, 8, 300, 4096, 4096),     # short prefix
+    (1, 8, 2, 16, 2, 8, 5000, 4096, 4096),    # window slides, ring buffer wraps
+    (1, 4, 4, 32, 1, 4, 700, 512, 512),       # cq2 codes, MHA group of 1
+    (1, 16, 2, 16, 1, 8, 257, 4096, 4096),    # cq1 codes, GQA 8
+])
+def test_decode_matches_oracle(device, batch, qh, kvh, groups, stages, d, length, window, cap):
+    q, kc, vc, kt, vt = _case(length + qh, batch, qh, kvh, groups, stages, d, length, cap)
+    print(f"decode B={batch} QH={qh} KVH={kvh} G={groups} S={stages} len={length} win={window}", flush=True)
+    out = jkv.decode_attention(
+        q.to(device), kc.to(device), vc.to(device), kt.half().to(device), vt.half().to(device),
+        torch.full((batch,), length, dtype=torch.int32, device=device), window=window,
+    )
+    expect = _expect(q, kc, vc, kt, vt, length, window, cap)
+    err = float((out.cpu().float() - expect.float()).abs().max())
+    assert err <= ATOL, f"max abs error {err}"
+
+
+def test_ragged_lengths_and_cache_append(device):
+    batch = 3
+    q, kc, vc, kt, vt = _case(5, batch, 8, 2, 16, 2, 8, 0, 1024)
+    lengths = torch.tensor([1, 333, 1024], dtype=torch.int32)
+    out = jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device),
+                               vt.half().to(device), lengths.to(device), window=4096)
+    for b in range(batch):
+        L = int(lengths[b])
+        e = _expect(q[b : b + 1], kc[b : b + 1], vc[b : b + 1], kt, vt, L, 4096, 1024)
+        err = float((out[b : b + 1].cpu().float() - e.float()).abs().max())
+        assert err <= ATOL, f"batch {b} length {L}: {err}"
+    # PackedCodeCache: appends land at position % capacity
+    cache = jkv.PackedCodeCache(1, 2, 16, 2, capacity=8, device=device)
+    seq = torch.randint(0, 256, (1, 2, 11, 16, 2), dtype=torch.uint8, device=device)
+    cache.append(seq[:, :, :5], seq[:, :, :5])
+    cache.append(seq[:, :, 5:11], seq[:, :, 5:11])
+    assert cache.length == 11 and int(cache.lengths[0]) == 11
+    for p in range(3, 11):
+        assert torch.equal(cache.key[:, :, p % 8], seq[:, :, p])

@@ -1,0 +1,167 @@
+"""Encode parity on the MI355X: HIP kernels vs the CPU oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import jointkv_amd as jkv
+from oracle import jointkv_oracle as ref
+
+from parity import assert_codes, assert_recon_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def test_config1_grouped_cq_full_size(device):
+    # [1,8,2048,128] fp16 with 4 outlier channels per head,
+    # codebooks [8,16,256,8] N(0,1), seed 8601 (K then V).
+    gen = _gen(8601)
+    key = ref.synthetic_states(gen, 1, 8, 2048)
+    value = ref.synthetic_states(gen, 1, 8, 2048)
+    kbook = ref.synthetic_tables(gen, (8, 16, 256, 8), (1.0,), stage_axis=0)
+    vbook = ref.synthetic_tables(gen, (8, 16, 256, 8), (1.0,), stage_axis=0)
+    for states, books in ((key, kbook), (value, vbook)):
+        print(f"config1 grouped CQ {tuple(states.shape)} x {tuple(books.shape)}", flush=True)
+        out, codes = jkv.hard_grouped_cq(states.to(device), books.to(device))
+        r_out, r_codes, d1, d2 = ref.hard_grouped_cq(states, books, return_margins=True)
+        res = assert_codes(codes[..., None], r_codes[..., None], d1[..., None], d2[..., None])
+        rows = (codes.cpu() == r_codes)
+        # per-group rows: compare 8-dim slices
+        o = out.cpu().reshape(1, 8, 2048, 16, 8)
+        r = r_out.detach().reshape(1, 8, 2048, 16, 8)
+        assert_recon_rows(o, r, rows)
+        assert codes.dtype == torch.uint8 and codes.shape == (1, 8, 2048, 16)
+        assert res["agreement"] >= 0.9999
+
+
+@pytest.mark.parametrize("tokens,batch", [(512, 1), (300, 2)])
+def test_grouped_residual_two_stage(device, tokens, batch):
+    # G2 geometry of BASELINE config 2 (16 groups x 8 dims, 2 stages, s2 sigma 0.5)
+    gen = _gen(8601 + tokens)
+    states = ref.synthetic_states(gen, batch, 8, tokens)
+    tables = ref.synthetic_tables(gen, (8, 16, 2, 256, 8), (1.0, 0.5), stage_axis=2)
+    print(f"G2 encode B={batch} T={tokens}", flush=True)
+    exits, codes = jkv.hard_grouped_residual_vq(states.to(device), tables.to(device), prefixes=(1, 2))
+    r_exits, r_codes, d1, d2 = ref.grouped_residual_vq(states, tables, prefixes=(1, 2), return_margins=True)
+    res = assert_codes(codes, r_codes, d1, d2)
+    for depth in (1, 2):
+        o = exits[depth].cpu().reshape(batch, 8, tokens, 16, 8)
+        r = r_exits[depth].detach().reshape(batch, 8, tokens, 16, 8)
+        assert_recon_rows(o, r, res["prefix_ok"])
+
+
+def test_cq2_geometry_d4(device):
+    # reference cq2 cell: [8,32,256,4] (BASELINE config 3 geometry)
+    gen = _gen(8602)
+    states = ref.synthetic_states(gen, 2, 8, 256)
+    books = ref.synthetic_tables(gen, (8, 32, 256, 4), (1.0,), stage_axis=0)
+    out, codes = jkv.hard_grouped_cq(states.to(device), books.to(device))
+    r_out, r_codes, d1, d2 = ref.hard_grouped_cq(states, books, return_margins=True)
+    res = assert_codes(codes[..., None], r_codes[..., None], d1[..., None], d2[..., None])
+    assert_recon_rows(out.cpu().reshape(2, 8, 256, 32, 4), r_out.detach().reshape(2, 8, 256, 32, 4),
+                      codes.cpu() == r_codes)
+
+
+@pytest.mark.parametrize("seed,dtype,dim,stages,clusters", [
+    (7, torch.float32, 4, 3, 4),
+    (9, torch.float32, 4, 3, 4),
+    (10, torch.float16, 4, 3, 4),
+    (43, torch.float32, 3, 2, 8),
+    (5, torch.bfloat16, 16, 3, 64),
+    (6, torch.float16, 128, 2, 256),
+])
+def test_residual_vq_generic_geometries(device, seed, dtype, dim, stages, clusters):
+    # the reference's own tiny cases (tests/test_closed_loop_vq.py) and wider ones
+    gen = _gen(seed)
+    states = torch.randn(1, 2, 37, dim, generator=gen).to(dtype)
+    tables = torch.randn(2, stages, clusters, dim, generator=gen)
+    prefixes = tuple(range(1, stages + 1))
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=prefixes)
+    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=prefixes,
+                                                          return_margins=True)
+    res = assert_codes(codes, r_codes, d1, d2, agreement=0.99)
+    for depth in prefixes:
+        assert exits[depth].dtype == dtype
+        assert_recon_rows(exits[depth].cpu(), r_exits[depth].detach(), res["prefix_ok"])
+
+
+@pytest.mark.parametrize("seed", [41, 42])
+def test_whitened_search(device, seed):
+    gen = _gen(seed)
+    states = torch.randn(1, 2, 64, 8, generator=gen).half()
+    tables = torch.randn(2, 3, 32, 8, generator=gen)
+    w = torch.randn(2, 8, 8, generator=gen)
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=(3,),
+                                              assignment_whiteners=w.to(device))
+    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=(3,),
+                                                          assignment_whiteners=w, return_margins=True)
+    res = assert_codes(codes, r_codes, d1, d2, agreement=0.99)
+    assert_recon_rows(exits[3].cpu(), r_exits[3].detach(), res["prefix_ok"])
+    # grouped CQ with a per-(head, group) selector whitener
+    books = torch.randn(2, 4, 256, 2, generator=gen)
+    f = torch.randn(2, 4, 2, 2, generator=gen)
+    st = torch.randn(1, 2, 64, 8, generator=gen)
+    out, c = jkv.hard_grouped_cq(st.to(device), books.to(device), selector_whiteners=f.to(device))
+    r_out, r_c, e1, e2 = ref.hard_grouped_cq(st, books, selector_whiteners=f, return_margins=True)
+    assert_codes(c[..., None], r_c[..., None], e1[..., None], e2[..., None], agreement=0.99)
+
+
+def test_edge_cases_empty_ragged_and_ties(device):
+    tables = torch.randn(2, 2, 256, 8)
+    # empty token axis
+    exits, codes = jkv.hard_grouped_residual_vq(torch.zeros(1, 2, 0, 16, dtype=torch.float16, device=device),
+                                                tables.reshape(2, 1, 2, 256, 8).expand(2, 2, 2, 256, 8).contiguous().to(device),
+                                                prefixes=(2,))
+    assert codes.shape == (1, 2, 0, 2, 2) and exits[2].shape == (1, 2, 0, 16)
+    # ragged tile: 17 rows; duplicated codewords -> lowest index wins (argmin)
+    dup = torch.randn(1, 1, 256, 8)
+    dup[0, 0, 200] = dup[0, 0, 3]
+    states = dup[0, 0, 3].repeat(1, 1, 17, 1).half()
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), dup.to(device), prefixes=(1,))
+    assert bool((codes.cpu() == 3).all())
+    # non-contiguous states view (strided heads)
+    base = ref.synthetic_states(_gen(3), 1, 4, 33)
+    view = base[:, ::2]
+    t = ref.synthetic_tables(_gen(4), (2, 16, 2, 256, 8), (1.0, 0.5), stage_axis=2)
+    e1, c1 = jkv.hard_grouped_residual_vq(view.to(device), t.to(device), prefixes=(2,))
+    e2, c2 = jkv.hard_grouped_residual_vq(view.contiguous().to(device), t.to(device), prefixes=(2,))
+    assert torch.equal(c1, c2) and torch.equal(e1[2], e2[2])
+
+
+def test_inputs_are_not_mutated(device):
+    gen = _gen(170817)
+    states = ref.synthetic_states(gen, 1, 2, 64).to(device)
+    tables = ref.synthetic_tables(gen, (2, 16, 2, 256, 8), (1.0, 0.5), stage_axis=2).to(device)
+    s0, t0 = states.clone(), tables.clone()
+    jkv.hard_grouped_residual_vq(states, tables, prefixes=(2,))
+    assert torch.equal(states, s0) and torch.equal(tables, t0)
+
+
+def test_full_size_layer_properties(device):
+    # BASELINE config 2 at full per-layer size: [1,8,8192,128], G2 tables.
+    gen = _gen(8601)
+    states = ref.synthetic_states(gen, 1, 8, 8192).to(device)
+    tables = ref.synthetic_tables(gen, (8, 16, 2, 256, 8), (1.0, 0.5), stage_axis=2).to(device)
+    exits, codes = jkv.hard_grouped_residual_vq(states, tables, prefixes=(1, 2))
+    # exits equal the frozen decode of the codes (two independent kernels)
+    flat = tables.reshape(128, 2, 256, 8)
+    for depth in (1, 2):
+        dec = jkv.closed_loop_vq._ops.rvq_decode(codes, flat, depth=depth, dtype=torch.float16)
+        assert torch.equal(dec, exits[depth])
+    # a sampled subset checked against the oracle
+    sub = slice(4096, 4096 + 256)
+    r_exits, r_codes, d1, d2 = ref.grouped_residual_vq(states[:, :, sub].cpu(), tables.cpu(), prefixes=(2,),
+                                                       return_margins=True)
+    assert_codes(codes[:, :, sub], r_codes, d1, d2)
+    # stage-1 optimality: the chosen word is at least as close (fp64) as every other
+    x = states[0, :, :512].float().reshape(8, 512, 16, 8).cpu().double()
+    c1 = tables[:, :, 0].cpu().double()  # [8,16,256,8]
+    dist = ((x[:, :, :, None, :] - c1[:, None]) ** 2).sum(-1)  # [8,512,16,256]
+    chosen = dist.gather(-1, codes[0, :, :512, :, 0].long().cpu()[..., None])[..., 0]
+    best = dist.min(-1).values
+    assert bool(((chosen - best) <= 1e-3 * best.clamp_min(1e-9)).all())

@@ -159,9 +159,9 @@ def test_full_size_layer_properties(device):
                                                        return_margins=True)
     assert_codes(codes[:, :, sub], r_codes, d1, d2)
     # stage-1 optimality: the chosen word is at least as close (fp64) as every other
-    x = states[0, :, :512].float().reshape(8, 512, 16, 8).cpu().double()
+    x = states[0, :, :64].float().reshape(8, 64, 16, 8).cpu().double()
     c1 = tables[:, :, 0].cpu().double()  # [8,16,256,8]
-    dist = ((x[:, :, :, None, :] - c1[:, None]) ** 2).sum(-1)  # [8,512,16,256]
-    chosen = dist.gather(-1, codes[0, :, :512, :, 0].long().cpu()[..., None])[..., 0]
+    dist = ((x[:, :, :, None, :] - c1[:, None]) ** 2).sum(-1)  # [8,64,16,256]
+    chosen = dist.gather(-1, codes[0, :, :64, :, 0].long().cpu()[..., None])[..., 0]
     best = dist.min(-1).values
     assert bool(((chosen - best) <= 1e-3 * best.clamp_min(1e-9)).all())

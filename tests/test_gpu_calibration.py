@@ -144,8 +144,18 @@ def test_grouped_cq_codec_identity_selector(device):
     raw_k = ref.synthetic_states(gen, 1, 8, 64).to(device)
     raw_v = ref.synthetic_states(gen, 1, 8, 64).to(device)
     q = codec(0, raw_k, raw_v)
-    o, c = jkv.hard_grouped_cq(raw_k, books_k[0].to(device), selector_whiteners=eye.to(device))
+    # the identity selector is recognised at construction: same kernel and
+    # bits as the unwhitened call
+    o, c = jkv.hard_grouped_cq(raw_k, books_k[0].to(device))
     assert torch.equal(q.key_indices, c) and torch.equal(q.key, o)
+    # the explicitly whitened (generic fp32) path agrees with the oracle to the
+    # margin rule; near-ties may resolve differently between the two kernels
+    ow, cw = jkv.hard_grouped_cq(raw_k, books_k[0].to(device), selector_whiteners=eye.to(device))
+    _r, r_c, d1, d2 = ref.hard_grouped_cq(raw_k.cpu(), books_k[0], selector_whiteners=eye, return_margins=True)
+    from parity import assert_codes
+
+    assert_codes(cw[..., None], r_c[..., None], d1[..., None], d2[..., None], agreement=0.999)
+    assert_codes(c[..., None], r_c[..., None], d1[..., None], d2[..., None], agreement=0.999)
     with pytest.raises(ValueError, match="one fixed-rate uniform mode"):
         codec(0, raw_k, raw_v, mode="x")
 

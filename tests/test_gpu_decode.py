@@ -57,11 +57,15 @@ def test_ragged_lengths_and_cache_append(device):
     batch = 3
     q, kc, vc, kt, vt = _case(5, batch, 8, 2, 16, 2, 8, 0, 1024)
     lengths = torch.tensor([1, 333, 1024], dtype=torch.int32)
+    # capacity 1024 slots serves a 1024-token window
     out = jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device),
-                               vt.half().to(device), lengths.to(device), window=4096)
+                               vt.half().to(device), lengths.to(device), window=1024)
+    with pytest.raises(ValueError, match="capacity"):
+        jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device),
+                             vt.half().to(device), lengths.to(device), window=4096)
     for b in range(batch):
         L = int(lengths[b])
-        e = _expect(q[b : b + 1], kc[b : b + 1], vc[b : b + 1], kt, vt, L, 4096, 1024)
+        e = _expect(q[b : b + 1], kc[b : b + 1], vc[b : b + 1], kt, vt, L, 1024, 1024)
         err = float((out[b : b + 1].cpu().float() - e.float()).abs().max())
         assert err <= ATOL, f"batch {b} length {L}: {err}"
     # PackedCodeCache: appends land at position % capacity

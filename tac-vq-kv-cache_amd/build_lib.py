@@ -32,6 +32,8 @@ CXXFLAGS = [
     "-std=c++17",
     "-fPIC",
     "-munsafe-fp-atomics",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Xclang",
     "-target-feature",
     "-Xclang",

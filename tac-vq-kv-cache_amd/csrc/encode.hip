@@ -2,12 +2,12 @@
 //
 // Two kernels share one argument block:
 //  * rvq_encode_mfma<D,S>: fp16 states, d in {4,8}, K=256, S<=2, no whitener.
-//    One wave owns one (head, group) problem and a range of rows.  The
-//    problem's codebooks live in VGPRs as the A operand of
-//    v_mfma_f32_16x16x32_f16 (codewords x contraction slots); a tile of 16
-//    rows is the B operand.  The contraction packs [r_hi | r_lo | norm]
-//    so one MFMA yields -(|r|^2 + |c|^2 - 2 r.c + delta)/2 for 16 codewords
-//    x 16 rows with fp32 accumulation; the argmin is a min over keys that
+//    A workgroup owns one (head, group) problem and a chunk of rows; the
+//    problem's codebooks are staged in LDS and feed the A operand of
+//    v_mfma_f32_16x16x32_f16 (codewords x contraction slots); 16-row tiles
+//    are the B operand.  The contraction packs [x | -c_prev | norm] so one
+//    MFMA yields -(|r - c|^2 + delta)/2 for 16 codewords x 16 rows with exact
+//    products and fp32 accumulation; the argmin is a min over keys that
 //    carry the codeword index in their low bits.
 //  * rvq_encode_generic<DT,DMAX>: any dtype, d<=128, K<=256, any S, optional
 //    whitener; one thread per row, fp32 distances in the reference's
@@ -28,8 +28,6 @@ struct EncodeArgs {
   int32_t n_exits;
   int32_t exit_depth[JKV_MAX_EXITS];
   void* recon[JKV_MAX_EXITS];
-  int64_t rows_per_unit;  // rows handled by one wave (mfma kernel)
-  int64_t n_units;
 };
 
 // ---------------------------------------------------------------------------
@@ -139,24 +137,30 @@ __global__ __launch_bounds__(256) void rvq_encode_generic(EncodeArgs a) {
 // ---------------------------------------------------------------------------
 // MFMA kernel for d in {4, 8}, K = 256, S in {1, 2}, fp16 states.
 //
-// v_mfma_f32_16x16x32_f16 operand layout (wave64):
-//   A[i][k]: lane = i + 16*(k/8), element k%8      (i = codeword in chunk)
-//   B[k][j]: lane = j + 16*(k/8), element k%8      (j = row in tile)
+// Workgroup = 4 waves on one (head, group) problem; the problem's S
+// codebooks are staged once in LDS as two planes, c (fp16) and
+// [n_hi, n_lo] with n = |c|^2/2 split into two fp16 halves.  Each wave
+// encodes 4 tiles of 16 rows per iteration (independent MFMA chains).
+//
+// v_mfma_f32_16x16x32_f16 (wave64), i = codeword in chunk, j = row in tile:
+//   A[i][k]: lane = i + 16*(k/8), element k%8
+//   B[k][j]: lane = j + 16*(k/8), element k%8
 //   D[i][j]: lane = j + 16*(i/4), element i%4
-// Contraction slots (k):
-//   d=8: [ 0.. 7] r_hi . c   [ 8..15] r_lo . c   [16,17] (-1).(|c|^2/2 hi,lo)
-//   d=4: [ 0.. 3] r_hi . c   [ 4.. 7] r_lo . c   [ 8, 9] (-1).(|c|^2/2 hi,lo)
-// C input: -(|r|^2 + delta)/2 for every codeword of the row.
-// Result: D = -(dist + delta)/2 < 0; as unsigned bit patterns negative
-// floats order by magnitude, so min over bits = min distance.  The low 6
-// bits are replaced by (chunk<<2 | i%4) before the min; the lane group adds
-// the remaining 2 index bits in the cross-lane step (8 bits total).
-
-template <int D>
-struct MfmaGeom {
-  // lanes holding the residual-hi/lo slots and the norm slot
-  static constexpr int kNormLaneGroup = (D == 8) ? 2 : 1;
-};
+// Contraction slots (lane group lg = lane/16 owns slots 8lg..8lg+7):
+//   d=8: lg0  x . c   lg1  (-c_prev) . c   lg2  (-1,-1,-b_hi,-b_lo) . (n_hi,n_lo,16,16)
+//   d=4: lg0  [x,-c_prev] . [c,c]          lg1  (-1,-1,-b_hi,-b_lo) . (n_hi,n_lo,16,16)
+// Remaining lane groups carry B = 0 (their A entries are finite LDS data).
+// The norm plane also carries (16, 16) against the row's -(beta/16) in two
+// fp16 halves, beta = (|r|^2 + delta)/2, so with C = 0
+//   D[i][j] = c_i.(x - c_prev) - |c_i|^2/2 - (|r|^2 + delta)/2
+//           = -(|r - c_i|^2 + delta)/2  < 0,
+// exact in the products (fp16 x fp16) and fp32 in the sum.  As unsigned bit
+// patterns negative floats order by magnitude, so the row's nearest codeword
+// is the min over keys (bits & ~63) | (chunk<<2 | i%4); the lane group adds
+// the last two index bits in the cross-lane step (ties -> lowest index).
+// delta = 2^-8 (|r|^2 + max|c|^2) keeps every key negative despite fp32
+// rounding and the approximate |r|^2; it is common to all codewords of the
+// row, so it never changes the order.
 
 __device__ __forceinline__ uint32_t umin3(uint32_t a, uint32_t b, uint32_t c) {
   return min(min(a, b), c);
@@ -170,214 +174,325 @@ __device__ __forceinline__ uint32_t lane_group_min(uint32_t v) {
   return min((uint32_t)s32[0], (uint32_t)s32[1]);
 }
 
-template <int D, int S>
-__global__ __launch_bounds__(256) void rvq_encode_mfma(EncodeArgs a) {
-  __shared__ half_t lds_tab[4][S][256][D];  // per-wave fp16 codebook copy
+__device__ __forceinline__ float dot2_acc(half8 a, half8 b) {
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    half2v x = {a[e], a[e + 1]};
+    half2v y = {b[e], b[e + 1]};
+    acc = __builtin_amdgcn_fdot2(x, y, acc, false);
+  }
+  return acc;
+}
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int lg = lane >> 4;  // lane group
+static const int kTiles = 4;                      // 16-row tiles per wave iteration
+static const int kRowsPerWave = kTiles * 16;      // rows per wave iteration
+static const int kRowsPerIter = 4 * kRowsPerWave; // rows per workgroup iteration
+// Prefetching the next iteration's rows into registers costs 16 VGPRs and
+// spills at 4 waves/SIMD; measured slower, so it stays off.
+static const bool kPrefetchRows = false;
+
+struct MfmaArgs {
+  EncodeArgs e;
+  void* recon_depth[2];  // reconstruction at depth 1 / 2 (or null)
+  int64_t rows_per_wg;
+  int64_t n_chunks;      // row chunks per problem
+};
+
+template <int D, int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void rvq_encode_mfma(MfmaArgs m) {
+  const EncodeArgs& a = m.e;
+  // LDS codebook image, two contiguous 16-byte planes per stage so that 16
+  // consecutive codewords are one conflict-free 256-byte row:
+  //   lo[s][k] = c_k          (d=4: [c_k, c_k])
+  //   hi[s][k] = [n_hi, n_lo, 16, 16, 0, 0, 0, 0],  n = |c_k|^2 / 2
+  __shared__ half8 tab_lo[S][256];
+  __shared__ half8 tab_hi[S][256];
+  __shared__ float s_ncmax[S][4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lg = lane >> 4;
   const int ln = lane & 15;
 
-  const uint32_t nblocks = gridDim.x;
-  const int64_t unit = (int64_t)xcd_remap(blockIdx.x, nblocks) * 4 + wave;
+  // logical block: group fastest, then head, then row chunk
+  const uint32_t L = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t P = a.H * a.G;
-  const bool active = unit < a.n_units;
-  const int64_t p = active ? unit % P : 0;
-  const int64_t range = active ? unit / P : 0;
-  const int64_t h = p / a.G, g = p % a.G;
+  const bool active = (int64_t)L < P * m.n_chunks;
+  const int64_t g = active ? (int64_t)L % a.G : 0;
+  const int64_t h = active ? ((int64_t)L / a.G) % a.H : 0;
+  const int64_t chunk = active ? (int64_t)L / P : 0;
+  const int64_t p = h * a.G + g;
 
-  // ---- A operand image and LDS codebook copy ----------------------------
-  half8 aimg[S][16];
-  float delta_scale[S];
+  // ---- stage the fp16-deployed codebooks (one codeword per thread) ----
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    float ncmax = 0.f;
+    const float* src = a.tables + ((p * S + s) * 256 + tid) * D;
+    half_t cw[D];
+    if (D == 8) {
+      const float4 v0 = ((const float4*)src)[0];
+      const float4 v1 = ((const float4*)src)[1];
+      const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int kidx = c * 16 + ln;
-      const float* src = a.tables + ((p * S + s) * 256 + kidx) * D;
-      half_t cw[D];
-      float nc = 0.f;
+      for (int i = 0; i < 8; ++i) cw[i] = (half_t)f[i];
+    } else {
+      const float4 v0 = ((const float4*)src)[0];
+      const float f[4] = {v0.x, v0.y, v0.z, v0.w};
 #pragma unroll
-      for (int i = 0; i < D; ++i) {
-        cw[i] = (half_t)src[i];
-        float f = (float)cw[i];
-        nc = fmaf(f, f, nc);
-      }
-      ncmax = fmaxf(ncmax, nc);
-      const float halfn = 0.5f * nc;
-      const half_t nhi = (half_t)halfn;
-      const half_t nlo = (half_t)(halfn - (float)nhi);
-      half8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (half_t)0.f;
-      if (D == 8) {
-        if (lg <= 1) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = cw[e % D];
-        } else if (lg == 2) {
-          v[0] = nhi;
-          v[1] = nlo;
-        }
-      } else {
-        if (lg == 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = cw[e % D];
-        } else if (lg == 1) {
-          v[0] = nhi;
-          v[1] = nlo;
-        }
-      }
-      aimg[s][c] = v;
-      if (lg == 0) {
-#pragma unroll
-        for (int i = 0; i < D; ++i) lds_tab[wave][s][kidx][i] = cw[i];
-      }
+      for (int i = 0; i < 4; ++i) cw[i] = (half_t)f[i];
     }
-    // max |c|^2 over the codebook (wave reduction)
+    float nc = 0.f;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-      ncmax = fmaxf(ncmax, __shfl_xor(ncmax, off, 64));
-    delta_scale[s] = ncmax;
+    for (int i = 0; i < D; ++i) nc = fmaf((float)cw[i], (float)cw[i], nc);
+    const float halfn = 0.5f * nc;
+    const half_t nhi = (half_t)halfn;
+    const half_t nlo = (half_t)(halfn - (float)nhi);
+    half8 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      lo[e] = cw[e % D];
+      hi[e] = (half_t)0.f;
+    }
+    hi[0] = nhi;
+    hi[1] = nlo;
+    hi[2] = (half_t)16.f;  // row-bias slots: 16 * (beta/16)_hi + 16 * (beta/16)_lo
+    hi[3] = (half_t)16.f;
+    tab_lo[s][tid] = lo;
+    tab_hi[s][tid] = hi;
+    float mx = nc;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) s_ncmax[s][wave] = mx;
   }
   __syncthreads();
   if (!active) return;
+  float ncmax[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    ncmax[s] = fmaxf(fmaxf(s_ncmax[s][0], s_ncmax[s][1]), fmaxf(s_ncmax[s][2], s_ncmax[s][3]));
 
-  // ---- B operand constants ------------------------------------------------
-  const int norm_lg = MfmaGeom<D>::kNormLaneGroup;
+  // this lane's A plane: d=8 lanes 0-31 read c, 32-63 the norm plane;
+  // d=4 lanes 0-15 read [c,c], 16-63 the norm plane (B is zero past slot 9)
+  const bool a_hi = (D == 8) ? (lg >= 2) : (lg >= 1);
+  const half8* plane = a_hi ? &tab_hi[0][0] : &tab_lo[0][0];
+
   const int64_t rows = a.B * a.T;
-  const int64_t row_begin = range * a.rows_per_unit;
-  int64_t row_end = row_begin + a.rows_per_unit;
-  if (row_end > rows) row_end = rows;
-  const int64_t Dfull = a.G * D;
+  const int64_t r_begin = chunk * m.rows_per_wg;
+  int64_t r_end = r_begin + m.rows_per_wg;
+  if (r_end > rows) r_end = rows;
   const _Float16* states = (const _Float16*)a.states;
+  const int64_t Dfull = a.G * D;
+  const int64_t head_x = h * a.sh + g * D;             // states offset of (h, g)
+  const int64_t head_c = h * a.ch + g * S;             // codes offset of (h, g)
+  const int64_t out_bstride = a.H * a.T * Dfull;       // recon is contiguous
+  const int64_t head_o = h * a.T * Dfull + g * D;
 
-  for (int64_t tile = row_begin; tile < row_end; tile += 16) {
-    const int64_t row = tile + ln;
-    const bool valid = row < row_end;
-    const int64_t rb = valid ? row / a.T : 0;
-    const int64_t rt = valid ? row % a.T : 0;
-    // every lane holds the 16-row tile's residual for its row (lane & 15)
-    float r[D];
-    {
-      const _Float16* xp = states + rb * a.sb + h * a.sh + rt * a.st + g * D;
+  half8 neg_one_slot;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) neg_one_slot[e] = (half_t)0.f;
+  neg_one_slot[0] = (half_t)-1.f;
+  neg_one_slot[1] = (half_t)-1.f;
+
+  // (batch, token) of the wave's first row, advanced incrementally
+  int64_t base = r_begin + wave * kRowsPerWave;
+  int64_t b0 = base / a.T;
+  int64_t t0 = base - b0 * a.T;
+
+  // Wave-uniform description of one iteration (64 rows).  In the common
+  // case all rows sit in one batch entry and every address is a uniform
+  // base plus (row in iteration) * stride; otherwise rows are located one by
+  // one.
+  struct Iter {
+    int64_t at, xb, cb, ob;
+    bool fast;
+  };
+  auto plan = [&](int64_t at) {
+    Iter it;
+    it.at = at;
+    it.fast = t0 + kRowsPerWave <= a.T && at + kRowsPerWave <= r_end;
+    it.xb = b0 * a.sb + head_x + t0 * a.st;
+    it.cb = b0 * a.cb + head_c + t0 * a.ct;
+    it.ob = b0 * out_bstride + head_o + t0 * Dfull;
+    t0 += kRowsPerIter;
+    while (t0 >= a.T) {
+      t0 -= a.T;
+      ++b0;
+    }
+    return it;
+  };
+  // per-lane offsets of tile i: (valid, states, codes, reconstruction)
+  auto locate = [&](const Iter& it, int i, uint32_t* xo, uint32_t* co, uint32_t* oo) -> bool {
+    const uint32_t rr = (uint32_t)(i * 16 + ln);
+    if (it.fast) {
+      *xo = (uint32_t)it.xb + rr * (uint32_t)a.st;
+      *co = (uint32_t)it.cb + rr * (uint32_t)a.ct;
+      *oo = (uint32_t)it.ob + rr * (uint32_t)Dfull;
+      return true;
+    }
+    // rows, strides and offsets fit in 32 bits on this path (host-checked)
+    const uint32_t row = (uint32_t)it.at + rr;
+    const bool valid = row < (uint32_t)r_end;
+    const uint32_t rw = valid ? row : (uint32_t)r_begin;
+    const uint32_t T32 = (uint32_t)a.T;
+    const uint32_t rb = rw / T32, rt = rw - rb * T32;
+    *xo = rb * (uint32_t)a.sb + (uint32_t)head_x + rt * (uint32_t)a.st;
+    *co = rb * (uint32_t)a.cb + (uint32_t)head_c + rt * (uint32_t)a.ct;
+    *oo = rb * (uint32_t)out_bstride + (uint32_t)head_o + rt * (uint32_t)Dfull;
+    return valid;
+  };
+  auto load_x = [&](const Iter& it, half8* dst) {
+#pragma unroll
+    for (int i = 0; i < kTiles; ++i) {
+      uint32_t xo, co, oo;
+      locate(it, i, &xo, &co, &oo);
       if (D == 8) {
-        half8 xv = valid ? *(const half8*)xp : half8{};
-#pragma unroll
-        for (int i = 0; i < D; ++i) r[i] = (float)xv[i];
+        dst[i] = *(const half8*)(states + xo);
       } else {
-        half4 xv = valid ? *(const half4*)xp : half4{};
-#pragma unroll
-        for (int i = 0; i < D; ++i) r[i] = (float)xv[i];
+        const half4 v = *(const half4*)(states + xo);
+        dst[i] = half8{v[0], v[1], v[2], v[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
       }
     }
-    float dec[D];
+  };
+
+  half8 x[kTiles];
+  Iter cur = plan(base);
+  if (base < r_end) load_x(cur, x);
+
+  for (; base < r_end; base += kRowsPerIter) {
+    // prefetch the next iteration's rows while this one computes
+    half8 x_next[kTiles];
+    const bool more = kPrefetchRows && base + kRowsPerIter < r_end;
+    const Iter nxt = plan(base + kRowsPerIter);
+    if (more) load_x(nxt, x_next);
+    uint32_t code_bytes[kTiles];
 #pragma unroll
-    for (int i = 0; i < D; ++i) dec[i] = 0.f;
-    uint32_t code_bytes = 0;
+    for (int i = 0; i < kTiles; ++i) code_bytes[i] = 0u;
 
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      // hi/lo split of the fp32 residual (exact for s == 0: fp16 inputs)
-      half_t rhi[D], rlo[D];
-      float rr = 0.f;
+      half8 bop[kTiles];
 #pragma unroll
-      for (int i = 0; i < D; ++i) {
-        rhi[i] = (half_t)r[i];
-        rlo[i] = (half_t)(r[i] - (float)rhi[i]);
-        rr = fmaf(r[i], r[i], rr);
-      }
-      half8 bop;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bop[e] = (half_t)0.f;
-      if (D == 8) {
-        if (lg == 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) bop[e] = rhi[e % D];
-        } else if (lg == 1) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) bop[e] = rlo[e % D];
+      for (int i = 0; i < kTiles; ++i) {
+        // stage-1 codeword (zero before stage 2), re-read from LDS
+        half8 cprev = half8{};
+        if (s > 0) {
+          cprev = tab_lo[0][code_bytes[i] & 255u];
+          if (D == 4) cprev = half8{cprev[0], cprev[1], cprev[2], cprev[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
         }
-      } else {
-        if (lg == 0) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            bop[e] = rhi[e];
-            bop[e + 4] = rlo[e];
-          }
+        // row bias beta = (|r|^2 + delta)/2 enters through the norm plane's
+        // (16, 16) slots as -(beta/16) split into two fp16 halves; |r|^2 comes
+        // from the fp16-rounded residual, delta covers that and fp32 rounding
+        const half8 rh = x[i] - cprev;
+        const float rr = dot2_acc(rh, rh);
+        const float beta16 = (rr + (rr + ncmax[s]) * 0x1p-8f) * (0.5f / 16.f) + 0x1p-60f;
+        const half_t bh = (half_t)beta16;
+        const half_t bl = (half_t)(beta16 - (float)bh);
+        half8 normb = neg_one_slot;
+        normb[2] = -bh;
+        normb[3] = -bl;
+        const half8 negc = -cprev;
+        half8 b;
+        if (D == 8) {
+          b = (lg == 0) ? x[i] : (lg == 1) ? negc : (lg == 2) ? normb : half8{};
+        } else {
+          const half8 xc = half8{x[i][0], x[i][1], x[i][2], x[i][3], negc[0], negc[1], negc[2], negc[3]};
+          b = (lg == 0) ? xc : (lg == 1) ? normb : half8{};
         }
+        bop[i] = b;
       }
-      if (lg == norm_lg) {
-        bop[0] = (half_t)-1.f;
-        bop[1] = (half_t)-1.f;
-      }
-      // delta dominates the fp32 rounding of the accumulation so every key
-      // stays strictly negative; it is common to all codewords of the row.
-      const float delta = (rr + delta_scale[s]) * 0x1p-16f + 0x1p-100f;
-      const float cval = -0.5f * (rr + delta);
-      const float4v cin = {cval, cval, cval, cval};
-
-      uint32_t best = 0xFFFFFFFFu;
+      const float4v zero4 = {0.f, 0.f, 0.f, 0.f};
+      uint32_t best[kTiles];
+#pragma unroll
+      for (int i = 0; i < kTiles; ++i) best[i] = 0xFFFFFFFFu;
+      const half8* pl = plane + s * 256 + ln;
+      // software pipeline: the MFMAs of chunk c+1 run while the keys of
+      // chunk c are reduced (scheduling barriers keep ~2 chunks in flight)
+      half8 af_next = pl[0];
+      float4v acc[2][kTiles];
+#pragma unroll
+      for (int i = 0; i < kTiles; ++i)
+        acc[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af_next, bop[i], zero4, 0, 0, 0);
+      af_next = pl[16];
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
-        float4v acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aimg[s][c], bop, cin, 0, 0, 0);
-        uint32_t k0 = (__float_as_uint(acc[0]) & ~63u) | (uint32_t)(c * 4 + 0);
-        uint32_t k1 = (__float_as_uint(acc[1]) & ~63u) | (uint32_t)(c * 4 + 1);
-        uint32_t k2 = (__float_as_uint(acc[2]) & ~63u) | (uint32_t)(c * 4 + 2);
-        uint32_t k3 = (__float_as_uint(acc[3]) & ~63u) | (uint32_t)(c * 4 + 3);
-        best = umin3(umin3(k0, k1, k2), k3, best);
-      }
-      // codeword index = chunk*16 + lane_group*4 + i%4
-      const uint32_t tag = best & 63u;
-      const uint32_t kidx = ((tag >> 2) << 4) | ((uint32_t)lg << 2) | (tag & 3u);
-      const uint32_t key = lane_group_min((best & ~255u) | kidx);
-      const uint32_t kstar = key & 255u;
-      code_bytes |= kstar << (8 * s);
-      // residual / decoded update with the fp16-deployed codeword
-      const half_t* cw = &lds_tab[wave][s][kstar][0];
-      float cf[D];
-      if (D == 8) {
-        half8 cv = *(const half8*)cw;
+        const int cur = c & 1;
+        const half8 af = af_next;
+        if (c + 2 < 16) af_next = pl[(c + 2) * 16];
 #pragma unroll
-        for (int i = 0; i < D; ++i) cf[i] = (float)cv[i];
-      } else {
-        half4 cv = *(const half4*)cw;
+        for (int i = 0; i < kTiles; ++i) {
+          if (c + 1 < 16)
+            acc[cur ^ 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop[i], zero4, 0, 0, 0);
+          const float4v v = acc[cur][i];
+          const uint32_t k0 = (__float_as_uint(v[0]) & ~63u) | (uint32_t)(c * 4 + 0);
+          const uint32_t k1 = (__float_as_uint(v[1]) & ~63u) | (uint32_t)(c * 4 + 1);
+          const uint32_t k2 = (__float_as_uint(v[2]) & ~63u) | (uint32_t)(c * 4 + 2);
+          const uint32_t k3 = (__float_as_uint(v[3]) & ~63u) | (uint32_t)(c * 4 + 3);
+          best[i] = umin3(umin3(k0, k1, k2), k3, best[i]);
+          // pin the running minimum here: without it the compiler sinks the
+          // key reduction of later tiles past the stage epilogue and keeps
+          // every MFMA result of the stage live
+          asm volatile("" : "+v"(best[i]));
+        }
+        // issue order per chunk: one MFMA of chunk c+1, then the six key
+        // operations of one tile of chunk c, four times, so both the MFMA and
+        // the VALU pipe always have work from this wave
 #pragma unroll
-        for (int i = 0; i < D; ++i) cf[i] = (float)cv[i];
+        for (int i = 0; i < kTiles; ++i) {
+          if (c + 1 < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int i = 0; i < D; ++i) {
-        r[i] -= cf[i];
-        dec[i] += cf[i];
-      }
-      // exits at depth s+1
-      if (lg == 0 && valid) {
-        for (int e = 0; e < a.n_exits; ++e) {
-          if (a.exit_depth[e] != s + 1 || a.recon[e] == nullptr) continue;
-          _Float16* op = (_Float16*)a.recon[e] + (rb * a.H + h) * a.T * Dfull + rt * Dfull + g * D;
+      for (int i = 0; i < kTiles; ++i) {
+        const uint32_t tag = best[i] & 63u;
+        const uint32_t kidx = ((tag >> 2) << 4) | ((uint32_t)lg << 2) | (tag & 3u);
+        const uint32_t kstar = lane_group_min((best[i] & ~255u) | kidx) & 255u;
+        code_bytes[i] |= kstar << (8 * s);
+        half8 cw = tab_lo[s][kstar];
+        if (D == 4) cw = half8{cw[0], cw[1], cw[2], cw[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
+        // depth-2 reconstruction fp16(fp32(c1) + fp32(c2)): the sum of two fp16
+        // words is exact in fp32 or, when it is not, too small to move the
+        // fp16 rounding, so one fp16 add gives the same bits.
+        half8 dec = cw;
+        if (s > 0) {
+          half8 c1 = tab_lo[0][code_bytes[i] & 255u];
+          if (D == 4) c1 = half8{c1[0], c1[1], c1[2], c1[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
+          dec = c1 + cw;
+        }
+        void* out = m.recon_depth[s];
+        uint32_t xo, co, oo;
+        const bool valid = locate(cur, i, &xo, &co, &oo);
+        if (out != nullptr && lg == 0 && valid) {
+          _Float16* op = (_Float16*)out + oo;
           if (D == 8) {
-            half8 o;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = (half_t)dec[i];
-            *(half8*)op = o;
+            *(half8*)op = dec;
           } else {
-            half4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = (half_t)dec[i];
-            *(half4*)op = o;
+            *(half4*)op = half4{dec[0], dec[1], dec[2], dec[3]};
           }
         }
       }
     }
-    if (lg == 0 && valid) {
-      uint8_t* cp = a.codes + rb * a.cb + h * a.ch + rt * a.ct + g * S;
-      if (S == 1) {
-        cp[0] = (uint8_t)code_bytes;
-      } else {
-        *(uint16_t*)cp = (uint16_t)code_bytes;
+#pragma unroll
+    for (int i = 0; i < kTiles; ++i) {
+      uint32_t xo, co, oo;
+      const bool valid = locate(cur, i, &xo, &co, &oo);
+      if (lg == 0 && valid) {
+        uint8_t* cp = a.codes + co;
+        if (S == 1) {
+          cp[0] = (uint8_t)code_bytes[i];
+        } else {
+          *(uint16_t*)cp = (uint16_t)code_bytes[i];
+        }
       }
     }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < kTiles; ++i) x[i] = x_next[i];
+    }
+    cur = nxt;
   }
 }
 
@@ -398,19 +513,21 @@ static int launch_generic(const EncodeArgs& a, hipStream_t stream) {
 }
 
 template <int D, int S>
-static int launch_mfma(EncodeArgs a, hipStream_t stream) {
-  const int64_t rows = a.B * a.T;
-  const int64_t P = a.H * a.G;
-  // rows per wave: enough to amortise the codebook load, enough waves to
-  // fill 256 CUs x 8 waves.
-  int64_t rpu = 1024;
-  while (rpu > 64 && P * ceil_div(rows, rpu) < 256 * 8) rpu >>= 1;
-  a.rows_per_unit = rpu;
-  a.n_units = P * ceil_div(rows, rpu);
-  int64_t nblocks = ceil_div(a.n_units, 4);
+static int launch_mfma(const EncodeArgs& e, hipStream_t stream) {
+  MfmaArgs m = {};
+  m.e = e;
+  for (int i = 0; i < e.n_exits; ++i) m.recon_depth[e.exit_depth[i] - 1] = e.recon[i];
+  const int64_t rows = e.B * e.T;
+  const int64_t P = e.H * e.G;
+  // rows per workgroup: amortise the codebook staging, fill 256 CUs x 4 WGs
+  int64_t rpw = 4096;
+  while (rpw > kRowsPerIter && P * ceil_div(rows, rpw) < 256 * 4) rpw >>= 1;
+  m.rows_per_wg = rpw;
+  m.n_chunks = ceil_div(rows, rpw);
+  int64_t nblocks = P * m.n_chunks;
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < (int64_t)1 << 31, "grid too large");
-  hipLaunchKernelGGL((rvq_encode_mfma<D, S>), dim3((uint32_t)nblocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((rvq_encode_mfma<D, S>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }
@@ -480,9 +597,21 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
   bool recon_aligned = true;
   for (int e = 0; e < n_exits; ++e)
     if (a.recon[e] && ((uintptr_t)a.recon[e]) % 16 != 0) recon_aligned = false;
-  const bool fast = states_dtype == JKV_F16 && whiteners == nullptr && K == 256 &&
+  bool distinct_exits = true;
+  for (int i = 0; i < n_exits; ++i)
+    for (int j = 0; j < i; ++j)
+      if (exit_depths[i] == exit_depths[j]) distinct_exits = false;
+  // the MFMA path addresses states, codes and reconstructions with 32-bit
+  // element offsets
+  const int64_t x_span = (B - 1) * stride_b + (H - 1) * stride_h + (T - 1) * stride_t + G * d;
+  const int64_t c_span = (B - 1) * code_stride_b + (H - 1) * code_stride_h + (T - 1) * code_stride_t + G * S;
+  const bool offsets32 = stride_b >= 0 && stride_h >= 0 && stride_t >= 0 && code_stride_b >= 0 &&
+                         code_stride_h >= 0 && code_stride_t >= 0 && x_span < ((int64_t)1 << 31) &&
+                         c_span < ((int64_t)1 << 31) && B * H * T * G * d < ((int64_t)1 << 31);
+  const bool fast = offsets32 && states_dtype == JKV_F16 && whiteners == nullptr && K == 256 &&
                     (d == 8 || d == 4) && (S == 1 || S == 2) && aligned16 && codes_aligned &&
-                    recon_aligned;
+                    recon_aligned && distinct_exits && B * T < ((int64_t)1 << 31) &&
+                    T < ((int64_t)1 << 31);
   if (fast) {
     if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
     return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);

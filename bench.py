@@ -177,14 +177,14 @@ def decode_workload(args, device):
             cache.key[:, :, slot] = kc[:, :, 0]
             cache.value[:, :, slot] = vc[:, :, 0]
             _ops.decode_attention(q, cache.key, cache.value, kt16, vt16, lengths, window=window,
-                                  rope_theta=10000.0)
+                                  rope_theta=10000.0, max_length=window)
 
     ms = timed(step, args.steps, args.warmup)
     # attention kernels alone
     def attn_only():
         for cache, (_kt, _vt, kt16, vt16) in zip(caches, tabs):
             _ops.decode_attention(q, cache.key, cache.value, kt16, vt16, lengths, window=window,
-                                  rope_theta=10000.0)
+                                  rope_theta=10000.0, max_length=window)
 
     attn_ms = timed(attn_only, args.steps, 1)
     bytes_per_layer = 2 * batch * kvh * window * GROUPS * STAGES + 2 * kvh * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 2 + 2 * batch * qh * HEAD_DIM * 2

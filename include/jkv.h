@@ -147,6 +147,8 @@ int jkv_scale_sgd(int32_t n, float* const* params, float* const* grads,
  *   lengths  [B] int32 device: tokens in the cache including the new one;
  *            query position = lengths[b]-1; visible keys are the last
  *            min(window, lengths[b]) positions
+ *   rope_table  jkv_rope_table() output covering positions [0, rope_len),
+ *            rope_len > max(lengths) - 1
  *   out      [B,QH,D] fp16 contiguous
  *   workspace  jkv_decode_workspace_bytes() bytes (split-KV partials)
  */
@@ -159,9 +161,20 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b,
                          const void* k_tables, const void* v_tables, int64_t B,
                          int64_t QH, int64_t KVH, int64_t G, int64_t d,
                          int64_t S, int64_t K, const int32_t* lengths,
-                         int64_t window, float rope_theta, void* out,
-                         void* workspace, int64_t workspace_bytes,
-                         jkv_stream_t stream);
+                         int64_t window, const void* rope_table,
+                         int64_t rope_len, void* out, void* workspace,
+                         int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
+ * Rotary (cos, sin) table for head_dim 128, fp16 pairs [n_pos][64][2]:
+ * angle = fp32(p) * inv_freq[i] in fp32, cos/sin in fp32 rounded to fp16 —
+ * the arithmetic of the reference's rotary module
+ * (transformers' MistralRotaryEmbedding behind
+ * experiments_followup_mistral/evaluate_mistral_longbench.py:102,113,117).
+ * inv_freq: 64 fp32 device values (computed on the host the same way).
+ */
+int jkv_rope_table(const float* inv_freq, int64_t n_pos, void* out,
+                   jkv_stream_t stream);
 
 /* fp32 -> fp16 copy (the deploy round trip tables.half()), n elements. */
 int jkv_f32_to_f16(const float* src, void* dst, int64_t n, jkv_stream_t stream);

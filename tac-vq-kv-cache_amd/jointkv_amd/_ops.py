@@ -191,6 +191,32 @@ def f32_to_f16(tensor: torch.Tensor) -> torch.Tensor:
     return out
 
 
+_ROPE_CACHE: dict[tuple, torch.Tensor] = {}
+
+
+def rotary_inv_freq(head_dim: int, theta: float) -> torch.Tensor:
+    """inv_freq = 1 / theta^(arange(0, D, 2) / D), computed in fp32 on the CPU
+    exactly as the reference's rotary module does (transformers' default rope
+    init behind evaluate_mistral_longbench.py:102,113,117)."""
+
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+
+
+def rope_table(device: torch.device, theta: float, n_pos: int) -> torch.Tensor:
+    """Cached fp16 (cos, sin) table [n_pos', 64, 2] with n_pos' >= n_pos."""
+
+    key = (str(device), float(theta))
+    table = _ROPE_CACHE.get(key)
+    if table is not None and table.shape[0] >= n_pos:
+        return table
+    size = 1 << max(12, (max(n_pos, 1) - 1).bit_length())
+    inv = rotary_inv_freq(128, theta).to(device)
+    table = torch.empty((size, 64, 2), dtype=torch.float16, device=device)
+    _lib.check(_lib.load().jkv_rope_table(inv.data_ptr(), size, table.data_ptr(), _lib.stream_handle(device)))
+    _ROPE_CACHE[key] = table
+    return table
+
+
 def decode_attention(
     q: torch.Tensor,
     key_codes: torch.Tensor,
@@ -201,12 +227,15 @@ def decode_attention(
     *,
     window: int,
     rope_theta: float,
+    max_length: int | None = None,
 ) -> torch.Tensor:
     """One decode step of GQA attention straight from the packed code cache.
 
     ``q[B,QH,D]`` fp16 (pre-RoPE), codes ``[B,KVH,cap,G,S]`` uint8, fp16
     deployed tables ``[KVH*G,S,K,d]``, ``lengths[B]`` int32 (cache length
-    including the new token).  Returns ``[B,QH,D]`` fp16.
+    including the new token).  ``max_length`` bounds ``lengths`` (the rotary
+    table is sized from it); when omitted it is read from the device, which
+    synchronises.  Returns ``[B,QH,D]`` fp16.
     """
 
     device = _lib.require_device(q, key_codes, value_codes, key_tables16, value_tables16, lengths)
@@ -233,6 +262,9 @@ def decode_attention(
     if lengths.dtype != torch.int32 or lengths.shape != (batch,):
         raise ValueError("lengths must be int32 [B]")
     lengths = lengths.contiguous()
+    if max_length is None:
+        max_length = int(lengths.max().item()) if batch else 1
+    table = rope_table(device, rope_theta, int(max_length) + 1)
     lib = _lib.load()
     out = torch.empty((batch, qheads, dim), dtype=torch.float16, device=device)
     ws_bytes = int(lib.jkv_decode_workspace_bytes(batch, qheads, dim, int(window)))
@@ -241,7 +273,7 @@ def decode_attention(
         q.data_ptr(), q.stride(0), q.stride(1), key_codes.data_ptr(), value_codes.data_ptr(),
         key_codes.stride(0), key_codes.stride(1), cap, key_tables16.data_ptr(),
         value_tables16.data_ptr(), batch, qheads, kvheads, groups, d, stages, clusters,
-        lengths.data_ptr(), int(window), float(rope_theta), out.data_ptr(),
+        lengths.data_ptr(), int(window), table.data_ptr(), int(table.shape[0]), out.data_ptr(),
         workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
     )
     _lib.check(code)

@@ -51,6 +51,7 @@ def decode_attention(
     *,
     window: int = MISTRAL_WINDOW,
     rope_theta: float = MISTRAL_ROPE_THETA,
+    max_length: int | None = None,
 ) -> torch.Tensor:
     """Attention output for one new token per sequence.
 
@@ -59,7 +60,8 @@ def decode_attention(
     position p in slot ``p % cap``.  ``lengths[b]`` counts the cached tokens
     including the new one, so the query sits at position ``lengths[b]-1``
     and sees the last ``min(window, lengths[b])`` positions (the reference's
-    ``LayerCache.visible``).  Returns ``[B,QH,1,D]`` (or ``[B,QH,D]``) fp16.
+    ``LayerCache.visible``).  ``max_length`` (an upper bound of ``lengths``)
+    avoids a device read.  Returns ``[B,QH,1,D]`` (or ``[B,QH,D]``) fp16.
     """
 
     squeeze = query.ndim == 3
@@ -71,7 +73,7 @@ def decode_attention(
         value_codes = value_codes.unflatten(-1, (groups, stages))
     out = _ops.decode_attention(
         q, key_codes, value_codes, key_tables16, value_tables16, lengths,
-        window=window, rope_theta=rope_theta,
+        window=window, rope_theta=rope_theta, max_length=max_length,
     )
     return out if squeeze else out.unsqueeze(2)
 

@@ -72,11 +72,14 @@ def test_decode_rejects_unsupported_geometry():
     # placeholder pointers would launch a kernel.
     lib = _lib.load()
     rc = lib.jkv_decode_attention(1, 0, 0, 1, 1, 0, 0, 4096, 1, 1, 1, 32, 8, 8, 8, 2, 256, 1,
-                                  4096, 10000.0, 1, 1, 1 << 30, None)
+                                  4096, 1, 8192, 1, 1, 1 << 30, None)
     assert rc == _lib.JKV_EINVAL and b"head_dim" in lib.jkv_last_error()
     rc = lib.jkv_decode_attention(1, 0, 0, 1, 1, 0, 0, 100, 1, 1, 1, 32, 8, 16, 8, 2, 256, 1,
-                                  4096, 10000.0, 1, 1, 1 << 30, None)
+                                  4096, 1, 8192, 1, 1, 1 << 30, None)
     assert rc == _lib.JKV_EINVAL and b"capacity" in lib.jkv_last_error()
+    rc = lib.jkv_decode_attention(1, 0, 0, 1, 1, 0, 0, 4096, 1, 1, 1, 32, 8, 16, 8, 2, 256, 1,
+                                  4096, 1, 0, 1, 1, 1 << 30, None)
+    assert rc == _lib.JKV_EINVAL and b"rotary" in lib.jkv_last_error()
 
 
 def test_product_rejects_host_tensors_loudly():

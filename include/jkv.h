@@ -88,10 +88,12 @@ int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b,
                    const float* tables, int64_t S, int64_t K, int32_t depth,
                    void* out, int32_t out_dtype, jkv_stream_t stream);
 
-/* Bytes of device workspace jkv_rvq_scatter_grad needs. */
+/* Bytes of device workspace jkv_rvq_scatter_grad needs for this geometry,
+ * gradient dtype and determinism request. */
 int64_t jkv_rvq_scatter_workspace_bytes(int64_t B, int64_t H, int64_t T,
                                         int64_t G, int64_t d, int64_t S,
-                                        int64_t K, int32_t deterministic);
+                                        int64_t K, int32_t grad_dtype,
+                                        int32_t deterministic);
 
 /*
  * Straight-through codebook gradient: for every stage s,
@@ -99,11 +101,18 @@ int64_t jkv_rvq_scatter_workspace_bytes(int64_t B, int64_t H, int64_t T,
  *       sum over exits e with exit_depths[e] > s of fp32(grads[e][.., g*d:(g+1)*d])
  * Replaces the autograd backward of torch.gather at
  * closed_loop_vq.py:376-381 (via the deploy STE :298) and cq_tac.py:98-99.
- * grads[e] are [B,H,T,G*d] contiguous in grad_dtype.  deterministic != 0
- * selects a fixed summation order (per 256-row chunk an in-order sum per
- * codeword, then the chunk partials summed in chunk order; needs
- * jkv_rvq_scatter_workspace_bytes() of workspace); otherwise LDS-privatised
- * bins are flushed with global fp32 atomics.
+ * grads[e] are [B,H,T,G*d] contiguous in grad_dtype.
+ * When d is a multiple of 4, a block holds the bins of one (head, group,
+ * stage, slice of 8 or 4 dims) in LDS.  fp16 gradients are summed exactly in
+ * 64-bit fixed point (value * 2^24) and rounded to fp32 once, so the result
+ * is the correctly rounded sum and identical from run to run; bf16/fp32
+ * gradients are summed with fp32 LDS atomics.  Other d, or gradient buffers
+ * not aligned to the slice, use global fp32 atomics.
+ * deterministic != 0 asks for a run-to-run identical result: fp16 gradients
+ * already give one (and then must be aligned to the slice, else
+ * JKV_EINVAL); bf16/fp32 gradients take fixed-order sums (per 256-row chunk
+ * an in-order sum per codeword, then the chunk partials in chunk order).
+ * May need jkv_rvq_scatter_workspace_bytes() of workspace.
  */
 int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads,
                          int32_t grad_dtype, const int32_t* exit_depths,

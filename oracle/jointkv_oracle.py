@@ -264,23 +264,32 @@ def frozen_decode(codes: torch.Tensor, tables: torch.Tensor, depth: int, dtype: 
     ).to(dtype)
 
 
-def table_gradient(grads: Sequence[torch.Tensor], exits: Sequence[int], codes: torch.Tensor, table_shape) -> torch.Tensor:
+def table_gradient(
+    grads: Sequence[torch.Tensor],
+    exits: Sequence[int],
+    codes: torch.Tensor,
+    table_shape,
+    accumulate: torch.dtype = torch.float32,
+) -> torch.Tensor:
     """Closed form of the gather backward: codes [B,H,T,G,S], grads [B,H,T,G*d].
 
     grad[p,s,k,:] = sum over rows with code[.., g, s] = k of
     sum_{exits e: depth_e > s} fp32(grads_e[.., g*d:(g+1)*d]).
     This is what autograd computes for closed_loop_vq.py:376-381 / cq_tac.py:98-99.
+    ``accumulate=torch.float64`` sums in fp64 and returns fp64: for fp16
+    gradients at test sizes that sum is exact, so ``.float()`` of it is the
+    correctly rounded fp32 result.
     """
 
     batch, heads, tokens, groups, stages = map(int, codes.shape)
     problems, _s, clusters, d = map(int, table_shape)
-    out = torch.zeros(table_shape, dtype=torch.float32)
+    out = torch.zeros(table_shape, dtype=accumulate)
     flat_codes = codes.long().permute(1, 3, 0, 2, 4).reshape(problems, batch * tokens, stages)
     for s in range(stages):
         g = None
         for grad, depth in zip(grads, exits):
             if depth > s:
-                gf = grad.float().reshape(batch, heads, tokens, groups, d).permute(1, 3, 0, 2, 4).reshape(
+                gf = grad.to(accumulate).reshape(batch, heads, tokens, groups, d).permute(1, 3, 0, 2, 4).reshape(
                     problems, batch * tokens, d
                 )
                 g = gf if g is None else g + gf

@@ -1,5 +1,22 @@
 // Straight-through codebook gradient scatter-add (the backward of the
 // reference's torch.gather over fp16-deployed fp32 masters).
+//
+// grad_tables[h*G+g, s, k, :] += sum over rows whose stage-s code is k of the
+// exit-summed upstream slice g*d:(g+1)*d.  Three kernels:
+//   scatter_bins_kernel    LDS-privatised bins of one (head, group, stage,
+//                          slice of 4 or 8 dims) over a chunk of rows (any d
+//                          that is a multiple of 4).  fp16 gradients
+//                          accumulate in exact 64-bit fixed point (every fp16
+//                          value is an integer multiple of 2^-24), so the sum
+//                          is exact, rounded to fp32 once, and bit-identical
+//                          from run to run; bf16/fp32 gradients use fp32 LDS
+//                          atomics.
+//   scatter_global_kernel  global fp32 atomics (misaligned gradients, or d not
+//                          a multiple of 4).
+//   scatter_det_*          fixed-order fp32 sums for bf16/fp32 gradients when
+//                          a deterministic result is asked for.
+#include <type_traits>
+
 #include "jkv_common.h"
 
 namespace jkv {
@@ -14,8 +31,7 @@ struct ScatterArgs {
   float* grad_tables;  // [H*G,S,K,d]
   int64_t rows_per_chunk;
   int64_t n_chunks;
-  int32_t groups_per_block;  // privatised groups per block (LDS path)
-  float* partials;           // deterministic path workspace
+  void* partials;            // per-chunk partial bins (workspace)
 };
 
 template <int DT>
@@ -26,56 +42,218 @@ __device__ __forceinline__ float grad_sum(const ScatterArgs& a, int s, int64_t o
   return acc;
 }
 
-// LDS-privatised bins for `groups_per_block` groups of one head over a chunk
-// of rows; one global fp32 atomic per touched bin element at the end.
-template <int DT>
-__global__ __launch_bounds__(256) void scatter_lds_kernel(ScatterArgs a) {
-  extern __shared__ float bins[];  // [gpb][S][K][d]
-  const int gpb = a.groups_per_block;
-  const int64_t per_group = a.S * a.K * a.d;
-  const int64_t nbins = gpb * per_group;
-  for (int64_t i = threadIdx.x; i < nbins; i += blockDim.x) bins[i] = 0.f;
-  __syncthreads();
+// fp16 value times 2^24 as an exact integer (|result| < 2^40).
+__device__ __forceinline__ long long fp16_fixed(uint32_t h) {
+  const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
+  const long long mag = e ? (long long)(m | 1024u) << (e - 1u) : (long long)m;
+  return (h & 0x8000u) ? -mag : mag;
+}
 
-  const int64_t n_quads = ceil_div(a.G, gpb);
-  const int64_t chunk = blockIdx.x % a.n_chunks;
-  const int64_t hq = blockIdx.x / a.n_chunks;
-  const int64_t h = hq / n_quads, q = hq % n_quads;
-  const int64_t rows = a.B * a.T;
-  const int64_t r0 = chunk * a.rows_per_chunk;
-  int64_t r1 = r0 + a.rows_per_chunk;
-  if (r1 > rows) r1 = rows;
-  const int64_t D = a.G * a.d;
-  // work items: (row, local group, dim) with dim fastest -> coalesced reads
-  const int64_t items = (r1 - r0) * gpb * a.d;
-  for (int64_t it = threadIdx.x; it < items; it += blockDim.x) {
-    const int64_t i = it % a.d;
-    const int64_t gl = (it / a.d) % gpb;
-    const int64_t row = r0 + it / (a.d * gpb);
-    const int64_t g = q * gpb + gl;
-    if (g >= a.G) continue;
-    const int64_t b = row / a.T, t = row % a.T;
-    const int64_t off = ((b * a.H + h) * a.T + t) * D + g * a.d + i;
-    const uint8_t* cp = a.codes + b * a.cb + h * a.ch + t * a.ct + g * a.S;
-    float* gbins = bins + gl * per_group;
-    for (int s = 0; s < (int)a.S; ++s) {
-      const float v = grad_sum<DT>(a, s, off);
-      if (v != 0.f) atomicAdd(&gbins[((int64_t)s * a.K + cp[s]) * a.d + i], v);
+__device__ __forceinline__ float fixed_to_float(long long v) {
+  return (float)v * 5.9604644775390625e-8f;  // 2^-24: exact scaling
+}
+
+// D gradient elements at element offset `off` (a multiple of D, base
+// aligned to D elements) with one vector load, as the accumulator type:
+// exact fixed point for fp16 (Acc = long long, `bad` flags inf/nan) or fp32.
+template <int DT, int D, typename Acc>
+__device__ __forceinline__ void load_slice(const void* base, int64_t off, Acc (&v)[D],
+                                           uint32_t& bad) {
+  typedef typename Elem<DT>::T T;
+  typedef T TV __attribute__((ext_vector_type(D)));
+  if constexpr (std::is_same<Acc, long long>::value) {
+    typedef uint16_t UV __attribute__((ext_vector_type(D)));
+    const UV x = *(const UV*)((const uint16_t*)base + off);
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      v[i] = fp16_fixed(x[i]);
+      bad |= ((x[i] & 0x7C00u) == 0x7C00u);
     }
-  }
-  __syncthreads();
-  for (int64_t i = threadIdx.x; i < nbins; i += blockDim.x) {
-    const float v = bins[i];
-    if (v == 0.f) continue;
-    const int64_t gl = i / per_group;
-    const int64_t g = q * gpb + gl;
-    if (g >= a.G) continue;
-    const int64_t p = h * a.G + g;
-    atomicAdd(&a.grad_tables[p * per_group + (i % per_group)], v);
+  } else {
+    const TV x = *(const TV*)((const T*)base + off);
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      if constexpr (DT == JKV_BF16) {
+        v[i] = __uint_as_float((uint32_t)x[i] << 16);
+      } else {
+        v[i] = (float)x[i];
+      }
+    }
   }
 }
 
-// Direct global atomics (bins too large to privatise, e.g. d = 128).
+__device__ __forceinline__ void lds_add(long long* p, long long v) {
+  atomicAdd((unsigned long long*)p, (unsigned long long)v);  // ds_add_u64
+}
+__device__ __forceinline__ void lds_add(float* p, float v) { atomicAdd(p, v); }
+
+// One block per (head h, group g, stage s, slice j of D dims of the group)
+// over a chunk of rows: the block owns bins grad[h*G+g, s, :, j*D:(j+1)*D],
+// held in LDS ([K][D+1]; the pad element spreads consecutive codewords over
+// the banks), and every row adds its exit-summed D-dim slice to the bin of its
+// stage-s code with an LDS atomic.  Splitting by bins rather than by rows
+// means no block's bins overlap another's when the rows are not chunked: the
+// block adds them straight into the gradient.  With several row chunks each
+// block stores its bins as the chunk's partial and a reduce kernel sums them.
+// Logical blocks run slice, stage, group, head, chunk from fastest to
+// slowest; xcd_remap keeps consecutive logical blocks on one XCD, so the
+// blocks that read the same rows (one head) share an L2.
+//
+// Fixed-point mode (fp16): if a slice holds inf or nan the block discards its
+// bins and adds every slice of its chunk with global fp32 atomics instead,
+// which gives the IEEE inf/nan outcome of a floating-point sum.
+template <int DT, int D>
+__global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
+  constexpr bool kFixed = DT == JKV_F16;
+  constexpr int U = 4;  // rows per thread with their loads in flight together
+  typedef typename std::conditional<kFixed, long long, float>::type Acc;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  Acc* bins = (Acc*)lds_raw;
+  __shared__ uint32_t nonfinite;
+
+  const int S = (int)a.S, K = (int)a.K, d = (int)a.d;
+  const uint32_t n_slices = (uint32_t)(d / D);
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t j = bid % n_slices;
+  const uint32_t s = (bid / n_slices) % (uint32_t)S;
+  const uint32_t p = (bid / (n_slices * S)) % (uint32_t)(a.H * a.G);
+  const uint32_t chunk = bid / (n_slices * S * (uint32_t)(a.H * a.G));
+  const uint32_t h = p / (uint32_t)a.G, g = p % (uint32_t)a.G;
+  const int per_out = K * D;
+  float* const out_base = a.grad_tables + (((int64_t)p * S + s) * K) * d + (int64_t)j * D;
+  Acc* const part_base =
+      (Acc*)a.partials + ((((int64_t)chunk * a.H * a.G + p) * S + s) * K) * d + (int64_t)j * D;
+
+  bool active = false;  // some exit reaches stage s
+  for (int e = 0; e < a.n_exits; ++e) active = active || a.exit_depth[e] > (int)s;
+  if (!active) {
+    if (a.n_chunks > 1)
+      for (int i = threadIdx.x; i < per_out; i += blockDim.x)
+        part_base[(int64_t)(i / D) * d + i % D] = (Acc)0;
+    return;
+  }
+  for (int i = threadIdx.x; i < K * (D + 1); i += blockDim.x) bins[i] = (Acc)0;
+  if (threadIdx.x == 0) nonfinite = 0u;
+  __syncthreads();
+
+  const int64_t rows = a.B * a.T;
+  const int64_t r0 = (int64_t)chunk * a.rows_per_chunk;
+  int64_t r1 = r0 + a.rows_per_chunk;
+  if (r1 > rows) r1 = rows;
+  const int64_t Dfull = a.G * d;
+  const int64_t col = (int64_t)g * d + (int64_t)j * D;
+  const uint32_t T32 = (uint32_t)a.T;
+  uint32_t bad = 0u;
+
+  // Visits the rows of the chunk U at a time: row_fn(offsets, codes, valid).
+  auto for_rows = [&](auto&& row_fn) {
+    for (int64_t row0 = r0 + threadIdx.x; row0 < r1; row0 += (int64_t)U * blockDim.x) {
+      int64_t offs[U];
+      uint32_t cv[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t row = row0 + (int64_t)u * blockDim.x;
+        ok[u] = row < r1;
+        const uint32_t rw = (uint32_t)(ok[u] ? row : r0);
+        const uint32_t b = rw / T32, t = rw - b * T32;
+        offs[u] = (((int64_t)b * a.H + h) * a.T + t) * Dfull + col;
+        cv[u] = a.codes[(int64_t)b * a.cb + (int64_t)h * a.ch + (int64_t)t * a.ct +
+                        (int64_t)g * S + s];
+      }
+      row_fn(offs, cv, ok);
+    }
+  };
+
+  for_rows([&](const int64_t(&offs)[U], const uint32_t(&cv)[U], const bool(&ok)[U]) {
+    Acc v[U][D];
+    if (a.n_exits == 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_slice<DT, D>(a.grads[0], offs[u], v[u], bad);
+    } else {
+      // stage s takes the sum of the exits deeper than s
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < D; ++i) v[u][i] = (Acc)0;
+      for (int e = 0; e < a.n_exits; ++e) {
+        if (a.exit_depth[e] <= (int)s) continue;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          Acc x[D];
+          load_slice<DT, D>(a.grads[e], offs[u], x, bad);
+#pragma unroll
+          for (int i = 0; i < D; ++i) v[u][i] += x[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      Acc* bin = bins + cv[u] * (D + 1);
+#pragma unroll
+      for (int i = 0; i < D; ++i) lds_add(&bin[i], v[u][i]);
+    }
+  });
+  if constexpr (kFixed) {
+    if (bad) atomicOr(&nonfinite, 1u);
+  }
+  __syncthreads();
+
+  if (kFixed && nonfinite) {
+    // fp32 sums with global atomics (exit sums in exit order, as grad_sum)
+    for_rows([&](const int64_t(&offs)[U], const uint32_t(&cv)[U], const bool(&ok)[U]) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!ok[u]) continue;
+        float* dst = out_base + (int64_t)cv[u] * d;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+          float acc = 0.f;
+          for (int e = 0; e < a.n_exits; ++e)
+            if (a.exit_depth[e] > (int)s) acc += Elem<DT>::load(a.grads[e], offs[u] + i);
+          if (acc != 0.f || acc != acc) atomicAdd(&dst[i], acc);
+        }
+      }
+    });
+    if (a.n_chunks > 1)
+      for (int i = threadIdx.x; i < per_out; i += blockDim.x)
+        part_base[(int64_t)(i / D) * d + i % D] = (Acc)0;
+    return;
+  }
+  for (int i = threadIdx.x; i < per_out; i += blockDim.x) {
+    const int k = i / D, c = i - k * D;
+    const Acc v = bins[k * (D + 1) + c];
+    if (a.n_chunks == 1) {
+      if constexpr (kFixed) {
+        out_base[(int64_t)k * d + c] += fixed_to_float(v);
+      } else {
+        out_base[(int64_t)k * d + c] += v;
+      }
+    } else {
+      part_base[(int64_t)k * d + c] = v;
+    }
+  }
+}
+
+// grad[p, ...] += sum over chunks of the per-chunk partials: an exact integer
+// sum for fixed-point partials, else an fp32 sum in chunk order.
+template <typename Acc>
+__global__ __launch_bounds__(256) void scatter_chunk_reduce_kernel(ScatterArgs a,
+                                                                   int64_t per_chunk) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= per_chunk) return;
+  const Acc* part = (const Acc*)a.partials;
+  Acc acc = (Acc)0;
+  for (int64_t c = 0; c < a.n_chunks; ++c) acc += part[c * per_chunk + idx];
+  if constexpr (std::is_same<Acc, long long>::value) {
+    a.grad_tables[idx] += fixed_to_float(acc);
+  } else {
+    a.grad_tables[idx] += acc;
+  }
+}
+
+// Direct global atomics, one thread per gradient element.
 template <int DT>
 __global__ __launch_bounds__(256) void scatter_global_kernel(ScatterArgs a) {
   const int64_t D = a.G * a.d;
@@ -91,7 +269,8 @@ __global__ __launch_bounds__(256) void scatter_global_kernel(ScatterArgs a) {
   const int64_t p = h * a.G + g;
   for (int s = 0; s < (int)a.S; ++s) {
     const float v = grad_sum<DT>(a, s, idx);
-    if (v != 0.f) atomicAdd(&a.grad_tables[((p * a.S + s) * a.K + cp[s]) * a.d + i], v);
+    if (v != 0.f || v != v)
+      atomicAdd(&a.grad_tables[((p * a.S + s) * a.K + cp[s]) * a.d + i], v);
   }
 }
 
@@ -121,26 +300,71 @@ __global__ __launch_bounds__(256) void scatter_det_partial_kernel(ScatterArgs a)
     if (a.codes[b * a.cb + h * a.ch + t * a.ct + g * a.S + s] != k) continue;
     acc += grad_sum<DT>(a, (int)s, ((b * a.H + h) * a.T + t) * D + g * a.d + i);
   }
-  a.partials[idx] = acc;
-}
-
-// Deterministic path, pass 2: grad += sum over chunks in chunk order.
-__global__ __launch_bounds__(256) void scatter_det_reduce_kernel(ScatterArgs a) {
-  const int64_t per_chunk = a.H * a.G * a.S * a.K * a.d;
-  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= per_chunk) return;
-  float acc = 0.f;
-  for (int64_t c = 0; c < a.n_chunks; ++c) acc += a.partials[c * per_chunk + idx];
-  a.grad_tables[idx] += acc;
+  ((float*)a.partials)[idx] = acc;
 }
 
 static const int64_t kDetRowsPerChunk = 256;
+
+// Plan of scatter_bins_kernel.  Tuning knobs: the block count to reach and
+// the minimum rows per chunk (a chunk's partial is as large as its bins).
+#ifndef JKV_SCATTER_TARGET_BLOCKS
+#define JKV_SCATTER_TARGET_BLOCKS 256
+#endif
+#ifndef JKV_SCATTER_MIN_ROWS
+#define JKV_SCATTER_MIN_ROWS 2048
+#endif
+
+struct BinsPlan {
+  bool ok;
+  bool fixed;      // exact 64-bit fixed-point bins (fp16 gradients)
+  int32_t slice;   // dims per block (D): 8 or 4, dividing d
+  int64_t chunks;  // row chunks (power of two)
+  size_t lds;      // dynamic LDS bytes per block
+  int64_t workspace;
+};
+
+static BinsPlan bins_plan(int64_t B, int64_t T, int64_t H, int64_t G, int64_t d, int64_t S,
+                          int64_t K, int32_t grad_dtype) {
+  BinsPlan r = {false, false, 0, 1, 0, 0};
+  const int64_t rows = B * T;
+  if (d % 4 != 0 || rows >= ((int64_t)1 << 31)) return r;
+  r.slice = d % 8 == 0 ? 8 : 4;
+  // fixed point: |bin| < rows * 8 exits * 2^40 must stay below 2^63
+  r.fixed = grad_dtype == JKV_F16 && rows <= ((int64_t)1 << 20);
+  const int64_t acc_bytes = r.fixed ? 8 : 4;
+  const int64_t blocks = H * G * S * (d / r.slice);
+  if (blocks >= ((int64_t)1 << 24)) return r;
+  int64_t chunks = 1;
+  while (blocks * chunks < JKV_SCATTER_TARGET_BLOCKS &&
+         ceil_div(rows, chunks * 2) >= JKV_SCATTER_MIN_ROWS)
+    chunks *= 2;
+  r.ok = true;
+  r.chunks = chunks;
+  r.lds = (size_t)(K * (r.slice + 1) * acc_bytes);
+  r.workspace = chunks > 1 ? chunks * H * G * S * K * d * acc_bytes : 0;
+  return r;
+}
+
+// The deterministic request is met by the fixed-point bins (exact sums);
+// otherwise it takes the ordered two-pass kernels.
+static bool use_ordered(const BinsPlan& plan, int32_t deterministic) {
+  return deterministic && !(plan.ok && plan.fixed);
+}
+
+static int64_t scatter_workspace(int64_t B, int64_t H, int64_t T, int64_t G, int64_t d, int64_t S,
+                                 int64_t K, int32_t grad_dtype, int32_t deterministic) {
+  const BinsPlan plan = bins_plan(B, T, H, G, d, S, K, grad_dtype);
+  if (use_ordered(plan, deterministic))
+    return ceil_div(B * T, kDetRowsPerChunk) * H * G * S * K * d * (int64_t)sizeof(float);
+  return plan.ok ? plan.workspace : 0;
+}
 
 template <int DT>
 static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) {
   const int64_t rows = a.B * a.T;
   const int64_t P = a.H * a.G;
-  if (deterministic) {
+  const BinsPlan plan = bins_plan(a.B, a.T, a.H, a.G, a.d, a.S, a.K, DT);
+  if (use_ordered(plan, deterministic)) {
     a.rows_per_chunk = kDetRowsPerChunk;
     a.n_chunks = ceil_div(rows, kDetRowsPerChunk);
     const int64_t per_chunk = P * a.S * a.K * a.d;
@@ -148,29 +372,42 @@ static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) 
                        dim3((uint32_t)ceil_div(per_chunk * a.n_chunks, 256)), dim3(256), 0,
                        stream, a);
     JKV_CHECK_LAUNCH();
-    hipLaunchKernelGGL(scatter_det_reduce_kernel, dim3((uint32_t)ceil_div(per_chunk, 256)),
-                       dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(scatter_chunk_reduce_kernel<float>,
+                       dim3((uint32_t)ceil_div(per_chunk, 256)), dim3(256), 0, stream, a,
+                       per_chunk);
     JKV_CHECK_LAUNCH();
     return JKV_OK;
   }
-  const int64_t per_group_bytes = a.S * a.K * a.d * (int64_t)sizeof(float);
-  const int64_t lds_budget = 64 * 1024;
-  if (per_group_bytes <= lds_budget) {
-    int64_t gpb = lds_budget / per_group_bytes;
-    if (gpb > a.G) gpb = a.G;
-    if (gpb > 16) gpb = 16;
-    a.groups_per_block = (int32_t)gpb;
-    const int64_t n_quads = ceil_div(a.G, gpb);
-    int64_t rpc = 4096;
-    while (rpc > 64 && a.H * n_quads * ceil_div(rows, rpc) < 1024) rpc >>= 1;
-    a.rows_per_chunk = rpc;
-    a.n_chunks = ceil_div(rows, rpc);
-    const int64_t blocks = a.H * n_quads * a.n_chunks;
-    hipLaunchKernelGGL(scatter_lds_kernel<DT>, dim3((uint32_t)blocks), dim3(256),
-                       (size_t)(gpb * per_group_bytes), stream, a);
+  bool aligned = true;
+  const uintptr_t align = (uintptr_t)(plan.ok ? plan.slice * sizeof(typename Elem<DT>::T) : 1);
+  for (int e = 0; e < a.n_exits; ++e) aligned = aligned && ((uintptr_t)a.grads[e] % align == 0);
+  JKV_CHECK_ARG(aligned || !deterministic,
+                "deterministic scatter needs gradient buffers aligned to 8 (or 4) elements");
+  if (plan.ok && aligned) {
+    a.n_chunks = plan.chunks;
+    a.rows_per_chunk = ceil_div(rows, plan.chunks);
+    const dim3 grid((uint32_t)(P * a.S * (a.d / plan.slice) * plan.chunks));
+    if (plan.slice == 8) {
+      hipLaunchKernelGGL((scatter_bins_kernel<DT, 8>), grid, dim3(1024), plan.lds, stream, a);
+    } else {
+      hipLaunchKernelGGL((scatter_bins_kernel<DT, 4>), grid, dim3(1024), plan.lds, stream, a);
+    }
     JKV_CHECK_LAUNCH();
+    if (a.n_chunks > 1) {
+      const int64_t per_chunk = P * a.S * a.K * a.d;
+      const dim3 rgrid((uint32_t)ceil_div(per_chunk, 256));
+      if (plan.fixed) {
+        hipLaunchKernelGGL(scatter_chunk_reduce_kernel<long long>, rgrid, dim3(256), 0, stream,
+                           a, per_chunk);
+      } else {
+        hipLaunchKernelGGL(scatter_chunk_reduce_kernel<float>, rgrid, dim3(256), 0, stream, a,
+                           per_chunk);
+      }
+      JKV_CHECK_LAUNCH();
+    }
     return JKV_OK;
   }
+  // misaligned gradients or d not a multiple of 4: global atomics
   const int64_t n = rows * a.H * a.G * a.d;
   hipLaunchKernelGGL(scatter_global_kernel<DT>, dim3((uint32_t)ceil_div(n, 256)), dim3(256), 0,
                      stream, a);
@@ -183,9 +420,9 @@ static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) 
 extern "C" {
 
 int64_t jkv_rvq_scatter_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t G, int64_t d,
-                                        int64_t S, int64_t K, int32_t deterministic) {
-  if (!deterministic) return 0;
-  return jkv::ceil_div(B * T, jkv::kDetRowsPerChunk) * H * G * S * K * d * (int64_t)sizeof(float);
+                                        int64_t S, int64_t K, int32_t grad_dtype,
+                                        int32_t deterministic) {
+  return jkv::scatter_workspace(B, H, T, G, d, S, K, grad_dtype, deterministic);
 }
 
 int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads, int32_t grad_dtype,
@@ -199,6 +436,8 @@ int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads, int32_t grad
   JKV_CHECK_ARG(n_exits >= 1 && n_exits <= JKV_MAX_EXITS, "1..%d exits", JKV_MAX_EXITS);
   JKV_CHECK_ARG(B >= 0 && H > 0 && T >= 0 && G > 0 && d > 0 && S > 0 && K > 0 && K <= 256,
                 "invalid scatter geometry");
+  JKV_CHECK_ARG(grad_dtype == JKV_F16 || grad_dtype == JKV_BF16 || grad_dtype == JKV_F32,
+                "unknown gradient dtype %d", grad_dtype);
   if (B * T == 0) return JKV_OK;
   JKV_CHECK_ARG(codes && grad_tables && grads, "null buffer");
   ScatterArgs a = {};
@@ -213,17 +452,16 @@ int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads, int32_t grad
   a.cb = code_stride_b; a.ch = code_stride_h; a.ct = code_stride_t;
   a.B = B; a.H = H; a.T = T; a.G = G; a.d = d; a.S = S; a.K = K;
   a.grad_tables = grad_tables;
-  if (deterministic) {
-    const int64_t need = jkv_rvq_scatter_workspace_bytes(B, H, T, G, d, S, K, 1);
+  const int64_t need = scatter_workspace(B, H, T, G, d, S, K, grad_dtype, deterministic);
+  if (need > 0) {
     JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                  "deterministic scatter needs %lld bytes of workspace", (long long)need);
-    a.partials = (float*)workspace;
+                  "scatter needs %lld bytes of workspace", (long long)need);
+    a.partials = workspace;
   }
   switch (grad_dtype) {
     case JKV_F16: return launch_scatter<JKV_F16>(a, deterministic, stream);
     case JKV_BF16: return launch_scatter<JKV_BF16>(a, deterministic, stream);
-    case JKV_F32: return launch_scatter<JKV_F32>(a, deterministic, stream);
-    default: return set_error(JKV_EINVAL, "unknown gradient dtype %d", grad_dtype);
+    default: return launch_scatter<JKV_F32>(a, deterministic, stream);
   }
 }
 

@@ -118,8 +118,13 @@ def rvq_scatter_grad(
         raise ValueError("gradient tables must be contiguous fp32")
     dtype = grads[0].dtype
     grads = [g.to(dtype).contiguous() for g in grads]
+    # the kernel loads 8- or 4-element slices with one vector load each, which
+    # needs the buffer aligned to the slice (a view may not be)
+    align = (8 if d % 8 == 0 else 4) * grads[0].element_size()
+    grads = [g if g.data_ptr() % align == 0 else g.clone() for g in grads]
     lib = _lib.load()
-    ws_bytes = int(lib.jkv_rvq_scatter_workspace_bytes(batch, heads, tokens, groups, d, stages, clusters, int(deterministic)))
+    ws_bytes = int(lib.jkv_rvq_scatter_workspace_bytes(
+        batch, heads, tokens, groups, d, stages, clusters, _lib.dtype_code(dtype), int(deterministic)))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
     code = lib.jkv_rvq_scatter_grad(
         len(grads), _lib.ptr_array(ctypes.c_void_p, [g.data_ptr() for g in grads]),

@@ -62,8 +62,24 @@ def test_workspace_queries():
     lib = _lib.load()
     assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 0) == 0
     assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 1) == 8 * 16 * 2 * 256 * 8 * 4
-    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, 0) == 0
-    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, 1) == 2 * 8 * 16 * 2 * 256 * 8 * 4
+    F16, BF16 = _lib.JKV_F16, _lib.JKV_BF16
+    bins = 8 * 16 * 2 * 256 * 8  # [H*G,S,K,d] of the config-5 V codebooks
+    # one chunk of rows: bins go straight into the gradient
+    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, F16, 0) == 0
+    # fp16 sums are exact (fixed point), so a deterministic request needs nothing more
+    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, F16, 1) == 0
+    # bf16 deterministic: ordered partials per 256-row chunk
+    assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, BF16, 1) == 2 * bins * 4
+    # one block per (head, group, stage, 8 dims) already fills the chip: no chunks
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 16, 8, 2, 256, F16, 0) == 0
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 1, 128, 2, 256, F16, 0) == 0
+    # one head: 32 blocks, so 4 row chunks of 2048 rows with per-chunk partials,
+    # 64-bit for fixed point and 32-bit otherwise
+    head = 16 * 2 * 256 * 8
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 1, 2048, 16, 8, 2, 256, F16, 0) == 4 * head * 8
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 1, 2048, 16, 8, 2, 256, _lib.JKV_F32, 0) == 4 * head * 4
+    # d not a multiple of 4: global atomics, no workspace
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 1, 2048, 1, 6, 2, 256, F16, 0) == 0
     assert lib.jkv_decode_workspace_bytes(16, 32, 128, 4096) == 16 * 32 * 16 * 130 * 4
 
 
@@ -80,6 +96,17 @@ def test_decode_rejects_unsupported_geometry():
     rc = lib.jkv_decode_attention(1, 0, 0, 1, 1, 0, 0, 4096, 1, 1, 1, 32, 8, 16, 8, 2, 256, 1,
                                   4096, 1, 0, 1, 1, 1 << 30, None)
     assert rc == _lib.JKV_EINVAL and b"rotary" in lib.jkv_last_error()
+
+
+def test_scatter_rejects_misaligned_deterministic_gradients():
+    # Validation fails before any launch: the gradient pointer (2) is not
+    # aligned to an 8-element fp16 slice and a deterministic sum was asked for.
+    lib = _lib.load()
+    grads = _lib.ptr_array(ctypes.c_void_p, [2])
+    depths = _lib.ptr_array(ctypes.c_int32, [2])
+    rc = lib.jkv_rvq_scatter_grad(1, grads, _lib.JKV_F16, depths, 1, 512, 256, 32, 1, 8, 8, 16,
+                                  8, 2, 256, 1, 1, None, 0, None)
+    assert rc == _lib.JKV_EINVAL and b"aligned" in lib.jkv_last_error()
 
 
 def test_product_rejects_host_tensors_loudly():

@@ -108,3 +108,109 @@ def test_gradient_sum_invariant_full_layer(device):
     idx = (torch.arange(128, device=device)[:, None, None] * 2 + torch.arange(2, device=device)[None, :, None]) * 256 + flat
     counts.index_add_(0, idx.reshape(-1), torch.ones(idx.numel(), device=device))
     assert int(counts.sum()) == 4 * 2048 * 8 * 16 * 2
+
+
+def _random_scatter_case(gen, batch, heads, tokens, groups, d, stages, n_exits, dtype, scale=0.03):
+    codes = torch.randint(0, 256, (batch, heads, tokens, groups, stages), generator=gen, dtype=torch.int32)
+    grads = [(torch.randn(batch, heads, tokens, groups * d, generator=gen) * scale).to(dtype) for _ in range(n_exits)]
+    return codes.to(torch.uint8), grads
+
+
+EXACT_CASES = [
+    # (B, H, T, G, d, S, exits): one chunk, row chunks (one head), several
+    # exits, full-vector RVQ (d = 128 in 8-dim slices), grouped CQ (d = 4)
+    (4, 8, 200, 16, 8, 2, (2,)),
+    (4, 1, 2048, 16, 8, 2, (2,)),
+    (4, 1, 2048, 16, 8, 2, (1, 2)),
+    (2, 2, 300, 1, 128, 3, (1, 3)),
+    (2, 2, 100, 32, 4, 1, (1,)),
+]
+
+
+@pytest.mark.parametrize("case", EXACT_CASES)
+def test_fp16_scatter_is_the_correctly_rounded_exact_sum(device, case):
+    # fp16 gradients are summed in exact fixed point: every bin equals the fp32
+    # rounding of the exact sum (fp64 is exact at these sizes), bit for bit.
+    from jointkv_amd import _ops
+
+    batch, heads, tokens, groups, d, stages, exits = case
+    gen = torch.Generator().manual_seed(8621 + tokens + d + len(exits))
+    codes, grads = _random_scatter_case(gen, batch, heads, tokens, groups, d, stages, len(exits), torch.float16)
+    shape = (heads * groups, stages, 256, d)
+    expect = ref.table_gradient(grads, exits, codes, shape, accumulate=torch.float64).float()
+    got = torch.zeros(shape, device=device)
+    _ops.rvq_scatter_grad([g.to(device) for g in grads], exits, codes.to(device), got, group_dim=d)
+    assert torch.equal(got.cpu(), expect)
+    # accumulation into an existing gradient: one more fp32 add per bin
+    _ops.rvq_scatter_grad([g.to(device) for g in grads], exits, codes.to(device), got, group_dim=d)
+    assert torch.equal(got.cpu(), expect + expect)
+
+
+def test_scatter_global_atomic_path(device):
+    # d not a multiple of 4 takes global fp32 atomics
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(8623)
+    codes, grads = _random_scatter_case(gen, 2, 2, 150, 3, 6, 2, 2, torch.float16)
+    shape = (6, 2, 256, 6)
+    expect = ref.table_gradient(grads, (1, 2), codes, shape)
+    got = torch.zeros(shape, device=device)
+    _ops.rvq_scatter_grad([g.to(device) for g in grads], (1, 2), codes.to(device), got, group_dim=6)
+    assert _rel(got, expect) <= GRAD_RTOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("deterministic", [False, True])
+def test_bf16_fp32_scatter_matches_oracle(device, dtype, deterministic):
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(8629)
+    codes, grads = _random_scatter_case(gen, 2, 4, 600, 32, 4, 1, 1, dtype)
+    expect = ref.table_gradient(grads, (1,), codes, (128, 1, 256, 4))
+    got = torch.zeros(128, 1, 256, 4, device=device)
+    _ops.rvq_scatter_grad([g.to(device) for g in grads], (1,), codes.to(device), got, group_dim=4,
+                          deterministic=deterministic)
+    assert _rel(got, expect) <= GRAD_RTOL
+    if deterministic:
+        again = torch.zeros_like(got)
+        _ops.rvq_scatter_grad([g.to(device) for g in grads], (1,), codes.to(device), again, group_dim=4,
+                              deterministic=True)
+        assert torch.equal(got, again)
+
+
+def test_fp16_scatter_nonfinite_gradients(device):
+    # inf / nan slices: the IEEE outcome of a floating-point sum per bin
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(8641)
+    codes, grads = _random_scatter_case(gen, 1, 2, 3000, 16, 8, 2, 1, torch.float16)
+    g = grads[0]
+    g[0, 0, 5, 3] = float("inf")
+    g[0, 1, 2999, 17] = float("-inf")
+    g[0, 1, 100, 40] = float("nan")
+    expect = ref.table_gradient([g], (2,), codes, (32, 2, 256, 8), accumulate=torch.float64).float()
+    got = torch.zeros(32, 2, 256, 8, device=device)
+    _ops.rvq_scatter_grad([g.to(device)], (2,), codes.to(device), got, group_dim=8)
+    got = got.cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(expect))
+    assert torch.equal(torch.isinf(got), torch.isinf(expect))
+    assert torch.equal(got[torch.isinf(got)], expect[torch.isinf(expect)])
+    finite = torch.isfinite(expect)
+    torch.testing.assert_close(got[finite], expect[finite], rtol=1e-5, atol=1e-6)
+
+
+def test_scatter_misaligned_gradient_view(device):
+    # a contiguous view whose start is not aligned to d elements
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(8647)
+    codes, grads = _random_scatter_case(gen, 1, 2, 300, 16, 8, 2, 1, torch.float16)
+    flat = torch.zeros(grads[0].numel() + 1, dtype=torch.float16)
+    flat[1:] = grads[0].reshape(-1)
+    view = flat.to(device)[1:].view(grads[0].shape)
+    assert view.data_ptr() % 16 != 0
+    expect = ref.table_gradient(grads, (2,), codes, (32, 2, 256, 8), accumulate=torch.float64).float()
+    for deterministic in (False, True):
+        got = torch.zeros(32, 2, 256, 8, device=device)
+        _ops.rvq_scatter_grad([view], (2,), codes.to(device), got, group_dim=8, deterministic=deterministic)
+        assert torch.equal(got.cpu(), expect)

@@ -86,6 +86,58 @@ def timed(fn, steps, warmup):
     return start.elapsed_time(stop) / steps  # ms per step
 
 
+def per_launch_ms(launches, repeats: int = 3) -> float:
+    """Average time of one call in `launches`, from two HIP events on the
+    launching stream around all of them.  A spin kernel queued first keeps the
+    stream busy while the host enqueues, so the calls run back to back and the
+    events time the kernels rather than host launch gaps.  Median of
+    `repeats` passes."""
+
+    import torch
+
+    passes = []
+    for _ in range(repeats):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(100_000_000)
+        a.record()
+        for fn in launches:
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        passes.append(a.elapsed_time(b) / len(launches))
+    return sorted(passes)[len(passes) // 2]
+
+
+def measured_traffic(kernel_profile: Path) -> int | None:
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE
+    (scaled by a copy-kernel calibration), read from the committed profile
+    summary; None when the summary is absent."""
+
+    if not kernel_profile.is_file():
+        return None
+    for line in kernel_profile.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def copy_calibration() -> None:
+    """A plain 256 MiB device copy, four times: profiled with FETCH_SIZE and
+    WRITE_SIZE it gives the counters' scale (reads 256 MiB, writes 256 MiB per
+    dispatch)."""
+
+    import torch
+
+    x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    x.fill_(1.0)
+    for _ in range(4):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log("copy calibration: 4 x (256 MiB read + 256 MiB written)")
+
+
 def encode_workload(args, device):
     import torch
     from jointkv_amd import _ops
@@ -104,16 +156,9 @@ def encode_workload(args, device):
             _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
 
     ms = timed(step, args.steps, args.warmup)
-    # per-launch kernel time with events bracketing each launch
-    durations = []
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in layers]
-    for (a, b), (states, tables) in zip(ev, layers):
-        a.record()
-        _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
-        b.record()
-    torch.cuda.synchronize()
-    durations = [a.elapsed_time(b) for a, b in ev]
-    avg_launch_ms = sum(durations) / len(durations)
+    avg_launch_ms = per_launch_ms(
+        [lambda st=st, tb=tb: _ops.rvq_encode(st, tb, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+         for st, tb in layers])
     vecs_per_launch = HEADS * args.tokens
     flops_per_launch = vecs_per_launch * FLOP_PER_VEC_G2
     bytes_per_launch = vecs_per_launch * (HEAD_DIM * 2 + GROUPS * STAGES + HEAD_DIM * 2) + HEADS * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 4
@@ -187,10 +232,15 @@ def decode_workload(args, device):
                                   rope_theta=10000.0, max_length=window)
 
     attn_ms = timed(attn_only, args.steps, 1)
+    attn_layer_ms = per_launch_ms(
+        [lambda c=c, t=t: _ops.decode_attention(q, c.key, c.value, t[2], t[3], lengths, window=window,
+                                                rope_theta=10000.0, max_length=window)
+         for c, t in zip(caches, tabs)])
     bytes_per_layer = 2 * batch * kvh * window * GROUPS * STAGES + 2 * kvh * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 2 + 2 * batch * qh * HEAD_DIM * 2
     return {
         "us_per_step": ms * 1e3,
         "attention_us_per_step": attn_ms * 1e3,
+        "attention_kernels_us_per_layer": attn_layer_ms * 1e3,
         "hbm_bytes_per_step": bytes_per_layer * LAYERS,
         "hbm_frac": bytes_per_layer * LAYERS / (attn_ms / 1e3) / (HBM_PEAK_GBS * 1e9),
     }
@@ -269,7 +319,12 @@ def main() -> int:
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
     parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,vstep,cq2,cpu")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the hot path has no multi-GPU leg "
               "(per-head sharding needs no exchange; see DESIGN.md)", file=sys.stderr)
@@ -320,7 +375,7 @@ def main() -> int:
             "peak": MFMA_FP16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic(ROOT / "profiles" / "rvq_encode_mfma_g2_config2.md"),
             "kernel": "rvq_encode_mfma<8,2>",
             "avg_launch_us": enc["avg_launch_ms"] * 1e3,
             "algorithmic_flop_per_launch": enc["flops_per_launch"],

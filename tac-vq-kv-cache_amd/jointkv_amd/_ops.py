@@ -270,15 +270,19 @@ def decode_attention(
     if max_length is None:
         max_length = int(lengths.max().item()) if batch else 1
     table = rope_table(device, rope_theta, int(max_length) + 1)
+    # no sequence sees more than min(window, max_length) keys, so that span is
+    # the kernel's window (same visible set; smaller workspace; a cache may be
+    # shorter than the model's window)
+    span = max(1, min(int(window), int(max_length)))
     lib = _lib.load()
     out = torch.empty((batch, qheads, dim), dtype=torch.float16, device=device)
-    ws_bytes = int(lib.jkv_decode_workspace_bytes(batch, qheads, dim, int(window)))
+    ws_bytes = int(lib.jkv_decode_workspace_bytes(batch, qheads, dim, span))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     code = lib.jkv_decode_attention(
         q.data_ptr(), q.stride(0), q.stride(1), key_codes.data_ptr(), value_codes.data_ptr(),
         key_codes.stride(0), key_codes.stride(1), cap, key_tables16.data_ptr(),
         value_tables16.data_ptr(), batch, qheads, kvheads, groups, d, stages, clusters,
-        lengths.data_ptr(), int(window), table.data_ptr(), int(table.shape[0]), out.data_ptr(),
+        lengths.data_ptr(), span, table.data_ptr(), int(table.shape[0]), out.data_ptr(),
         workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
     )
     _lib.check(code)

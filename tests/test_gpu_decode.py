@@ -60,9 +60,14 @@ def test_ragged_lengths_and_cache_append(device):
     # capacity 1024 slots serves a 1024-token window
     out = jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device),
                                vt.half().to(device), lengths.to(device), window=1024)
+    # a 4096 window over sequences of at most 1024 tokens sees the same keys
+    wide = jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device),
+                                vt.half().to(device), lengths.to(device), window=4096)
+    assert torch.equal(wide, out)
+    # but a declared length beyond the ring's capacity is refused
     with pytest.raises(ValueError, match="capacity"):
         jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device),
-                             vt.half().to(device), lengths.to(device), window=4096)
+                             vt.half().to(device), lengths.to(device), window=4096, max_length=2048)
     for b in range(batch):
         L = int(lengths[b])
         e = _expect(q[b : b + 1], kc[b : b + 1], vc[b : b + 1], kt, vt, L, 1024, 1024)

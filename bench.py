@@ -11,6 +11,8 @@ Extra measurements in the same JSON line:
   decode   config 4: fused packed-code GQA decode (32q/8kv, B16, 4096 window,
            G2 codes), one new token per step over 32 layers (encode + append +
            attention per layer), us/step
+  prefill  config 4: 2048-token causal prefill chunk (B16, 32q/8kv), us per
+           layer and MFMA fraction
   vstep    config 5: V-only STE calibration step over 32 layers at
            [4,8,2048,128] (encode fwd, scatter bwd, global clip, SGD), steps/s
   cq2      config 3: reference cq2 grouped-CQ encode ([8,32,256,4]) of
@@ -246,6 +248,39 @@ def decode_workload(args, device):
     }
 
 
+def prefill_workload(args, device):
+    """Config 4 prefill chunk: 2048 tokens, B16, 32/8 heads, causal with the
+    4096 sliding window, fp16 K/V as the codec reconstructs them; 32 layers
+    per step over 4 distinct layer inputs (1.5 GiB, beyond the caches)."""
+
+    import torch
+    from jointkv_amd import _ops
+
+    batch, qh, kvh, tokens = 16, 32, 8, 2048
+    gen = torch.Generator(device=device).manual_seed(8601)
+    inputs = []
+    for _ in range(4):
+        q = torch.randn(batch, qh, tokens, HEAD_DIM, generator=gen, device=device).half()
+        k = torch.randn(batch, kvh, tokens, HEAD_DIM, generator=gen, device=device).half()
+        v = torch.randn(batch, kvh, tokens, HEAD_DIM, generator=gen, device=device).half()
+        inputs.append((q, k, v))
+    starts = torch.zeros(batch, dtype=torch.int32, device=device)
+
+    def layer(i):
+        q, k, v = inputs[i % len(inputs)]
+        return _ops.prefill_attention(q, k, v, starts, window=4096, rope_theta=10000.0, max_position=tokens - 1)
+
+    ms = timed(lambda: [layer(i) for i in range(LAYERS)], max(1, args.steps // 2), 1)
+    layer_ms = per_launch_ms([lambda i=i: layer(i) for i in range(LAYERS)])
+    flops = 4.0 * batch * qh * HEAD_DIM * tokens * (tokens + 1) / 2  # causal QK^T + PV
+    return {
+        "ms_per_step": ms,
+        "us_per_layer": layer_ms * 1e3,
+        "tflops": flops / (layer_ms / 1e3) / 1e12,
+        "mfma_frac": flops / (layer_ms / 1e3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+    }
+
+
 def vstep_workload(args, device):
     import torch
     from jointkv_amd import _ops
@@ -318,7 +353,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
-    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,vstep,cq2,cpu")
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,cq2,cpu")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
@@ -343,6 +378,9 @@ def main() -> int:
     if "decode" not in skip:
         log("decode workload (config 4)")
         extras["decode"] = decode_workload(args, device)
+    if "prefill" not in skip:
+        log("prefill workload (config 4 prefill chunk)")
+        extras["prefill"] = prefill_workload(args, device)
     if "vstep" not in skip:
         log("V-only step workload (config 5)")
         extras["v_only_step"] = vstep_workload(args, device)

@@ -175,6 +175,33 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b,
                          int64_t workspace_bytes, jkv_stream_t stream);
 
 /*
+ * Causal sliding-window GQA prefill attention over one chunk's quantized K̂/V̂.
+ * Replaces the prefill branch of attention_forward
+ * (experiments_followup_mistral/evaluate_mistral_longbench.py:101-111) and its
+ * training twin (experiments/train_full_model_closed_loop_vq.py:277-304):
+ * RoPE of q and K̂ at positions start_positions[b] + t (the reference's fp16
+ * rotary arithmetic), repeat_kv, and SDPA where query t sees keys s with
+ * s <= t and t - s < window (the model's causal + sliding-window mask).
+ *   q        [B,QH,T,128] fp16 pre-RoPE, element strides (b, h, t)
+ *   k, v     [B,KVH,T,128] fp16 pre-RoPE chunk K̂/V̂ (e.g. encode exits or
+ *            jkv_rvq_decode output), element strides (b, h, t)
+ *   start_positions  [B] int32 device
+ *   rope_table  jkv_rope_table() output, rope_len > max position
+ *   out      [B,QH,T,128] fp16 contiguous
+ * Strides must be multiples of 8 elements and buffers 16-byte aligned.
+ */
+int jkv_prefill_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                          int64_t q_stride_t, const void* k,
+                          int64_t k_stride_b, int64_t k_stride_h,
+                          int64_t k_stride_t, const void* v,
+                          int64_t v_stride_b, int64_t v_stride_h,
+                          int64_t v_stride_t, int64_t B, int64_t QH,
+                          int64_t KVH, int64_t T, int64_t D,
+                          const int32_t* start_positions, int64_t window,
+                          const void* rope_table, int64_t rope_len, void* out,
+                          jkv_stream_t stream);
+
+/*
  * Rotary (cos, sin) table for head_dim 128, fp16 pairs [n_pos][64][2]:
  * angle = fp32(p) * inv_freq[i] in fp32, cos/sin in fp32 rounded to fp16 —
  * the arithmetic of the reference's rotary module

@@ -423,6 +423,54 @@ def decode_attention(
     return out.to(torch.float16)
 
 
+def sliding_causal_mask(tokens: int, window: int) -> torch.Tensor:
+    """[T,T] bool: query t sees key s iff s <= t and t - s < window.
+
+    The causal mask with Mistral's sliding window (HF transformers 4.45.1
+    Mistral attention mask, third-party; restated) for a chunk whose
+    positions are consecutive.
+    """
+
+    t = torch.arange(tokens)
+    diff = t[:, None] - t[None, :]
+    return (diff >= 0) & (diff < window)
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    key_hat: torch.Tensor,
+    value_hat: torch.Tensor,
+    start_positions: Sequence[int],
+    *,
+    window: int = 4096,
+    theta: float = 10000.0,
+) -> torch.Tensor:
+    """The prefill branch of evaluate_mistral_longbench.py:101-111 (and its
+    training twin train_full_model_closed_loop_vq.py:277-304).
+
+    q [B,QH,T,D] fp16 pre-RoPE; key_hat/value_hat [B,KVH,T,D] fp16 (the
+    chunk's quantized K/V, pre-RoPE).  Positions of batch row b are
+    start_positions[b] + t.  RoPE(q), RoPE(K̂) in fp16, repeat_kv, SDPA with
+    the causal sliding-window mask in fp32 on the fp16 operands; output fp16
+    [B,QH,T,D].
+    """
+
+    batch, _qh, tokens, head_dim = map(int, q.shape)
+    groups = q.shape[1] // key_hat.shape[1]
+    mask = sliding_causal_mask(tokens, window)
+    outs = []
+    for b in range(batch):
+        pos = torch.arange(tokens) + int(start_positions[b])
+        c, s = rotary_cos_sin(pos, head_dim, theta)
+        qr = apply_rotary(q[b : b + 1], c[None, None], s[None, None])
+        kr = apply_rotary(key_hat[b : b + 1], c[None, None], s[None, None])
+        kr = kr.repeat_interleave(groups, dim=1)
+        vr = value_hat[b : b + 1].repeat_interleave(groups, dim=1)
+        out = F.scaled_dot_product_attention(qr.float(), kr.float(), vr.float(), attn_mask=mask, dropout_p=0.0)
+        outs.append(out.to(torch.float16))
+    return torch.cat(outs, dim=0)
+
+
 def attention_fp64(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
     """Textbook softmax(q k^T / sqrt(D)) v in fp64 (pin for the SDPA leg)."""
 

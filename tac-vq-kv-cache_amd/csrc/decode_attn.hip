@@ -11,6 +11,7 @@
 //  * the split's unnormalised (max, sum, out) go to a workspace that
 //    decode_combine folds into fp16 outputs.
 #include "jkv_common.h"
+#include "rotary.h"
 
 namespace jkv {
 
@@ -37,18 +38,6 @@ struct DecodeArgs {
   _Float16* out;
 };
 
-// HF rotary in fp16: (x * cos) + (rotate_half(x) * sin), every operation
-// rounded to fp16.  a = dims [0,64), b = dims [64,128) of one rotary pair.
-#pragma clang fp contract(off)
-__device__ __forceinline__ void rope16(half8 a, half8 b, half8 c, half8 s, half8* ra, half8* rb) {
-  const half8 ac = a * c;
-  const half8 bs = b * s;
-  const half8 bc = b * c;
-  const half8 as = a * s;
-  *ra = ac + (-bs);
-  *rb = bc + as;
-}
-#pragma clang fp contract(on)
 
 // fp16 words of dims [8*c8, 8*c8+8) of one token: fp16(sum_s fp32(word_s)).
 // The sum of two fp16 words is exact in fp32 or too small to move the fp16
@@ -90,19 +79,6 @@ __device__ __forceinline__ half8 rebuild8(const uint8_t* codes_tok, const _Float
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = (_Float16)acc[e];
     return r;
-  }
-}
-
-__device__ __forceinline__ void load_trig8(const half2v* row, int i0, half8* c, half8* s) {
-  // 8 consecutive frequencies starting at i0: (cos, sin) pairs -> two half8
-  const half8 p0 = *(const half8*)(row + i0);
-  const half8 p1 = *(const half8*)(row + i0 + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    (*c)[e] = p0[2 * e];
-    (*s)[e] = p0[2 * e + 1];
-    (*c)[e + 4] = p1[2 * e];
-    (*s)[e + 4] = p1[2 * e + 1];
   }
 }
 

@@ -1,0 +1,297 @@
+// Causal sliding-window GQA prefill attention over the chunk's quantized
+// fp16 K̂/V̂ (pre-RoPE), with the reference model's fp16 rotary applied to
+// q and K̂ at absolute positions start[b] + t.
+//
+// One workgroup of 4 waves per (batch, kv head, head group, block of query
+// rows).  Each wave owns one query head and 32 query rows (two 16-row
+// groups); the workgroup shares 64-key tiles of rotated K̂ ([key][dim]) and
+// V̂ᵀ ([dim][key]) in LDS.  Per tile and wave, on v_mfma_f32_16x16x32_f16:
+//   Sᵀ[key][row] = K̂ Qᵀ     A = K̂ rows from LDS, B = the wave's rotated q
+//   Oᵀ[dim][row] += V̂ᵀ Pᵀ   A = V̂ᵀ rows from LDS, B = fp16 P straight from
+//                           the Sᵀ accumulators (the contraction slots of
+//                           two 16-key groups are interleaved so that no
+//                           cross-lane move is needed)
+// with an online softmax in fp32 (base-2 exponent, scale folded in).
+#include <math.h>
+
+#include "jkv_common.h"
+#include "rotary.h"
+
+namespace jkv {
+
+static const int kPD = 128;            // head dim
+static const int kPKT = 64;            // keys per tile
+static const int kKStride = kPD + 8;   // K̂ tile row stride (halves): 272 B spreads keys over banks
+static const int kVStride = kPKT + 4;  // V̂ᵀ tile row stride (halves): 136 B
+
+struct PrefillArgs {
+  const _Float16* q;
+  int64_t qsb, qsh, qst;
+  const _Float16* k;
+  int64_t ksb, ksh, kst;
+  const _Float16* v;
+  int64_t vsb, vsh, vst;
+  int64_t B, QH, KVH, T;
+  const int32_t* start;  // [B] position of the chunk's first token
+  int64_t window;
+  const half2v* rope;  // [rope_len][64] (cos, sin)
+  int64_t rope_len;
+  _Float16* out;  // [B,QH,T,D] contiguous
+  int32_t heads_per_wg;  // HW: query heads per workgroup (min(NQ, 4))
+  int32_t row_sets;      // 4 / HW: 32-row sets per head in a workgroup
+  int32_t head_groups;   // NQ / HW
+};
+
+__device__ __forceinline__ float lane_group_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float lane_group_sum(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
+  __shared__ __align__(16) _Float16 k_lds[kPKT * kKStride];
+  __shared__ __align__(16) _Float16 v_lds[kPD * kVStride];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int HW = a.heads_per_wg, RS = a.row_sets;
+  const int64_t block_rows = 32 * (int64_t)RS;
+  const int64_t nqb = ceil_div(a.T, block_rows);
+  const int64_t qblk = nqb - 1 - (int64_t)blockIdx.x;  // longest key ranges first
+  const int64_t kvh = blockIdx.y / a.head_groups;
+  const int64_t hg = blockIdx.y % a.head_groups;
+  const int64_t b = blockIdx.z;
+  const int64_t NQ = a.QH / a.KVH;
+  const int64_t head = kvh * NQ + hg * HW + wave % HW;
+  const int64_t wg_row0 = qblk * block_rows;
+  int64_t wg_row1 = wg_row0 + block_rows;
+  if (wg_row1 > a.T) wg_row1 = a.T;
+  const int64_t row0 = wg_row0 + (wave / HW) * 32;  // this wave's first query row
+  const int64_t p0 = a.start[b];
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kPD);  // log2(e)/sqrt(D)
+
+  auto rope_row = [&](int64_t pos) -> const half2v* {
+    int64_t r = pos < 0 ? 0 : pos;
+    if (r >= a.rope_len) r = a.rope_len - 1;
+    return a.rope + r * 64;
+  };
+
+  // ---- the wave's rotated queries: B operand (8 dims of row ln per lane) ----
+  half8 qf[2][4];
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg) {
+    const int64_t row = row0 + 16 * rg + ln;
+    const bool ok = row < a.T;
+    const _Float16* qp = a.q + b * a.qsb + head * a.qsh + (ok ? row : 0) * a.qst;
+    const half2v* tr = rope_row(p0 + (ok ? row : 0));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int d0 = 32 * c + 8 * lg;  // < 64; partner d0 + 64
+      half8 x0 = *(const half8*)(qp + d0);
+      half8 x1 = *(const half8*)(qp + d0 + 64);
+      half8 cs, sn;
+      load_trig8(tr, d0, &cs, &sn);
+      half8 r0, r1;
+      rope16(x0, x1, cs, sn, &r0, &r1);
+      const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+      qf[rg][c] = ok ? r0 : zero;
+      qf[rg][c + 2] = ok ? r1 : zero;
+    }
+  }
+
+  float4v o[2][8];
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[rg][dt] = float4v{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY};
+  float l[2] = {0.f, 0.f};
+
+  int64_t kmin = wg_row0 - a.window + 1;
+  if (kmin < 0) kmin = 0;
+  const int64_t tile0 = kmin / kPKT;
+  const int64_t tile1 = ceil_div(wg_row1, kPKT);
+  const _Float16* kbase = a.k + b * a.ksb + kvh * a.ksh;
+  const _Float16* vbase = a.v + b * a.vsb + kvh * a.vsh;
+
+  for (int64_t tile = tile0; tile < tile1; ++tile) {
+    const int64_t key0 = tile * kPKT;
+    __syncthreads();  // previous tile's LDS reads are done
+    {
+      // K̂: thread -> key tid/4, dims {8p, 8p+32} and partners +64, rotated
+      const int kk = tid >> 2, part = tid & 3;
+      const int64_t key = key0 + kk;
+      const bool ok = key < a.T;
+      const _Float16* kp = kbase + (ok ? key : 0) * a.kst;
+      const half2v* tr = rope_row(p0 + (ok ? key : 0));
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int d0 = 8 * part + 32 * c;
+        half8 x0 = *(const half8*)(kp + d0);
+        half8 x1 = *(const half8*)(kp + d0 + 64);
+        half8 cs, sn, r0, r1;
+        load_trig8(tr, d0, &cs, &sn);
+        rope16(x0, x1, cs, sn, &r0, &r1);
+        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+        *(half8*)(k_lds + kk * kKStride + d0) = ok ? r0 : zero;
+        *(half8*)(k_lds + kk * kKStride + d0 + 64) = ok ? r1 : zero;
+      }
+      // V̂ᵀ: thread -> key tid%64, dims [32w, 32w+32)
+      const int vk = tid & 63, db = tid >> 6;
+      const int64_t vkey = key0 + vk;
+      const bool vok = vkey < a.T;
+      const _Float16* vp = vbase + (vok ? vkey : 0) * a.vst + 32 * db;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half8 x = *(const half8*)(vp + 8 * j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v_lds[(32 * db + 8 * j + e) * kVStride + vk] = vok ? x[e] : (_Float16)0.f;
+      }
+    }
+    __syncthreads();
+
+    // ---- Sᵀ for the wave's 32 rows: 4 key groups x 2 row groups ----
+    float4v s[4][2];
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) {
+      s[kg][0] = float4v{0.f, 0.f, 0.f, 0.f};
+      s[kg][1] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const half8 ka = *(const half8*)(k_lds + (16 * kg + ln) * kKStride + 32 * c + 8 * lg);
+        s[kg][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[0][c], s[kg][0], 0, 0, 0);
+        s[kg][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[1][c], s[kg][1], 0, 0, 0);
+      }
+    }
+    // ---- mask, online softmax, fp16 P in B-operand order ----
+    half8 pf[2][2];
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+      const int64_t qrow = row0 + 16 * rg + ln;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t key = key0 + 16 * kg + 4 * lg + e;
+          const int64_t diff = qrow - key;
+          const bool vis = diff >= 0 && diff < a.window && key < a.T;
+          const float v = vis ? s[kg][rg][e] * scale2 : -INFINITY;
+          s[kg][rg][e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = lane_group_max(mx);
+      const float m_new = fmaxf(m[rg], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m[rg] - m_use);
+      m[rg] = m_new;
+      float psum = 0.f;
+      float p[4][4];
+#pragma unroll
+      for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[kg][e] = __builtin_amdgcn_exp2f(s[kg][rg][e] - m_use);
+          psum += p[kg][e];
+        }
+      l[rg] = l[rg] * alpha + psum;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[rg][dt] *= alpha;
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[rg][kp][e] = (_Float16)p[2 * kp][e];
+          pf[rg][kp][e + 4] = (_Float16)p[2 * kp + 1][e];
+        }
+    }
+    // ---- Oᵀ += V̂ᵀ Pᵀ: contraction slot 8lg+e <-> key 32kp + 4lg + e (e < 4),
+    //      32kp + 16 + 4lg + e - 4 (e >= 4) ----
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        const _Float16* vr = v_lds + (16 * dt + ln) * kVStride + 32 * kp + 4 * lg;
+        const half4 lo = *(const half4*)vr;
+        const half4 hi = *(const half4*)(vr + 16);
+        const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[0][kp], o[0][dt], 0, 0, 0);
+        o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[1][kp], o[1][dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- normalise and store: lane holds dims 16dt + 4lg + e of row ln ----
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg) {
+    const int64_t row = row0 + 16 * rg + ln;
+    const float lt = lane_group_sum(l[rg]);
+    if (row >= a.T) continue;
+    const float inv = 1.0f / lt;
+    _Float16* op = a.out + ((b * a.QH + head) * a.T + row) * kPD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      half4 h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = (_Float16)(o[rg][dt][e] * inv);
+      *(half4*)(op + 16 * dt + 4 * lg) = h;
+    }
+  }
+}
+
+}  // namespace jkv
+
+extern "C" {
+
+int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k,
+                          int64_t k_sb, int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb,
+                          int64_t v_sh, int64_t v_st, int64_t B, int64_t QH, int64_t KVH,
+                          int64_t T, int64_t D, const int32_t* start_positions, int64_t window,
+                          const void* rope_table, int64_t rope_len, void* out,
+                          jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(D == kPD, "prefill attention supports head_dim 128, got %lld", (long long)D);
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0,
+                "invalid prefill geometry");
+  const int64_t NQ = QH / KVH;
+  JKV_CHECK_ARG((NQ & (NQ - 1)) == 0, "query heads per kv head must be a power of two");
+  JKV_CHECK_ARG(window >= 1, "window must be positive");
+  if (B == 0 || T == 0) return JKV_OK;
+  JKV_CHECK_ARG(q && k && v && out && start_positions && rope_table, "null buffer");
+  JKV_CHECK_ARG(rope_len >= 1, "rotary table is empty");
+  const int64_t strides[9] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st};
+  for (int i = 0; i < 9; ++i)
+    JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");
+  JKV_CHECK_ARG(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 == 0,
+                "prefill buffers must be 16-byte aligned");
+  PrefillArgs a = {};
+  a.q = (const _Float16*)q; a.qsb = q_sb; a.qsh = q_sh; a.qst = q_st;
+  a.k = (const _Float16*)k; a.ksb = k_sb; a.ksh = k_sh; a.kst = k_st;
+  a.v = (const _Float16*)v; a.vsb = v_sb; a.vsh = v_sh; a.vst = v_st;
+  a.B = B; a.QH = QH; a.KVH = KVH; a.T = T;
+  a.start = start_positions;
+  a.window = window;
+  a.rope = (const half2v*)rope_table;
+  a.rope_len = rope_len;
+  a.out = (_Float16*)out;
+  a.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
+  a.row_sets = 4 / a.heads_per_wg;
+  a.head_groups = (int32_t)(NQ / a.heads_per_wg);
+  const int64_t nqb = ceil_div(T, 32 * (int64_t)a.row_sets);
+  const int64_t gy = KVH * a.head_groups;
+  JKV_CHECK_ARG(nqb < ((int64_t)1 << 31) && gy <= 65535 && B <= 65535,
+                "prefill grid too large");
+  hipLaunchKernelGGL(prefill_attn_kernel, dim3((uint32_t)nqb, (uint32_t)gy, (uint32_t)B), dim3(256),
+                     0, stream, a);
+  JKV_CHECK_LAUNCH();
+  return JKV_OK;
+}
+
+}  // extern "C"

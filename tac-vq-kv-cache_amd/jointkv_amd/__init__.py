@@ -8,7 +8,13 @@ HIP kernels of ``libjkv.so``; there is no CPU fallback.
 """
 
 from . import _lib
-from .attention import PackedCodeCache, decode_attention, deploy_tables
+from .attention import (
+    PackedCodeCache,
+    decode_attention,
+    deploy_tables,
+    prefill_attention,
+    prefill_attention_from_codes,
+)
 from .budget import (
     CacheGeometry,
     StorageLedger,
@@ -45,6 +51,8 @@ __all__ = [
     "hard_grouped_residual_vq",
     "hard_residual_vq_exits",
     "pack_fixed_width",
+    "prefill_attention",
+    "prefill_attention_from_codes",
     "paired_prefix_rates",
     "prefix_index_bits",
     "residual_vq_ledger",

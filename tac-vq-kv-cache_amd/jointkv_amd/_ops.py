@@ -287,3 +287,51 @@ def decode_attention(
     )
     _lib.check(code)
     return out
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    start_positions: torch.Tensor,
+    *,
+    window: int,
+    rope_theta: float,
+    max_position: int,
+) -> torch.Tensor:
+    """Causal sliding-window GQA attention of one prefill chunk.
+
+    ``q[B,QH,T,128]``, ``key``/``value`` ``[B,KVH,T,128]`` fp16 pre-RoPE,
+    ``start_positions[B]`` int32 (position of each row's first token) and
+    ``max_position`` an upper bound of ``start + T - 1`` (sizes the rotary
+    table).  Returns ``[B,QH,T,128]`` fp16.
+    """
+
+    device = _lib.require_device(q, key, value, start_positions)
+    for name, t in (("query", q), ("key", key), ("value", value)):
+        if t.dtype != torch.float16 or t.ndim != 4 or t.shape[-1] != 128 or t.stride(-1) != 1:
+            raise ValueError(f"prefill {name} must be fp16 [B,H,T,128] with a contiguous last axis")
+    batch, qheads, tokens, dim = map(int, q.shape)
+    if key.shape != value.shape or key.shape[0] != batch or key.shape[2] != tokens:
+        raise ValueError("prefill query/key/value geometry differs")
+    kvheads = int(key.shape[1])
+    if qheads % kvheads:
+        raise ValueError("query heads must be a multiple of kv heads")
+    tensors = []
+    for t in (q, key, value):
+        if any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
+            t = t.contiguous()
+        tensors.append(t)
+    q, key, value = tensors
+    if start_positions.dtype != torch.int32 or start_positions.shape != (batch,):
+        raise ValueError("start_positions must be int32 [B]")
+    start_positions = start_positions.contiguous()
+    table = rope_table(device, rope_theta, int(max_position) + 1)
+    out = torch.empty((batch, qheads, tokens, dim), dtype=torch.float16, device=device)
+    code = _lib.load().jkv_prefill_attention(
+        q.data_ptr(), *q.stride()[:3], key.data_ptr(), *key.stride()[:3], value.data_ptr(),
+        *value.stride()[:3], batch, qheads, kvheads, tokens, dim, start_positions.data_ptr(),
+        int(window), table.data_ptr(), int(table.shape[0]), out.data_ptr(), _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return out

@@ -1,4 +1,5 @@
-"""Decode attention straight from a packed uint8 code cache.
+"""Attention consumers of the quantized cache: decode straight from a packed
+uint8 code cache, and prefill over a chunk's quantized K̂/V̂.
 
 The reference's LongBench decode loop (experiments_followup_mistral/
 evaluate_mistral_longbench.py:29-124) keeps uint8 codes *and* a decoded fp16
@@ -76,6 +77,73 @@ def decode_attention(
         window=window, rope_theta=rope_theta, max_length=max_length,
     )
     return out if squeeze else out.unsqueeze(2)
+
+
+def _start_tensor(start_positions, batch: int, tokens: int, device) -> tuple[torch.Tensor, int]:
+    """int32 [B] device starts and the largest position they reach."""
+
+    if isinstance(start_positions, torch.Tensor):
+        starts = start_positions.to(device=device, dtype=torch.int32).reshape(-1)
+        if starts.numel() == 1 and batch != 1:
+            starts = starts.expand(batch).contiguous()
+        top = int(starts.max().item()) if batch else 0
+    else:
+        values = [int(start_positions)] * batch if isinstance(start_positions, int) else [int(x) for x in start_positions]
+        starts = torch.tensor(values, dtype=torch.int32, device=device)
+        top = max(values) if values else 0
+    if starts.shape != (batch,):
+        raise ValueError("start positions must be one per batch row")
+    return starts, top + max(tokens, 1) - 1
+
+
+def prefill_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    start_positions=0,
+    *,
+    window: int = MISTRAL_WINDOW,
+    rope_theta: float = MISTRAL_ROPE_THETA,
+) -> torch.Tensor:
+    """Attention of a prefill chunk over its own quantized K̂/V̂.
+
+    The prefill branch of evaluate_mistral_longbench.py:101-111 (training
+    twin train_full_model_closed_loop_vq.py:277-304): RoPE of ``query``
+    ``[B,QH,T,128]`` and ``key`` ``[B,KVH,T,128]`` (fp16, pre-RoPE, e.g. the
+    codec's reconstructions) at positions ``start + t``, ``repeat_kv``, and
+    SDPA with the causal mask and Mistral's ``window``-token sliding window.
+    ``start_positions``: an int, a sequence of B ints or an int32 tensor.
+    Returns ``[B,QH,T,128]`` fp16.
+    """
+
+    batch, _qh, tokens, _d = map(int, query.shape)
+    starts, top = _start_tensor(start_positions, batch, tokens, query.device)
+    return _ops.prefill_attention(query, key, value, starts, window=window, rope_theta=rope_theta,
+                                  max_position=top)
+
+
+def prefill_attention_from_codes(
+    query: torch.Tensor,
+    key_codes: torch.Tensor,
+    value_codes: torch.Tensor,
+    key_tables16: torch.Tensor,
+    value_tables16: torch.Tensor,
+    start_positions=0,
+    *,
+    window: int = MISTRAL_WINDOW,
+    rope_theta: float = MISTRAL_ROPE_THETA,
+) -> torch.Tensor:
+    """:func:`prefill_attention` for a chunk given as uint8 codes.
+
+    ``key_codes``/``value_codes`` ``[B,KVH,T,G,S]`` and fp16 deployed tables
+    ``[KVH*G,S,K,d]``: K̂/V̂ are rebuilt once (fp16 of the fp32 stage sum,
+    the codec's reconstruction) and then attended.
+    """
+
+    stages = int(key_codes.shape[-1])
+    khat = _ops.rvq_decode(key_codes, key_tables16.float(), depth=stages, dtype=torch.float16)
+    vhat = _ops.rvq_decode(value_codes, value_tables16.float(), depth=stages, dtype=torch.float16)
+    return prefill_attention(query, khat, vhat, start_positions, window=window, rope_theta=rope_theta)
 
 
 class PackedCodeCache:

@@ -244,3 +244,30 @@ def test_synthetic_generator_is_reproducible():
     assert torch.equal(a, b)
     big = (a.float().abs() > 6).float().mean()
     assert a.dtype == torch.float16 and float(big) < 0.2
+
+
+def test_prefill_oracle_against_fp64_rows_and_masks():
+    # the window mask equals torch's is_causal when it does not bind, and each
+    # output row equals fp64 textbook attention over its visible keys
+    gen = torch.Generator().manual_seed(3)
+    mask = ref.sliding_causal_mask(40, 4096)
+    assert torch.equal(mask, torch.ones(40, 40, dtype=torch.bool).tril())
+    win = ref.sliding_causal_mask(40, 7)
+    assert int(win[39].sum()) == 7 and bool(win[39, 33]) and not bool(win[39, 32])
+    q = torch.randn(2, 4, 40, 128, generator=gen).half()
+    k = torch.randn(2, 2, 40, 128, generator=gen).half()
+    v = torch.randn(2, 2, 40, 128, generator=gen).half()
+    starts = (0, 1000)
+    for window in (4096, 7):
+        out = ref.prefill_attention(q, k, v, starts, window=window)
+        for b in range(2):
+            pos = torch.arange(40) + starts[b]
+            c, s = ref.rotary_cos_sin(pos, 128, 10000.0)
+            qr = ref.apply_rotary(q[b], c[None], s[None])
+            kr = ref.apply_rotary(k[b], c[None], s[None])
+            for hq in (0, 3):
+                for t in (0, 1, 17, 39):
+                    lo = max(0, t - window + 1)
+                    row = bf.attention_row(qr[hq, t].double().numpy(), kr[hq // 2, lo : t + 1].double().numpy(),
+                                           v[b, hq // 2, lo : t + 1].double().numpy())
+                    np.testing.assert_allclose(out[b, hq, t].float().numpy(), row, atol=2e-3)

@@ -202,7 +202,8 @@ int jkv_prefill_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           jkv_stream_t stream);
 
 /*
- * Rotary (cos, sin) table for head_dim 128, fp16 pairs [n_pos][64][2]:
+ * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of
+ * the 64 frequencies, then their sin):
  * angle = fp32(p) * inv_freq[i] in fp32, cos/sin in fp32 rounded to fp16 —
  * the arithmetic of the reference's rotary module
  * (transformers' MistralRotaryEmbedding behind

@@ -30,9 +30,10 @@ struct DecodeArgs {
   int64_t B, QH, KVH, G, d, S, K;
   const int32_t* lengths;
   int64_t window;
-  const half2v* rope;  // [rope_len][64] (cos, sin) fp16
+  const _Float16* rope;  // [rope_len][2][64]: cos row, sin row (fp16)
   int64_t rope_len;
   int32_t n_splits;
+  int32_t split_tokens;  // tokens per split
   float* ws_o;   // [B,QH,n_splits,D]
   float* ws_ml;  // [B,QH,n_splits,2]
   _Float16* out;
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
 
   // ---- rotated queries (fp16 rotary at position L-1) ----
   if (L > 0) {
-    const half2v* qrow = a.rope + ((L - 1) < a.rope_len ? (L - 1) : a.rope_len - 1) * 64;
+    const _Float16* qrow = a.rope + ((L - 1) < a.rope_len ? (L - 1) : a.rope_len - 1) * kRopeRow;
     for (int idx = tid; idx < NQ * 8; idx += blockDim.x) {
       const int h = idx / 8, c8 = idx % 8;  // dims [8c8, 8c8+8) and +64
       const _Float16* qp = a.q + b * a.qsb + (kvh * NQ + h) * a.qsh;
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       half8 k3 = rebuild8<D>(ct, a.kt, kvh, a.G, S, lg + 12);
       // the host sizes the table past every length; the clamp only keeps a
       // misuse from reading out of bounds
-      const half2v* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * 64;
+      const _Float16* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
       half8 c, s, r0, r1, r2, r3;
       load_trig8(trow, 8 * lg, &c, &s);
       rope16(k0, k2, c, s, &r0, &r2);
@@ -290,6 +291,322 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-table decode: one 512-thread workgroup (8 waves) per (kv head, batch
+// row, split of up to 2048 visible tokens).  The kv head's fp16 tables
+// ([G][S][K][d], 128 KiB at G2) are staged in LDS so every codeword gather is
+// an LDS read, and the split's code records stream through LDS in coalesced,
+// double-buffered 256-token chunks.  Wave w owns 32-key block w of every chunk
+// in both phases, so its scores never leave registers:
+//   K phase  K tables in LDS; per 16-key tile a lane rebuilds 32 dims of one
+//            key (four 8-dim chunks), rotates them with the reference's fp16
+//            rotary, and four v_mfma_f32_16x16x32_f16 give the tile's scores
+//            for every query head of the GQA group (Sᵀ = K̂ Qᵀ);
+//   softmax  split max and exp-sum per head; fp16 P in B-operand order;
+//   V phase  V tables in LDS; per 16-dim slice the wave rebuilds V̂ of its
+//            32 keys, transposes it through a small per-wave LDS tile, and one
+//            MFMA accumulates Oᵀ += V̂ᵀ Pᵀ (contraction slots of the two 16-key
+//            tiles interleaved to match the Sᵀ accumulator layout).
+// The split's (max, sum, out) go to decode_combine_kernel.
+
+static const int kLdsThreads = 512;
+static const int kLdsWaves = kLdsThreads / 64;
+static const int kLdsMaxSplit = 2048;      // 8 chunks: one register slot per chunk
+static const int kLdsChunk = 256;          // tokens per chunk: one 32-key block per wave
+static const int kLdsCodeBytes = 32;       // code-record bytes per token the buffers hold
+static const int kStgStride = 40;          // V̂ᵀ staging row stride (halves)
+
+// Code bytes of 8-dim chunk c8 of one token record (the chunk's 8/DG groups
+// x S stages are contiguous and aligned to their size).
+template <int DG>
+__device__ __forceinline__ uint32_t chunk_codes(const uint8_t* rec, int c8, int S) {
+  const int n = (8 / DG) * S;
+  const uint8_t* p = rec + c8 * n;
+  if (n == 4) return *(const uint32_t*)p;
+  if (n == 2) return *(const uint16_t*)p;
+  return *p;
+}
+
+// fp16 words of dims [8*c8, 8*c8+8) of one token from LDS tables [G][S][K][DG]
+// (S <= 2): fp16(fp32(c1) + fp32(c2)) equals the fp16 add of the two words.
+template <int DG>
+__device__ __forceinline__ half8 rebuild8_lds(const _Float16* tab, uint32_t codes, int c8, int S,
+                                              int K) {
+  if constexpr (DG == 8) {
+    const _Float16* base = tab + (c8 * S) * K * 8;
+    const half8 w0 = *(const half8*)(base + (codes & 0xffu) * 8);
+    if (S == 1) return w0;
+    const half8 w1 = *(const half8*)(base + K * 8 + ((codes >> 8) & 0xffu) * 8);
+    return w0 + w1;
+  } else {
+    half4 r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const _Float16* base = tab + ((2 * c8 + h) * S) * K * 4;
+      const uint32_t c = codes >> (8 * h * S);
+      const half4 w0 = *(const half4*)(base + (c & 0xffu) * 4);
+      if (S == 1) {
+        r[h] = w0;
+      } else {
+        const half4 w1 = *(const half4*)(base + K * 4 + ((c >> 8) & 0xffu) * 4);
+        r[h] = w0 + w1;
+      }
+    }
+    return half8{r[0][0], r[0][1], r[0][2], r[0][3], r[1][0], r[1][1], r[1][2], r[1][3]};
+  }
+}
+
+template <int DG, int NQ>
+__global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  const int S = (int)a.S, K = (int)a.K;
+  const int tab_halves = kHeadDim * S * K;  // G * S * K * DG with G * DG = 128
+  const int cb = (int)(a.G * a.S);          // code bytes per token (16 or 32)
+  _Float16* tab = (_Float16*)dyn;
+  uint8_t* cbuf = dyn + (size_t)tab_halves * 2;                        // [2][chunk][32]
+  _Float16* stg_all = (_Float16*)(cbuf + 2 * kLdsChunk * kLdsCodeBytes);  // [waves][16][stride]
+  float* red = (float*)(stg_all + kLdsWaves * 16 * kStgStride);        // [2][waves][NQ]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  _Float16* stg = stg_all + wave * 16 * kStgStride;
+  // logical block: split fastest, then batch row, then kv head (one kv head's
+  // tables stay in one XCD's L2)
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t split = bid % (uint32_t)a.n_splits;
+  const int64_t b = (bid / (uint32_t)a.n_splits) % (uint32_t)a.B;
+  const int64_t kvh = bid / ((uint32_t)a.n_splits * (uint32_t)a.B);
+  const int64_t L = a.lengths[b];
+  const int64_t n_vis = L < a.window ? L : a.window;
+  const int64_t t0 = L - n_vis + split * a.split_tokens;
+  int64_t t1 = t0 + a.split_tokens;
+  if (t1 > L) t1 = L;
+  const int ntok = t1 > t0 ? (int)(t1 - t0) : 0;
+  const int nchunks = (ntok + kLdsChunk - 1) / kLdsChunk;
+  const int64_t cbase = b * a.csb + kvh * a.csh;
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kHeadDim);  // log2(e)/sqrt(D)
+  auto rope_row = [&](int64_t pos) -> const _Float16* {
+    return a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
+  };
+  // one 16-byte piece of chunk c's code records: token i = tid*16/cb
+  const int pieces = kLdsChunk * cb / 16;
+  auto fetch_codes = [&](const uint8_t* codes, int c) -> uint4 {
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (tid < pieces) {
+      const int i = tid * 16 / cb, part = tid * 16 % cb;
+      const int t = c * kLdsChunk + i;
+      if (t < ntok) v = *(const uint4*)(codes + cbase + ((t0 + t) % a.cap) * cb + part);
+    }
+    return v;
+  };
+  auto store_codes = [&](uint4 v, int c) {
+    if (tid < pieces) {
+      const int i = tid * 16 / cb, part = tid * 16 % cb;
+      *(uint4*)(cbuf + (c & 1) * kLdsChunk * kLdsCodeBytes + i * cb + part) = v;
+    }
+  };
+  auto load_tables = [&](const _Float16* src_tab) {
+    const uint4* src = (const uint4*)(src_tab + kvh * (int64_t)tab_halves);
+    uint4* dst = (uint4*)tab;
+    const int n = tab_halves / 8;
+    for (int i0 = tid; i0 < n; i0 += 4 * kLdsThreads) {
+      uint4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * kLdsThreads;
+        if (i < n) v[u] = src[i];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * kLdsThreads;
+        if (i < n) dst[i] = v[u];
+      }
+    }
+  };
+
+  // ---- K tables and the first chunk of K codes into LDS ----
+  load_tables(a.kt);
+  if (nchunks > 0) store_codes(fetch_codes(a.kc, 0), 0);
+  // ---- rotated queries at position L-1: B operand, column ln = head ----
+  const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 qb[4];
+  {
+    const int64_t head = kvh * NQ + (ln < NQ ? ln : 0);
+    const _Float16* qp = a.q + b * a.qsb + head * a.qsh;
+    const _Float16* tr = rope_row(L > 0 ? L - 1 : 0);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int d0 = 32 * c + 8 * lg;
+      half8 x0, x1, cs, sn, r0, r1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x0[e] = qp[d0 + e];
+        x1[e] = qp[d0 + 64 + e];
+      }
+      load_trig8(tr, d0, &cs, &sn);
+      rope16(x0, x1, cs, sn, &r0, &r1);
+      qb[c] = ln < NQ ? r0 : zero8;
+      qb[c + 2] = ln < NQ ? r1 : zero8;
+    }
+  }
+  __syncthreads();
+
+  // ---- K phase.  Lane (key ln of a 16-key tile, lane group lg) owns 8-dim
+  // chunks 4c+lg (c = 0..3) = MFMA contraction slice c; chunks lg/lg+8 and
+  // lg+4/lg+12 are rotary partners.  sc[c][tl][e]: score of key 4lg+e of tile
+  // tl of the wave's block in chunk c, for head ln ----
+  float4v sc[kLdsMaxSplit / kLdsChunk][2];
+#pragma unroll
+  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c) {
+    sc[c][0] = float4v{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+    sc[c][1] = sc[c][0];
+    if (c >= nchunks) continue;
+    const uint4 next = (c + 1 < nchunks) ? fetch_codes(a.kc, c + 1) : uint4{0u, 0u, 0u, 0u};
+    const uint8_t* cur = cbuf + (c & 1) * kLdsChunk * kLdsCodeBytes;
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl) {
+      const int kb = 32 * wave + 16 * tl;  // first key of the tile in the chunk
+      const int tk = c * kLdsChunk + kb + ln;
+      const int64_t pos = t0 + (tk < ntok ? tk : 0);
+      const uint8_t* rec = cur + (kb + ln) * cb;
+      half8 k[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        k[q] = rebuild8_lds<DG>(tab, chunk_codes<DG>(rec, 4 * q + lg, S), 4 * q + lg, S, K);
+      const _Float16* tr = rope_row(pos);
+      half8 cs, sn, r[4];
+      load_trig8(tr, 8 * lg, &cs, &sn);
+      rope16(k[0], k[2], cs, sn, &r[0], &r[2]);
+      load_trig8(tr, 32 + 8 * lg, &cs, &sn);
+      rope16(k[1], k[3], cs, sn, &r[1], &r[3]);
+      float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[q], qb[q], acc, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = c * kLdsChunk + kb + 4 * lg + e;
+        sc[c][tl][e] = (ln < NQ && key < ntok) ? acc[e] * scale2 : -__builtin_inff();
+      }
+    }
+    __syncthreads();  // chunk c's records are consumed
+    if (c + 1 < nchunks) store_codes(next, c + 1);
+    __syncthreads();
+  }
+
+  // ---- split max and exp-sum per head (lanes ln < NQ carry head ln) ----
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fmaxf(sc[c][0][e], sc[c][1][e]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (lg == 0 && ln < NQ) red[wave * NQ + ln] = mx;
+  __syncthreads();
+  float mh[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < kLdsWaves; ++w) m = fmaxf(m, red[w * NQ + h]);
+    mh[h] = m;
+  }
+  const float m_lane = ln < NQ ? mh[ln < NQ ? ln : 0] : 0.f;
+  const float m_use = m_lane == -__builtin_inff() ? 0.f : m_lane;
+  half8 pf[kLdsMaxSplit / kLdsChunk];
+  float lsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pa = __builtin_amdgcn_exp2f(sc[c][0][e] - m_use);
+      const float pb = __builtin_amdgcn_exp2f(sc[c][1][e] - m_use);
+      lsum += pa + pb;
+      pf[c][e] = (_Float16)pa;
+      pf[c][e + 4] = (_Float16)pb;
+    }
+  }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (lg == 0 && ln < NQ) red[kLdsWaves * NQ + wave * NQ + ln] = lsum;
+  __syncthreads();
+  float lh[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kLdsWaves; ++w) l += red[kLdsWaves * NQ + w * NQ + h];
+    lh[h] = l;
+  }
+
+  // ---- V tables and the first chunk of V codes into LDS ----
+  load_tables(a.vt);
+  if (nchunks > 0) store_codes(fetch_codes(a.vc, 0), 0);
+  __syncthreads();
+
+  // ---- V phase: per 16-dim slice dt, lane (key L&31 of the block, chunk
+  // 2dt + L/32) rebuilds 8 dims, writes them transposed into the wave's
+  // staging tile, and lane (dim ln, lg) reads keys {4lg..4lg+3} and
+  // {16+4lg..16+4lg+3} as its A operand ----
+  float4v o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+  const int vkb = lane & 31, which = lane >> 5;
+#pragma unroll
+  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c) {
+    if (c >= nchunks) continue;
+    const uint4 next = (c + 1 < nchunks) ? fetch_codes(a.vc, c + 1) : uint4{0u, 0u, 0u, 0u};
+    const uint8_t* rec = cbuf + (c & 1) * kLdsChunk * kLdsCodeBytes + (32 * wave + vkb) * cb;
+    const bool vvalid = c * kLdsChunk + 32 * wave + vkb < ntok;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const int c8 = 2 * dt + which;
+      const half8 v = vvalid ? rebuild8_lds<DG>(tab, chunk_codes<DG>(rec, c8, S), c8, S, K) : zero8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) stg[(8 * which + e) * kStgStride + vkb] = v[e];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const half4 lo = *(const half4*)(stg + ln * kStgStride + 4 * lg);
+      const half4 hi = *(const half4*)(stg + ln * kStgStride + 16 + 4 * lg);
+      const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[c], o[dt], 0, 0, 0);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();  // chunk c's records are consumed
+    if (c + 1 < nchunks) store_codes(next, c + 1);
+    __syncthreads();
+  }
+
+  // ---- workgroup sum of the waves' Oᵀ (lane (head ln, lg) holds dims
+  // 16dt + 4lg + e) and the split's partial ----
+  __syncthreads();  // V tables no longer read: the area takes the partials
+  float* o_red = (float*)dyn;  // [waves][NQ][128]
+  if (ln < NQ) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o_red[(wave * NQ + ln) * kHeadDim + 16 * dt + 4 * lg + e] = o[dt][e];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < NQ * kHeadDim; idx += kLdsThreads) {
+    const int h = idx / kHeadDim, i = idx % kHeadDim;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kLdsWaves; ++w) v += o_red[(w * NQ + h) * kHeadDim + i];
+    const int64_t qh = kvh * NQ + h;
+    a.ws_o[((b * a.QH + qh) * a.n_splits + split) * kHeadDim + i] = v;
+    if (i == 0) {
+      float* ml = a.ws_ml + ((b * a.QH + qh) * a.n_splits + split) * 2;
+      // the combine works in natural-exponent units: m * ln 2
+      ml[0] = ntok > 0 ? mh[h] * 0.6931471805599453f : -__builtin_inff();
+      ml[1] = ntok > 0 ? lh[h] : 0.f;
+    }
+  }
+}
+
 // out[b,qh,:] = sum_s o_s e^{m_s-M} / sum_s l_s e^{m_s-M}
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
   const int64_t bq = blockIdx.x;  // b*QH + qh
@@ -308,23 +625,53 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
   a.out[bq * kHeadDim + i] = (_Float16)(Lsum > 0.f ? acc / Lsum : 0.f);
 }
 
-// Rotary table: (cos, sin) of position p and frequency i as the reference's
+// Rotary table: cos and sin of position p and frequency i as the reference's
 // rotary module computes them: angle = fp32(p) * inv_freq[i] in fp32,
 // cos/sin in fp32, then rounded to fp16.  inv_freq comes from the host.
+// Row p = [cos of the 64 frequencies | sin of the 64 frequencies].
 __global__ void rope_table_kernel(const float* __restrict__ inv_freq, int64_t n_pos,
-                                  half2v* __restrict__ out) {
+                                  _Float16* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= n_pos * 64) return;
   const int64_t p = idx / 64;
   const int i = (int)(idx % 64);
   const float ang = (float)p * inv_freq[i];
-  out[idx] = half2v{(_Float16)cosf(ang), (_Float16)sinf(ang)};
+  out[p * kRopeRow + i] = (_Float16)cosf(ang);
+  out[p * kRopeRow + 64 + i] = (_Float16)sinf(ang);
+}
+
+static const int64_t kMaxLds = 160 * 1024;
+
+// Dynamic LDS of decode_lds_kernel: tables, two code-record chunks, the
+// waves' staging tiles and the reductions.
+static int64_t lds_bytes(int64_t S, int64_t K, int64_t nq) {
+  return kHeadDim * S * K * 2 + 2 * kLdsChunk * kLdsCodeBytes +
+         kLdsWaves * 16 * kStgStride * 2 + 2 * kLdsWaves * nq * 4;
+}
+
+// Tokens per split of decode_lds_kernel (0: the geometry does not fit).
+static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int64_t window) {
+  if (S > 2 || G * S > kLdsCodeBytes || (G * S) % 16 != 0) return 0;
+  if (lds_bytes(S, K, nq) > kMaxLds) return 0;
+  if (kLdsWaves * nq * kHeadDim * 4 > kHeadDim * S * K * 2) return 0;  // partials fit the table area
+  const int64_t w = ceil_div(window, kLdsChunk) * kLdsChunk;
+  return w < kLdsMaxSplit ? w : kLdsMaxSplit;
 }
 
 template <int D, int NQ>
-static int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
-                     dim3(256), 0, stream, a);
+static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
+  const int64_t split = lds_ok ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
+  if (split > 0) {
+    a.split_tokens = (int32_t)split;
+    a.n_splits = (int32_t)ceil_div(a.window, split);
+    a.ws_ml = a.ws_o + a.B * a.QH * a.n_splits * kHeadDim;
+    const size_t lds = (size_t)lds_bytes(a.S, a.K, NQ);
+    hipLaunchKernelGGL((decode_lds_kernel<D, NQ>), dim3((uint32_t)(a.KVH * a.B * a.n_splits)),
+                       dim3(kLdsThreads), lds, stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
+                       dim3(256), 0, stream, a);
+  }
   JKV_CHECK_LAUNCH();
   hipLaunchKernelGGL(decode_combine_kernel, dim3((uint32_t)(a.B * a.QH)), dim3(kHeadDim), 0,
                      stream, a);
@@ -342,7 +689,7 @@ int jkv_rope_table(const float* inv_freq, int64_t n_pos, void* out, jkv_stream_t
   if (n_pos == 0) return JKV_OK;
   JKV_CHECK_ARG(inv_freq != nullptr && out != nullptr, "null buffer");
   hipLaunchKernelGGL(rope_table_kernel, dim3((uint32_t)ceil_div(n_pos * 64, 256)), dim3(256), 0,
-                     (hipStream_t)stream_, inv_freq, n_pos, (half2v*)out);
+                     (hipStream_t)stream_, inv_freq, n_pos, (_Float16*)out);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }
@@ -389,14 +736,19 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   a.B = B; a.QH = QH; a.KVH = KVH; a.G = G; a.d = d; a.S = S; a.K = K;
   a.lengths = lengths;
   a.window = window;
-  a.rope = (const half2v*)rope_table;
+  a.rope = (const _Float16*)rope_table;
   a.rope_len = rope_len;
   a.n_splits = (int32_t)ceil_div(window, kSplitTokens);
+  a.split_tokens = kSplitTokens;
   a.ws_o = (float*)workspace;
   a.ws_ml = a.ws_o + B * QH * a.n_splits * kHeadDim;
   a.out = (_Float16*)out;
+  // LDS-table kernel: code records and tables copied in 16-byte pieces
+  const bool lds_ok = ((uintptr_t)k_codes % 16 == 0) && ((uintptr_t)v_codes % 16 == 0) &&
+                      code_stride_b % 16 == 0 && code_stride_h % 16 == 0 &&
+                      ((uintptr_t)k_tables % 16 == 0) && ((uintptr_t)v_tables % 16 == 0);
 #define JKV_DEC(DD, NN) \
-  if (d == DD && nq == NN) return launch_decode<DD, NN>(a, stream);
+  if (d == DD && nq == NN) return launch_decode<DD, NN>(a, lds_ok, stream);
   JKV_DEC(8, 1) JKV_DEC(8, 2) JKV_DEC(8, 4) JKV_DEC(8, 8)
   JKV_DEC(4, 1) JKV_DEC(4, 2) JKV_DEC(4, 4) JKV_DEC(4, 8)
 #undef JKV_DEC

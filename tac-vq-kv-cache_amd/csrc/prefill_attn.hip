@@ -34,7 +34,7 @@ struct PrefillArgs {
   int64_t B, QH, KVH, T;
   const int32_t* start;  // [B] position of the chunk's first token
   int64_t window;
-  const half2v* rope;  // [rope_len][64] (cos, sin)
+  const _Float16* rope;  // [rope_len][2][64]: cos row, sin row
   int64_t rope_len;
   _Float16* out;  // [B,QH,T,D] contiguous
   int32_t heads_per_wg;  // HW: query heads per workgroup (min(NQ, 4))
@@ -75,10 +75,10 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
   const int64_t p0 = a.start[b];
   const float scale2 = 1.4426950408889634f / sqrtf((float)kPD);  // log2(e)/sqrt(D)
 
-  auto rope_row = [&](int64_t pos) -> const half2v* {
+  auto rope_row = [&](int64_t pos) -> const _Float16* {
     int64_t r = pos < 0 ? 0 : pos;
     if (r >= a.rope_len) r = a.rope_len - 1;
-    return a.rope + r * 64;
+    return a.rope + r * kRopeRow;
   };
 
   // ---- the wave's rotated queries: B operand (8 dims of row ln per lane) ----
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     const int64_t row = row0 + 16 * rg + ln;
     const bool ok = row < a.T;
     const _Float16* qp = a.q + b * a.qsb + head * a.qsh + (ok ? row : 0) * a.qst;
-    const half2v* tr = rope_row(p0 + (ok ? row : 0));
+    const _Float16* tr = rope_row(p0 + (ok ? row : 0));
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const int d0 = 32 * c + 8 * lg;  // < 64; partner d0 + 64
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
       const int64_t key = key0 + kk;
       const bool ok = key < a.T;
       const _Float16* kp = kbase + (ok ? key : 0) * a.kst;
-      const half2v* tr = rope_row(p0 + (ok ? key : 0));
+      const _Float16* tr = rope_row(p0 + (ok ? key : 0));
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int d0 = 8 * part + 32 * c;
@@ -278,7 +278,7 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   a.B = B; a.QH = QH; a.KVH = KVH; a.T = T;
   a.start = start_positions;
   a.window = window;
-  a.rope = (const half2v*)rope_table;
+  a.rope = (const _Float16*)rope_table;
   a.rope_len = rope_len;
   a.out = (_Float16*)out;
   a.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);

@@ -20,18 +20,14 @@ __device__ __forceinline__ void rope16(half8 a, half8 b, half8 c, half8 s, half8
 }
 #pragma clang fp contract(on)
 
-// 8 consecutive frequencies starting at i0 of one rotary-table row
-// ([64] (cos, sin) fp16 pairs) as two half8.
-__device__ __forceinline__ void load_trig8(const half2v* row, int i0, half8* c, half8* s) {
-  const half8 p0 = *(const half8*)(row + i0);
-  const half8 p1 = *(const half8*)(row + i0 + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    (*c)[e] = p0[2 * e];
-    (*s)[e] = p0[2 * e + 1];
-    (*c)[e + 4] = p1[2 * e];
-    (*s)[e + 4] = p1[2 * e + 1];
-  }
+// Rotary table row of one position: [2][64] fp16, cos of the 64 frequencies
+// then their sin.
+static const int kRopeRow = 128;
+
+// cos/sin of 8 consecutive frequencies starting at i0 of one table row.
+__device__ __forceinline__ void load_trig8(const _Float16* row, int i0, half8* c, half8* s) {
+  *c = *(const half8*)(row + i0);
+  *s = *(const half8*)(row + 64 + i0);
 }
 
 }  // namespace jkv

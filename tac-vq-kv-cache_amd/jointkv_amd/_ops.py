@@ -208,7 +208,8 @@ def rotary_inv_freq(head_dim: int, theta: float) -> torch.Tensor:
 
 
 def rope_table(device: torch.device, theta: float, n_pos: int) -> torch.Tensor:
-    """Cached fp16 (cos, sin) table [n_pos', 64, 2] with n_pos' >= n_pos."""
+    """Cached fp16 rotary table [n_pos', 2, 64] (cos row, sin row per position)
+    with n_pos' >= n_pos."""
 
     key = (str(device), float(theta))
     table = _ROPE_CACHE.get(key)
@@ -216,7 +217,7 @@ def rope_table(device: torch.device, theta: float, n_pos: int) -> torch.Tensor:
         return table
     size = 1 << max(12, (max(n_pos, 1) - 1).bit_length())
     inv = rotary_inv_freq(128, theta).to(device)
-    table = torch.empty((size, 64, 2), dtype=torch.float16, device=device)
+    table = torch.empty((size, 2, 64), dtype=torch.float16, device=device)
     _lib.check(_lib.load().jkv_rope_table(inv.data_ptr(), size, table.data_ptr(), _lib.stream_handle(device)))
     _ROPE_CACHE[key] = table
     return table

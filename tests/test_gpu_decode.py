@@ -40,6 +40,7 @@ def _expect(q, kc, vc, kt, vt, length, window, cap):
     (1, 8, 2, 16, 2, 8, 5000, 4096, 4096),    # window slides, ring buffer wraps
     (1, 4, 4, 32, 1, 4, 700, 512, 512),       # cq2 codes, MHA group of 1
     (1, 16, 2, 16, 1, 8, 257, 4096, 4096),    # cq1 codes, GQA 8
+    (1, 8, 2, 16, 3, 8, 600, 4096, 4096),     # three stages: the generic split kernel
 ])
 def test_decode_matches_oracle(device, batch, qh, kvh, groups, stages, d, length, window, cap):
     q, kc, vc, kt, vt = _case(length + qh, batch, qh, kvh, groups, stages, d, length, cap)

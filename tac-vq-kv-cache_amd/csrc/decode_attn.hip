@@ -313,42 +313,43 @@ static const int kLdsThreads = 512;
 static const int kLdsWaves = kLdsThreads / 64;
 static const int kLdsMaxSplit = 2048;      // 8 chunks: one register slot per chunk
 static const int kLdsChunk = 256;          // tokens per chunk: one 32-key block per wave
-static const int kLdsCodeBytes = 32;       // code-record bytes per token the buffers hold
-static const int kStgStride = 40;          // V̂ᵀ staging row stride (halves)
+static const int kLdsCodeBytes = 32;       // code-record bytes per token the buffer holds
+static const int kLdsK = 256;              // codewords per stage
+static const int kStgRows = 32;            // V̂ᵀ staging: 32 dims (two 16-dim slices) ...
+static const int kStgStride = 36;          // ... x 32 keys, row stride 72 B (conflict-free b32 writes)
 
 // Code bytes of 8-dim chunk c8 of one token record (the chunk's 8/DG groups
 // x S stages are contiguous and aligned to their size).
-template <int DG>
-__device__ __forceinline__ uint32_t chunk_codes(const uint8_t* rec, int c8, int S) {
-  const int n = (8 / DG) * S;
+template <int DG, int S>
+__device__ __forceinline__ uint32_t chunk_codes(const uint8_t* rec, int c8) {
+  constexpr int n = (8 / DG) * S;
   const uint8_t* p = rec + c8 * n;
-  if (n == 4) return *(const uint32_t*)p;
-  if (n == 2) return *(const uint16_t*)p;
+  if constexpr (n == 4) return *(const uint32_t*)p;
+  if constexpr (n == 2) return *(const uint16_t*)p;
   return *p;
 }
 
-// fp16 words of dims [8*c8, 8*c8+8) of one token from LDS tables [G][S][K][DG]
+// fp16 words of dims [8*c8, 8*c8+8) of one token from LDS tables [G][S][256][DG]
 // (S <= 2): fp16(fp32(c1) + fp32(c2)) equals the fp16 add of the two words.
-template <int DG>
-__device__ __forceinline__ half8 rebuild8_lds(const _Float16* tab, uint32_t codes, int c8, int S,
-                                              int K) {
+template <int DG, int S>
+__device__ __forceinline__ half8 rebuild8_lds(const _Float16* tab, uint32_t codes, int c8) {
   if constexpr (DG == 8) {
-    const _Float16* base = tab + (c8 * S) * K * 8;
+    const _Float16* base = tab + c8 * (S * kLdsK * 8);
     const half8 w0 = *(const half8*)(base + (codes & 0xffu) * 8);
-    if (S == 1) return w0;
-    const half8 w1 = *(const half8*)(base + K * 8 + ((codes >> 8) & 0xffu) * 8);
+    if constexpr (S == 1) return w0;
+    const half8 w1 = *(const half8*)(base + kLdsK * 8 + ((codes >> 8) & 0xffu) * 8);
     return w0 + w1;
   } else {
     half4 r[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const _Float16* base = tab + ((2 * c8 + h) * S) * K * 4;
+      const _Float16* base = tab + (2 * c8 + h) * (S * kLdsK * 4);
       const uint32_t c = codes >> (8 * h * S);
       const half4 w0 = *(const half4*)(base + (c & 0xffu) * 4);
-      if (S == 1) {
+      if constexpr (S == 1) {
         r[h] = w0;
       } else {
-        const half4 w1 = *(const half4*)(base + K * 4 + ((c >> 8) & 0xffu) * 4);
+        const half4 w1 = *(const half4*)(base + kLdsK * 4 + ((c >> 8) & 0xffu) * 4);
         r[h] = w0 + w1;
       }
     }
@@ -356,20 +357,26 @@ __device__ __forceinline__ half8 rebuild8_lds(const _Float16* tab, uint32_t code
   }
 }
 
-template <int DG, int NQ>
+// (a[e], b[e]) as one 32-bit word, e = 0..7
+__device__ __forceinline__ uint32_t pair_halves(half8 a, half8 b, int e) {
+  const half2v h = {a[e], b[e]};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+template <int DG, int NQ, int S>
 __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int S = (int)a.S, K = (int)a.K;
-  const int tab_halves = kHeadDim * S * K;  // G * S * K * DG with G * DG = 128
-  const int cb = (int)(a.G * a.S);          // code bytes per token (16 or 32)
+  constexpr int tab_halves = kHeadDim * S * kLdsK;  // G * S * K * DG with G * DG = 128
+  constexpr int kSlots = kLdsMaxSplit / kLdsChunk;
+  const int cb = (int)(a.G * S);  // code bytes per token (16 or 32)
   _Float16* tab = (_Float16*)dyn;
-  uint8_t* cbuf = dyn + (size_t)tab_halves * 2;                        // [2][chunk][32]
-  _Float16* stg_all = (_Float16*)(cbuf + 2 * kLdsChunk * kLdsCodeBytes);  // [waves][16][stride]
-  float* red = (float*)(stg_all + kLdsWaves * 16 * kStgStride);        // [2][waves][NQ]
+  uint8_t* cbuf = dyn + (size_t)tab_halves * 2;                           // [chunk][32]
+  _Float16* stg_all = (_Float16*)(cbuf + kLdsChunk * kLdsCodeBytes);      // [waves][32][36]
+  float* red = (float*)(stg_all + kLdsWaves * kStgRows * kStgStride);     // [2][waves][NQ]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
-  _Float16* stg = stg_all + wave * 16 * kStgStride;
+  _Float16* stg = stg_all + wave * kStgRows * kStgStride;
   // logical block: split fastest, then batch row, then kv head (one kv head's
   // tables stay in one XCD's L2)
   const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
@@ -384,9 +391,12 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
   const int ntok = t1 > t0 ? (int)(t1 - t0) : 0;
   const int nchunks = (ntok + kLdsChunk - 1) / kLdsChunk;
   const int64_t cbase = b * a.csb + kvh * a.csh;
+  const uint32_t cap = (uint32_t)a.cap;
+  const uint32_t slot0 = (uint32_t)(t0 % a.cap);  // ring slot of the split's first token
   const float scale2 = 1.4426950408889634f / sqrtf((float)kHeadDim);  // log2(e)/sqrt(D)
+  const int64_t rope_last = a.rope_len - 1;
   auto rope_row = [&](int64_t pos) -> const _Float16* {
-    return a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
+    return a.rope + (pos < rope_last ? pos : rope_last) * kRopeRow;
   };
   // one 16-byte piece of chunk c's code records: token i = tid*16/cb
   const int pieces = kLdsChunk * cb / 16;
@@ -395,38 +405,59 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     if (tid < pieces) {
       const int i = tid * 16 / cb, part = tid * 16 % cb;
       const int t = c * kLdsChunk + i;
-      if (t < ntok) v = *(const uint4*)(codes + cbase + ((t0 + t) % a.cap) * cb + part);
+      if (t < ntok) {
+        uint32_t slot = slot0 + (uint32_t)t;
+        if (slot >= cap) slot -= cap;
+        v = *(const uint4*)(codes + cbase + (int64_t)slot * cb + part);
+      }
     }
     return v;
   };
-  auto store_codes = [&](uint4 v, int c) {
+  auto store_codes = [&](uint4 v) {
     if (tid < pieces) {
       const int i = tid * 16 / cb, part = tid * 16 % cb;
-      *(uint4*)(cbuf + (c & 1) * kLdsChunk * kLdsCodeBytes + i * cb + part) = v;
+      *(uint4*)(cbuf + i * cb + part) = v;
     }
   };
+  // Tables go global -> LDS directly (global_load_lds_dwordx4: lane i of a
+  // wave lands at the wave's LDS base + 16 i), 8 KiB per workgroup-wide
+  // step.  The workgroups of one kv head (one XCD) copy the same tables at the
+  // same time; each starts at a different slice so the reads spread over the
+  // L2 channels.  The caller waits (vmcnt) and synchronises before use.
+  const int rot = (int)(bid % ((uint32_t)a.n_splits * (uint32_t)a.B));
   auto load_tables = [&](const _Float16* src_tab) {
     const uint4* src = (const uint4*)(src_tab + kvh * (int64_t)tab_halves);
     uint4* dst = (uint4*)tab;
-    const int n = tab_halves / 8;
-    for (int i0 = tid; i0 < n; i0 += 4 * kLdsThreads) {
-      uint4 v[4];
+    constexpr int n = tab_halves / 8;
+    static_assert(n % kLdsThreads == 0, "tables are whole 8 KiB slices");
+    constexpr int per = n / kLdsThreads;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * kLdsThreads;
-        if (i < n) v[u] = src[i];
-      }
+    for (int u = 0; u < per; ++u) {
+      const int uu = (u + rot) % per;
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(src + tid + uu * kLdsThreads),
+          (void __attribute__((address_space(3)))*)(dst + uu * kLdsThreads + wave * 64), 16, 0, 0);
+    }
+  };
+  // rotary rows of the two 16-key tiles of the wave's block in chunk c
+  auto fetch_trig = [&](int c, half8 (&tg)[2][4]) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * kLdsThreads;
-        if (i < n) dst[i] = v[u];
-      }
+    for (int tl = 0; tl < 2; ++tl) {
+      const int tk = c * kLdsChunk + 32 * wave + 16 * tl + ln;
+      const _Float16* tr = rope_row(t0 + (tk < ntok ? tk : 0));
+      load_trig8(tr, 8 * lg, &tg[tl][0], &tg[tl][1]);
+      load_trig8(tr, 32 + 8 * lg, &tg[tl][2], &tg[tl][3]);
     }
   };
 
-  // ---- K tables and the first chunk of K codes into LDS ----
+  // ---- every chunk's K code records into registers (one 16-byte piece per
+  // thread per chunk), the K tables and the first chunk into LDS ----
+  uint4 kcodes[kSlots];
+#pragma unroll
+  for (int c = 0; c < kSlots; ++c)
+    kcodes[c] = c < nchunks ? fetch_codes(a.kc, c) : uint4{0u, 0u, 0u, 0u};
   load_tables(a.kt);
-  if (nchunks > 0) store_codes(fetch_codes(a.kc, 0), 0);
+  if (nchunks > 0) store_codes(kcodes[0]);
   // ---- rotated queries at position L-1: B operand, column ln = head ----
   const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 qb[4];
@@ -449,36 +480,34 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
       qb[c + 2] = ln < NQ ? r1 : zero8;
     }
   }
+  half8 trig[2][4];
+  if (nchunks > 0) fetch_trig(0, trig);
+  __builtin_amdgcn_s_waitcnt(0);  // the tables' direct-to-LDS loads have landed
   __syncthreads();
 
   // ---- K phase.  Lane (key ln of a 16-key tile, lane group lg) owns 8-dim
-  // chunks 4c+lg (c = 0..3) = MFMA contraction slice c; chunks lg/lg+8 and
+  // chunks 4q+lg (q = 0..3) = MFMA contraction slice q; chunks lg/lg+8 and
   // lg+4/lg+12 are rotary partners.  sc[c][tl][e]: score of key 4lg+e of tile
   // tl of the wave's block in chunk c, for head ln ----
-  float4v sc[kLdsMaxSplit / kLdsChunk][2];
+  float4v sc[kSlots][2];
 #pragma unroll
-  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c) {
+  for (int c = 0; c < kSlots; ++c) {
     sc[c][0] = float4v{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
     sc[c][1] = sc[c][0];
     if (c >= nchunks) continue;
-    const uint4 next = (c + 1 < nchunks) ? fetch_codes(a.kc, c + 1) : uint4{0u, 0u, 0u, 0u};
-    const uint8_t* cur = cbuf + (c & 1) * kLdsChunk * kLdsCodeBytes;
+    const bool more = c + 1 < nchunks;
+    half8 tnext[2][4];
+    if (more) fetch_trig(c + 1, tnext);
 #pragma unroll
     for (int tl = 0; tl < 2; ++tl) {
       const int kb = 32 * wave + 16 * tl;  // first key of the tile in the chunk
-      const int tk = c * kLdsChunk + kb + ln;
-      const int64_t pos = t0 + (tk < ntok ? tk : 0);
-      const uint8_t* rec = cur + (kb + ln) * cb;
+      const uint8_t* rec = cbuf + (kb + ln) * cb;
       half8 k[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        k[q] = rebuild8_lds<DG>(tab, chunk_codes<DG>(rec, 4 * q + lg, S), 4 * q + lg, S, K);
-      const _Float16* tr = rope_row(pos);
-      half8 cs, sn, r[4];
-      load_trig8(tr, 8 * lg, &cs, &sn);
-      rope16(k[0], k[2], cs, sn, &r[0], &r[2]);
-      load_trig8(tr, 32 + 8 * lg, &cs, &sn);
-      rope16(k[1], k[3], cs, sn, &r[1], &r[3]);
+      for (int q = 0; q < 4; ++q) k[q] = rebuild8_lds<DG, S>(tab, chunk_codes<DG, S>(rec, 4 * q + lg), 4 * q + lg);
+      half8 r[4];
+      rope16(k[0], k[2], trig[tl][0], trig[tl][1], &r[0], &r[2]);
+      rope16(k[1], k[3], trig[tl][2], trig[tl][3], &r[1], &r[3]);
       float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[q], qb[q], acc, 0, 0, 0);
@@ -489,14 +518,26 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
       }
     }
     __syncthreads();  // chunk c's records are consumed
-    if (c + 1 < nchunks) store_codes(next, c + 1);
+    if (more) {
+      store_codes(kcodes[c + 1 < kSlots ? c + 1 : c]);
+#pragma unroll
+      for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) trig[tl][u] = tnext[tl][u];
+    }
     __syncthreads();
   }
+
+  // every chunk's V code records into registers while the softmax runs
+  uint4 vcodes[kSlots];
+#pragma unroll
+  for (int c = 0; c < kSlots; ++c)
+    vcodes[c] = c < nchunks ? fetch_codes(a.vc, c) : uint4{0u, 0u, 0u, 0u};
 
   // ---- split max and exp-sum per head (lanes ln < NQ carry head ln) ----
   float mx = -__builtin_inff();
 #pragma unroll
-  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c)
+  for (int c = 0; c < kSlots; ++c)
 #pragma unroll
     for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fmaxf(sc[c][0][e], sc[c][1][e]));
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -511,12 +552,14 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     for (int w = 0; w < kLdsWaves; ++w) m = fmaxf(m, red[w * NQ + h]);
     mh[h] = m;
   }
-  const float m_lane = ln < NQ ? mh[ln < NQ ? ln : 0] : 0.f;
+  float m_lane = 0.f;
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) m_lane = ln == h ? mh[h] : m_lane;
   const float m_use = m_lane == -__builtin_inff() ? 0.f : m_lane;
-  half8 pf[kLdsMaxSplit / kLdsChunk];
+  half8 pf[kSlots];
   float lsum = 0.f;
 #pragma unroll
-  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c) {
+  for (int c = 0; c < kSlots; ++c) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float pa = __builtin_amdgcn_exp2f(sc[c][0][e] - m_use);
@@ -541,49 +584,58 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
 
   // ---- V tables and the first chunk of V codes into LDS ----
   load_tables(a.vt);
-  if (nchunks > 0) store_codes(fetch_codes(a.vc, 0), 0);
+  if (nchunks > 0) store_codes(vcodes[0]);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  // ---- V phase: per 16-dim slice dt, lane (key L&31 of the block, chunk
-  // 2dt + L/32) rebuilds 8 dims, writes them transposed into the wave's
-  // staging tile, and lane (dim ln, lg) reads keys {4lg..4lg+3} and
-  // {16+4lg..16+4lg+3} as its A operand ----
+  // ---- V phase, two 16-dim slices (4 chunks of 8 dims) at a time: lane
+  // (chunk 4dp + (lane>>4), keys 2kp and 2kp+1 of the block, kp = lane&15)
+  // rebuilds 16 values, writes them transposed as (key pair) words into the
+  // wave's staging tile, and lane (dim ln, lg) of slice dt reads keys
+  // {4lg..4lg+3} and {16+4lg..16+4lg+3} of its dim as the A operand ----
   float4v o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = float4v{0.f, 0.f, 0.f, 0.f};
-  const int vkb = lane & 31, which = lane >> 5;
+  const int vq = lane >> 4, kp = lane & 15;
 #pragma unroll
-  for (int c = 0; c < kLdsMaxSplit / kLdsChunk; ++c) {
+  for (int c = 0; c < kSlots; ++c) {
     if (c >= nchunks) continue;
-    const uint4 next = (c + 1 < nchunks) ? fetch_codes(a.vc, c + 1) : uint4{0u, 0u, 0u, 0u};
-    const uint8_t* rec = cbuf + (c & 1) * kLdsChunk * kLdsCodeBytes + (32 * wave + vkb) * cb;
-    const bool vvalid = c * kLdsChunk + 32 * wave + vkb < ntok;
+    const bool more = c + 1 < nchunks;
+    const int kb0 = 32 * wave + 2 * kp;
+    const uint8_t* rec0 = cbuf + kb0 * cb;
+    const uint8_t* rec1 = rec0 + cb;
+    const bool ok0 = c * kLdsChunk + kb0 < ntok, ok1 = c * kLdsChunk + kb0 + 1 < ntok;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int c8 = 2 * dt + which;
-      const half8 v = vvalid ? rebuild8_lds<DG>(tab, chunk_codes<DG>(rec, c8, S), c8, S, K) : zero8;
+    for (int dp = 0; dp < 4; ++dp) {
+      const int c8 = 4 * dp + vq;
+      const half8 v0 = ok0 ? rebuild8_lds<DG, S>(tab, chunk_codes<DG, S>(rec0, c8), c8) : zero8;
+      const half8 v1 = ok1 ? rebuild8_lds<DG, S>(tab, chunk_codes<DG, S>(rec1, c8), c8) : zero8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) stg[(8 * which + e) * kStgStride + vkb] = v[e];
+      for (int e = 0; e < 8; ++e)
+        *(uint32_t*)(stg + (8 * vq + e) * kStgStride + 2 * kp) = pair_halves(v0, v1, e);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const half4 lo = *(const half4*)(stg + ln * kStgStride + 4 * lg);
-      const half4 hi = *(const half4*)(stg + ln * kStgStride + 16 + 4 * lg);
-      const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[c], o[dt], 0, 0, 0);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const _Float16* row = stg + (16 * h + ln) * kStgStride;
+        const half4 lo = *(const half4*)(row + 4 * lg);
+        const half4 hi = *(const half4*)(row + 16 + 4 * lg);
+        const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[2 * dp + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[c], o[2 * dp + h], 0, 0, 0);
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     __syncthreads();  // chunk c's records are consumed
-    if (c + 1 < nchunks) store_codes(next, c + 1);
+    if (more) store_codes(vcodes[c + 1 < kSlots ? c + 1 : c]);
     __syncthreads();
   }
 
   // ---- workgroup sum of the waves' Oᵀ (lane (head ln, lg) holds dims
   // 16dt + 4lg + e) and the split's partial ----
-  __syncthreads();  // V tables no longer read: the area takes the partials
-  float* o_red = (float*)dyn;  // [waves][NQ][128]
+  float* o_red = (float*)dyn;  // [waves][NQ][128], in the table area
   if (ln < NQ) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
@@ -642,17 +694,17 @@ __global__ void rope_table_kernel(const float* __restrict__ inv_freq, int64_t n_
 
 static const int64_t kMaxLds = 160 * 1024;
 
-// Dynamic LDS of decode_lds_kernel: tables, two code-record chunks, the
+// Dynamic LDS of decode_lds_kernel: tables, one code-record chunk, the
 // waves' staging tiles and the reductions.
-static int64_t lds_bytes(int64_t S, int64_t K, int64_t nq) {
-  return kHeadDim * S * K * 2 + 2 * kLdsChunk * kLdsCodeBytes +
-         kLdsWaves * 16 * kStgStride * 2 + 2 * kLdsWaves * nq * 4;
+static int64_t lds_bytes(int64_t S, int64_t nq) {
+  return kHeadDim * S * kLdsK * 2 + kLdsChunk * kLdsCodeBytes +
+         kLdsWaves * kStgRows * kStgStride * 2 + 2 * kLdsWaves * nq * 4;
 }
 
 // Tokens per split of decode_lds_kernel (0: the geometry does not fit).
 static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int64_t window) {
-  if (S > 2 || G * S > kLdsCodeBytes || (G * S) % 16 != 0) return 0;
-  if (lds_bytes(S, K, nq) > kMaxLds) return 0;
+  if (S > 2 || K != kLdsK || G * S > kLdsCodeBytes || (G * S) % 16 != 0) return 0;
+  if (lds_bytes(S, nq) > kMaxLds) return 0;
   if (kLdsWaves * nq * kHeadDim * 4 > kHeadDim * S * K * 2) return 0;  // partials fit the table area
   const int64_t w = ceil_div(window, kLdsChunk) * kLdsChunk;
   return w < kLdsMaxSplit ? w : kLdsMaxSplit;
@@ -665,9 +717,13 @@ static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
     a.split_tokens = (int32_t)split;
     a.n_splits = (int32_t)ceil_div(a.window, split);
     a.ws_ml = a.ws_o + a.B * a.QH * a.n_splits * kHeadDim;
-    const size_t lds = (size_t)lds_bytes(a.S, a.K, NQ);
-    hipLaunchKernelGGL((decode_lds_kernel<D, NQ>), dim3((uint32_t)(a.KVH * a.B * a.n_splits)),
-                       dim3(kLdsThreads), lds, stream, a);
+    const size_t lds = (size_t)lds_bytes(a.S, NQ);
+    const dim3 grid((uint32_t)(a.KVH * a.B * a.n_splits));
+    if (a.S == 2) {
+      hipLaunchKernelGGL((decode_lds_kernel<D, NQ, 2>), grid, dim3(kLdsThreads), lds, stream, a);
+    } else {
+      hipLaunchKernelGGL((decode_lds_kernel<D, NQ, 1>), grid, dim3(kLdsThreads), lds, stream, a);
+    }
   } else {
     hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
                        dim3(256), 0, stream, a);

@@ -62,10 +62,17 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
   const int HW = a.heads_per_wg, RS = a.row_sets;
   const int64_t block_rows = 32 * (int64_t)RS;
   const int64_t nqb = ceil_div(a.T, block_rows);
-  const int64_t qblk = nqb - 1 - (int64_t)blockIdx.x;  // longest key ranges first
-  const int64_t kvh = blockIdx.y / a.head_groups;
-  const int64_t hg = blockIdx.y % a.head_groups;
-  const int64_t b = blockIdx.z;
+  // logical block: query blocks fastest, then (kv head, head group), then
+  // batch row.  xcd_remap keeps the query blocks of one (batch, kv head) on
+  // one XCD, so its K/V tiles are fetched into one L2; longest key ranges go
+  // first within each.
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t gy = a.KVH * a.head_groups;
+  const int64_t qblk = nqb - 1 - (int64_t)(bid % (uint32_t)nqb);
+  const int64_t yz = bid / (uint32_t)nqb;
+  const int64_t kvh = (yz % gy) / a.head_groups;
+  const int64_t hg = (yz % gy) % a.head_groups;
+  const int64_t b = yz / gy;
   const int64_t NQ = a.QH / a.KVH;
   const int64_t head = kvh * NQ + hg * HW + wave % HW;
   const int64_t wg_row0 = qblk * block_rows;
@@ -285,11 +292,9 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   a.row_sets = 4 / a.heads_per_wg;
   a.head_groups = (int32_t)(NQ / a.heads_per_wg);
   const int64_t nqb = ceil_div(T, 32 * (int64_t)a.row_sets);
-  const int64_t gy = KVH * a.head_groups;
-  JKV_CHECK_ARG(nqb < ((int64_t)1 << 31) && gy <= 65535 && B <= 65535,
-                "prefill grid too large");
-  hipLaunchKernelGGL(prefill_attn_kernel, dim3((uint32_t)nqb, (uint32_t)gy, (uint32_t)B), dim3(256),
-                     0, stream, a);
+  const int64_t blocks = nqb * KVH * a.head_groups * B;
+  JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
+  hipLaunchKernelGGL(prefill_attn_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }

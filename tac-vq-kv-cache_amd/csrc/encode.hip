@@ -316,9 +316,9 @@ void rvq_encode_mfma(MfmaArgs m) {
     it.cb = b0 * a.cb + head_c + t0 * a.ct;
     it.ob = b0 * out_bstride + head_o + t0 * Dfull;
     t0 += kRowsPerIter;
-    while (t0 >= a.T) {
-      t0 -= a.T;
-      ++b0;
+    if (t0 >= a.T) {
+      b0 += t0 / a.T;
+      t0 %= a.T;
     }
     return it;
   };

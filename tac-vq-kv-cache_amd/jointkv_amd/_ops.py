@@ -29,11 +29,14 @@ def rvq_encode(
     group_dim: int,
     exits: Sequence[int],
     whiteners: torch.Tensor | None = None,
+    codes_out: torch.Tensor | None = None,
 ) -> tuple[list[torch.Tensor], torch.Tensor]:
     """Encode ``states[B,H,T,G*d]`` with fp32 masters ``tables[H*G,S,K,d]``.
 
     Returns (reconstructions at each requested exit depth in ``exits`` order,
-    codes ``[B,H,T,G,S]`` uint8).
+    codes ``[B,H,T,G,S]`` uint8).  ``codes_out`` (optional) is written in
+    place: any uint8 ``[B,H,T,G,S]`` view whose ``(G,S)`` block is contiguous,
+    e.g. the slots of a code cache.
     """
 
     device = _lib.require_device(states, tables, whiteners)
@@ -47,7 +50,13 @@ def rvq_encode(
         raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
     lib = _lib.load()
     states, (sb, sh, st) = _encode_states_strides(states)
-    codes = torch.empty((batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device)
+    if codes_out is None:
+        codes = torch.empty((batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device)
+    else:
+        codes = codes_out
+        if (codes.dtype != torch.uint8 or tuple(codes.shape) != (batch, heads, tokens, groups, stages)
+                or codes.stride(-1) != 1 or codes.stride(-2) != stages or codes.device != device):
+            raise ValueError("codes_out must be uint8 [B,H,T,G,S] with a contiguous (G,S) block")
     recon = [torch.empty((batch, heads, tokens, dim), dtype=states.dtype, device=device) for _ in exits]
     if whiteners is not None:
         whiteners = whiteners.detach().float().contiguous()

@@ -198,6 +198,27 @@ class PackedCodeCache:
         self._host_length += new
         self.lengths.fill_(self._host_length)
 
+    def encode_append(self, key: torch.Tensor, value: torch.Tensor, key_tables: torch.Tensor,
+                      value_tables: torch.Tensor, *, group_dim: int) -> None:
+        """Encode one new token per sequence (``key``/``value`` ``[B,KVH,1,G*d]``
+        fp16, fp32 masters ``[KVH*G,S,K,d]``) straight into the next slot.
+
+        The codes the codec would hand to ``LayerCache.append``
+        (evaluate_mistral_longbench.py:94-98) land in the ring buffer without
+        an intermediate tensor or copy.
+        """
+
+        if key.shape[2] != 1 or value.shape[2] != 1:
+            raise ValueError("encode_append takes one token per sequence")
+        slot = self._host_length % self.capacity
+        groups = self.key.shape[3]
+        _ops.rvq_encode(key, key_tables, groups=groups, group_dim=group_dim, exits=(),
+                        codes_out=self.key[:, :, slot : slot + 1])
+        _ops.rvq_encode(value, value_tables, groups=groups, group_dim=group_dim, exits=(),
+                        codes_out=self.value[:, :, slot : slot + 1])
+        self._host_length += 1
+        self.lengths.fill_(self._host_length)
+
     def payload_bytes(self) -> int:
         visible = min(self._host_length, self.capacity)
         per_slot = self.key.shape[3] * self.key.shape[4]

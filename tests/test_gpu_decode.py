@@ -82,3 +82,22 @@ def test_ragged_lengths_and_cache_append(device):
     assert cache.length == 11 and int(cache.lengths[0]) == 11
     for p in range(3, 11):
         assert torch.equal(cache.key[:, :, p % 8], seq[:, :, p])
+
+
+def test_encode_append_matches_encode_then_append(device):
+    # the codec's codes for one new token land in the ring slot in place
+    gen = torch.Generator().manual_seed(8609)
+    tables_k = ref.synthetic_tables(gen, (2 * 16, 2, 256, 8), (1.0, 0.5), stage_axis=1).to(device)
+    tables_v = ref.synthetic_tables(gen, (2 * 16, 2, 256, 8), (1.0, 0.5), stage_axis=1).to(device)
+    direct = jkv.PackedCodeCache(3, 2, 16, 2, capacity=4, device=device)
+    fused = jkv.PackedCodeCache(3, 2, 16, 2, capacity=4, device=device)
+    from jointkv_amd import _ops
+    for _step in range(6):  # wraps the 4-slot ring
+        k = ref.synthetic_states(gen, 3, 2, 1).to(device)
+        v = ref.synthetic_states(gen, 3, 2, 1).to(device)
+        _r, kc = _ops.rvq_encode(k, tables_k, groups=16, group_dim=8, exits=())
+        _r, vc = _ops.rvq_encode(v, tables_v, groups=16, group_dim=8, exits=())
+        direct.append(kc, vc)
+        fused.encode_append(k, v, tables_k, tables_v, group_dim=8)
+    assert torch.equal(direct.key, fused.key) and torch.equal(direct.value, fused.value)
+    assert torch.equal(direct.lengths, fused.lengths) and fused.length == 6

@@ -295,47 +295,43 @@ void rvq_encode_mfma(MfmaArgs m) {
   neg_one_slot[0] = (half_t)-1.f;
   neg_one_slot[1] = (half_t)-1.f;
 
-  // (batch, token) of the wave's first row, advanced incrementally
-  int64_t base = r_begin + wave * kRowsPerWave;
-  int64_t b0 = base / a.T;
-  int64_t t0 = base - b0 * a.T;
+  int64_t base = r_begin + wave * kRowsPerWave;  // the wave's first row
 
-  // Wave-uniform description of one iteration (64 rows).  In the common
-  // case all rows sit in one batch entry and every address is a uniform
-  // base plus (row in iteration) * stride; otherwise rows are located one by
-  // one.
+  // Wave-uniform description of one iteration (64 rows starting at row
+  // `at`).  In the common case all rows sit in one batch entry and every
+  // address is a uniform base plus (row in iteration) * stride; otherwise
+  // rows are located one by one.  Rows fit in 32 bits (host-checked).
   struct Iter {
     int64_t at, xb, cb, ob;
     bool fast;
   };
+  const uint32_t T32 = (uint32_t)a.T;
   auto plan = [&](int64_t at) {
     Iter it;
     it.at = at;
-    it.fast = t0 + kRowsPerWave <= a.T && at + kRowsPerWave <= r_end;
-    it.xb = b0 * a.sb + head_x + t0 * a.st;
-    it.cb = b0 * a.cb + head_c + t0 * a.ct;
-    it.ob = b0 * out_bstride + head_o + t0 * Dfull;
-    t0 += kRowsPerIter;
-    if (t0 >= a.T) {
-      b0 += t0 / a.T;
-      t0 %= a.T;
-    }
+    const uint32_t b0 = (uint32_t)at / T32;
+    const uint32_t t0 = (uint32_t)at - b0 * T32;
+    it.fast = t0 + kRowsPerWave <= T32 && at + kRowsPerWave <= r_end;
+    it.xb = (int64_t)b0 * a.sb + head_x + (int64_t)t0 * a.st;
+    it.cb = (int64_t)b0 * a.cb + head_c + (int64_t)t0 * a.ct;
+    it.ob = (int64_t)b0 * out_bstride + head_o + (int64_t)t0 * Dfull;
     return it;
   };
-  // per-lane offsets of tile i: (valid, states, codes, reconstruction)
+  // per-lane offsets of tile i: (valid, states, codes, reconstruction).  The
+  // row strides are below 2^24 (host-checked), so the full-rate 24-bit
+  // multiply replaces the quarter-rate 32-bit one.
   auto locate = [&](const Iter& it, int i, uint32_t* xo, uint32_t* co, uint32_t* oo) -> bool {
     const uint32_t rr = (uint32_t)(i * 16 + ln);
     if (it.fast) {
-      *xo = (uint32_t)it.xb + rr * (uint32_t)a.st;
-      *co = (uint32_t)it.cb + rr * (uint32_t)a.ct;
-      *oo = (uint32_t)it.ob + rr * (uint32_t)Dfull;
+      *xo = (uint32_t)it.xb + __umul24(rr, (uint32_t)a.st);
+      *co = (uint32_t)it.cb + __umul24(rr, (uint32_t)a.ct);
+      *oo = (uint32_t)it.ob + __umul24(rr, (uint32_t)Dfull);
       return true;
     }
     // rows, strides and offsets fit in 32 bits on this path (host-checked)
     const uint32_t row = (uint32_t)it.at + rr;
     const bool valid = row < (uint32_t)r_end;
     const uint32_t rw = valid ? row : (uint32_t)r_begin;
-    const uint32_t T32 = (uint32_t)a.T;
     const uint32_t rb = rw / T32, rt = rw - rb * T32;
     *xo = rb * (uint32_t)a.sb + (uint32_t)head_x + rt * (uint32_t)a.st;
     *co = rb * (uint32_t)a.cb + (uint32_t)head_c + rt * (uint32_t)a.ct;
@@ -605,9 +601,12 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
   // element offsets
   const int64_t x_span = (B - 1) * stride_b + (H - 1) * stride_h + (T - 1) * stride_t + G * d;
   const int64_t c_span = (B - 1) * code_stride_b + (H - 1) * code_stride_h + (T - 1) * code_stride_t + G * S;
+  // (and token strides below 2^24, for 24-bit multiplies)
   const bool offsets32 = stride_b >= 0 && stride_h >= 0 && stride_t >= 0 && code_stride_b >= 0 &&
                          code_stride_h >= 0 && code_stride_t >= 0 && x_span < ((int64_t)1 << 31) &&
-                         c_span < ((int64_t)1 << 31) && B * H * T * G * d < ((int64_t)1 << 31);
+                         c_span < ((int64_t)1 << 31) && B * H * T * G * d < ((int64_t)1 << 31) &&
+                         stride_t < ((int64_t)1 << 24) && code_stride_t < ((int64_t)1 << 24) &&
+                         G * d < ((int64_t)1 << 24);
   const bool fast = offsets32 && states_dtype == JKV_F16 && whiteners == nullptr && K == 256 &&
                     (d == 8 || d == 4) && (S == 1 || S == 2) && aligned16 && codes_aligned &&
                     recon_aligned && distinct_exits && B * T < ((int64_t)1 << 31) &&

@@ -2,10 +2,13 @@
 // fp16 K̂/V̂ (pre-RoPE), with the reference model's fp16 rotary applied to
 // q and K̂ at absolute positions start[b] + t.
 //
-// One workgroup of 4 waves per (batch, kv head, head group, block of query
+// One workgroup of 8 waves per (batch, kv head, head group, block of query
 // rows).  Each wave owns one query head and 32 query rows (two 16-row
-// groups); the workgroup shares 64-key tiles of rotated K̂ ([key][dim]) and
-// V̂ᵀ ([dim][key]) in LDS.  Per tile and wave, on v_mfma_f32_16x16x32_f16:
+// groups); the workgroup
+// shares 64-key tiles of rotated K̂ ([key][dim]) and V̂ᵀ ([dim][key]) in LDS,
+// double-buffered: the next tile's global loads are issued before the
+// current tile's MFMAs and land in the other buffer afterwards.  Per tile and
+// wave, on v_mfma_f32_16x16x32_f16:
 //   Sᵀ[key][row] = K̂ Qᵀ     A = K̂ rows from LDS, B = the wave's rotated q
 //   Oᵀ[dim][row] += V̂ᵀ Pᵀ   A = V̂ᵀ rows from LDS, B = fp16 P straight from
 //                           the Sᵀ accumulators (the contraction slots of
@@ -21,8 +24,11 @@ namespace jkv {
 
 static const int kPD = 128;            // head dim
 static const int kPKT = 64;            // keys per tile
+static const int kPThreads = 512;      // 8 waves
 static const int kKStride = kPD + 8;   // K̂ tile row stride (halves): 272 B spreads keys over banks
-static const int kVStride = kPKT + 4;  // V̂ᵀ tile row stride (halves): 136 B
+static const int kVStride = kPKT + 8;  // V̂ᵀ tile row stride (halves): 144 B, conflict-free pair writes
+static const int kKTile = kPKT * kKStride;
+static const int kVTile = kPD * kVStride;
 
 struct PrefillArgs {
   const _Float16* q;
@@ -38,7 +44,7 @@ struct PrefillArgs {
   int64_t rope_len;
   _Float16* out;  // [B,QH,T,D] contiguous
   int32_t heads_per_wg;  // HW: query heads per workgroup (min(NQ, 4))
-  int32_t row_sets;      // 4 / HW: 32-row sets per head in a workgroup
+  int32_t row_sets;      // 8 / HW: 32-row sets per head in a workgroup
   int32_t head_groups;   // NQ / HW
 };
 
@@ -53,9 +59,15 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
-  __shared__ __align__(16) _Float16 k_lds[kPKT * kKStride];
-  __shared__ __align__(16) _Float16 v_lds[kPD * kVStride];
+// (a[e], b[e]) as one 32-bit word
+__device__ __forceinline__ uint32_t pair16(half8 a, half8 b, int e) {
+  const half2v h = {a[e], b[e]};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+  __shared__ __align__(16) _Float16 k_lds[2][kKTile];
+  __shared__ __align__(16) _Float16 v_lds[2][kVTile];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
@@ -101,9 +113,8 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
       const int d0 = 32 * c + 8 * lg;  // < 64; partner d0 + 64
       half8 x0 = *(const half8*)(qp + d0);
       half8 x1 = *(const half8*)(qp + d0 + 64);
-      half8 cs, sn;
+      half8 cs, sn, r0, r1;
       load_trig8(tr, d0, &cs, &sn);
-      half8 r0, r1;
       rope16(x0, x1, cs, sn, &r0, &r1);
       const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
       qf[rg][c] = ok ? r0 : zero;
@@ -126,42 +137,56 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
   const _Float16* kbase = a.k + b * a.ksb + kvh * a.ksh;
   const _Float16* vbase = a.v + b * a.vsb + kvh * a.vsh;
 
+  // Tile loaders.  K̂: thread -> key tid/8, 8-dim chunk pair (p, p+8), p =
+  // tid%8, rotated before it is stored.  V̂: thread -> key pair tid%32, dims
+  // [8*(tid/32), +8), stored transposed as (key, key+1) words.
+  const int kk = tid >> 3, kpart = tid & 7;
+  const int vkp = tid & 31, vdb = tid >> 5;
+  struct TileRegs {
+    half8 k0, k1, v0, v1;
+  };
+  auto fetch = [&](int64_t tile, TileRegs& r) {
+    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int64_t key = tile * kPKT + kk;
+    const bool ok = key < a.T;
+    const _Float16* kp = kbase + (ok ? key : 0) * a.kst + 8 * kpart;
+    r.k0 = ok ? *(const half8*)kp : zero;
+    r.k1 = ok ? *(const half8*)(kp + 64) : zero;
+    const int64_t vk0 = tile * kPKT + 2 * vkp;
+    const bool ok0 = vk0 < a.T, ok1 = vk0 + 1 < a.T;
+    const _Float16* vp = vbase + 8 * vdb;
+    r.v0 = ok0 ? *(const half8*)(vp + vk0 * a.vst) : zero;
+    r.v1 = ok1 ? *(const half8*)(vp + (vk0 + 1) * a.vst) : zero;
+  };
+  auto store = [&](int64_t tile, const TileRegs& r, int buf) {
+    const int64_t key = tile * kPKT + kk;
+    const _Float16* tr = rope_row(p0 + (key < a.T ? key : 0));
+    half8 cs, sn, r0, r1;
+    load_trig8(tr, 8 * kpart, &cs, &sn);
+    rope16(r.k0, r.k1, cs, sn, &r0, &r1);
+    _Float16* kd = k_lds[buf] + kk * kKStride + 8 * kpart;
+    *(half8*)kd = r0;
+    *(half8*)(kd + 64) = r1;
+    _Float16* vd = v_lds[buf] + (8 * vdb) * kVStride + 2 * vkp;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) *(uint32_t*)(vd + e * kVStride) = pair16(r.v0, r.v1, e);
+  };
+
+  if (tile0 < tile1) {
+    TileRegs r;
+    fetch(tile0, r);
+    store(tile0, r, 0);
+  }
+  __syncthreads();
+
   for (int64_t tile = tile0; tile < tile1; ++tile) {
+    const int buf = (int)((tile - tile0) & 1);
     const int64_t key0 = tile * kPKT;
-    __syncthreads();  // previous tile's LDS reads are done
-    {
-      // K̂: thread -> key tid/4, dims {8p, 8p+32} and partners +64, rotated
-      const int kk = tid >> 2, part = tid & 3;
-      const int64_t key = key0 + kk;
-      const bool ok = key < a.T;
-      const _Float16* kp = kbase + (ok ? key : 0) * a.kst;
-      const _Float16* tr = rope_row(p0 + (ok ? key : 0));
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int d0 = 8 * part + 32 * c;
-        half8 x0 = *(const half8*)(kp + d0);
-        half8 x1 = *(const half8*)(kp + d0 + 64);
-        half8 cs, sn, r0, r1;
-        load_trig8(tr, d0, &cs, &sn);
-        rope16(x0, x1, cs, sn, &r0, &r1);
-        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-        *(half8*)(k_lds + kk * kKStride + d0) = ok ? r0 : zero;
-        *(half8*)(k_lds + kk * kKStride + d0 + 64) = ok ? r1 : zero;
-      }
-      // V̂ᵀ: thread -> key tid%64, dims [32w, 32w+32)
-      const int vk = tid & 63, db = tid >> 6;
-      const int64_t vkey = key0 + vk;
-      const bool vok = vkey < a.T;
-      const _Float16* vp = vbase + (vok ? vkey : 0) * a.vst + 32 * db;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const half8 x = *(const half8*)(vp + 8 * j);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          v_lds[(32 * db + 8 * j + e) * kVStride + vk] = vok ? x[e] : (_Float16)0.f;
-      }
-    }
-    __syncthreads();
+    const bool more = tile + 1 < tile1;
+    TileRegs nxt;
+    if (more) fetch(tile + 1, nxt);
+    const _Float16* kl = k_lds[buf];
+    const _Float16* vl = v_lds[buf];
 
     // ---- Sᵀ for the wave's 32 rows: 4 key groups x 2 row groups ----
     float4v s[4][2];
@@ -171,51 +196,63 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
       s[kg][1] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const half8 ka = *(const half8*)(k_lds + (16 * kg + ln) * kKStride + 32 * c + 8 * lg);
+        const half8 ka = *(const half8*)(kl + (16 * kg + ln) * kKStride + 32 * c + 8 * lg);
         s[kg][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[0][c], s[kg][0], 0, 0, 0);
         s[kg][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[1][c], s[kg][1], 0, 0, 0);
       }
     }
-    // ---- mask, online softmax, fp16 P in B-operand order ----
+    // ---- mask, online softmax, fp16 P in B-operand order.  Tiles wholly
+    // inside every row's causal window need no mask (wave-uniform test); the
+    // scale enters the exponent through one fma; the running output is only
+    // rescaled when some row's maximum moved ----
+    const bool full = key0 + kPKT - 1 <= row0 && row0 + 31 - key0 < a.window && key0 + kPKT <= a.T;
     half8 pf[2][2];
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
-      const int64_t qrow = row0 + 16 * rg + ln;
       float mx = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int kg = 0; kg < 4; ++kg)
+        for (int kg = 0; kg < 4; ++kg)
+          mx = fmaxf(fmaxf(mx, fmaxf(s[kg][rg][0], s[kg][rg][1])), fmaxf(s[kg][rg][2], s[kg][rg][3]));
+      } else {
+        const int64_t qrow = row0 + 16 * rg + ln;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t key = key0 + 16 * kg + 4 * lg + e;
-          const int64_t diff = qrow - key;
-          const bool vis = diff >= 0 && diff < a.window && key < a.T;
-          const float v = vis ? s[kg][rg][e] * scale2 : -INFINITY;
-          s[kg][rg][e] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = lane_group_max(mx);
+        for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t key = key0 + 16 * kg + 4 * lg + e;
+            const int64_t diff = qrow - key;
+            const bool vis = diff >= 0 && diff < a.window && key < a.T;
+            const float v = vis ? s[kg][rg][e] : -INFINITY;
+            s[kg][rg][e] = v;
+            mx = fmaxf(mx, v);
+          }
+      }
+      mx = lane_group_max(mx) * scale2;
       const float m_new = fmaxf(m[rg], mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m[rg] - m_use);
       m[rg] = m_new;
       float psum = 0.f;
-      float p[4][4];
 #pragma unroll
       for (int kg = 0; kg < 4; ++kg)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          p[kg][e] = __builtin_amdgcn_exp2f(s[kg][rg][e] - m_use);
-          psum += p[kg][e];
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[kg][rg][e], scale2, -m_use));
+          s[kg][rg][e] = p;
+          psum += p;
         }
       l[rg] = l[rg] * alpha + psum;
+      if (__any(alpha != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[rg][dt] *= alpha;
+        for (int dt = 0; dt < 8; ++dt) o[rg][dt] *= alpha;
+      }
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pf[rg][kp][e] = (_Float16)p[2 * kp][e];
-          pf[rg][kp][e + 4] = (_Float16)p[2 * kp + 1][e];
+          pf[rg][kp][e] = (_Float16)s[2 * kp][rg][e];
+          pf[rg][kp][e + 4] = (_Float16)s[2 * kp + 1][rg][e];
         }
     }
     // ---- Oᵀ += V̂ᵀ Pᵀ: contraction slot 8lg+e <-> key 32kp + 4lg + e (e < 4),
@@ -224,7 +261,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
-        const _Float16* vr = v_lds + (16 * dt + ln) * kVStride + 32 * kp + 4 * lg;
+        const _Float16* vr = vl + (16 * dt + ln) * kVStride + 32 * kp + 4 * lg;
         const half4 lo = *(const half4*)vr;
         const half4 hi = *(const half4*)(vr + 16);
         const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -232,6 +269,9 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
         o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[1][kp], o[1][dt], 0, 0, 0);
       }
     }
+    // ---- the next tile into the other buffer ----
+    if (more) store(tile + 1, nxt, buf ^ 1);
+    __syncthreads();
   }
 
   // ---- normalise and store: lane holds dims 16dt + 4lg + e of row ln ----
@@ -289,12 +329,12 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   a.rope_len = rope_len;
   a.out = (_Float16*)out;
   a.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
-  a.row_sets = 4 / a.heads_per_wg;
+  a.row_sets = 8 / a.heads_per_wg;
   a.head_groups = (int32_t)(NQ / a.heads_per_wg);
   const int64_t nqb = ceil_div(T, 32 * (int64_t)a.row_sets);
   const int64_t blocks = nqb * KVH * a.head_groups * B;
   JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-  hipLaunchKernelGGL(prefill_attn_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(prefill_attn_kernel, dim3((uint32_t)blocks), dim3(kPThreads), 0, stream, a);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }

@@ -160,7 +160,11 @@ __global__ __launch_bounds__(256) void rvq_encode_generic(EncodeArgs a) {
 // the last two index bits in the cross-lane step (ties -> lowest index).
 // delta = 2^-8 (|r|^2 + max|c|^2) keeps every key negative despite fp32
 // rounding and the approximate |r|^2; it is common to all codewords of the
-// row, so it never changes the order.
+// row, so it never changes the order.  Stage 1 takes |r|^2 = |x|^2 from a
+// dot product; stage 2 reads |x - c_1|^2 off stage 1's winning key
+// (-2 D_min - delta_1, its magnitude rounded down by the cleared index
+// bits, under 2^-15 relative) and widens delta_2 by 2^-10 delta_1 to cover
+// that and the |x|^2-scaled rounding of D_min.
 
 __device__ __forceinline__ uint32_t umin3(uint32_t a, uint32_t b, uint32_t c) {
   return min(min(a, b), c);
@@ -188,9 +192,6 @@ __device__ __forceinline__ float dot2_acc(half8 a, half8 b) {
 static const int kTiles = 4;                      // 16-row tiles per wave iteration
 static const int kRowsPerWave = kTiles * 16;      // rows per wave iteration
 static const int kRowsPerIter = 4 * kRowsPerWave; // rows per workgroup iteration
-// Prefetching the next iteration's rows into registers costs 16 VGPRs and
-// spills at 4 waves/SIMD; measured slower, so it stays off.
-static const bool kPrefetchRows = false;
 
 struct MfmaArgs {
   EncodeArgs e;
@@ -207,13 +208,16 @@ void rvq_encode_mfma(MfmaArgs m) {
   // consecutive codewords are one conflict-free 256-byte row:
   //   lo[s][k] = c_k          (d=4: [c_k, c_k])
   //   hi[s][k] = [n_hi, n_lo, 16, 16, 0, 0, 0, 0],  n = |c_k|^2 / 2
+  //   neg[k]   = -c_k of stage 1 (d=4: [-c_k, -c_k]), the stage-2 B slots
   __shared__ half8 tab_lo[S][256];
   __shared__ half8 tab_hi[S][256];
+  __shared__ half8 tab_neg[S > 1 ? 256 : 1];
   __shared__ float s_ncmax[S][4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform, so row planning and addressing stay in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lg = lane >> 4;
   const int ln = lane & 15;
 
@@ -261,6 +265,7 @@ void rvq_encode_mfma(MfmaArgs m) {
     hi[3] = (half_t)16.f;
     tab_lo[s][tid] = lo;
     tab_hi[s][tid] = hi;
+    if (S > 1 && s == 0) tab_neg[tid] = -lo;
     float mx = nc;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -357,47 +362,54 @@ void rvq_encode_mfma(MfmaArgs m) {
   if (base < r_end) load_x(cur, x);
 
   for (; base < r_end; base += kRowsPerIter) {
-    // prefetch the next iteration's rows while this one computes
-    half8 x_next[kTiles];
-    const bool more = kPrefetchRows && base + kRowsPerIter < r_end;
+    const bool more = base + kRowsPerIter < r_end;
     const Iter nxt = plan(base + kRowsPerIter);
-    if (more) load_x(nxt, x_next);
     uint32_t code_bytes[kTiles];
+    // stage 1's winning D (negative) and delta_1 per row, for stage 2's bias
+    float dwin[kTiles], delta1[kTiles];
 #pragma unroll
-    for (int i = 0; i < kTiles; ++i) code_bytes[i] = 0u;
+    for (int i = 0; i < kTiles; ++i) {
+      code_bytes[i] = 0u;
+      dwin[i] = 0.f;
+      delta1[i] = 0.f;
+    }
 
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       half8 bop[kTiles];
 #pragma unroll
       for (int i = 0; i < kTiles; ++i) {
-        // stage-1 codeword (zero before stage 2), re-read from LDS
-        half8 cprev = half8{};
-        if (s > 0) {
-          cprev = tab_lo[0][code_bytes[i] & 255u];
-          if (D == 4) cprev = half8{cprev[0], cprev[1], cprev[2], cprev[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
-        }
         // row bias beta = (|r|^2 + delta)/2 enters through the norm plane's
-        // (16, 16) slots as -(beta/16) split into two fp16 halves; |r|^2 comes
-        // from the fp16-rounded residual, delta covers that and fp32 rounding
-        const half8 rh = x[i] - cprev;
-        const float rr = dot2_acc(rh, rh);
-        const float beta16 = (rr + (rr + ncmax[s]) * 0x1p-8f) * (0.5f / 16.f) + 0x1p-60f;
+        // (16, 16) slots as -(beta/16) split into two fp16 halves
+        float rr, delta;
+        half8 negc = half8{};
+        if (s == 0) {
+          rr = dot2_acc(x[i], x[i]);
+          delta = (rr + ncmax[0]) * 0x1p-8f;
+          delta1[i] = delta;
+        } else {
+          negc = tab_neg[code_bytes[i] & 255u];  // -c_1 (d=4: [-c_1, -c_1])
+          rr = fmaxf(-2.f * dwin[i] - delta1[i], 0.f);
+          delta = (rr + ncmax[s]) * 0x1p-8f + delta1[i] * 0x1p-10f;
+        }
+        const float beta16 = (rr + delta) * (0.5f / 16.f) + 0x1p-60f;
         const half_t bh = (half_t)beta16;
         const half_t bl = (half_t)(beta16 - (float)bh);
         half8 normb = neg_one_slot;
         normb[2] = -bh;
         normb[3] = -bl;
-        const half8 negc = -cprev;
         half8 b;
         if (D == 8) {
           b = (lg == 0) ? x[i] : (lg == 1) ? negc : (lg == 2) ? normb : half8{};
         } else {
-          const half8 xc = half8{x[i][0], x[i][1], x[i][2], x[i][3], negc[0], negc[1], negc[2], negc[3]};
+          const half8 xc = half8{x[i][0], x[i][1], x[i][2], x[i][3], negc[4], negc[5], negc[6], negc[7]};
           b = (lg == 0) ? xc : (lg == 1) ? normb : half8{};
         }
         bop[i] = b;
       }
+      // the rows are consumed: load the next iteration's into the same
+      // registers, in flight during this stage's MFMA loop
+      if (s == S - 1 && more) load_x(nxt, x);
       const float4v zero4 = {0.f, 0.f, 0.f, 0.f};
       uint32_t best[kTiles];
 #pragma unroll
@@ -445,7 +457,9 @@ void rvq_encode_mfma(MfmaArgs m) {
       for (int i = 0; i < kTiles; ++i) {
         const uint32_t tag = best[i] & 63u;
         const uint32_t kidx = ((tag >> 2) << 4) | ((uint32_t)lg << 2) | (tag & 3u);
-        const uint32_t kstar = lane_group_min((best[i] & ~255u) | kidx) & 255u;
+        const uint32_t kfull = lane_group_min((best[i] & ~255u) | kidx);
+        const uint32_t kstar = kfull & 255u;
+        if (s + 1 < S) dwin[i] = __uint_as_float(kfull & ~255u);
         code_bytes[i] |= kstar << (8 * s);
         half8 cw = tab_lo[s][kstar];
         if (D == 4) cw = half8{cw[0], cw[1], cw[2], cw[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
@@ -483,10 +497,6 @@ void rvq_encode_mfma(MfmaArgs m) {
           *(uint16_t*)cp = (uint16_t)code_bytes[i];
         }
       }
-    }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < kTiles; ++i) x[i] = x_next[i];
     }
     cur = nxt;
   }

@@ -39,7 +39,9 @@ def test_config1_grouped_cq_full_size(device):
         assert res["agreement"] >= 0.9999
 
 
-@pytest.mark.parametrize("tokens,batch", [(512, 1), (300, 2)])
+# (1500, 3): 4500 rows per problem give workgroups two 256-row iterations
+# each, with batch boundaries inside iterations and a ragged last chunk
+@pytest.mark.parametrize("tokens,batch", [(512, 1), (300, 2), (1500, 3)])
 def test_grouped_residual_two_stage(device, tokens, batch):
     # G2 geometry of BASELINE config 2 (16 groups x 8 dims, 2 stages, s2 sigma 0.5)
     gen = _gen(8601 + tokens)
@@ -55,15 +57,19 @@ def test_grouped_residual_two_stage(device, tokens, batch):
         assert_recon_rows(o, r, res["prefix_ok"])
 
 
-def test_cq2_geometry_d4(device):
+# (2, 256): one iteration per workgroup; (4, 2048): BASELINE config 3's
+# [4,8,2048,128], four 256-row iterations per workgroup
+@pytest.mark.parametrize("batch,tokens", [(2, 256), (4, 2048)])
+def test_cq2_geometry_d4(device, batch, tokens):
     # reference cq2 cell: [8,32,256,4] (BASELINE config 3 geometry)
     gen = _gen(8602)
-    states = ref.synthetic_states(gen, 2, 8, 256)
+    states = ref.synthetic_states(gen, batch, 8, tokens)
     books = ref.synthetic_tables(gen, (8, 32, 256, 4), (1.0,), stage_axis=0)
+    print(f"cq2 encode B={batch} T={tokens}", flush=True)
     out, codes = jkv.hard_grouped_cq(states.to(device), books.to(device))
     r_out, r_codes, d1, d2 = ref.hard_grouped_cq(states, books, return_margins=True)
     res = assert_codes(codes[..., None], r_codes[..., None], d1[..., None], d2[..., None])
-    assert_recon_rows(out.cpu().reshape(2, 8, 256, 32, 4), r_out.detach().reshape(2, 8, 256, 32, 4),
+    assert_recon_rows(out.cpu().reshape(batch, 8, tokens, 32, 4), r_out.detach().reshape(batch, 8, tokens, 32, 4),
                       codes.cpu() == r_codes)
 
 
@@ -153,11 +159,13 @@ def test_full_size_layer_properties(device):
     for depth in (1, 2):
         dec = jkv.closed_loop_vq._ops.rvq_decode(codes, flat, depth=depth, dtype=torch.float16)
         assert torch.equal(dec, exits[depth])
-    # a sampled subset checked against the oracle
-    sub = slice(4096, 4096 + 256)
-    r_exits, r_codes, d1, d2 = ref.grouped_residual_vq(states[:, :, sub].cpu(), tables.cpu(), prefixes=(2,),
+    # every token checked against the oracle (workgroups here run four
+    # 256-row iterations, so this covers rows past the first iteration)
+    r_exits, r_codes, d1, d2 = ref.grouped_residual_vq(states.cpu(), tables.cpu(), prefixes=(2,),
                                                        return_margins=True)
-    assert_codes(codes[:, :, sub], r_codes, d1, d2)
+    res = assert_codes(codes, r_codes, d1, d2)
+    assert_recon_rows(exits[2].cpu().reshape(1, 8, 8192, 16, 8), r_exits[2].detach().reshape(1, 8, 8192, 16, 8),
+                      res["prefix_ok"])
     # stage-1 optimality: the chosen word is at least as close (fp64) as every other
     x = states[0, :, :64].float().reshape(8, 64, 16, 8).cpu().double()
     c1 = tables[:, :, 0].cpu().double()  # [8,16,256,8]

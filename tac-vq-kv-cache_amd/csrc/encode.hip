@@ -138,26 +138,32 @@ __global__ __launch_bounds__(256) void rvq_encode_generic(EncodeArgs a) {
 // MFMA kernel for d in {4, 8}, K = 256, S in {1, 2}, fp16 states.
 //
 // Workgroup = 4 waves on one (head, group) problem; the problem's S
-// codebooks are staged once in LDS as two planes, c (fp16) and
-// [n_hi, n_lo] with n = |c|^2/2 split into two fp16 halves.  Each wave
-// encodes 4 tiles of 16 rows per iteration (independent MFMA chains).
+// codebooks are staged once in LDS: plane lo[s][k] = c_k (d=4: [c_k, c_k])
+// and plane hi[k] = [n_hi, n_lo, 16, 16] of stage 1 then of stage 2, with
+// n = |c_k|^2/2 split into two fp16 halves.  A wave encodes 64 rows per
+// iteration; lane L owns row L of the 64 for everything that is per row
+// (bias, winner, outputs).
 //
-// v_mfma_f32_16x16x32_f16 (wave64), i = codeword in chunk, j = row in tile:
-//   A[i][k]: lane = i + 16*(k/8), element k%8
-//   B[k][j]: lane = j + 16*(k/8), element k%8
-//   D[i][j]: lane = j + 16*(i/4), element i%4
-// Contraction slots (lane group lg = lane/16 owns slots 8lg..8lg+7):
-//   d=8: lg0  x . c   lg1  (-c_prev) . c   lg2  (-1,-1,-b_hi,-b_lo) . (n_hi,n_lo,16,16)
-//   d=4: lg0  [x,-c_prev] . [c,c]          lg1  (-1,-1,-b_hi,-b_lo) . (n_hi,n_lo,16,16)
-// Remaining lane groups carry B = 0 (their A entries are finite LDS data).
-// The norm plane also carries (16, 16) against the row's -(beta/16) in two
-// fp16 halves, beta = (|r|^2 + delta)/2, so with C = 0
+// Stage 1 runs on v_mfma_f32_32x32x16_f16 (two 32-row tiles, 32-codeword
+// chunks), stage 2 on v_mfma_f32_16x16x32_f16 (four 16-row tiles, 16-codeword
+// chunks); i = codeword in chunk, j = row in tile, slot group sg = k/8:
+//   stage 1 (K = 16): sg0  x . c  (d=4: [x,0] . [c,c])   sg1  bias . hi
+//   stage 2 (K = 32): d=8: sg0  x . c   sg1  (-c_1) . c   sg2  bias . hi
+//                     d=4: sg0  [x,-c_1] . [c,c]          sg1  bias . hi
+// where bias = (-1,-1,-b_hi,-b_lo, 0,0,0,0) in stage 1 and
+// (0,0,0,0, -1,-1,-b_hi,-b_lo) in stage 2 picks that stage's half of hi.
+// Other slot groups are zero.  A 32x32 product costs half as much per
+// distance as a 16x16 one, but stage 2's 20 slots need K = 32.  Each row
+// owner writes its row's B slots into a per-wave LDS image [slot group][row];
+// a lane then reads its tile's operand as one 16-byte word.  hi carries (16, 16) against the
+// row's -(beta/16) in two fp16 halves, beta = (|r|^2 + delta)/2, so with C = 0
 //   D[i][j] = c_i.(x - c_prev) - |c_i|^2/2 - (|r|^2 + delta)/2
 //           = -(|r - c_i|^2 + delta)/2  < 0,
 // exact in the products (fp16 x fp16) and fp32 in the sum.  As unsigned bit
 // patterns negative floats order by magnitude, so the row's nearest codeword
-// is the min over keys (bits & ~63) | (chunk<<2 | i%4); the lane group adds
-// the last two index bits in the cross-lane step (ties -> lowest index).
+// is the min over keys (bits & ~255) | index: in-lane keys carry
+// 16*chunk + i%4, the lane group adds 4*(i/4) before the cross-lane step
+// (ties -> lowest index, torch.argmin's rule).
 // delta = 2^-8 (|r|^2 + max|c|^2) keeps every key negative despite fp32
 // rounding and the approximate |r|^2; it is common to all codewords of the
 // row, so it never changes the order.  Stage 1 takes |r|^2 = |x|^2 from a
@@ -170,12 +176,19 @@ __device__ __forceinline__ uint32_t umin3(uint32_t a, uint32_t b, uint32_t c) {
   return min(min(a, b), c);
 }
 
-__device__ __forceinline__ uint32_t lane_group_min(uint32_t v) {
-  // min over lanes {j, j+16, j+32, j+48}
-  auto s16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  uint32_t m = min((uint32_t)s16[0], (uint32_t)s16[1]);
-  auto s32 = __builtin_amdgcn_permlane32_swap(m, m, false, false);
-  return min((uint32_t)s32[0], (uint32_t)s32[1]);
+// Min over the four lane groups of tile lg's key: after the call lane
+// (lg, j) holds the minimum of b[lg] over lanes {j, j+16, j+32, j+48}.
+// Lane rows are 16 lanes; permlane32_swap exchanges rows {2,3} of its first
+// operand with rows {0,1} of its second, permlane16_swap rows {1,3} of its
+// first with rows {0,2} of its second.
+__device__ __forceinline__ uint32_t tile_row_min(uint32_t b0, uint32_t b1, uint32_t b2,
+                                                 uint32_t b3) {
+  auto p02 = __builtin_amdgcn_permlane32_swap(b0, b2, false, false);
+  const uint32_t t02 = min((uint32_t)p02[0], (uint32_t)p02[1]);  // rows 0-1: tile 0, 2-3: tile 2
+  auto p13 = __builtin_amdgcn_permlane32_swap(b1, b3, false, false);
+  const uint32_t t13 = min((uint32_t)p13[0], (uint32_t)p13[1]);  // rows 0-1: tile 1, 2-3: tile 3
+  auto q = __builtin_amdgcn_permlane16_swap(t02, t13, false, false);
+  return min((uint32_t)q[0], (uint32_t)q[1]);
 }
 
 __device__ __forceinline__ float dot2_acc(half8 a, half8 b) {
@@ -187,6 +200,25 @@ __device__ __forceinline__ float dot2_acc(half8 a, half8 b) {
     acc = __builtin_amdgcn_fdot2(x, y, acc, false);
   }
   return acc;
+}
+
+// a - b as four packed fp16 subtractions
+__device__ __forceinline__ half8 sub8(half8 a, half8 b) {
+  half8 r;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const half2v t = half2v{a[e], a[e + 1]} - half2v{b[e], b[e + 1]};
+    r[e] = t[0];
+    r[e + 1] = t[1];
+  }
+  return r;
+}
+
+// LDS writes of one wave become visible to the wave's other lanes
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 static const int kTiles = 4;                      // 16-row tiles per wave iteration
@@ -204,14 +236,18 @@ template <int D, int S>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void rvq_encode_mfma(MfmaArgs m) {
   const EncodeArgs& a = m.e;
-  // LDS codebook image, two contiguous 16-byte planes per stage so that 16
-  // consecutive codewords are one conflict-free 256-byte row:
-  //   lo[s][k] = c_k          (d=4: [c_k, c_k])
-  //   hi[s][k] = [n_hi, n_lo, 16, 16, 0, 0, 0, 0],  n = |c_k|^2 / 2
-  //   neg[k]   = -c_k of stage 1 (d=4: [-c_k, -c_k]), the stage-2 B slots
+  // slot groups with data (bias sits where the lanes read plane hi):
+  // stage 1 [x, bias]; stage 2 d=8 [x, -c_1, bias], d=4 [[x,-c_1], bias]
+  constexpr int kSgX = 0;
+  constexpr int kSgC = (D == 8 && S > 1) ? 1 : 0;  // d=4: upper half of sg0
+  constexpr int kSgBias1 = 1;                       // stage 1 (K = 16)
+  constexpr int kSgBias = (D == 8) ? 2 : 1;         // later stages (K = 32)
+  constexpr int kSlotGroups = (D == 8 && S > 1) ? 3 : 2;
   __shared__ half8 tab_lo[S][256];
-  __shared__ half8 tab_hi[S][256];
-  __shared__ half8 tab_neg[S > 1 ? 256 : 1];
+  __shared__ half8 tab_hi[256];
+  // per-wave B images [slot group][tile][row] plus one shared zero plane
+  __shared__ half8 bimg[4][kSlotGroups][kTiles][16];
+  __shared__ half8 bzero[kTiles][16];
   __shared__ float s_ncmax[S][4];
 
   const int tid = threadIdx.x;
@@ -231,6 +267,7 @@ void rvq_encode_mfma(MfmaArgs m) {
   const int64_t p = h * a.G + g;
 
   // ---- stage the fp16-deployed codebooks (one codeword per thread) ----
+  half8 hi = half8{};
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     const float* src = a.tables + ((p * S + s) * 256 + tid) * D;
@@ -253,24 +290,24 @@ void rvq_encode_mfma(MfmaArgs m) {
     const float halfn = 0.5f * nc;
     const half_t nhi = (half_t)halfn;
     const half_t nlo = (half_t)(halfn - (float)nhi);
-    half8 lo, hi;
+    half8 lo;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      lo[e] = cw[e % D];
-      hi[e] = (half_t)0.f;
-    }
-    hi[0] = nhi;
-    hi[1] = nlo;
-    hi[2] = (half_t)16.f;  // row-bias slots: 16 * (beta/16)_hi + 16 * (beta/16)_lo
-    hi[3] = (half_t)16.f;
+    for (int e = 0; e < 8; ++e) lo[e] = cw[e % D];
+    hi[4 * s + 0] = nhi;
+    hi[4 * s + 1] = nlo;
+    hi[4 * s + 2] = (half_t)16.f;  // bias slots: 16 * (beta/16)_hi + 16 * (beta/16)_lo
+    hi[4 * s + 3] = (half_t)16.f;
     tab_lo[s][tid] = lo;
-    tab_hi[s][tid] = hi;
-    if (S > 1 && s == 0) tab_neg[tid] = -lo;
     float mx = nc;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     if (lane == 0) s_ncmax[s][wave] = mx;
   }
+  tab_hi[tid] = hi;
+  // this lane's B rows start as zero
+#pragma unroll
+  for (int sg = 0; sg < kSlotGroups; ++sg) bimg[wave][sg][lg][ln] = half8{};
+  bzero[tid >> 4 & 3][tid & 15] = half8{};
   __syncthreads();
   if (!active) return;
   float ncmax[S];
@@ -279,9 +316,14 @@ void rvq_encode_mfma(MfmaArgs m) {
     ncmax[s] = fmaxf(fmaxf(s_ncmax[s][0], s_ncmax[s][1]), fmaxf(s_ncmax[s][2], s_ncmax[s][3]));
 
   // this lane's A plane: d=8 lanes 0-31 read c, 32-63 the norm plane;
-  // d=4 lanes 0-15 read [c,c], 16-63 the norm plane (B is zero past slot 9)
+  // d=4 lanes 0-15 read [c,c], 16-63 the norm plane (B is zero past slot 15)
   const bool a_hi = (D == 8) ? (lg >= 2) : (lg >= 1);
-  const half8* plane = a_hi ? &tab_hi[0][0] : &tab_lo[0][0];
+  const half8* plane_lo = &tab_lo[0][0];
+  // this lane's B operand words: slot group lg of tile i, or zeros
+  const half8* bsrc = (lg < kSlotGroups) ? &bimg[wave][lg][0][ln] : &bzero[0][ln];
+  // the words this lane writes for its own row: slot group sg, tile lg, row ln
+  half8* bdst = &bimg[wave][0][lg][ln];
+  constexpr int kSgStride = kTiles * 16;  // half8 words between slot groups
 
   const int64_t rows = a.B * a.T;
   const int64_t r_begin = chunk * m.rows_per_wg;
@@ -293,12 +335,6 @@ void rvq_encode_mfma(MfmaArgs m) {
   const int64_t head_c = h * a.ch + g * S;             // codes offset of (h, g)
   const int64_t out_bstride = a.H * a.T * Dfull;       // recon is contiguous
   const int64_t head_o = h * a.T * Dfull + g * D;
-
-  half8 neg_one_slot;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) neg_one_slot[e] = (half_t)0.f;
-  neg_one_slot[0] = (half_t)-1.f;
-  neg_one_slot[1] = (half_t)-1.f;
 
   int64_t base = r_begin + wave * kRowsPerWave;  // the wave's first row
 
@@ -322,11 +358,11 @@ void rvq_encode_mfma(MfmaArgs m) {
     it.ob = (int64_t)b0 * out_bstride + head_o + (int64_t)t0 * Dfull;
     return it;
   };
-  // per-lane offsets of tile i: (valid, states, codes, reconstruction).  The
+  // offsets of this lane's row (valid, states, codes, reconstruction).  The
   // row strides are below 2^24 (host-checked), so the full-rate 24-bit
   // multiply replaces the quarter-rate 32-bit one.
-  auto locate = [&](const Iter& it, int i, uint32_t* xo, uint32_t* co, uint32_t* oo) -> bool {
-    const uint32_t rr = (uint32_t)(i * 16 + ln);
+  auto locate = [&](const Iter& it, uint32_t* xo, uint32_t* co, uint32_t* oo) -> bool {
+    const uint32_t rr = (uint32_t)lane;
     if (it.fast) {
       *xo = (uint32_t)it.xb + __umul24(rr, (uint32_t)a.st);
       *co = (uint32_t)it.cb + __umul24(rr, (uint32_t)a.ct);
@@ -343,165 +379,209 @@ void rvq_encode_mfma(MfmaArgs m) {
     *oo = rb * (uint32_t)out_bstride + (uint32_t)head_o + rt * (uint32_t)Dfull;
     return valid;
   };
-  auto load_x = [&](const Iter& it, half8* dst) {
-#pragma unroll
-    for (int i = 0; i < kTiles; ++i) {
-      uint32_t xo, co, oo;
-      locate(it, i, &xo, &co, &oo);
-      if (D == 8) {
-        dst[i] = *(const half8*)(states + xo);
-      } else {
-        const half4 v = *(const half4*)(states + xo);
-        dst[i] = half8{v[0], v[1], v[2], v[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
-      }
-    }
+  auto load_x = [&](const Iter& it) -> half8 {
+    uint32_t xo, co, oo;
+    locate(it, &xo, &co, &oo);
+    if (D == 8) return *(const half8*)(states + xo);
+    const half4 v = *(const half4*)(states + xo);
+    return half8{v[0], v[1], v[2], v[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
+  };
+  // stage s's bias slots (-1, -1, -(beta/16) in two fp16 halves) in half s
+  // of the word, zeros in the other half
+  auto bias_slots = [&](int s, float rr, float delta) -> half8 {
+    const float beta16 = (rr + delta) * (0.5f / 16.f) + 0x1p-60f;
+    const half_t bh = (half_t)beta16;
+    const half_t bl = (half_t)(beta16 - (float)bh);
+    half8 w = half8{};
+    w[4 * s + 0] = (half_t)-1.f;
+    w[4 * s + 1] = (half_t)-1.f;
+    w[4 * s + 2] = -bh;
+    w[4 * s + 3] = -bl;
+    return w;
   };
 
-  half8 x[kTiles];
+  const uint32_t lg4 = (uint32_t)lg << 2;
+  // the key mask lives in a VGPR so that each key is one v_and_or_b32 with
+  // its index tag (not an inline constant) in a scalar register
+  uint32_t kmask = ~255u;
+  asm volatile("" : "+v"(kmask));
+
+  // Stage 1 on v_mfma_f32_32x32x16_f16: its 12 slots [x | bias] fit K = 16,
+  // and a 32x32 product costs half as much per distance as a 16x16 one.
+  //   A[i][k]: lane i + 32*(k/8)   B[k][j]: lane j + 32*(k/8)
+  //   D[i][j]: lane j + 32*((i/4)%2), element 4*(i/8) + i%4
+  // Two 32-row tiles per wave, eight 32-codeword chunks; lane (h, j) reads
+  // slot group h of row 32t + j and, as A, codeword i = j of plane lo or hi.
+  const int h32 = lane >> 5, j32 = lane & 31;
+  const uint32_t h4 = (uint32_t)h32 << 2;
+  const half8* b32src = &bimg[wave][h32][0][0] + j32;
+  const half8* a32src = (h32 ? &tab_hi[0] : plane_lo) + j32;
+  auto stage_first = [&]() -> uint32_t {
+    half8 bop[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) bop[t] = b32src[32 * t];
+    const float16v zero16 = {};
+    uint32_t best[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
+    half8 af_next = a32src[0];
+    float16v acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af_next, bop[t], zero16, 0, 0, 0);
+    af_next = a32src[32];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int cur_b = c & 1;
+      const half8 af = af_next;
+      if (c + 2 < 8) af_next = a32src[(c + 2) * 32];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (c + 1 < 8)
+          acc[cur_b ^ 1][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bop[t], zero16, 0, 0, 0);
+        const float16v v = acc[cur_b][t];
+        uint32_t k[16];
+#pragma unroll
+        for (int el = 0; el < 16; ++el)
+          k[el] = (__float_as_uint(v[el]) & kmask) | (uint32_t)(32 * c + 8 * (el >> 2) + (el & 3));
+        uint32_t m = best[t];
+#pragma unroll
+        for (int el = 0; el < 16; el += 2) m = umin3(k[el], k[el + 1], m);
+        best[t] = m;
+        asm volatile("" : "+v"(best[t]));
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (c + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 24, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // this lane's row L: tile L/32, the minimum over both lane halves
+    auto p = __builtin_amdgcn_permlane32_swap(best[0] | h4, best[1] | h4, false, false);
+    return min((uint32_t)p[0], (uint32_t)p[1]);
+  };
+
+  // Later stages on v_mfma_f32_16x16x32_f16 (20 slots): four 16-row tiles,
+  // sixteen 16-codeword chunks.
+  auto stage_next = [&]() -> uint32_t {
+    constexpr int s = 1;
+    half8 bop[kTiles];
+#pragma unroll
+    for (int i = 0; i < kTiles; ++i) bop[i] = bsrc[i * 16];
+
+    const float4v zero4 = {0.f, 0.f, 0.f, 0.f};
+    uint32_t best[kTiles];
+#pragma unroll
+    for (int i = 0; i < kTiles; ++i) best[i] = 0xFFFFFFFFu;
+    const half8* pl = (a_hi ? &tab_hi[0] : plane_lo + s * 256) + ln;
+    // software pipeline: the MFMAs of chunk c+1 run while the keys of
+    // chunk c are reduced
+    half8 af_next = pl[0];
+    float4v acc[2][kTiles];
+#pragma unroll
+    for (int i = 0; i < kTiles; ++i)
+      acc[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af_next, bop[i], zero4, 0, 0, 0);
+    af_next = pl[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int cur_b = c & 1;
+      const half8 af = af_next;
+      if (c + 2 < 16) af_next = pl[(c + 2) * 16];
+#pragma unroll
+      for (int i = 0; i < kTiles; ++i) {
+        if (c + 1 < 16)
+          acc[cur_b ^ 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop[i], zero4, 0, 0, 0);
+        const float4v v = acc[cur_b][i];
+        const uint32_t k0 = (__float_as_uint(v[0]) & kmask) | (uint32_t)(c * 16 + 0);
+        const uint32_t k1 = (__float_as_uint(v[1]) & kmask) | (uint32_t)(c * 16 + 1);
+        const uint32_t k2 = (__float_as_uint(v[2]) & kmask) | (uint32_t)(c * 16 + 2);
+        const uint32_t k3 = (__float_as_uint(v[3]) & kmask) | (uint32_t)(c * 16 + 3);
+        best[i] = umin3(umin3(k0, k1, k2), k3, best[i]);
+        // pin the running minimum here: without it the compiler sinks the
+        // key reduction of later tiles past the stage epilogue and keeps
+        // every MFMA result of the stage live
+        asm volatile("" : "+v"(best[i]));
+      }
+      // issue order per chunk: one MFMA of chunk c+1, then the six key
+      // operations of one tile of chunk c, four times
+#pragma unroll
+      for (int i = 0; i < kTiles; ++i) {
+        if (c + 1 < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // this lane's row: the winner over all four lane groups
+    return tile_row_min(best[0] | lg4, best[1] | lg4, best[2] | lg4, best[3] | lg4);
+  };
+  half8 x = half8{};
   Iter cur = plan(base);
-  if (base < r_end) load_x(cur, x);
+  if (base < r_end) x = load_x(cur);
 
   for (; base < r_end; base += kRowsPerIter) {
     const bool more = base + kRowsPerIter < r_end;
     const Iter nxt = plan(base + kRowsPerIter);
-    uint32_t code_bytes[kTiles];
-    // stage 1's winning D (negative) and delta_1 per row, for stage 2's bias
-    float dwin[kTiles], delta1[kTiles];
-#pragma unroll
-    for (int i = 0; i < kTiles; ++i) {
-      code_bytes[i] = 0u;
-      dwin[i] = 0.f;
-      delta1[i] = 0.f;
-    }
+    uint32_t xo, co, oo;
+    const bool valid = locate(cur, &xo, &co, &oo);
 
+    // stage-1 B rows of this lane's row: x, no previous codeword, bias
+    const float rr1 = dot2_acc(x, x);
+    const float delta1 = (rr1 + ncmax[0]) * 0x1p-8f;
+    bdst[kSgX * kSgStride] = x;  // d=4: [x, 0]
+    bdst[kSgBias1 * kSgStride] = bias_slots(0, rr1, delta1);
+    // x is consumed: the next iteration's row loads during this one
+    if (more) x = load_x(nxt);
+
+    uint32_t code = 0u;
+    half8 negc1 = half8{};  // -c_1 of this lane's row
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      half8 bop[kTiles];
-#pragma unroll
-      for (int i = 0; i < kTiles; ++i) {
-        // row bias beta = (|r|^2 + delta)/2 enters through the norm plane's
-        // (16, 16) slots as -(beta/16) split into two fp16 halves
-        float rr, delta;
-        half8 negc = half8{};
-        if (s == 0) {
-          rr = dot2_acc(x[i], x[i]);
-          delta = (rr + ncmax[0]) * 0x1p-8f;
-          delta1[i] = delta;
-        } else {
-          negc = tab_neg[code_bytes[i] & 255u];  // -c_1 (d=4: [-c_1, -c_1])
-          rr = fmaxf(-2.f * dwin[i] - delta1[i], 0.f);
-          delta = (rr + ncmax[s]) * 0x1p-8f + delta1[i] * 0x1p-10f;
-        }
-        const float beta16 = (rr + delta) * (0.5f / 16.f) + 0x1p-60f;
-        const half_t bh = (half_t)beta16;
-        const half_t bl = (half_t)(beta16 - (float)bh);
-        half8 normb = neg_one_slot;
-        normb[2] = -bh;
-        normb[3] = -bl;
-        half8 b;
+      wave_lds_sync();
+      uint32_t kmin;
+      if (s == 0) {
+        kmin = stage_first();
+      } else {
+        kmin = stage_next();
+      }
+      const uint32_t kstar = kmin & 255u;
+      code |= kstar << (8 * s);
+      half8 cw = tab_lo[s][kstar];
+      if (s + 1 < S) {
+        // stage-2 B rows: -c_1 and the bias from |x - c_1|^2
+        negc1 = -cw;
+        const float rr2 = fmaxf(-2.f * __uint_as_float(kmin & ~255u) - delta1, 0.f);
+        const float delta2 = (rr2 + ncmax[s + 1]) * 0x1p-8f + delta1 * 0x1p-10f;
         if (D == 8) {
-          b = (lg == 0) ? x[i] : (lg == 1) ? negc : (lg == 2) ? normb : half8{};
+          bdst[kSgC * kSgStride] = negc1;
         } else {
-          const half8 xc = half8{x[i][0], x[i][1], x[i][2], x[i][3], negc[4], negc[5], negc[6], negc[7]};
-          b = (lg == 0) ? xc : (lg == 1) ? normb : half8{};
+          ((half4*)&bdst[kSgX * kSgStride])[1] = half4{negc1[0], negc1[1], negc1[2], negc1[3]};
         }
-        bop[i] = b;
+        bdst[kSgBias * kSgStride] = bias_slots(s + 1, rr2, delta2);
       }
-      // the rows are consumed: load the next iteration's into the same
-      // registers, in flight during this stage's MFMA loop
-      if (s == S - 1 && more) load_x(nxt, x);
-      const float4v zero4 = {0.f, 0.f, 0.f, 0.f};
-      uint32_t best[kTiles];
-#pragma unroll
-      for (int i = 0; i < kTiles; ++i) best[i] = 0xFFFFFFFFu;
-      const half8* pl = plane + s * 256 + ln;
-      // software pipeline: the MFMAs of chunk c+1 run while the keys of
-      // chunk c are reduced (scheduling barriers keep ~2 chunks in flight)
-      half8 af_next = pl[0];
-      float4v acc[2][kTiles];
-#pragma unroll
-      for (int i = 0; i < kTiles; ++i)
-        acc[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af_next, bop[i], zero4, 0, 0, 0);
-      af_next = pl[16];
-#pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const int cur = c & 1;
-        const half8 af = af_next;
-        if (c + 2 < 16) af_next = pl[(c + 2) * 16];
-#pragma unroll
-        for (int i = 0; i < kTiles; ++i) {
-          if (c + 1 < 16)
-            acc[cur ^ 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop[i], zero4, 0, 0, 0);
-          const float4v v = acc[cur][i];
-          const uint32_t k0 = (__float_as_uint(v[0]) & ~63u) | (uint32_t)(c * 4 + 0);
-          const uint32_t k1 = (__float_as_uint(v[1]) & ~63u) | (uint32_t)(c * 4 + 1);
-          const uint32_t k2 = (__float_as_uint(v[2]) & ~63u) | (uint32_t)(c * 4 + 2);
-          const uint32_t k3 = (__float_as_uint(v[3]) & ~63u) | (uint32_t)(c * 4 + 3);
-          best[i] = umin3(umin3(k0, k1, k2), k3, best[i]);
-          // pin the running minimum here: without it the compiler sinks the
-          // key reduction of later tiles past the stage epilogue and keeps
-          // every MFMA result of the stage live
-          asm volatile("" : "+v"(best[i]));
-        }
-        // issue order per chunk: one MFMA of chunk c+1, then the six key
-        // operations of one tile of chunk c, four times, so both the MFMA and
-        // the VALU pipe always have work from this wave
-#pragma unroll
-        for (int i = 0; i < kTiles; ++i) {
-          if (c + 1 < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int i = 0; i < kTiles; ++i) {
-        const uint32_t tag = best[i] & 63u;
-        const uint32_t kidx = ((tag >> 2) << 4) | ((uint32_t)lg << 2) | (tag & 3u);
-        const uint32_t kfull = lane_group_min((best[i] & ~255u) | kidx);
-        const uint32_t kstar = kfull & 255u;
-        if (s + 1 < S) dwin[i] = __uint_as_float(kfull & ~255u);
-        code_bytes[i] |= kstar << (8 * s);
-        half8 cw = tab_lo[s][kstar];
-        if (D == 4) cw = half8{cw[0], cw[1], cw[2], cw[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
-        // depth-2 reconstruction fp16(fp32(c1) + fp32(c2)): the sum of two fp16
-        // words is exact in fp32 or, when it is not, too small to move the
-        // fp16 rounding, so one fp16 add gives the same bits.
-        half8 dec = cw;
-        if (s > 0) {
-          half8 c1 = tab_lo[0][code_bytes[i] & 255u];
-          if (D == 4) c1 = half8{c1[0], c1[1], c1[2], c1[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
-          dec = c1 + cw;
-        }
-        void* out = m.recon_depth[s];
-        uint32_t xo, co, oo;
-        const bool valid = locate(cur, i, &xo, &co, &oo);
-        if (out != nullptr && lg == 0 && valid) {
-          _Float16* op = (_Float16*)out + oo;
-          if (D == 8) {
-            *(half8*)op = dec;
-          } else {
-            *(half4*)op = half4{dec[0], dec[1], dec[2], dec[3]};
-          }
+      // depth-(s+1) reconstruction fp16(fp32(c1) + fp32(c2)): the sum of two
+      // fp16 words is exact in fp32 or, when it is not, too small to move the
+      // fp16 rounding, so one fp16 add gives the same bits.
+      void* out = m.recon_depth[s];
+      if (out != nullptr && valid) {
+        const half8 dec = (s > 0) ? sub8(cw, negc1) : cw;
+        _Float16* op = (_Float16*)out + oo;
+        if (D == 8) {
+          *(half8*)op = dec;
+        } else {
+          *(half4*)op = half4{dec[0], dec[1], dec[2], dec[3]};
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < kTiles; ++i) {
-      uint32_t xo, co, oo;
-      const bool valid = locate(cur, i, &xo, &co, &oo);
-      if (lg == 0 && valid) {
-        uint8_t* cp = a.codes + co;
-        if (S == 1) {
-          cp[0] = (uint8_t)code_bytes[i];
-        } else {
-          *(uint16_t*)cp = (uint16_t)code_bytes[i];
-        }
+    if (valid) {
+      uint8_t* cp = a.codes + co;
+      if (S == 1) {
+        cp[0] = (uint8_t)code;
+      } else {
+        *(uint16_t*)cp = (uint16_t)code;
       }
     }
     cur = nxt;
   }
 }
-
 // ---------------------------------------------------------------------------
 template <int DT>
 static int launch_generic(const EncodeArgs& a, hipStream_t stream) {

@@ -158,9 +158,10 @@ def encode_workload(args, device):
             _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
 
     ms = timed(step, args.steps, args.warmup)
-    avg_launch_ms = per_launch_ms(
-        [lambda st=st, tb=tb: _ops.rvq_encode(st, tb, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
-         for st, tb in layers])
+    # the timed region's HIP events over its back-to-back launches: a launch
+    # takes ~40 us while the host enqueues one in a few, so the queue never
+    # drains and the average is the kernel's own duration
+    avg_launch_ms = ms / len(layers)
     vecs_per_launch = HEADS * args.tokens
     flops_per_launch = vecs_per_launch * FLOP_PER_VEC_G2
     bytes_per_launch = vecs_per_launch * (HEAD_DIM * 2 + GROUPS * STAGES + HEAD_DIM * 2) + HEADS * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 4

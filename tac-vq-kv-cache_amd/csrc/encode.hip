@@ -3,12 +3,13 @@
 // Two kernels share one argument block:
 //  * rvq_encode_mfma<D,S>: fp16 states, d in {4,8}, K=256, S<=2, no whitener.
 //    A workgroup owns one (head, group) problem and a chunk of rows; the
-//    problem's codebooks are staged in LDS and feed the A operand of
-//    v_mfma_f32_16x16x32_f16 (codewords x contraction slots); 16-row tiles
-//    are the B operand.  The contraction packs [x | -c_prev | norm] so one
-//    MFMA yields -(|r - c|^2 + delta)/2 for 16 codewords x 16 rows with exact
-//    products and fp32 accumulation; the argmin is a min over keys that
-//    carry the codeword index in their low bits.
+//    problem's codebooks are staged in LDS and feed the A operand of the
+//    MFMAs (codewords x contraction slots; 32x32x16 in stage 1, 16x16x32 in
+//    stage 2); row tiles are the B operand.  The contraction packs
+//    [x | -c_prev | norm] so one MFMA yields -(|r - c|^2 + delta)/2 for a
+//    tile of codewords x rows with exact products and fp32 accumulation; the
+//    argmin is a min over keys that carry the codeword index in their low
+//    bits.
 //  * rvq_encode_generic<DT,DMAX>: any dtype, d<=128, K<=256, any S, optional
 //    whitener; one thread per row, fp32 distances in the reference's
 //    |r|^2 + |c|^2 - 2 r.c form.

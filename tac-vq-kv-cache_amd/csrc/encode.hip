@@ -156,15 +156,18 @@ __global__ __launch_bounds__(256) void rvq_encode_generic(EncodeArgs a) {
 // Other slot groups are zero.  A 32x32 product costs half as much per
 // distance as a 16x16 one, but stage 2's 20 slots need K = 32.  Each row
 // owner writes its row's B slots into a per-wave LDS image [slot group][row];
-// a lane then reads its tile's operand as one 16-byte word.  hi carries (16, 16) against the
-// row's -(beta/16) in two fp16 halves, beta = (|r|^2 + delta)/2, so with C = 0
+// a lane then reads its tile's operand as one 16-byte word.  hi carries
+// (16, 16) against the row's -(beta/16) in two fp16 halves,
+// beta = (|r|^2 + delta)/2, so with C = 0
 //   D[i][j] = c_i.(x - c_prev) - |c_i|^2/2 - (|r|^2 + delta)/2
 //           = -(|r - c_i|^2 + delta)/2  < 0,
 // exact in the products (fp16 x fp16) and fp32 in the sum.  As unsigned bit
 // patterns negative floats order by magnitude, so the row's nearest codeword
-// is the min over keys (bits & ~255) | index: in-lane keys carry
-// 16*chunk + i%4, the lane group adds 4*(i/4) before the cross-lane step
-// (ties -> lowest index, torch.argmin's rule).
+// is the min over keys (bits & ~255) | index: in-lane keys carry the index
+// bits a lane's accumulator element fixes (stage 1: 32*chunk + 8*(i/8) + i%4,
+// stage 2: 16*chunk + i%4) and the lane's bits of the index (4*(i/4)%2 resp.
+// 4*(i/4)) are added before the cross-lane step (ties -> lowest index,
+// torch.argmin's rule).
 // delta = 2^-8 (|r|^2 + max|c|^2) keeps every key negative despite fp32
 // rounding and the approximate |r|^2; it is common to all codewords of the
 // row, so it never changes the order.  Stage 1 takes |r|^2 = |x|^2 from a
@@ -201,18 +204,6 @@ __device__ __forceinline__ float dot2_acc(half8 a, half8 b) {
     acc = __builtin_amdgcn_fdot2(x, y, acc, false);
   }
   return acc;
-}
-
-// a - b as four packed fp16 subtractions
-__device__ __forceinline__ half8 sub8(half8 a, half8 b) {
-  half8 r;
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const half2v t = half2v{a[e], a[e + 1]} - half2v{b[e], b[e + 1]};
-    r[e] = t[0];
-    r[e + 1] = t[1];
-  }
-  return r;
 }
 
 // LDS writes of one wave become visible to the wave's other lanes
@@ -563,7 +554,7 @@ void rvq_encode_mfma(MfmaArgs m) {
       // fp16 rounding, so one fp16 add gives the same bits.
       void* out = m.recon_depth[s];
       if (out != nullptr && valid) {
-        const half8 dec = (s > 0) ? sub8(cw, negc1) : cw;
+        const half8 dec = (s > 0) ? sub_h8(cw, negc1) : cw;
         _Float16* op = (_Float16*)out + oo;
         if (D == 8) {
           *(half8*)op = dec;

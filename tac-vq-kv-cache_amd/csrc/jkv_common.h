@@ -81,6 +81,18 @@ template <> struct Elem<JKV_F32> {
 // fp16 deploy round trip of an fp32 master value (tables.half().float()).
 __device__ __forceinline__ float deploy16(float v) { return (float)(_Float16)v; }
 
+// a - b on eight fp16 lanes as a sign flip of b and four packed adds (IEEE
+// a + (-b) is a - b).  Written out because an 8-wide fp16 subtraction is
+// otherwise split into scalar subtractions and repacks.
+__device__ __forceinline__ half8 sub_h8(half8 a, half8 b) {
+  uint4 y = __builtin_bit_cast(uint4, b);
+  y.x ^= 0x80008000u;
+  y.y ^= 0x80008000u;
+  y.z ^= 0x80008000u;
+  y.w ^= 0x80008000u;
+  return a + __builtin_bit_cast(half8, y);
+}
+
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Map a linear block index so that consecutive logical blocks land on the

@@ -15,7 +15,7 @@ __device__ __forceinline__ void rope16(half8 a, half8 b, half8 c, half8 s, half8
   const half8 bs = b * s;
   const half8 bc = b * c;
   const half8 as = a * s;
-  *ra = ac - bs;  // == ac + (-bs): IEEE subtraction is that addition
+  *ra = sub_h8(ac, bs);
   *rb = bc + as;
 }
 #pragma clang fp contract(on)

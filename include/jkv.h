@@ -46,7 +46,10 @@ int jkv_version(void);
 /* Thread-local text of the last error raised by this thread. */
 const char* jkv_last_error(void);
 
-/* Bytes of device workspace jkv_rvq_encode needs for this geometry. */
+/* Bytes of device workspace jkv_rvq_encode needs for this geometry: the
+ * whitened selector tables, or for full-vector codebooks (d = 128, K = 256,
+ * S <= 32, no whitener) the fp16-deployed tables of the MFMA kernel.  Given
+ * less, a full-vector call runs on the one-row-per-thread kernel instead. */
 int64_t jkv_rvq_encode_workspace_bytes(int64_t H, int64_t G, int64_t S,
                                        int64_t K, int64_t d,
                                        int32_t has_whitener);

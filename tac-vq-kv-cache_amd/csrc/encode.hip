@@ -13,23 +13,9 @@
 //  * rvq_encode_generic<DT,DMAX>: any dtype, d<=128, K<=256, any S, optional
 //    whitener; one thread per row, fp32 distances in the reference's
 //    |r|^2 + |c|^2 - 2 r.c form.
-#include "jkv_common.h"
+#include "encode_args.h"
 
 namespace jkv {
-
-struct EncodeArgs {
-  const void* states;
-  int64_t sb, sh, st;  // element strides of the B, H, T axes
-  int64_t B, H, T, G, d, S, K;
-  const float* tables;      // fp32 masters [P,S,K,d]
-  const float* sel_tables;  // whitened selector tables [P,S,K,d] or null
-  const float* whiteners;   // [P,d,d] or null
-  uint8_t* codes;
-  int64_t cb, ch, ct;  // byte strides of the B, H, T axes
-  int32_t n_exits;
-  int32_t exit_depth[JKV_MAX_EXITS];
-  void* recon[JKV_MAX_EXITS];
-};
 
 // ---------------------------------------------------------------------------
 // Whitened selector tables: sel[p,s,k,i] = sum_e fp16(C[p,s,k,e]) * W[p,i,e]
@@ -616,8 +602,9 @@ extern "C" {
 
 int64_t jkv_rvq_encode_workspace_bytes(int64_t H, int64_t G, int64_t S, int64_t K,
                                        int64_t d, int32_t has_whitener) {
-  if (!has_whitener) return 0;
-  return H * G * S * K * d * (int64_t)sizeof(float);
+  if (has_whitener) return H * G * S * K * d * (int64_t)sizeof(float);
+  if (d == 128 && K == 256 && S >= 1 && S <= 32) return jkv::full_workspace_bytes(H * G, S);
+  return 0;
 }
 
 int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t H,
@@ -697,6 +684,12 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
     if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
     return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);
   }
+  // full-vector codebooks on MFMA (fp16-deployed tables in the workspace)
+  const bool full = states_dtype == JKV_F16 && whiteners == nullptr && d == 128 && K == 256 &&
+                    S <= 32 && aligned16 && recon_aligned && distinct_exits && workspace != nullptr &&
+                    workspace_bytes >= full_workspace_bytes(H * G, S) &&
+                    ((uintptr_t)workspace) % 16 == 0;
+  if (full) return launch_full(a, workspace, stream);
   switch (states_dtype) {
     case JKV_F16: return launch_generic<JKV_F16>(a, stream);
     case JKV_BF16: return launch_generic<JKV_BF16>(a, stream);

@@ -1,0 +1,27 @@
+// Argument block shared by the encode kernels (encode.hip, encode_full.hip).
+#pragma once
+
+#include "jkv_common.h"
+
+namespace jkv {
+
+struct EncodeArgs {
+  const void* states;
+  int64_t sb, sh, st;  // element strides of the B, H, T axes
+  int64_t B, H, T, G, d, S, K;
+  const float* tables;      // fp32 masters [P,S,K,d]
+  const float* sel_tables;  // whitened selector tables [P,S,K,d] or null
+  const float* whiteners;   // [P,d,d] or null
+  uint8_t* codes;
+  int64_t cb, ch, ct;  // byte strides of the B, H, T axes
+  int32_t n_exits;
+  int32_t exit_depth[JKV_MAX_EXITS];
+  void* recon[JKV_MAX_EXITS];
+};
+
+// Full-vector residual VQ (d = 128, K = 256) on MFMA: workspace it needs for
+// P problems of S stages, whether a call can take it, and its launch.
+int64_t full_workspace_bytes(int64_t P, int64_t S);
+int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream);
+
+}  // namespace jkv

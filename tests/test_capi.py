@@ -62,6 +62,11 @@ def test_workspace_queries():
     lib = _lib.load()
     assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 0) == 0
     assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 1) == 8 * 16 * 2 * 256 * 8 * 4
+    # full-vector codebooks: fp16 tables + bias plane + max norm per (head, stage)
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 0) == 8 * 2 * (256 * 128 * 2 + 256 * 16 + 64)
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 33, 256, 128, 0) == 0
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 128, 128, 0) == 0
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 1) == 8 * 2 * 256 * 128 * 4
     F16, BF16 = _lib.JKV_F16, _lib.JKV_BF16
     bins = 8 * 16 * 2 * 256 * 8  # [H*G,S,K,d] of the config-5 V codebooks
     # one chunk of rows: bins go straight into the gradient

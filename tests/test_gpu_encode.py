@@ -96,6 +96,39 @@ def test_residual_vq_generic_geometries(device, seed, dtype, dim, stages, cluste
         assert_recon_rows(exits[depth].cpu(), r_exits[depth].detach(), res["prefix_ok"])
 
 
+# full-vector codebooks (d = 128, K = 256): the MFMA kernel with fp16-deployed
+# tables in the workspace; ragged rows, many stages, exits at several depths
+@pytest.mark.parametrize("batch,tokens,stages,prefixes", [
+    (1, 300, 2, (1, 2)),
+    (2, 77, 4, (2, 4)),
+    (1, 40, 16, (1, 8, 16)),
+])
+def test_full_vector_residual_vq(device, batch, tokens, stages, prefixes):
+    gen = _gen(700 + stages)
+    states = ref.synthetic_states(gen, batch, 8, tokens)
+    tables = ref.synthetic_tables(gen, (8, stages, 256, 128), tuple(0.8 ** s for s in range(stages)), stage_axis=1)
+    print(f"full-vector encode B={batch} T={tokens} S={stages}", flush=True)
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=prefixes)
+    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=prefixes, return_margins=True)
+    assert_codes(codes, r_codes, d1, d2)
+    for depth in prefixes:
+        rows = (codes.cpu().long()[..., :depth] == r_codes.long()[..., :depth]).all(-1)
+        assert_recon_rows(exits[depth].cpu(), r_exits[depth].detach(), rows)
+
+
+def test_full_vector_config3_literal(device):
+    # the literal reading of BASELINE config 3: [4,8,2048,128] with two
+    # full-dim stages [8,2,256,128] (s1 N(0,1), s2 sigma 0.5), every token
+    gen = _gen(8601)
+    states = ref.synthetic_states(gen, 4, 8, 2048)
+    tables = ref.synthetic_tables(gen, (8, 2, 256, 128), (1.0, 0.5), stage_axis=1)
+    print("full-vector encode config 3 literal [4,8,2048,128] S=2", flush=True)
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=(2,))
+    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=(2,), return_margins=True)
+    res = assert_codes(codes, r_codes, d1, d2)
+    assert_recon_rows(exits[2].cpu(), r_exits[2].detach(), res["prefix_ok"])
+
+
 @pytest.mark.parametrize("seed", [41, 42])
 def test_whitened_search(device, seed):
     gen = _gen(seed)

@@ -4,9 +4,9 @@
 // the C2 configuration).
 //
 // full_tables_kernel deploys the fp32 masters once per call into the
-// workspace: fp16 tables [P][S][256][128], a bias plane [P][S][256] of
-// (n_hi, n_lo, 2^12, 2^12, 0, 0, 0, 0) with n = |c|^2/2 in two fp16 halves,
-// and 16 partial maxima of |c|^2 per (problem, stage).
+// workspace: fp16 tables [P][S][256][128], the fp32 plane -|c|^2/2 [P][S][256]
+// (from the fp16 codewords the search multiplies) and 16 partial maxima of
+// |c|^2 per (problem, stage).
 //
 // rvq_encode_full_kernel: one workgroup of up to 8 waves per (problem, block
 // of 16 rows per wave).  Stage tables stream through LDS with direct
@@ -20,16 +20,17 @@
 // for kk = 0..3): the input x (fp16) and the running reconstruction `dec`
 // (fp32, the reference's `decoded` buffer, summed in stage order).  Stage s
 // searches with the fp32 residual r = x - dec, carried as r_hi + r_lo (two
-// fp16 words, |r - r_hi - r_lo| <= 2^-22 |r|):
-//   D[i][j] = c_i.r_hi + c_i.r_lo - |c_i|^2/2 - (|r|^2 + delta)/2
-// over 4 + 4 K-steps of 32 dims plus one bias step (stage 1: r = x, 4 + 1).
+// fp16 words, |r - r_hi - r_lo| <= 2^-22 |r|).  The accumulator starts at
+// -|c_i|^2/2 and gathers c_i.r_hi + c_i.r_lo over 4 + 4 K-steps of 32 dims
+// (stage 1: r = x, 4 steps); one fp32 subtraction then gives
+//   D''[i][j] = c_i.r - |c_i|^2/2 - (|r|^2 + delta)/2 - M = -(|r - c_i|^2 + delta)/2 - M.
 // Near-ties are far more common at d = 128 than at d = 8, so the key keeps the
-// whole mantissa: the row bias also carries a power of two M >= 2 (|r|^2 +
-// max|c|^2 + delta) > 4 max_i (|r - c_i|^2 + delta)/2, which puts every D'' =
-// D - M of the row in the one binade [-2M, -M).  Sign and exponent are then
-// common to the row and key = (bits(D'') << 9) | index orders by distance at
-// 2^-23 M, ties to the lowest index.  delta = 2^-8 (|r|^2 + max|c|^2) keeps
-// every D below zero; M is a per-row constant and never changes the order.
+// whole mantissa: M is a power of two >= 2 (|r|^2 + max|c|^2 + delta) > 2 max_i
+// (|r - c_i|^2 + delta)/2, which puts every D'' of the row in the one binade
+// (-2M, -M).  Sign and exponent are then common to the row and key =
+// (bits(D'') << 9) | index orders by distance at 2^-23 M, ties to the lowest
+// index.  delta = 2^-8 (|r|^2 + max|c|^2) keeps every D'' below -M; M is a
+// per-row constant and never changes the order.
 #include "encode_args.h"
 
 namespace jkv {
@@ -39,11 +40,11 @@ static const int kFullK = 256;
 static const int kFullMaxS = 32;
 static const int kFullTabHalves = kFullK * kFullD;         // one stage table
 static const int kFullTabBytes = kFullTabHalves * 2;      // 64 KiB
-static const int kFullBufBytes = kFullTabBytes + kFullK * 16;  // + bias plane
+static const int kFullBufBytes = kFullTabBytes + kFullK * 4;  // + -|c|^2/2 plane
 static const int kFullMaxWaves = 8;
 
 int64_t full_workspace_bytes(int64_t P, int64_t S) {
-  return P * S * ((int64_t)kFullTabBytes + kFullK * 16 + 16 * 4);
+  return P * S * ((int64_t)kFullTabBytes + kFullK * 4 + 16 * 4);
 }
 
 // One block per (problem, stage, 16 codewords): lane (codeword ci, chunk q)
@@ -52,7 +53,7 @@ int64_t full_workspace_bytes(int64_t P, int64_t S) {
 // partial maxima of a stage).
 __global__ __launch_bounds__(256) void full_tables_kernel(const float* __restrict__ masters,
                                                           _Float16* __restrict__ tab16,
-                                                          half8* __restrict__ bias_plane,
+                                                          float* __restrict__ nhalf,
                                                           float* __restrict__ ncmax_part) {
   const int64_t ps = blockIdx.x >> 4;  // (problem, stage)
   const int part = blockIdx.x & 15;
@@ -69,13 +70,7 @@ __global__ __launch_bounds__(256) void full_tables_kernel(const float* __restric
   for (int e = 0; e < 8; ++e) nc = fmaf((float)w[e], (float)w[e], nc);
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) nc += __shfl_xor(nc, off, 16);
-  if (q == 0) {
-    const float halfn = 0.5f * nc;
-    const half_t nhi = (half_t)halfn;
-    const half_t nlo = (half_t)(halfn - (float)nhi);
-    bias_plane[ps * kFullK + k] =
-        half8{nhi, nlo, (half_t)4096.f, (half_t)4096.f, (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
-  }
+  if (q == 0) nhalf[ps * kFullK + k] = -0.5f * nc;
   __shared__ float red[4];
   float mx = nc;
 #pragma unroll
@@ -88,7 +83,7 @@ __global__ __launch_bounds__(256) void full_tables_kernel(const float* __restric
 struct FullArgs {
   EncodeArgs e;
   const _Float16* tab16;
-  const half8* bias_plane;
+  const float* nhalf;
   const float* ncmax;
   int64_t row_blocks;  // row blocks per problem
 };
@@ -111,13 +106,80 @@ __device__ __forceinline__ uint32_t lane_group_min_u(uint32_t v) {
   return min((uint32_t)s32[0], (uint32_t)s32[1]);
 }
 
-__global__ __launch_bounds__(512) void rvq_encode_full_kernel(FullArgs f) {
+// Distances of a wave's 16 rows to the stage's 256 codewords: 16 steps (four
+// passes of four K-steps over four 16-codeword chunks); returns the lane's
+// smallest key.  A operands run two steps ahead through a three-slot ring; a
+// pass's accumulator seeds (-|c|^2/2) load at the start of the pass before,
+// alternating between two seed sets so each pass accumulates in place; the
+// caller's `dma(step)` issues a sixteenth of the next stage's table loads in
+// each step.  Everything is unrolled, so LDS addresses are a per-lane base
+// plus an immediate offset; scheduling barriers keep the order as written.
+template <bool LO, typename Dma>
+__device__ __forceinline__ uint32_t full_search(const half8* __restrict__ tabA, const float* __restrict__ nhA,
+                                                const half8 (&bh)[4], const half8 (&bl)[4], float bm, int lg,
+                                                int j, Dma&& dma) {
+  // chunk (4kk + lg) of codeword 16m + j sits at tabA[(16m + j) * 16 + ((4kk + lg) ^ j)]
+  const half8* ak[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) ak[kk] = tabA + j * 16 + ((4 * kk + lg) ^ j);
+  const float* nl = nhA + 4 * lg;
+  uint32_t best = 0xFFFFFFFFu;
+  half8 ring[3][4];
+  float4v seed[2][4];
+  auto load_step = [&](int i) {
+    const int c = 4 * (i >> 2), kk = i & 3;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ring[i % 3][u] = ak[kk][(c + u) * 256];
+  };
+  auto load_seeds = [&](int pass) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) seed[pass & 1][u] = *(const float4v*)(nl + 16 * (4 * pass + u));
+  };
+  load_seeds(0);
+  load_step(0);
+  load_step(1);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int pass = i >> 2, kk = i & 3;
+    if (i + 2 < 16) load_step(i + 2);
+    if (kk == 0 && pass + 1 < 4) load_seeds(pass + 1);
+    dma(i);
+    float4v (&acc)[4] = seed[pass & 1];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ring[i % 3][u], bh[kk], acc[u], 0, 0, 0);
+      if (LO) acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ring[i % 3][u], bl[kk], acc[u], 0, 0, 0);
+    }
+    if (kk == 3) {
+      // key = mantissa of D'' above the index: lanes add the low bits v (0..3)
+      // per value and the chunk bits 16 (c + u) per chunk after its minimum
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t k0 = (__float_as_uint(acc[u][0] - bm) << 9) | 0u;
+        const uint32_t k1 = (__float_as_uint(acc[u][1] - bm) << 9) | 1u;
+        const uint32_t k2 = (__float_as_uint(acc[u][2] - bm) << 9) | 2u;
+        const uint32_t k3 = (__float_as_uint(acc[u][3] - bm) << 9) | 3u;
+        const uint32_t m = min(umin3_f(k0, k1, k2), k3) | (uint32_t)(16 * (4 * pass + u));
+        best = min(best, m);
+      }
+      // the pass's keys are final here (left to itself the compiler sinks them
+      // to the end, keeping all 16 accumulators live); emits nothing
+      asm volatile("" : "+v"(best));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return best;
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   const EncodeArgs& a = f.e;
-  extern __shared__ __align__(16) unsigned char lds[];  // 2 x (table + bias plane)
+  extern __shared__ __align__(16) unsigned char lds[];  // 2 x (table + -|c|^2/2 plane)
+  __shared__ float ncm_s[kFullMaxS];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nw = (int)(blockDim.x >> 6);
+  constexpr int nw = NW;  // 4 or 8 waves
   const int lg = lane >> 4, j = lane & 15;
 
   // logical block: row blocks of one problem are consecutive (one table set
@@ -136,26 +198,51 @@ __global__ __launch_bounds__(512) void rvq_encode_full_kernel(FullArgs f) {
   const int64_t b = rw / a.T, t = rw - (rw / a.T) * a.T;
   const _Float16* xrow = (const _Float16*)a.states + b * a.sb + h * a.sh + t * a.st + g * kFullD;
 
-  // stage tables: 64 direct loads of 1 KiB (4 codeword rows) plus 4 of the
-  // bias plane, spread over the waves
+  // stage tables: 64 direct buffer->LDS loads of 1 KiB (4 codeword rows) plus
+  // one of the -|c|^2/2 plane.  Wave w issues loads k = w + nw*i, i < 64/nw;
+  // load k carries codeword rows 4k..4k+3, lane (lg, q) chunk q of row 4k + lg
+  // into swizzled slot q ^ ((4k + lg) & 15).  With nw a multiple of 4 that slot
+  // is the same for every i, so each load is one per-lane 32-bit offset plus a
+  // uniform one.  (MUBUF rather than global_load_lds: the compiler's wait
+  // counting treats the latter as a flat access to both memories and then
+  // drains every LDS read to zero, which undoes the search's prefetching.)
+  constexpr int per_wave = 64 / nw;
+  const int rlane = 4 * wave + lg;  // row 4k + lg for i = 0
+  const uint32_t lane_off = (uint32_t)(rlane * kFullD + 8 * ((lane & 15) ^ (rlane & 15))) * 2u;
+  const __amdgpu_buffer_rsrc_t tab_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(f.tab16 + (int64_t)p * S * kFullTabHalves), (short)0, S * kFullTabBytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t plane_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(f.nhalf + (int64_t)p * S * kFullK), (short)0, S * kFullK * 4, 0x00020000);
+  auto dma_load = [&](int s, int buf, int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        tab_rsrc, (__attribute__((address_space(3))) void*)(lds + buf * kFullBufBytes + (wave + nw * i) * 1024), 16,
+        lane_off, (uint32_t)(s * kFullTabBytes + i * nw * 1024), 0, 0);
+  };
+  auto dma_plane = [&](int s, int buf) {
+    if (wave == nw - 1) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          plane_rsrc, (__attribute__((address_space(3))) void*)(lds + buf * kFullBufBytes + kFullTabBytes), 16,
+          (uint32_t)lane * 16u, (uint32_t)(s * kFullK * 4), 0, 0);
+    }
+  };
+  // step t of 16 issues this wave's loads [t * per_wave / 16, (t + 1) * per_wave / 16)
+  auto dma_step = [&](int s, int buf, int t) {
+#pragma unroll
+    for (int i = (t * per_wave) >> 4; i < ((t + 1) * per_wave) >> 4; ++i) dma_load(s, buf, i);
+    if (t == 0) dma_plane(s, buf);
+  };
   auto dma_stage = [&](int s, int buf) {
-    unsigned char* base = lds + buf * kFullBufBytes;
-    const _Float16* src_tab = f.tab16 + ((int64_t)p * S + s) * kFullTabHalves;
-    for (int k = wave; k < 64; k += nw) {
-      const int r = 4 * k + (lane >> 4), q = lane & 15;
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(src_tab + r * kFullD + 8 * (q ^ (r & 15))),
-          (void __attribute__((address_space(3)))*)(base + k * 1024), 16, 0, 0);
-    }
-    const half8* src_bias = f.bias_plane + ((int64_t)p * S + s) * kFullK;
-    for (int k = wave; k < 4; k += nw) {
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(src_bias + 64 * k + lane),
-          (void __attribute__((address_space(3)))*)(base + kFullTabBytes + k * 1024), 16, 0, 0);
-    }
+    for (int t = 0; t < 16; ++t) dma_step(s, buf, t);
   };
 
   dma_stage(0, 0);
+  if (tid < S) {
+    const float* part = f.ncmax + ((int64_t)p * S + tid) * 16;
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, part[i]);
+    ncm_s[tid] = m;
+  }
   half8 x[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) x[kk] = *(const half8*)(xrow + 32 * kk + 8 * lg);
@@ -170,15 +257,22 @@ __global__ __launch_bounds__(512) void rvq_encode_full_kernel(FullArgs f) {
 
   const uint32_t lg4 = (uint32_t)lg << 2;
   const half8 zero8 = {};
-  const float4v zero4 = {0.f, 0.f, 0.f, 0.f};
+  // 1.0 the compiler cannot see: fma(fp16 -> fp32 operand, one, c) then stays
+  // one v_fma_mix (convert and add in one instruction; fma(a, 1, c) rounds
+  // once, exactly like a + c) instead of a conversion plus an add
+  float one = 1.0f;
+  asm volatile("" : "+v"(one));
   const int64_t Dfull = a.G * kFullD;
   const int64_t out_off = ((b * a.H + h) * a.T + t) * Dfull + g * kFullD;
 
   for (int s = 0; s < S; ++s) {
     const int buf = s & 1;
-    if (s + 1 < S) dma_stage(s + 1, buf ^ 1);
+    const bool next = s + 1 < S;
+    auto dma = [&](int t) {
+      if (next) dma_step(s + 1, buf ^ 1, t);
+    };
     const half8* tabA = (const half8*)(lds + buf * kFullBufBytes);
-    const half8* biasA = (const half8*)(lds + buf * kFullBufBytes + kFullTabBytes);
+    const float* nhA = (const float*)(lds + buf * kFullBufBytes + kFullTabBytes);
 
     // ---- B operands of this stage: r = x - dec as r_hi + r_lo, |r|^2 ----
     half8 bh[4], bl[4];
@@ -196,74 +290,23 @@ __global__ __launch_bounds__(512) void rvq_encode_full_kernel(FullArgs f) {
       for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float r = (float)x[kk][e] - dec[kk][e];
+          const float r = fmaf((float)x[kk][e], one, -dec[kk][e]);
           const half_t hi = (half_t)r;
           bh[kk][e] = hi;
-          bl[kk][e] = (half_t)(r - (float)hi);
+          bl[kk][e] = (half_t)fmaf((float)hi, -one, r);
           rr = fmaf(r, r, rr);
         }
       }
     }
     rr = lane_group_sum_f(rr);
-    float ncm = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ncm = fmaxf(ncm, f.ncmax[((int64_t)p * S + s) * 16 + i]);
+    const float ncm = ncm_s[s];
     const float delta = (rr + ncm) * 0x1p-8f;
     // M = 2^(e+2) for rr + ncm + delta in [2^e, 2^(e+1))
     const float M = __uint_as_float((__float_as_uint(rr + ncm + delta) & 0x7F800000u) + (2u << 23));
-    const float beta_s = ((rr + delta) * 0.5f + M) * 0x1p-12f;
-    const half_t bhi = (half_t)beta_s;
-    const half_t blo = (half_t)(beta_s - (float)bhi);
-    const half8 bbias = lg == 0 ? half8{(half_t)-1.f, (half_t)-1.f, -bhi, -blo, (half_t)0.f, (half_t)0.f,
-                                        (half_t)0.f, (half_t)0.f}
-                                : zero8;
+    const float bm = (rr + delta) * 0.5f + M;
 
-    // ---- distances to the 256 codewords, two 16-codeword chunks at a time ----
-    uint32_t best = 0xFFFFFFFFu;
-    auto keys = [&](const float4v& v, int c) {
-      const uint32_t k0 = (__float_as_uint(v[0]) << 9) | (uint32_t)(16 * c + 0);
-      const uint32_t k1 = (__float_as_uint(v[1]) << 9) | (uint32_t)(16 * c + 1);
-      const uint32_t k2 = (__float_as_uint(v[2]) << 9) | (uint32_t)(16 * c + 2);
-      const uint32_t k3 = (__float_as_uint(v[3]) << 9) | (uint32_t)(16 * c + 3);
-      best = umin3_f(umin3_f(k0, k1, k2), k3, best);
-    };
-    const bool lo = s > 0;
-    // four independent 16-codeword chunks per pass (a rolled loop: unrolled,
-    // the compiler hoists every chunk's A loads)
-#pragma unroll 1
-    for (int c = 0; c < 16; c += 4) {
-      float4v acc[4];
-      int w[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc[u] = zero4;
-        w[u] = 16 * (c + u) + j;
-      }
-      // A operands of K-step kk+1 load while kk's MFMAs run
-      half8 A[2][4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) A[0][u] = tabA[w[u] * 16 + (lg ^ (w[u] & 15))];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        if (kk + 1 < 4) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) A[(kk + 1) & 1][u] = tabA[w[u] * 16 + ((4 * (kk + 1) + lg) ^ (w[u] & 15))];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kk & 1][u], bh[kk], acc[u], 0, 0, 0);
-        if (lo) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kk & 1][u], bl[kk], acc[u], 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lg == 0 ? biasA[w[u]] : zero8, bbias, acc[u], 0, 0, 0);
-        keys(acc[u], c + u);
-      }
-    }
+    const uint32_t best = s == 0 ? full_search<false>(tabA, nhA, bh, bl, bm, lg, j, dma)
+                                 : full_search<true>(tabA, nhA, bh, bl, bm, lg, j, dma);
     // the row's winner over the four lane groups (lanes j + 16 lg hold row j)
     const uint32_t idx = lane_group_min_u(best | lg4) & 255u;
     if (valid && lg == 0) code_row[s] = (uint8_t)idx;
@@ -273,7 +316,7 @@ __global__ __launch_bounds__(512) void rvq_encode_full_kernel(FullArgs f) {
     for (int kk = 0; kk < 4; ++kk) {
       const half8 cw = tabA[idx * 16 + ((4 * kk + lg) ^ (idx & 15))];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dec[kk][e] += (float)cw[e];
+      for (int e = 0; e < 8; ++e) dec[kk][e] = fmaf((float)cw[e], one, dec[kk][e]);
     }
     if (valid) {
       for (int ex = 0; ex < a.n_exits; ++ex) {
@@ -299,29 +342,33 @@ int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
   const int64_t S = a.S;
   unsigned char* ws = (unsigned char*)workspace;
   _Float16* tab16 = (_Float16*)ws;
-  half8* bias_plane = (half8*)(ws + P * S * (int64_t)kFullTabBytes);
-  float* ncmax = (float*)(ws + P * S * ((int64_t)kFullTabBytes + kFullK * 16));
+  float* nhalf = (float*)(ws + P * S * (int64_t)kFullTabBytes);
+  float* ncmax = (float*)(ws + P * S * ((int64_t)kFullTabBytes + kFullK * 4));
   JKV_CHECK_ARG(P * S * 16 < ((int64_t)1 << 31), "too many (problem, stage) tables");
   hipLaunchKernelGGL(full_tables_kernel, dim3((uint32_t)(P * S * 16)), dim3(256), 0, stream, a.tables,
-                     tab16, bias_plane, ncmax);
+                     tab16, nhalf, ncmax);
   JKV_CHECK_LAUNCH();
 
   FullArgs f = {};
   f.e = a;
   f.tab16 = tab16;
-  f.bias_plane = bias_plane;
+  f.nhalf = nhalf;
   f.ncmax = ncmax;
   // waves per workgroup: 8 (128 rows) unless that leaves the chip short of
   // workgroups; each workgroup holds most of a CU's LDS
   const int64_t rows = a.B * a.T;
   int nw = kFullMaxWaves;
-  while (nw > 2 && P * ceil_div(rows, 16 * nw) < 256) nw >>= 1;
+  while (nw > 4 && P * ceil_div(rows, 16 * nw) < 256) nw >>= 1;  // nw in {4, 8}
   f.row_blocks = ceil_div(rows, 16 * nw);
   int64_t nblocks = P * f.row_blocks;
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
-  hipLaunchKernelGGL(rvq_encode_full_kernel, dim3((uint32_t)nblocks), dim3(64 * nw), 2 * kFullBufBytes,
-                     stream, f);
+  if (nw == 8)
+    hipLaunchKernelGGL(rvq_encode_full_kernel<8>, dim3((uint32_t)nblocks), dim3(64 * 8), 2 * kFullBufBytes,
+                       stream, f);
+  else
+    hipLaunchKernelGGL(rvq_encode_full_kernel<4>, dim3((uint32_t)nblocks), dim3(64 * 4), 2 * kFullBufBytes,
+                       stream, f);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }

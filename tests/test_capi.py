@@ -62,8 +62,8 @@ def test_workspace_queries():
     lib = _lib.load()
     assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 0) == 0
     assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 1) == 8 * 16 * 2 * 256 * 8 * 4
-    # full-vector codebooks: fp16 tables + bias plane + max norm per (head, stage)
-    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 0) == 8 * 2 * (256 * 128 * 2 + 256 * 16 + 64)
+    # full-vector codebooks: fp16 tables + -|c|^2/2 plane + partial max norms per (head, stage)
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 0) == 8 * 2 * (256 * 128 * 2 + 256 * 4 + 64)
     assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 33, 256, 128, 0) == 0
     assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 128, 128, 0) == 0
     assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 1) == 8 * 2 * 256 * 128 * 4

@@ -195,6 +195,36 @@ def cq2_workload(args, device):
     return {"ms_per_step": ms, "tokens_per_s": 4 * 2048 / (ms / 1e3)}
 
 
+def full_vector_workload(args, device):
+    """Config 3 read literally: two full-vector (d = 128) residual stages per
+    (layer, K/V), 32 layers x {K,V} x [4,8,2048,128], tables [8,2,256,128]."""
+    import torch
+    from jointkv_amd import _ops
+
+    gen = torch.Generator(device=device).manual_seed(8601)
+    tensors = []
+    for _ in range(LAYERS * 2):
+        states = make_states(gen, 4, HEADS, 2048, device)
+        tables = make_tables(gen, (HEADS, 2, CLUSTERS, HEAD_DIM), (1.0, 0.5), 1, device)
+        tensors.append((states, tables))
+
+    def step():
+        for states, tables in tensors:
+            _ops.rvq_encode(states, tables, groups=1, group_dim=HEAD_DIM, exits=(2,))
+
+    ms = timed(step, max(1, args.steps // 2), 1)
+    vecs = 4 * HEADS * 2048
+    flops = vecs * 2 * CLUSTERS * HEAD_DIM * 2  # two stages, 256 codewords, 128 dims, multiply-add
+    launch_us = ms * 1e3 / len(tensors)
+    return {
+        "ms_per_step": ms,
+        "tokens_per_s": 4 * 2048 / (ms / 1e3),
+        "us_per_encode": launch_us,
+        "tflops": flops / (launch_us * 1e-6) / 1e12,
+        "mfma_frac": flops / (launch_us * 1e-6) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+    }
+
+
 def decode_workload(args, device):
     import torch
     import jointkv_amd as jkv
@@ -355,7 +385,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
-    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,cq2,cpu")
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,cq2,full,cpu")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
@@ -377,6 +407,9 @@ def main() -> int:
     if "cq2" not in skip:
         log("cq2 workload (config 3)")
         extras["cq2_encode"] = cq2_workload(args, device)
+    if "full" not in skip:
+        log("full-vector workload (config 3, literal two-stage reading)")
+        extras["full_vector_encode"] = full_vector_workload(args, device)
     if "decode" not in skip:
         log("decode workload (config 4)")
         extras["decode"] = decode_workload(args, device)

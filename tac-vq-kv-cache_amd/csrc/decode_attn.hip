@@ -357,6 +357,49 @@ __device__ __forceinline__ half8 rebuild8_lds(const _Float16* tab, uint32_t code
   }
 }
 
+// Codes of the four 8-dim chunks 4q + sel (q = 0..3) of one token, from its
+// whole code record held as dwords w[].  A chunk has n = (8/DG)*S code bytes
+// (1, 2 or 4) at byte (4q + sel)*n = 4*(q*n) + sel*n of the record.
+template <int DG, int S>
+__device__ __forceinline__ void record_codes(const uint32_t* w, int sel, uint32_t (&out)[4]) {
+  constexpr int n = (8 / DG) * S;
+  // v_perm_b32 picks bytes of the 8-byte pair (hi:lo) by a per-lane selector
+  // (selector byte 0x0c yields zero), so no lane indexes an array
+  const uint32_t off = (uint32_t)(sel * n) & 7u;  // first code byte within its dword pair
+  const uint32_t pick = n == 1   ? (off | 0x0c0c0c00u)
+                        : n == 2 ? (off | ((off + 1) << 8) | 0x0c0c0000u)
+                                 : (off | ((off + 1) << 8) | ((off + 2) << 16) | ((off + 3) << 24));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (n == 4) {
+      // dword 4q + sel: pair (4q, 4q+1) or (4q+2, 4q+3), then the pair's half
+      const uint32_t p01 = __builtin_amdgcn_perm(w[4 * q + 1], w[4 * q], pick);
+      const uint32_t p23 = __builtin_amdgcn_perm(w[4 * q + 3], w[4 * q + 2], pick);
+      const uint32_t m = 0u - (((uint32_t)sel >> 1) & 1u);
+      out[q] = (p01 & ~m) | (p23 & m);
+    } else if constexpr (n == 2) {
+      // bytes 2 sel, 2 sel + 1 of the pair (w[2q], w[2q+1])
+      out[q] = __builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], pick);
+    } else {
+      // byte sel of w[q] (sel < 4)
+      out[q] = __builtin_amdgcn_perm(w[q], w[q], pick);
+    }
+  }
+}
+
+// a token's whole code record (kCb a multiple of 16 bytes, 16-byte aligned in LDS)
+template <int kCb>
+__device__ __forceinline__ void read_record(const uint8_t* rec, uint32_t (&w)[kCb / 4]) {
+#pragma unroll
+  for (int i = 0; i < kCb / 16; ++i) {
+    const uint4 v = *(const uint4*)(rec + 16 * i);
+    w[4 * i] = v.x;
+    w[4 * i + 1] = v.y;
+    w[4 * i + 2] = v.z;
+    w[4 * i + 3] = v.w;
+  }
+}
+
 // (a[e], b[e]) as one 32-bit word, e = 0..7
 __device__ __forceinline__ uint32_t pair_halves(half8 a, half8 b, int e) {
   const half2v h = {a[e], b[e]};
@@ -368,7 +411,8 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char dyn[];
   constexpr int tab_halves = kHeadDim * S * kLdsK;  // G * S * K * DG with G * DG = 128
   constexpr int kSlots = kLdsMaxSplit / kLdsChunk;
-  const int cb = (int)(a.G * S);  // code bytes per token (16 or 32)
+  constexpr int kCb = (kHeadDim / DG) * S;  // code bytes per token (16 or 32)
+  const int cb = kCb;
   _Float16* tab = (_Float16*)dyn;
   uint8_t* cbuf = dyn + (size_t)tab_halves * 2;                           // [chunk][32]
   _Float16* stg_all = (_Float16*)(cbuf + kLdsChunk * kLdsCodeBytes);      // [waves][32][36]
@@ -501,10 +545,31 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
 #pragma unroll
     for (int tl = 0; tl < 2; ++tl) {
       const int kb = 32 * wave + 16 * tl;  // first key of the tile in the chunk
-      const uint8_t* rec = cbuf + (kb + ln) * cb;
+      // the key's whole record (the four lanes of a key read the same bytes),
+      // then all eight gathers of the lane's four chunks at once
+      uint32_t w[kCb / 4];
+      read_record<kCb>(cbuf + (kb + ln) * kCb, w);
+      uint32_t cc[4];
+      record_codes<DG, S>(w, lg, cc);
       half8 k[4];
+      if constexpr (DG == 8) {
+        // every stage word of the four chunks first, then the sums (left to
+        // itself the scheduler waits for each pair before issuing the next)
+        half8 g[4][S];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) k[q] = rebuild8_lds<DG, S>(tab, chunk_codes<DG, S>(rec, 4 * q + lg), 4 * q + lg);
+        for (int q = 0; q < 4; ++q) {
+          const _Float16* base = tab + (4 * q + lg) * (S * kLdsK * 8);
+#pragma unroll
+          for (int st = 0; st < S; ++st)
+            g[q][st] = *(const half8*)(base + st * kLdsK * 8 + ((cc[q] >> (8 * st)) & 0xffu) * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) k[q] = S == 2 ? g[q][0] + g[q][S - 1] : g[q][0];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) k[q] = rebuild8_lds<DG, S>(tab, cc[q], 4 * q + lg);
+      }
       half8 r[4];
       rope16(k[0], k[2], trig[tl][0], trig[tl][1], &r[0], &r[2]);
       rope16(k[1], k[3], trig[tl][2], trig[tl][3], &r[1], &r[3]);
@@ -602,14 +667,28 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     if (c >= nchunks) continue;
     const bool more = c + 1 < nchunks;
     const int kb0 = 32 * wave + 2 * kp;
-    const uint8_t* rec0 = cbuf + kb0 * cb;
-    const uint8_t* rec1 = rec0 + cb;
     const bool ok0 = c * kLdsChunk + kb0 < ntok, ok1 = c * kLdsChunk + kb0 + 1 < ntok;
+    // both keys' records once per chunk; slice dp+1's gathers go out before
+    // slice dp's transpose
+    uint32_t w0[kCb / 4], w1[kCb / 4];
+    read_record<kCb>(cbuf + kb0 * kCb, w0);
+    read_record<kCb>(cbuf + (kb0 + 1) * kCb, w1);
+    uint32_t cc0[4], cc1[4];
+    record_codes<DG, S>(w0, vq, cc0);
+    record_codes<DG, S>(w1, vq, cc1);
+    // gathers run for every key (a record past the split's tokens still holds
+    // code bytes, so the reads stay inside the tables) and the sums of keys
+    // past it are then zeroed: selects, not branches around the reads
+    half8 vn0 = rebuild8_lds<DG, S>(tab, cc0[0], vq);
+    half8 vn1 = rebuild8_lds<DG, S>(tab, cc1[0], vq);
 #pragma unroll
     for (int dp = 0; dp < 4; ++dp) {
-      const int c8 = 4 * dp + vq;
-      const half8 v0 = ok0 ? rebuild8_lds<DG, S>(tab, chunk_codes<DG, S>(rec0, c8), c8) : zero8;
-      const half8 v1 = ok1 ? rebuild8_lds<DG, S>(tab, chunk_codes<DG, S>(rec1, c8), c8) : zero8;
+      const half8 v0 = ok0 ? vn0 : zero8, v1 = ok1 ? vn1 : zero8;
+      if (dp + 1 < 4) {
+        const int c8n = 4 * (dp + 1) + vq;
+        vn0 = rebuild8_lds<DG, S>(tab, cc0[dp + 1], c8n);
+        vn1 = rebuild8_lds<DG, S>(tab, cc1[dp + 1], c8n);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         *(uint32_t*)(stg + (8 * vq + e) * kStgStride + 2 * kp) = pair_halves(v0, v1, e);

@@ -494,13 +494,12 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     }
   };
 
-  // ---- every chunk's K code records into registers (one 16-byte piece per
-  // thread per chunk), the K tables and the first chunk into LDS ----
+  // ---- the K tables and the first chunk's code records into LDS; the other
+  // chunks' records (one 16-byte piece per thread per chunk) load into
+  // registers once the K phase has started ----
   uint4 kcodes[kSlots];
-#pragma unroll
-  for (int c = 0; c < kSlots; ++c)
-    kcodes[c] = c < nchunks ? fetch_codes(a.kc, c) : uint4{0u, 0u, 0u, 0u};
   load_tables(a.kt);
+  kcodes[0] = nchunks > 0 ? fetch_codes(a.kc, 0) : uint4{0u, 0u, 0u, 0u};
   if (nchunks > 0) store_codes(kcodes[0]);
   // ---- rotated queries at position L-1: B operand, column ln = head ----
   const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -528,6 +527,9 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
   if (nchunks > 0) fetch_trig(0, trig);
   __builtin_amdgcn_s_waitcnt(0);  // the tables' direct-to-LDS loads have landed
   __syncthreads();
+#pragma unroll
+  for (int c = 1; c < kSlots; ++c)
+    kcodes[c] = c < nchunks ? fetch_codes(a.kc, c) : uint4{0u, 0u, 0u, 0u};
 
   // ---- K phase.  Lane (key ln of a 16-key tile, lane group lg) owns 8-dim
   // chunks 4q+lg (q = 0..3) = MFMA contraction slice q; chunks lg/lg+8 and
@@ -542,15 +544,17 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     const bool more = c + 1 < nchunks;
     half8 tnext[2][4];
     if (more) fetch_trig(c + 1, tnext);
+    // both tiles' key records (the four lanes of a key read the same bytes),
+    // so tile 1's gathers can go out while tile 0 computes
+    uint32_t wrec[2][kCb / 4];
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl) read_record<kCb>(cbuf + (32 * wave + 16 * tl + ln) * kCb, wrec[tl]);
 #pragma unroll
     for (int tl = 0; tl < 2; ++tl) {
       const int kb = 32 * wave + 16 * tl;  // first key of the tile in the chunk
-      // the key's whole record (the four lanes of a key read the same bytes),
-      // then all eight gathers of the lane's four chunks at once
-      uint32_t w[kCb / 4];
-      read_record<kCb>(cbuf + (kb + ln) * kCb, w);
+      // all eight gathers of the lane's four chunks at once
       uint32_t cc[4];
-      record_codes<DG, S>(w, lg, cc);
+      record_codes<DG, S>(wrec[tl], lg, cc);
       half8 k[4];
       if constexpr (DG == 8) {
         // every stage word of the four chunks first, then the sums (left to
@@ -593,11 +597,12 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     __syncthreads();
   }
 
-  // every chunk's V code records into registers while the softmax runs
+  // the K phase's last barrier has passed: every wave is done with the K
+  // tables, so the V tables and the first chunk of V records load while the
+  // softmax runs
+  load_tables(a.vt);
   uint4 vcodes[kSlots];
-#pragma unroll
-  for (int c = 0; c < kSlots; ++c)
-    vcodes[c] = c < nchunks ? fetch_codes(a.vc, c) : uint4{0u, 0u, 0u, 0u};
+  vcodes[0] = nchunks > 0 ? fetch_codes(a.vc, 0) : uint4{0u, 0u, 0u, 0u};
 
   // ---- split max and exp-sum per head (lanes ln < NQ carry head ln) ----
   float mx = -__builtin_inff();
@@ -647,11 +652,14 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
     lh[h] = l;
   }
 
-  // ---- V tables and the first chunk of V codes into LDS ----
-  load_tables(a.vt);
+  // ---- the V tables have landed; the first chunk of V codes into LDS, the
+  // other chunks' records into registers behind the V phase ----
   if (nchunks > 0) store_codes(vcodes[0]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+#pragma unroll
+  for (int c = 1; c < kSlots; ++c)
+    vcodes[c] = c < nchunks ? fetch_codes(a.vc, c) : uint4{0u, 0u, 0u, 0u};
 
   // ---- V phase, two 16-dim slices (4 chunks of 8 dims) at a time: lane
   // (chunk 4dp + (lane>>4), keys 2kp and 2kp+1 of the block, kp = lane&15)

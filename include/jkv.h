@@ -155,7 +155,9 @@ int jkv_scale_sgd(int32_t n, float* const* params, float* const* grads,
  *   q        [B,QH,D] fp16 (pre-RoPE), row stride q_stride_b / q_stride_h
  *   k_codes, v_codes  [B,KVH,cap,G,S] uint8 (byte strides b, h; token
  *            stride G*S); key position p lives in slot p % cap
- *   k_tables, v_tables  fp16 deployed codebooks [KVH*G,S,K,d]
+ *   k_tables, v_tables  fp16 deployed codebooks [KVH*G,S,K,d]; K = 256,
+ *            G*d = 128 with d in {4, 8} (S <= 8) or d = 128, G = 1
+ *            (full-vector codebooks, S <= 32)
  *   lengths  [B] int32 device: tokens in the cache including the new one;
  *            query position = lengths[b]-1; visible keys are the last
  *            min(window, lengths[b]) positions

@@ -43,10 +43,24 @@ struct DecodeArgs {
 // fp16 words of dims [8*c8, 8*c8+8) of one token: fp16(sum_s fp32(word_s)).
 // The sum of two fp16 words is exact in fp32 or too small to move the fp16
 // rounding, so for S = 2 one fp16 add gives the same bits; S > 2 sums in fp32.
+// D = 128 is one full-vector group (G = 1): the chunk is the 16-byte slice
+// c8 of every stage's 256-byte codeword, read from L2.
 template <int D>
 __device__ __forceinline__ half8 rebuild8(const uint8_t* codes_tok, const _Float16* tab,
                                           int64_t kvh, int64_t G, int S, int c8) {
-  if (D == 8) {
+  if (D == 128) {
+    const _Float16* base = tab + kvh * S * 256 * 128 + 8 * c8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < S; ++s) {
+      const half8 w = *(const half8*)(base + (s * 256 + codes_tok[s]) * 128);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += (float)w[e];
+    }
+    half8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (_Float16)acc[e];
+    return r;
+  } else if (D == 8) {
     const int g = c8;
     const _Float16* base = tab + ((kvh * G + g) * S) * 256 * 8;
     if (S == 2) {
@@ -799,8 +813,11 @@ static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int
 
 template <int D, int NQ>
 static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
-  const int64_t split = lds_ok ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
-  if (split > 0) {
+  const int64_t split = lds_ok && D != 128 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
+  if constexpr (D == 128) {
+    hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
+                       dim3(256), 0, stream, a);
+  } else if (split > 0) {
     a.split_tokens = (int32_t)split;
     a.n_splits = (int32_t)ceil_div(a.window, split);
     a.ws_ml = a.ws_o + a.B * a.QH * a.n_splits * kHeadDim;
@@ -855,9 +872,10 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   JKV_CHECK_ARG(G * d == kHeadDim, "decode attention supports head_dim 128 (got %lld)",
                 (long long)(G * d));
   JKV_CHECK_ARG(K == 256, "decode attention expects 256-entry codebooks");
-  JKV_CHECK_ARG(d == 8 || d == 4, "decode attention supports group dims 4 and 8 (got %lld)",
-                (long long)d);
-  JKV_CHECK_ARG(S >= 1 && S <= 8, "decode attention supports 1..8 stages");
+  JKV_CHECK_ARG(d == 8 || d == 4 || d == 128,
+                "decode attention supports group dims 4, 8 and 128 (got %lld)", (long long)d);
+  JKV_CHECK_ARG(S >= 1 && S <= (d == 128 ? 32 : 8), "decode attention supports 1..%d stages for group dim %lld",
+                d == 128 ? 32 : 8, (long long)d);
   JKV_CHECK_ARG(window > 0 && cap > 0, "window and cache capacity must be positive");
   JKV_CHECK_ARG(cap >= window, "cache capacity below the attention window");
   JKV_CHECK_ARG(rope_len > 0, "rotary table is empty");
@@ -894,6 +912,7 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   if (d == DD && nq == NN) return launch_decode<DD, NN>(a, lds_ok, stream);
   JKV_DEC(8, 1) JKV_DEC(8, 2) JKV_DEC(8, 4) JKV_DEC(8, 8)
   JKV_DEC(4, 1) JKV_DEC(4, 2) JKV_DEC(4, 4) JKV_DEC(4, 8)
+  JKV_DEC(128, 1) JKV_DEC(128, 2) JKV_DEC(128, 4) JKV_DEC(128, 8)
 #undef JKV_DEC
   return set_error(JKV_ENOTSUP, "unsupported decode geometry");
 }

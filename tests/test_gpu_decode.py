@@ -19,7 +19,7 @@ def _case(seed, batch, qh, kvh, groups, stages, d, length, cap):
     q = torch.randn(batch, qh, 1, 128, generator=gen).half()
     kc = torch.randint(0, 256, (batch, kvh, cap, groups, stages), generator=gen, dtype=torch.uint8)
     vc = torch.randint(0, 256, (batch, kvh, cap, groups, stages), generator=gen, dtype=torch.uint8)
-    sig = (1.0, 0.5, 0.25, 0.125)[:stages]
+    sig = (1.0, 0.5, 0.25, 0.125)[:stages] if stages <= 4 else tuple(0.8 ** s for s in range(stages))
     kt = ref.synthetic_tables(gen, (kvh * groups, stages, 256, d), sig, stage_axis=1)
     vt = ref.synthetic_tables(gen, (kvh * groups, stages, 256, d), sig, stage_axis=1)
     return q, kc, vc, kt, vt
@@ -41,6 +41,8 @@ def _expect(q, kc, vc, kt, vt, length, window, cap):
     (1, 4, 4, 32, 1, 4, 700, 512, 512),       # cq2 codes, MHA group of 1
     (1, 16, 2, 16, 1, 8, 257, 4096, 4096),    # cq1 codes, GQA 8
     (1, 8, 2, 16, 3, 8, 600, 4096, 4096),     # three stages: the generic split kernel
+    (1, 8, 2, 1, 4, 128, 600, 4096, 4096),    # full-vector codebooks, 4 stages (codewords from L2)
+    (2, 32, 8, 1, 16, 128, 700, 256, 512),    # full-vector R16 geometry, sliding window, ring wraps
 ])
 def test_decode_matches_oracle(device, batch, qh, kvh, groups, stages, d, length, window, cap):
     q, kc, vc, kt, vt = _case(length + qh, batch, qh, kvh, groups, stages, d, length, cap)
@@ -101,3 +103,33 @@ def test_encode_append_matches_encode_then_append(device):
         fused.encode_append(k, v, tables_k, tables_v, group_dim=8)
     assert torch.equal(direct.key, fused.key) and torch.equal(direct.value, fused.value)
     assert torch.equal(direct.lengths, fused.lengths) and fused.length == 6
+
+
+def test_full_vector_cache_serving_loop(device):
+    # R16-style codec (one 128-dim group, 16 stages): each step encodes the new
+    # token into the ring slot and attends over the packed codes
+    from jointkv_amd import _ops
+    gen = torch.Generator().manual_seed(8611)
+    stages, kvh, batch, cap = 16, 2, 2, 8
+    sig = tuple(0.8 ** s for s in range(stages))
+    tables_k = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1)
+    tables_v = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1)
+    tk, tv = tables_k.to(device), tables_v.to(device)
+    direct = jkv.PackedCodeCache(batch, kvh, 1, stages, capacity=cap, device=device)
+    fused = jkv.PackedCodeCache(batch, kvh, 1, stages, capacity=cap, device=device)
+    for step in range(11):  # wraps the 8-slot ring
+        k = ref.synthetic_states(gen, batch, kvh, 1).to(device)
+        v = ref.synthetic_states(gen, batch, kvh, 1).to(device)
+        _r, kc = _ops.rvq_encode(k, tk, groups=1, group_dim=128, exits=())
+        _r, vc = _ops.rvq_encode(v, tv, groups=1, group_dim=128, exits=())
+        direct.append(kc, vc)
+        fused.encode_append(k, v, tk, tv, group_dim=128)
+        print(f"full-vector serving step {step}", flush=True)
+    assert torch.equal(direct.key, fused.key) and torch.equal(direct.value, fused.value)
+    length = fused.length
+    q = torch.randn(batch, 8, 1, 128, generator=gen).half()
+    out = jkv.decode_attention(q.to(device), fused.key, fused.value, tk.half(), tv.half(), fused.lengths,
+                               window=cap)
+    expect = _expect(q, fused.key.cpu(), fused.value.cpu(), tables_k, tables_v, length, cap, cap)
+    err = float((out.cpu().float() - expect.float()).abs().max())
+    assert err <= ATOL, f"max abs error {err}"

@@ -180,6 +180,26 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b,
                          int64_t workspace_bytes, jkv_stream_t stream);
 
 /*
+ * Decode attention over a decoded fp16 K̂/V̂ window, the reference's own
+ * decode path (evaluate_mistral_longbench.py:112-122 over LayerCache's
+ * decoded_key/decoded_value, :44-70), for codecs whose codewords do not fit
+ * the packed-code kernel's LDS (full-vector R16/R32 tables).  Same rotary,
+ * GQA, window and output as jkv_decode_attention.
+ *   k_window, v_window  [B,KVH,cap,128] fp16, rows contiguous and 16-byte
+ *            aligned; element strides kv_stride_b / kv_stride_h; key
+ *            position p lives in slot p % cap
+ *   workspace  jkv_decode_workspace_bytes(B, QH, 128, window) bytes
+ */
+int jkv_decode_attention_window(const void* q, int64_t q_stride_b,
+                                int64_t q_stride_h, const void* k_window,
+                                const void* v_window, int64_t kv_stride_b,
+                                int64_t kv_stride_h, int64_t cap, int64_t B,
+                                int64_t QH, int64_t KVH, const int32_t* lengths,
+                                int64_t window, const void* rope_table,
+                                int64_t rope_len, void* out, void* workspace,
+                                int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
  * Causal sliding-window GQA prefill attention over one chunk's quantized K̂/V̂.
  * Replaces the prefill branch of attention_forward
  * (experiments_followup_mistral/evaluate_mistral_longbench.py:101-111) and its

@@ -44,11 +44,15 @@ struct DecodeArgs {
 // The sum of two fp16 words is exact in fp32 or too small to move the fp16
 // rounding, so for S = 2 one fp16 add gives the same bits; S > 2 sums in fp32.
 // D = 128 is one full-vector group (G = 1): the chunk is the 16-byte slice
-// c8 of every stage's 256-byte codeword, read from L2.
+// c8 of every stage's 256-byte codeword, read from L2.  D = 0 reads a decoded
+// fp16 window instead of codes (the 256-byte row is the token's record).
 template <int D>
 __device__ __forceinline__ half8 rebuild8(const uint8_t* codes_tok, const _Float16* tab,
                                           int64_t kvh, int64_t G, int S, int c8) {
-  if (D == 128) {
+  if (D == 0) {
+    // decoded window: the token's "record" is its fp16 row of 128 values
+    return *(const half8*)(codes_tok + 16 * c8);
+  } else if (D == 128) {
     const _Float16* base = tab + kvh * S * 256 * 128 + 8 * c8;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < S; ++s) {
@@ -813,8 +817,8 @@ static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int
 
 template <int D, int NQ>
 static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
-  const int64_t split = lds_ok && D != 128 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
-  if constexpr (D == 128) {
+  const int64_t split = lds_ok && D != 128 && D != 0 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
+  if constexpr (D == 128 || D == 0) {
     hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
                        dim3(256), 0, stream, a);
   } else if (split > 0) {
@@ -915,6 +919,54 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   JKV_DEC(128, 1) JKV_DEC(128, 2) JKV_DEC(128, 4) JKV_DEC(128, 8)
 #undef JKV_DEC
   return set_error(JKV_ENOTSUP, "unsupported decode geometry");
+}
+
+int jkv_decode_attention_window(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_window, const void* v_window, int64_t kv_stride_b,
+                                int64_t kv_stride_h, int64_t cap, int64_t B, int64_t QH, int64_t KVH,
+                                const int32_t* lengths, int64_t window, const void* rope_table,
+                                int64_t rope_len, void* out, void* workspace, int64_t workspace_bytes,
+                                jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && QH % KVH == 0, "invalid head geometry");
+  JKV_CHECK_ARG(window > 0 && cap > 0, "window and cache capacity must be positive");
+  JKV_CHECK_ARG(cap >= window, "cache capacity below the attention window");
+  JKV_CHECK_ARG(rope_len > 0, "rotary table is empty");
+  const int64_t nq = QH / KVH;
+  JKV_CHECK_ARG(nq == 1 || nq == 2 || nq == 4 || nq == 8, "GQA group of %lld query heads",
+                (long long)nq);
+  if (B == 0) return JKV_OK;
+  JKV_CHECK_ARG(q && k_window && v_window && lengths && out && rope_table, "null buffer");
+  JKV_CHECK_ARG(((uintptr_t)k_window % 16 == 0) && ((uintptr_t)v_window % 16 == 0) && kv_stride_b % 8 == 0 &&
+                    kv_stride_h % 8 == 0,
+                "decoded windows need 16-byte aligned rows");
+  const int64_t need = jkv_decode_workspace_bytes(B, QH, kHeadDim, window);
+  JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                "decode attention needs %lld bytes of workspace", (long long)need);
+  DecodeArgs a = {};
+  a.q = (const _Float16*)q;
+  a.qsb = q_stride_b; a.qsh = q_stride_h;
+  // each token's record is its 256-byte fp16 row
+  a.kc = (const uint8_t*)k_window; a.vc = (const uint8_t*)v_window;
+  a.csb = kv_stride_b * 2; a.csh = kv_stride_h * 2; a.cap = cap;
+  a.kt = nullptr; a.vt = nullptr;
+  a.B = B; a.QH = QH; a.KVH = KVH; a.G = kHeadDim * 2; a.d = 0; a.S = 1; a.K = 0;
+  a.lengths = lengths;
+  a.window = window;
+  a.rope = (const _Float16*)rope_table;
+  a.rope_len = rope_len;
+  a.n_splits = (int32_t)ceil_div(window, kSplitTokens);
+  a.split_tokens = kSplitTokens;
+  a.ws_o = (float*)workspace;
+  a.ws_ml = a.ws_o + B * QH * a.n_splits * kHeadDim;
+  a.out = (_Float16*)out;
+  switch (nq) {
+    case 1: return launch_decode<0, 1>(a, false, stream);
+    case 2: return launch_decode<0, 2>(a, false, stream);
+    case 4: return launch_decode<0, 4>(a, false, stream);
+    default: return launch_decode<0, 8>(a, false, stream);
+  }
 }
 
 }  // extern "C"

@@ -9,8 +9,10 @@ HIP kernels of ``libjkv.so``; there is no CPU fallback.
 
 from . import _lib
 from .attention import (
+    DecodedWindowCache,
     PackedCodeCache,
     decode_attention,
+    decode_attention_window,
     deploy_tables,
     prefill_attention,
     prefill_attention_from_codes,
@@ -39,11 +41,13 @@ __all__ = [
     "CacheGeometry",
     "ClosedLoopGroupedCQ",
     "ClosedLoopUniformResidualVQ",
+    "DecodedWindowCache",
     "PackedCodeCache",
     "QuantizedKV",
     "StorageLedger",
     "clip_codebook_gradients",
     "decode_attention",
+    "decode_attention_window",
     "deploy_tables",
     "dynamic_bpa",
     "frozen_assignment_reconstruction",

@@ -57,6 +57,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
     ),
+    "jkv_decode_attention_window": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
+         _i64, _vp],
+    ),
     "jkv_prefill_attention": (
         ctypes.c_int,
         [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -299,6 +299,60 @@ def decode_attention(
     return out
 
 
+def decode_attention_window(
+    q: torch.Tensor,
+    key_window: torch.Tensor,
+    value_window: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    window: int,
+    rope_theta: float,
+    max_length: int | None = None,
+) -> torch.Tensor:
+    """One decode step of GQA attention over decoded fp16 K̂/V̂ windows.
+
+    ``q[B,QH,128]`` fp16 (pre-RoPE), windows ``[B,KVH,cap,128]`` fp16 (rows
+    contiguous) with position p in slot ``p % cap``, ``lengths[B]`` int32
+    (cache length including the new token).  Returns ``[B,QH,128]`` fp16.
+    """
+
+    device = _lib.require_device(q, key_window, value_window, lengths)
+    if q.dtype != torch.float16 or q.ndim != 3 or q.stride(-1) != 1:
+        raise ValueError("decode queries must be fp16 [B,QH,D] with a contiguous last axis")
+    batch, qheads, dim = map(int, q.shape)
+    if key_window.shape != value_window.shape or key_window.dtype != torch.float16 or key_window.ndim != 4:
+        raise ValueError("decoded windows must be two fp16 [B,KVH,cap,128] tensors of one shape")
+    wb, kvheads, cap, wd = map(int, key_window.shape)
+    if wb != batch or wd != dim:
+        raise ValueError("query and decoded window geometry differ")
+    for w in (key_window, value_window):
+        if w.stride(-1) != 1 or w.stride(-2) != dim:
+            raise ValueError("decoded windows need contiguous [cap,128] blocks")
+    if key_window.stride() != value_window.stride():
+        raise ValueError("key/value windows need identical strides")
+    if lengths.dtype != torch.int32 or lengths.shape != (batch,):
+        raise ValueError("lengths must be int32 [B]")
+    lengths = lengths.contiguous()
+    if max_length is None:
+        max_length = int(lengths.max().item()) if batch else 1
+    if int(max_length) > cap and int(window) > cap:
+        raise ValueError("a sequence longer than the window ring's capacity needs window <= capacity")
+    table = rope_table(device, rope_theta, int(max_length) + 1)
+    span = max(1, min(int(window), int(max_length)))
+    lib = _lib.load()
+    out = torch.empty((batch, qheads, dim), dtype=torch.float16, device=device)
+    ws_bytes = int(lib.jkv_decode_workspace_bytes(batch, qheads, dim, span))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    code = lib.jkv_decode_attention_window(
+        q.data_ptr(), q.stride(0), q.stride(1), key_window.data_ptr(), value_window.data_ptr(),
+        key_window.stride(0), key_window.stride(1), cap, batch, qheads, kvheads, lengths.data_ptr(), span,
+        table.data_ptr(), int(table.shape[0]), out.data_ptr(), workspace.data_ptr(), ws_bytes,
+        _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return out
+
+
 def prefill_attention(
     q: torch.Tensor,
     key: torch.Tensor,

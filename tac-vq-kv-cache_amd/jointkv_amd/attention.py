@@ -79,6 +79,33 @@ def decode_attention(
     return out if squeeze else out.unsqueeze(2)
 
 
+def decode_attention_window(
+    query: torch.Tensor,
+    key_window: torch.Tensor,
+    value_window: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    window: int = MISTRAL_WINDOW,
+    rope_theta: float = MISTRAL_ROPE_THETA,
+    max_length: int | None = None,
+) -> torch.Tensor:
+    """:func:`decode_attention` over decoded fp16 K̂/V̂ instead of codes.
+
+    The reference's own decode branch (evaluate_mistral_longbench.py:112-122)
+    over ``LayerCache``'s decoded window (:44-70), for codecs whose codewords
+    do not fit the packed-code kernel (full-vector R16/R32 tables: 1 MiB of
+    fp16 codewords per kv head at 16 stages).  ``key_window``/``value_window``
+    ``[B,KVH,cap,128]`` fp16 hold position p in slot ``p % cap`` (see
+    :class:`DecodedWindowCache`); the rest is as in :func:`decode_attention`.
+    """
+
+    squeeze = query.ndim == 3
+    q = query if squeeze else query.reshape(query.shape[0], query.shape[1], query.shape[-1])
+    out = _ops.decode_attention_window(q, key_window, value_window, lengths, window=window,
+                                       rope_theta=rope_theta, max_length=max_length)
+    return out if squeeze else out.unsqueeze(2)
+
+
 def _start_tensor(start_positions, batch: int, tokens: int, device) -> tuple[torch.Tensor, int]:
     """int32 [B] device starts and the largest position they reach."""
 
@@ -223,3 +250,103 @@ class PackedCodeCache:
         visible = min(self._host_length, self.capacity)
         per_slot = self.key.shape[3] * self.key.shape[4]
         return 2 * self.key.shape[0] * self.key.shape[1] * visible * per_slot
+
+
+class DecodedWindowCache:
+    """Per-layer cache that keeps the decoded fp16 K̂/V̂ window, as the
+    reference's ``LayerCache`` does (evaluate_mistral_longbench.py:29-78,
+    its "declared evaluation acceleration workspace" :57), plus the uint8
+    code payload.
+
+    Both live in ring buffers (slot ``position % capacity``) instead of
+    ``torch.cat`` + slicing, so an append costs O(new tokens).  Use it for
+    codecs the packed-code kernel does not serve at speed (full-vector
+    R16/R32 tables); attend with :meth:`attention`.
+    """
+
+    def __init__(
+        self,
+        batch: int,
+        kv_heads: int,
+        groups: int,
+        stages: int,
+        *,
+        capacity: int = MISTRAL_WINDOW,
+        head_dim: int = 128,
+        device: torch.device | str = "cuda",
+    ) -> None:
+        if min(batch, kv_heads, groups, stages, capacity) <= 0 or head_dim != 128:
+            raise ValueError("invalid decoded-window cache geometry")
+        self.codes = PackedCodeCache(batch, kv_heads, groups, stages, capacity=capacity, device=device)
+        shape = (batch, kv_heads, capacity, head_dim)
+        self.decoded_key = torch.zeros(shape, dtype=torch.float16, device=device)
+        self.decoded_value = torch.zeros(shape, dtype=torch.float16, device=device)
+        self.capacity = capacity
+
+    @property
+    def length(self) -> int:
+        return self.codes.length
+
+    @property
+    def lengths(self) -> torch.Tensor:
+        return self.codes.lengths
+
+    def append(self, key_codes: torch.Tensor, value_codes: torch.Tensor, decoded_key: torch.Tensor,
+               decoded_value: torch.Tensor) -> None:
+        """``LayerCache.append`` (:44-60): codes ``[B,KVH,T,G,S]`` and the
+        codec's fp16 reconstructions ``[B,KVH,T,128]`` for T new positions."""
+
+        new = int(key_codes.shape[2])
+        if decoded_key.shape[2] != new or decoded_value.shape[2] != new:
+            raise ValueError("codes and decoded rows cover different tokens")
+        if decoded_key.dtype != torch.float16 or decoded_value.dtype != torch.float16:
+            raise ValueError("decoded rows must be fp16")
+        start_length = self.codes.length
+        self.codes.append(key_codes, value_codes)
+        if new > self.capacity:
+            decoded_key = decoded_key[:, :, -self.capacity :]
+            decoded_value = decoded_value[:, :, -self.capacity :]
+            start_length += new - self.capacity
+            new = self.capacity
+        start = start_length % self.capacity
+        first = min(new, self.capacity - start)
+        self.decoded_key[:, :, start : start + first] = decoded_key[:, :, :first]
+        self.decoded_value[:, :, start : start + first] = decoded_value[:, :, :first]
+        if first < new:
+            self.decoded_key[:, :, : new - first] = decoded_key[:, :, first:]
+            self.decoded_value[:, :, : new - first] = decoded_value[:, :, first:]
+
+    def encode_append(self, key: torch.Tensor, value: torch.Tensor, key_tables: torch.Tensor,
+                      value_tables: torch.Tensor, *, group_dim: int) -> None:
+        """Run the codec on one new token per sequence (``[B,KVH,1,128]``
+        fp16, fp32 masters ``[KVH*G,S,K,d]``): its codes go to the payload
+        ring and its full-depth reconstructions to the decoded window, as
+        evaluate_mistral_longbench.py:94-98 hands both to ``LayerCache``."""
+
+        if key.shape[2] != 1 or value.shape[2] != 1:
+            raise ValueError("encode_append takes one token per sequence")
+        groups, stages = self.codes.key.shape[3], self.codes.key.shape[4]
+        slot = self.codes.length % self.capacity
+        recon_k, _ = _ops.rvq_encode(key, key_tables, groups=groups, group_dim=group_dim, exits=(stages,),
+                                     codes_out=self.codes.key[:, :, slot : slot + 1])
+        recon_v, _ = _ops.rvq_encode(value, value_tables, groups=groups, group_dim=group_dim,
+                                     exits=(stages,), codes_out=self.codes.value[:, :, slot : slot + 1])
+        self.decoded_key[:, :, slot : slot + 1] = recon_k[0]
+        self.decoded_value[:, :, slot : slot + 1] = recon_v[0]
+        self.codes._host_length += 1
+        self.codes.lengths.fill_(self.codes._host_length)
+
+    def attention(self, query: torch.Tensor, *, window: int | None = None,
+                  rope_theta: float = MISTRAL_ROPE_THETA) -> torch.Tensor:
+        """Decode attention of ``query`` ``[B,QH,1,128]`` over the window."""
+
+        return decode_attention_window(query, self.decoded_key, self.decoded_value, self.codes.lengths,
+                                       window=self.capacity if window is None else window,
+                                       rope_theta=rope_theta, max_length=self.codes.length)
+
+    def payload_bytes(self) -> int:
+        return self.codes.payload_bytes()
+
+    def decode_workspace_bytes(self) -> int:
+        visible = min(self.codes.length, self.capacity)
+        return 2 * self.decoded_key.shape[0] * self.decoded_key.shape[1] * visible * self.decoded_key.shape[3] * 2

@@ -103,6 +103,27 @@ def test_decode_rejects_unsupported_geometry():
     assert rc == _lib.JKV_EINVAL and b"rotary" in lib.jkv_last_error()
 
 
+def test_decode_window_rejects_bad_arguments():
+    # validation only: every call below fails before a launch
+    lib = _lib.load()
+    # capacity below the window
+    rc = lib.jkv_decode_attention_window(1, 0, 0, 16, 16, 0, 0, 100, 1, 32, 8, 1, 4096, 1, 8192, 1, 1,
+                                         1 << 30, None)
+    assert rc == _lib.JKV_EINVAL and b"capacity" in lib.jkv_last_error()
+    # rows not 16-byte aligned
+    rc = lib.jkv_decode_attention_window(1, 0, 0, 18, 16, 0, 0, 4096, 1, 32, 8, 1, 4096, 1, 8192, 1, 1,
+                                         1 << 30, None)
+    assert rc == _lib.JKV_EINVAL and b"aligned" in lib.jkv_last_error()
+    # GQA group of 3 query heads
+    rc = lib.jkv_decode_attention_window(1, 0, 0, 16, 16, 0, 0, 4096, 1, 24, 8, 1, 4096, 1, 8192, 1, 1,
+                                         1 << 30, None)
+    assert rc == _lib.JKV_EINVAL and b"GQA" in lib.jkv_last_error()
+    # workspace too small
+    rc = lib.jkv_decode_attention_window(1, 0, 0, 16, 16, 0, 0, 4096, 1, 32, 8, 1, 4096, 1, 8192, 1, 1,
+                                         16, None)
+    assert rc == _lib.JKV_EINVAL and b"workspace" in lib.jkv_last_error()
+
+
 def test_scatter_rejects_misaligned_deterministic_gradients():
     # Validation fails before any launch: the gradient pointer (2) is not
     # aligned to an 8-element fp16 slice and a deterministic sum was asked for.

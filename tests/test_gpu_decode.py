@@ -133,3 +133,49 @@ def test_full_vector_cache_serving_loop(device):
     expect = _expect(q, fused.key.cpu(), fused.value.cpu(), tables_k, tables_v, length, cap, cap)
     err = float((out.cpu().float() - expect.float()).abs().max())
     assert err <= ATOL, f"max abs error {err}"
+
+
+@pytest.mark.parametrize("batch,qh,kvh,length,window,cap", [
+    (2, 32, 8, 4096, 4096, 4096),   # config 4 heads, full window
+    (1, 8, 2, 700, 256, 512),       # sliding window, ring wraps
+    (3, 8, 8, 37, 4096, 64),        # short prefix, MHA
+])
+def test_decode_window_matches_oracle(device, batch, qh, kvh, length, window, cap):
+    gen = torch.Generator().manual_seed(length + 7)
+    q = torch.randn(batch, qh, 1, 128, generator=gen).half()
+    kw = torch.randn(batch, kvh, cap, 128, generator=gen).half()
+    vw = torch.randn(batch, kvh, cap, 128, generator=gen).half()
+    print(f"window decode B={batch} QH={qh} KVH={kvh} len={length} win={window} cap={cap}", flush=True)
+    out = jkv.decode_attention_window(
+        q.to(device), kw.to(device), vw.to(device),
+        torch.full((batch,), length, dtype=torch.int32, device=device), window=window)
+    start = max(0, length - min(window, cap))
+    pos = torch.arange(start, length)
+    expect = ref.decode_attention(q, kw[:, :, pos % cap].contiguous(), vw[:, :, pos % cap].contiguous(),
+                                  length - 1, pos)
+    err = float((out.cpu().float() - expect.float()).abs().max())
+    assert err <= ATOL, f"max abs error {err}"
+
+
+def test_decoded_window_cache_equals_packed_decode(device):
+    # the same codec step fills both caches; attention over the decoded window
+    # and over the packed codes sees identical K̂/V̂ rows, so identical outputs
+    gen = torch.Generator().manual_seed(8617)
+    stages, kvh, batch, cap = 16, 2, 2, 8
+    sig = tuple(0.8 ** s for s in range(stages))
+    tk = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1).to(device)
+    tv = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1).to(device)
+    win = jkv.DecodedWindowCache(batch, kvh, 1, stages, capacity=cap, device=device)
+    packed = jkv.PackedCodeCache(batch, kvh, 1, stages, capacity=cap, device=device)
+    for step in range(11):  # wraps the 8-slot rings
+        k = ref.synthetic_states(gen, batch, kvh, 1).to(device)
+        v = ref.synthetic_states(gen, batch, kvh, 1).to(device)
+        win.encode_append(k, v, tk, tv, group_dim=128)
+        packed.encode_append(k, v, tk, tv, group_dim=128)
+        q = torch.randn(batch, 8, 1, 128, generator=gen).half().to(device)
+        a = win.attention(q)
+        b = jkv.decode_attention(q, packed.key, packed.value, tk.half(), tv.half(), packed.lengths,
+                                 window=cap, max_length=packed.length)
+        assert torch.equal(a, b), f"step {step}: window and packed decode differ"
+    assert torch.equal(win.codes.key, packed.key) and win.length == packed.length == 11
+    assert win.payload_bytes() == packed.payload_bytes()

@@ -17,6 +17,7 @@ namespace jkv {
 
 static const int kHeadDim = 128;
 static const int kSplitTokens = 256;  // tokens per split (workgroup)
+static const int kWinSplitTokens = 512;  // tokens per split over a decoded window (streamed rows)
 static const int kMaxCodeBytes = 64;  // code records staged in LDS up to this size
 
 struct DecodeArgs {
@@ -104,12 +105,15 @@ __device__ __forceinline__ half8 rebuild8(const uint8_t* codes_tok, const _Float
 template <int D, int NQ>
 __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   __shared__ _Float16 q_lds[NQ][kHeadDim];
-  __shared__ float s_lds[NQ][kSplitTokens];
+  constexpr int kTok = D == 0 ? kWinSplitTokens : kSplitTokens;
+  __shared__ float s_lds[NQ][kTok];
   __shared__ float red[NQ][4][2];
   __shared__ float o_red[4][NQ][kHeadDim];
   // the split's K and V code records (up to 64 bytes per token), fetched once
-  __shared__ __align__(16) uint8_t kc_lds[kSplitTokens * kMaxCodeBytes];
-  __shared__ __align__(16) uint8_t vc_lds[kSplitTokens * kMaxCodeBytes];
+  // (a decoded window, D = 0, reads its rows from global memory instead)
+  constexpr int kRecLds = D == 0 ? 16 : kTok * kMaxCodeBytes;
+  __shared__ __align__(16) uint8_t kc_lds[kRecLds];
+  __shared__ __align__(16) uint8_t vc_lds[kRecLds];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -121,8 +125,8 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   const int64_t L = a.lengths[b];
   const int64_t n_vis = L < a.window ? L : a.window;
   const int64_t start = L - n_vis;
-  const int64_t t0 = start + split * kSplitTokens;
-  int64_t t1 = t0 + kSplitTokens;
+  const int64_t t0 = start + split * kTok;
+  int64_t t1 = t0 + kTok;
   if (t1 > L) t1 = L;
   const int ntok = t1 > t0 ? (int)(t1 - t0) : 0;
   const float scale = 1.0f / sqrtf((float)kHeadDim);
@@ -151,7 +155,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     }
   }
   // ---- the split's code records into LDS, 16-byte chunks, one pass ----
-  const bool codes_in_lds = code_bytes <= kMaxCodeBytes && (code_bytes % 16) == 0;
+  const bool codes_in_lds = D != 0 && code_bytes <= kMaxCodeBytes && (code_bytes % 16) == 0;
   if (codes_in_lds) {
     const int per_tok = (int)(code_bytes / 16);
     const int64_t kbase = b * a.csb + kvh * a.csh;
@@ -184,23 +188,32 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
         qb[m][e] = (ln < NQ) ? q_lds[ln < NQ ? ln : 0][(4 * m + lg) * 8 + e] : (_Float16)0.f;
     }
     const int ntiles = (ntok + 15) / 16;
-    for (int tile = wave; tile < ntiles; tile += 4) {
+    // a tile's key rows and rotary rows, loaded one tile ahead of their use
+    struct KTile {
+      half8 k[4], c0, s0, c1, s1;
+    };
+    auto load_ktile = [&](int tile, KTile& kt) {
       const int tt = tile * 16 + ln;
       const bool valid = tt < ntok;
       const int64_t pos = valid ? t0 + tt : t0;
       const uint8_t* ct = key_codes(valid ? tt : 0);
-      half8 k0 = rebuild8<D>(ct, a.kt, kvh, a.G, S, lg);
-      half8 k1 = rebuild8<D>(ct, a.kt, kvh, a.G, S, lg + 4);
-      half8 k2 = rebuild8<D>(ct, a.kt, kvh, a.G, S, lg + 8);
-      half8 k3 = rebuild8<D>(ct, a.kt, kvh, a.G, S, lg + 12);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) kt.k[q] = rebuild8<D>(ct, a.kt, kvh, a.G, S, lg + 4 * q);
       // the host sizes the table past every length; the clamp only keeps a
       // misuse from reading out of bounds
       const _Float16* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
-      half8 c, s, r0, r1, r2, r3;
-      load_trig8(trow, 8 * lg, &c, &s);
-      rope16(k0, k2, c, s, &r0, &r2);
-      load_trig8(trow, 8 * (lg + 4), &c, &s);
-      rope16(k1, k3, c, s, &r1, &r3);
+      load_trig8(trow, 8 * lg, &kt.c0, &kt.s0);
+      load_trig8(trow, 8 * (lg + 4), &kt.c1, &kt.s1);
+    };
+    KTile nxt;
+    if (wave < ntiles) load_ktile(wave, nxt);
+    for (int tile = wave; tile < ntiles; tile += 4) {
+      const KTile cur = nxt;
+      if (tile + 4 < ntiles) load_ktile(tile + 4, nxt);
+      const bool valid = tile * 16 + ln < ntok;
+      half8 r0, r1, r2, r3;
+      rope16(cur.k[0], cur.k[2], cur.c0, cur.s0, &r0, &r2);
+      rope16(cur.k[1], cur.k[3], cur.c1, cur.s1, &r1, &r3);
       if (!valid) {
         r0 = half8{}; r1 = half8{}; r2 = half8{}; r3 = half8{};
       }
@@ -259,14 +272,22 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     for (int h = 0; h < NQ; ++h)
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
-    // four tokens per step so their codeword gathers are in flight together
-    for (int j0 = tl; j0 < ntok; j0 += 64) {
-      half8 v[4];
+    // four tokens per step so their loads are in flight together, and the
+    // next step's four go out before this step's products
+    half8 vn[4];
+    auto load_v = [&](int j0, half8 (&v)[4]) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int j = j0 + 16 * u;
         v[u] = rebuild8<D>(value_codes(j < ntok ? j : j0), a.vt, kvh, a.G, S, ch);
       }
+    };
+    if (tl < ntok) load_v(tl, vn);
+    for (int j0 = tl; j0 < ntok; j0 += 64) {
+      half8 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = vn[u];
+      if (j0 + 64 < ntok) load_v(j0 + 64, vn);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int j = j0 + 16 * u;
@@ -956,8 +977,8 @@ int jkv_decode_attention_window(const void* q, int64_t q_stride_b, int64_t q_str
   a.window = window;
   a.rope = (const _Float16*)rope_table;
   a.rope_len = rope_len;
-  a.n_splits = (int32_t)ceil_div(window, kSplitTokens);
-  a.split_tokens = kSplitTokens;
+  a.n_splits = (int32_t)ceil_div(window, kWinSplitTokens);  // within the queried workspace
+  a.split_tokens = kWinSplitTokens;
   a.ws_o = (float*)workspace;
   a.ws_ml = a.ws_o + B * QH * a.n_splits * kHeadDim;
   a.out = (_Float16*)out;

@@ -7,7 +7,7 @@ attention over packed code caches.  All device work runs in the hand-written
 HIP kernels of ``libjkv.so``; there is no CPU fallback.
 """
 
-from . import _lib
+from . import _lib, artifacts
 from .attention import (
     DecodedWindowCache,
     PackedCodeCache,
@@ -38,6 +38,7 @@ from .packed_nested import pack_fixed_width, unpack_fixed_width
 from .uniform_depth_tac import ClosedLoopUniformResidualVQ
 
 __all__ = [
+    "artifacts",
     "CacheGeometry",
     "ClosedLoopGroupedCQ",
     "ClosedLoopUniformResidualVQ",

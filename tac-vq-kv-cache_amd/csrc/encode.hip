@@ -37,6 +37,67 @@ __global__ void selector_tables_kernel(const float* __restrict__ tables,
   sel[idx] = acc;
 }
 
+// The same tables for d = 128, tiled: one 256-thread block per (p, s, 64
+// codewords) holds W^T (64 KiB) and the codewords transposed (32 KiB) in LDS;
+// thread (tx, ty) accumulates outputs i = 8tx..8tx+7 of codewords
+// k = 4ty..4ty+3 over e in order, so every value equals the one-thread-per-
+// output kernel's bit for bit.
+__global__ __launch_bounds__(256) void selector_tables128_kernel(const float* __restrict__ tables,
+                                                                 const float* __restrict__ whiteners,
+                                                                 float* __restrict__ sel, int64_t S) {
+  constexpr int kD = 128, kKTile = 64;
+  extern __shared__ __align__(16) float sm[];
+  float* wt = sm;              // [e][i]
+  float* ct = sm + kD * kD;    // [e][k]
+  const int64_t blk = blockIdx.x;
+  const int64_t ps = blk / (256 / kKTile);  // (p, s)
+  const int k0 = (int)(blk % (256 / kKTile)) * kKTile;
+  const int64_t p = ps / S;
+  const int tid = threadIdx.x;
+  const float* wsrc = whiteners + p * kD * kD;
+  for (int idx = tid; idx < kD * kD / 4; idx += 256) {
+    const int i = idx / (kD / 4), e4 = (idx % (kD / 4)) * 4;
+    const float4 v = *(const float4*)(wsrc + i * kD + e4);
+    wt[(e4 + 0) * kD + i] = v.x;
+    wt[(e4 + 1) * kD + i] = v.y;
+    wt[(e4 + 2) * kD + i] = v.z;
+    wt[(e4 + 3) * kD + i] = v.w;
+  }
+  const float* csrc = tables + (ps * 256 + k0) * kD;
+  for (int idx = tid; idx < kKTile * kD / 4; idx += 256) {
+    const int k = idx / (kD / 4), e4 = (idx % (kD / 4)) * 4;
+    const float4 v = *(const float4*)(csrc + k * kD + e4);
+    ct[(e4 + 0) * kKTile + k] = deploy16(v.x);
+    ct[(e4 + 1) * kKTile + k] = deploy16(v.y);
+    ct[(e4 + 2) * kKTile + k] = deploy16(v.z);
+    ct[(e4 + 3) * kKTile + k] = deploy16(v.w);
+  }
+  __syncthreads();
+  const int tx = tid & 15, ty = tid >> 4;
+  float acc[4][8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[j][u] = 0.f;
+  for (int e = 0; e < kD; ++e) {
+    const float4 c4 = *(const float4*)(ct + e * kKTile + 4 * ty);
+    const float4 w0 = *(const float4*)(wt + e * kD + 8 * tx);
+    const float4 w1 = *(const float4*)(wt + e * kD + 8 * tx + 4);
+    const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[j][u] = fmaf(cv[j], wv[u], acc[j][u]);
+  }
+  float* dst = sel + (ps * 256 + k0 + 4 * ty) * kD + 8 * tx;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    *(float4*)(dst + j * kD) = float4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+    *(float4*)(dst + j * kD + 4) = float4{acc[j][4], acc[j][5], acc[j][6], acc[j][7]};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Generic fp32 kernel.
 template <int DT, int DMAX>
@@ -649,8 +710,14 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
                   "whitened encode needs %lld bytes of workspace", (long long)need);
     float* sel = (float*)workspace;
     int64_t n = H * G * S * K * d;
-    hipLaunchKernelGGL(selector_tables_kernel, dim3((uint32_t)ceil_div(n, 256)), dim3(256), 0,
-                       stream, tables, whiteners, sel, H * G, S, K, d);
+    if (d == 128 && K == 256 && ((uintptr_t)tables) % 16 == 0 && ((uintptr_t)whiteners) % 16 == 0 &&
+        ((uintptr_t)sel) % 16 == 0) {
+      hipLaunchKernelGGL(selector_tables128_kernel, dim3((uint32_t)(H * G * S * 4)), dim3(256),
+                         (128 * 128 + 128 * 64) * sizeof(float), stream, tables, whiteners, sel, S);
+    } else {
+      hipLaunchKernelGGL(selector_tables_kernel, dim3((uint32_t)ceil_div(n, 256)), dim3(256), 0,
+                         stream, tables, whiteners, sel, H * G, S, K, d);
+    }
     JKV_CHECK_LAUNCH();
     a.sel_tables = sel;
   }

@@ -150,6 +150,22 @@ def test_whitened_search(device, seed):
     assert_codes(c[..., None], r_c[..., None], e1[..., None], e2[..., None], agreement=0.99)
 
 
+def test_whitened_search_full_vector(device):
+    # d = 128 assignment whitener (upper triangular, as GSRQ fitting leaves
+    # it): selector tables come from the tiled d = 128 kernel
+    gen = _gen(43)
+    sig = (1.0, 0.8, 0.64, 0.512)
+    states = ref.synthetic_states(gen, 1, 2, 96, 128)
+    tables = ref.synthetic_tables(gen, (2, 4, 256, 128), sig, stage_axis=1)
+    w = torch.triu(torch.randn(2, 128, 128, generator=gen) * 0.1) + torch.eye(128)
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=(2, 4),
+                                              assignment_whiteners=w.to(device))
+    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=(2, 4),
+                                                          assignment_whiteners=w, return_margins=True)
+    res = assert_codes(codes, r_codes, d1, d2, agreement=0.99)
+    assert_recon_rows(exits[4].cpu(), r_exits[4].detach(), res["prefix_ok"])
+
+
 def test_edge_cases_empty_ragged_and_ties(device):
     tables = torch.randn(2, 2, 256, 8)
     # empty token axis

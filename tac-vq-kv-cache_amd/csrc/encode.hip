@@ -663,8 +663,9 @@ extern "C" {
 
 int64_t jkv_rvq_encode_workspace_bytes(int64_t H, int64_t G, int64_t S, int64_t K,
                                        int64_t d, int32_t has_whitener) {
-  if (has_whitener) return H * G * S * K * d * (int64_t)sizeof(float);
-  if (d == 128 && K == 256 && S >= 1 && S <= 32) return jkv::full_workspace_bytes(H * G, S);
+  const bool full = d == 128 && K == 256 && S >= 1 && S <= 32;
+  if (has_whitener) return full ? jkv::full_wh_workspace_bytes(H * G, S) : H * G * S * K * d * (int64_t)sizeof(float);
+  if (full) return jkv::full_workspace_bytes(H * G, S);
   return 0;
 }
 
@@ -704,24 +705,6 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
     a.recon[e] = recon ? recon[e] : nullptr;
   }
 
-  if (whiteners != nullptr) {
-    int64_t need = jkv_rvq_encode_workspace_bytes(H, G, S, K, d, 1);
-    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                  "whitened encode needs %lld bytes of workspace", (long long)need);
-    float* sel = (float*)workspace;
-    int64_t n = H * G * S * K * d;
-    if (d == 128 && K == 256 && ((uintptr_t)tables) % 16 == 0 && ((uintptr_t)whiteners) % 16 == 0 &&
-        ((uintptr_t)sel) % 16 == 0) {
-      hipLaunchKernelGGL(selector_tables128_kernel, dim3((uint32_t)(H * G * S * 4)), dim3(256),
-                         (128 * 128 + 128 * 64) * sizeof(float), stream, tables, whiteners, sel, S);
-    } else {
-      hipLaunchKernelGGL(selector_tables_kernel, dim3((uint32_t)ceil_div(n, 256)), dim3(256), 0,
-                         stream, tables, whiteners, sel, H * G, S, K, d);
-    }
-    JKV_CHECK_LAUNCH();
-    a.sel_tables = sel;
-  }
-
   const bool aligned16 = (((uintptr_t)states) % 16 == 0) && stride_b % 8 == 0 &&
                          stride_h % 8 == 0 && stride_t % 8 == 0;
   const bool codes_aligned = (S == 1) || ((((uintptr_t)codes) % 2 == 0) && code_stride_b % 2 == 0 &&
@@ -751,12 +734,34 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
     if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
     return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);
   }
-  // full-vector codebooks on MFMA (fp16-deployed tables in the workspace)
-  const bool full = states_dtype == JKV_F16 && whiteners == nullptr && d == 128 && K == 256 &&
-                    S <= 32 && aligned16 && recon_aligned && distinct_exits && workspace != nullptr &&
-                    workspace_bytes >= full_workspace_bytes(H * G, S) &&
-                    ((uintptr_t)workspace) % 16 == 0;
+  // full-vector codebooks on MFMA (fp16-deployed tables in the workspace),
+  // plain or whitened
+  const bool full = states_dtype == JKV_F16 && d == 128 && K == 256 && S <= 32 && aligned16 &&
+                    recon_aligned && distinct_exits && workspace != nullptr &&
+                    ((uintptr_t)workspace) % 16 == 0 &&
+                    (whiteners == nullptr
+                         ? workspace_bytes >= full_workspace_bytes(H * G, S)
+                         : workspace_bytes >= full_wh_workspace_bytes(H * G, S) && ((uintptr_t)whiteners) % 16 == 0);
   if (full) return launch_full(a, workspace, stream);
+  if (whiteners != nullptr) {
+    int64_t need = jkv_rvq_encode_workspace_bytes(H, G, S, K, d, 1);
+    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "whitened encode needs %lld bytes of workspace", (long long)need);
+    float* sel = (float*)workspace;
+    int64_t n = H * G * S * K * d;
+    if (d == 128 && K == 256 && ((uintptr_t)tables) % 16 == 0 && ((uintptr_t)whiteners) % 16 == 0 &&
+        ((uintptr_t)sel) % 16 == 0) {
+      hipLaunchKernelGGL(selector_tables128_kernel, dim3((uint32_t)(H * G * S * 4)), dim3(256),
+                         (128 * 128 + 128 * 64) * sizeof(float), stream, tables, whiteners, sel, S);
+    } else {
+      hipLaunchKernelGGL(selector_tables_kernel, dim3((uint32_t)ceil_div(n, 256)), dim3(256), 0,
+                         stream, tables, whiteners, sel, H * G, S, K, d);
+    }
+    JKV_CHECK_LAUNCH();
+    a.sel_tables = sel;
+  }
+
+
   switch (states_dtype) {
     case JKV_F16: return launch_generic<JKV_F16>(a, stream);
     case JKV_BF16: return launch_generic<JKV_BF16>(a, stream);

@@ -20,8 +20,10 @@ struct EncodeArgs {
 };
 
 // Full-vector residual VQ (d = 128, K = 256) on MFMA: workspace it needs for
-// P problems of S stages, whether a call can take it, and its launch.
+// P problems of S stages (without and with an assignment whitener) and its
+// launch (whitened when a.whiteners is set).
 int64_t full_workspace_bytes(int64_t P, int64_t S);
+int64_t full_wh_workspace_bytes(int64_t P, int64_t S);  // with an assignment whitener
 int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream);
 
 }  // namespace jkv

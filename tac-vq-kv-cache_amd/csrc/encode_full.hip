@@ -47,6 +47,17 @@ int64_t full_workspace_bytes(int64_t P, int64_t S) {
   return P * S * ((int64_t)kFullTabBytes + kFullK * 4 + 16 * 4);
 }
 
+// Whitened search (selector whitener W per problem, M = W^T W): the same
+// tables plus M c per codeword (fp32, the u update), M in fp32 and M's rows,
+// permuted into the B-operand order, as hi and lo fp16 planes.
+static const int64_t kWhMcBytes = (int64_t)kFullK * kFullD * 4;  // per (problem, stage)
+static const int64_t kWhMBytes = (int64_t)kFullD * kFullD * 4;   // per problem
+static const int64_t kWhPermBytes = kFullTabBytes;               // hi + lo planes per problem
+
+int64_t full_wh_workspace_bytes(int64_t P, int64_t S) {
+  return full_workspace_bytes(P, S) + P * S * kWhMcBytes + P * (kWhMBytes + kWhPermBytes);
+}
+
 // One block per (problem, stage, 16 codewords): lane (codeword ci, chunk q)
 // converts 8 dims, the 16 lanes of a codeword sum its norm, and the block
 // writes the largest |c|^2 of its 16 codewords (the main kernel folds the 16
@@ -80,11 +91,118 @@ __global__ __launch_bounds__(256) void full_tables_kernel(const float* __restric
   if (tid == 0) ncmax_part[ps * 16 + part] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// M = W^T W per problem (one 256-thread block, W in LDS), and M's rows as
+// hi/lo fp16 planes in the order the mat-vec u = M x leaves in the search's
+// B-operand layout: plane row 16c + i holds M row 32(c/2) + 8(i/4) + 4(c%2) +
+// i%4, so output chunk c, lane group lg, element v of the mat-vec is dim
+// 32(c/2) + 8lg + 4(c%2) + v (chunk c/2, word 4(c%2) + v of the lane's
+// B operand).  Hi plane rows 0..127, lo plane rows 128..255.
+__global__ __launch_bounds__(256) void full_whiten_m_kernel(const float* __restrict__ whiteners,
+                                                            float* __restrict__ m_out,
+                                                            _Float16* __restrict__ perm) {
+  extern __shared__ __align__(16) float wsh[];  // W [e][i]
+  const int64_t p = blockIdx.x;
+  const float* w = whiteners + p * kFullD * kFullD;
+  for (int idx = threadIdx.x; idx < kFullD * kFullD; idx += 256) wsh[idx] = w[idx];
+  __syncthreads();
+  float* mp = m_out + p * kFullD * kFullD;
+  _Float16* hi = perm + p * 2 * kFullD * kFullD;
+  _Float16* lo = hi + kFullD * kFullD;
+  for (int idx = threadIdx.x; idx < kFullD * kFullD; idx += 256) {
+    const int i = idx / kFullD, jj = idx % kFullD;
+    float acc = 0.f;
+    for (int e = 0; e < kFullD; ++e) acc = fmaf(wsh[e * kFullD + i], wsh[e * kFullD + jj], acc);
+    mp[idx] = acc;
+  }
+  for (int idx = threadIdx.x; idx < kFullD * kFullD; idx += 256) {
+    const int r = idx / kFullD, col = idx % kFullD;
+    const int c = r >> 4, i = r & 15;
+    const int src = 32 * (c >> 1) + 8 * (i >> 2) + 4 * (c & 1) + (i & 3);
+    // the same sum in the same order as M[src][col] above
+    float v = 0.f;
+    for (int e = 0; e < kFullD; ++e) v = fmaf(wsh[e * kFullD + src], wsh[e * kFullD + col], v);
+    const half_t h = (half_t)v;
+    hi[idx] = h;
+    lo[idx] = (half_t)(v - (float)h);
+  }
+}
+
+// M c for every codeword (fp32, tiled like selector_tables128_kernel: one
+// 256-thread block per (problem, stage, 64 codewords), M^T = M in LDS), the
+// selector norms |W c|^2 = c . M c as the -|c'|^2/2 plane, and four partial
+// maxima of |c'|^2 (the other twelve partial slots are zero).
+__global__ __launch_bounds__(256) void full_whiten_tables_kernel(const _Float16* __restrict__ tab16,
+                                                                 const float* __restrict__ m_all,
+                                                                 float* __restrict__ mc, float* __restrict__ nhalf,
+                                                                 float* __restrict__ ncmax_part, int64_t S) {
+  constexpr int kKTile = 64;
+  extern __shared__ __align__(16) float sm[];
+  float* mt = sm;                    // [e][i] = M[i][e] = M[e][i]
+  float* ct = sm + kFullD * kFullD;  // [e][k]
+  __shared__ float red[4];
+  const int64_t ps = blockIdx.x >> 2;
+  const int part = blockIdx.x & 3;
+  const int k0 = part * kKTile;
+  const int64_t p = ps / S;
+  const int tid = threadIdx.x;
+  const float* msrc = m_all + p * kFullD * kFullD;
+  for (int idx = tid; idx < kFullD * kFullD / 4; idx += 256)
+    *(float4*)(mt + 4 * idx) = *(const float4*)(msrc + 4 * idx);
+  const _Float16* csrc = tab16 + (ps * kFullK + k0) * kFullD;
+  for (int idx = tid; idx < kKTile * kFullD; idx += 256) {
+    const int k = idx / kFullD, e = idx % kFullD;
+    ct[e * kKTile + k] = (float)csrc[k * kFullD + e];
+  }
+  __syncthreads();
+  const int tx = tid & 15, ty = tid >> 4;
+  float acc[4][8];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[jj][u] = 0.f;
+  for (int e = 0; e < kFullD; ++e) {
+    const float4 c4 = *(const float4*)(ct + e * kKTile + 4 * ty);
+    const float4 m0 = *(const float4*)(mt + e * kFullD + 8 * tx);
+    const float4 m1 = *(const float4*)(mt + e * kFullD + 8 * tx + 4);
+    const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+    const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[jj][u] = fmaf(cv[jj], mv[u], acc[jj][u]);
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int k = k0 + 4 * ty + jj;
+    float* dst = mc + (ps * kFullK + k) * kFullD + 8 * tx;
+    *(float4*)dst = float4{acc[jj][0], acc[jj][1], acc[jj][2], acc[jj][3]};
+    *(float4*)(dst + 4) = float4{acc[jj][4], acc[jj][5], acc[jj][6], acc[jj][7]};
+    // |c'|^2 = c . (M c) over this thread's 8 dims, summed over the 16 tx lanes
+    float nc = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) nc = fmaf(ct[(8 * tx + u) * kKTile + 4 * ty + jj], acc[jj][u], nc);
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) nc += __shfl_xor(nc, off, 16);
+    if (tx == 0) nhalf[ps * kFullK + k] = -0.5f * nc;
+    mx = fmaxf(mx, nc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 16; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  if (tid < 4) {
+    ncmax_part[ps * 16 + 4 * part + tid] = tid == 0 ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : 0.f;
+  }
+}
+
 struct FullArgs {
   EncodeArgs e;
   const _Float16* tab16;
   const float* nhalf;
   const float* ncmax;
+  const float* mc;          // whitened: M c per codeword [P][S][256][128]
+  const _Float16* mperm;    // whitened: M's permuted rows, hi and lo planes [P][256][128]
   int64_t row_blocks;  // row blocks per problem
 };
 
@@ -171,7 +289,13 @@ __device__ __forceinline__ uint32_t full_search(const half8* __restrict__ tabA, 
   return best;
 }
 
-template <int NW>
+// WH: assignment in selector space (whitener W, M = W^T W).  Scores use the
+// raw fp16 codewords against u = W^T r' (r' the selector residual), since
+// c' . r' = (W c) . r' = c . u:
+//   u starts at M x, and each stage subtracts M c of its winner;
+//   |r'|^2 starts at x . u and each stage subtracts 2 c . u and adds |c'|^2
+//   (this only sets the row's binade, never the order within the row).
+template <int NW, bool WH>
 __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   const EncodeArgs& a = f.e;
   extern __shared__ __align__(16) unsigned char lds[];  // 2 x (table + -|c|^2/2 plane)
@@ -236,6 +360,16 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   };
 
   dma_stage(0, 0);
+  if constexpr (WH) {
+    // M's permuted hi/lo rows (256 rows, like a stage table) into buffer 1
+    const __amdgpu_buffer_rsrc_t perm_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(f.mperm + (int64_t)p * kFullTabHalves), (short)0, kFullTabBytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < per_wave; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          perm_rsrc, (__attribute__((address_space(3))) void*)(lds + kFullBufBytes + (wave + nw * i) * 1024), 16,
+          lane_off, (uint32_t)(i * nw * 1024), 0, 0);
+  }
   if (tid < S) {
     const float* part = f.ncmax + ((int64_t)p * S + tid) * 16;
     float m = 0.f;
@@ -265,6 +399,35 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   const int64_t Dfull = a.G * kFullD;
   const int64_t out_off = ((b * a.H + h) * a.T + t) * Dfull + g * kFullD;
 
+  // whitened state: u in the B-operand layout (dims 32kk + 8lg + e) and |r'|^2
+  float u[4][8];
+  float rr_sel = 0.f;
+  if constexpr (WH) {
+    // u = M x: output chunk c of 16 permuted rows, lane (lg, i) reads plane
+    // row 16c + i (hi) and 128 + 16c + i (lo); element v lands on dim
+    // 32(c/2) + 8lg + 4(c%2) + v
+    const half8* tabM = (const half8*)(lds + kFullBufBytes);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int q = (4 * kk + lg) ^ j;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(tabM[(16 * c + j) * 16 + q], x[kk], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(tabM[(128 + 16 * c + j) * 16 + q], x[kk], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) u[c >> 1][4 * (c & 1) + v] = acc[v];
+    }
+    float xu = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xu = fmaf((float)x[kk][e], u[kk][e], xu);
+    rr_sel = lane_group_sum_f(xu);
+    __syncthreads();  // every wave is done with M before stage 1's table lands there
+  }
+
   for (int s = 0; s < S; ++s) {
     const int buf = s & 1;
     const bool next = s + 1 < S;
@@ -277,7 +440,17 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
     // ---- B operands of this stage: r = x - dec as r_hi + r_lo, |r|^2 ----
     half8 bh[4], bl[4];
     float rr = 0.f;
-    if (s == 0) {
+    if constexpr (WH) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const half_t hi = (half_t)u[kk][e];
+          bh[kk][e] = hi;
+          bl[kk][e] = (half_t)fmaf((float)hi, -one, u[kk][e]);
+        }
+      }
+    } else if (s == 0) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         bh[kk] = x[kk];
@@ -298,25 +471,55 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
         }
       }
     }
-    rr = lane_group_sum_f(rr);
+    if constexpr (WH) {
+      rr = fmaxf(rr_sel, 0.f);
+    } else {
+      rr = lane_group_sum_f(rr);
+    }
     const float ncm = ncm_s[s];
     const float delta = (rr + ncm) * 0x1p-8f;
     // M = 2^(e+2) for rr + ncm + delta in [2^e, 2^(e+1))
     const float M = __uint_as_float((__float_as_uint(rr + ncm + delta) & 0x7F800000u) + (2u << 23));
     const float bm = (rr + delta) * 0.5f + M;
 
-    const uint32_t best = s == 0 ? full_search<false>(tabA, nhA, bh, bl, bm, lg, j, dma)
-                                 : full_search<true>(tabA, nhA, bh, bl, bm, lg, j, dma);
+    const uint32_t best = (s == 0 && !WH) ? full_search<false>(tabA, nhA, bh, bl, bm, lg, j, dma)
+                                          : full_search<true>(tabA, nhA, bh, bl, bm, lg, j, dma);
     // the row's winner over the four lane groups (lanes j + 16 lg hold row j)
     const uint32_t idx = lane_group_min_u(best | lg4) & 255u;
     if (valid && lg == 0) code_row[s] = (uint8_t)idx;
 
     // ---- dec += C[idx] (fp32, stage order) and the exits at depth s+1 ----
+    float4 mcw[4][2];
+    if constexpr (WH) {
+      // the winner's M c row (dims 32kk + 8lg .. +8), in flight during the rest
+      const float* mrow = f.mc + (((int64_t)p * S + s) * kFullK + idx) * kFullD + 8 * lg;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        mcw[kk][0] = *(const float4*)(mrow + 32 * kk);
+        mcw[kk][1] = *(const float4*)(mrow + 32 * kk + 4);
+      }
+    }
+    float cu = 0.f;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const half8 cw = tabA[idx * 16 + ((4 * kk + lg) ^ (idx & 15))];
 #pragma unroll
       for (int e = 0; e < 8; ++e) dec[kk][e] = fmaf((float)cw[e], one, dec[kk][e]);
+      if constexpr (WH) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cu = fmaf((float)cw[e], u[kk][e], cu);
+      }
+    }
+    if constexpr (WH) {
+      // |r' - c'|^2 = |r'|^2 - 2 c . u + |c'|^2, then u -= M c
+      rr_sel = rr_sel - 2.f * lane_group_sum_f(cu) - 2.f * nhA[idx];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float mv[8] = {mcw[kk][0].x, mcw[kk][0].y, mcw[kk][0].z, mcw[kk][0].w,
+                             mcw[kk][1].x, mcw[kk][1].y, mcw[kk][1].z, mcw[kk][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[kk][e] -= mv[e];
+      }
     }
     if (valid) {
       for (int ex = 0; ex < a.n_exits; ++ex) {
@@ -340,6 +543,7 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
 int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
   const int64_t P = a.H * a.G;
   const int64_t S = a.S;
+  const bool wh = a.whiteners != nullptr;
   unsigned char* ws = (unsigned char*)workspace;
   _Float16* tab16 = (_Float16*)ws;
   float* nhalf = (float*)(ws + P * S * (int64_t)kFullTabBytes);
@@ -354,21 +558,40 @@ int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
   f.tab16 = tab16;
   f.nhalf = nhalf;
   f.ncmax = ncmax;
+  if (wh) {
+    unsigned char* rest = ws + full_workspace_bytes(P, S);
+    float* mc = (float*)rest;
+    float* m_all = (float*)(rest + P * S * kWhMcBytes);
+    _Float16* mperm = (_Float16*)(rest + P * S * kWhMcBytes + P * kWhMBytes);
+    hipLaunchKernelGGL(full_whiten_m_kernel, dim3((uint32_t)P), dim3(256), kFullD * kFullD * sizeof(float), stream,
+                       a.whiteners, m_all, mperm);
+    JKV_CHECK_LAUNCH();
+    // the whitened norms overwrite the raw ones in the plane and the maxima
+    hipLaunchKernelGGL(full_whiten_tables_kernel, dim3((uint32_t)(P * S * 4)), dim3(256),
+                       (kFullD * kFullD + kFullD * 64) * sizeof(float), stream, tab16, m_all, mc, nhalf, ncmax, S);
+    JKV_CHECK_LAUNCH();
+    f.mc = mc;
+    f.mperm = mperm;
+  }
   // waves per workgroup: 8 (128 rows) unless that leaves the chip short of
   // workgroups; each workgroup holds most of a CU's LDS
   const int64_t rows = a.B * a.T;
   int nw = kFullMaxWaves;
   while (nw > 4 && P * ceil_div(rows, 16 * nw) < 256) nw >>= 1;  // nw in {4, 8}
+  if (wh) nw = 4;  // the whitened state (u) needs the registers of one wave per SIMD
   f.row_blocks = ceil_div(rows, 16 * nw);
   int64_t nblocks = P * f.row_blocks;
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
-  if (nw == 8)
-    hipLaunchKernelGGL(rvq_encode_full_kernel<8>, dim3((uint32_t)nblocks), dim3(64 * 8), 2 * kFullBufBytes,
-                       stream, f);
+  if (wh)
+    hipLaunchKernelGGL((rvq_encode_full_kernel<4, true>), dim3((uint32_t)nblocks), dim3(64 * 4),
+                       2 * kFullBufBytes, stream, f);
+  else if (nw == 8)
+    hipLaunchKernelGGL((rvq_encode_full_kernel<8, false>), dim3((uint32_t)nblocks), dim3(64 * 8),
+                       2 * kFullBufBytes, stream, f);
   else
-    hipLaunchKernelGGL(rvq_encode_full_kernel<4>, dim3((uint32_t)nblocks), dim3(64 * 4), 2 * kFullBufBytes,
-                       stream, f);
+    hipLaunchKernelGGL((rvq_encode_full_kernel<4, false>), dim3((uint32_t)nblocks), dim3(64 * 4),
+                       2 * kFullBufBytes, stream, f);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }

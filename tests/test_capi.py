@@ -66,7 +66,11 @@ def test_workspace_queries():
     assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 0) == 8 * 2 * (256 * 128 * 2 + 256 * 4 + 64)
     assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 33, 256, 128, 0) == 0
     assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 128, 128, 0) == 0
-    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 1) == 8 * 2 * 256 * 128 * 4
+    # whitened full-vector: plus M c per codeword (fp32), M and its hi/lo planes per head
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 1, 2, 256, 128, 1) == (
+        8 * 2 * (256 * 128 * 2 + 256 * 4 + 64) + 8 * 2 * 256 * 128 * 4 + 8 * (128 * 128 * 4 + 256 * 128 * 2))
+    # whitened elsewhere: fp32 selector tables
+    assert lib.jkv_rvq_encode_workspace_bytes(8, 16, 2, 256, 8, 1) == 8 * 16 * 2 * 256 * 8 * 4
     F16, BF16 = _lib.JKV_F16, _lib.JKV_BF16
     bins = 8 * 16 * 2 * 256 * 8  # [H*G,S,K,d] of the config-5 V codebooks
     # one chunk of rows: bins go straight into the gradient

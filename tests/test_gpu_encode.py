@@ -150,20 +150,28 @@ def test_whitened_search(device, seed):
     assert_codes(c[..., None], r_c[..., None], e1[..., None], e2[..., None], agreement=0.99)
 
 
-def test_whitened_search_full_vector(device):
+@pytest.mark.parametrize("heads,tokens,stages,prefixes", [
+    (2, 96, 4, (2, 4)),
+    (2, 300, 16, (1, 8, 16)),
+    (8, 512, 2, (1, 2)),
+])
+def test_whitened_search_full_vector(device, heads, tokens, stages, prefixes):
     # d = 128 assignment whitener (upper triangular, as GSRQ fitting leaves
-    # it): selector tables come from the tiled d = 128 kernel
-    gen = _gen(43)
-    sig = (1.0, 0.8, 0.64, 0.512)
-    states = ref.synthetic_states(gen, 1, 2, 96, 128)
-    tables = ref.synthetic_tables(gen, (2, 4, 256, 128), sig, stage_axis=1)
-    w = torch.triu(torch.randn(2, 128, 128, generator=gen) * 0.1) + torch.eye(128)
-    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=(2, 4),
+    # it): the whitened full-vector MFMA kernel
+    gen = _gen(43 + stages)
+    sig = tuple(0.8 ** s for s in range(stages))
+    states = ref.synthetic_states(gen, 1, heads, tokens, 128)
+    tables = ref.synthetic_tables(gen, (heads, stages, 256, 128), sig, stage_axis=1)
+    w = torch.triu(torch.randn(heads, 128, 128, generator=gen) * 0.1) + torch.eye(128)
+    print(f"whitened full-vector H={heads} T={tokens} S={stages}", flush=True)
+    exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=prefixes,
                                               assignment_whiteners=w.to(device))
-    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=(2, 4),
+    r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=prefixes,
                                                           assignment_whiteners=w, return_margins=True)
-    res = assert_codes(codes, r_codes, d1, d2, agreement=0.99)
-    assert_recon_rows(exits[4].cpu(), r_exits[4].detach(), res["prefix_ok"])
+    assert_codes(codes, r_codes, d1, d2)
+    for depth in prefixes:
+        rows = (codes.cpu().long()[..., :depth] == r_codes.long()[..., :depth]).all(-1)
+        assert_recon_rows(exits[depth].cpu(), r_exits[depth].detach(), rows)
 
 
 def test_edge_cases_empty_ragged_and_ties(device):

@@ -91,44 +91,42 @@ __global__ __launch_bounds__(256) void full_tables_kernel(const float* __restric
   if (tid == 0) ncmax_part[ps * 16 + part] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// M = W^T W per problem (one 256-thread block, W in LDS), and M's rows as
-// hi/lo fp16 planes in the order the mat-vec u = M x leaves in the search's
-// B-operand layout: plane row 16c + i holds M row 32(c/2) + 8(i/4) + 4(c%2) +
-// i%4, so output chunk c, lane group lg, element v of the mat-vec is dim
-// 32(c/2) + 8lg + 4(c%2) + v (chunk c/2, word 4(c%2) + v of the lane's
-// B operand).  Hi plane rows 0..127, lo plane rows 128..255.
+// M = W^T W per problem, and M's rows as hi/lo fp16 planes in the order the
+// mat-vec u = M x leaves in the search's B-operand layout: plane row 16c + i
+// holds M row 32(c/2) + 8(i/4) + 4(c%2) + i%4, so output chunk c, lane group
+// lg, element v of the mat-vec is dim 32(c/2) + 8lg + 4(c%2) + v (chunk c/2,
+// word 4(c%2) + v of the lane's B operand).  Hi plane rows 0..127, lo plane
+// rows 128..255.  One 256-thread block per (problem, 8 plane rows), W in LDS;
+// each block writes the M rows its plane rows come from.
 __global__ __launch_bounds__(256) void full_whiten_m_kernel(const float* __restrict__ whiteners,
                                                             float* __restrict__ m_out,
                                                             _Float16* __restrict__ perm) {
   extern __shared__ __align__(16) float wsh[];  // W [e][i]
-  const int64_t p = blockIdx.x;
+  const int64_t p = blockIdx.x >> 4;
+  const int r0 = (blockIdx.x & 15) * 8;
   const float* w = whiteners + p * kFullD * kFullD;
-  for (int idx = threadIdx.x; idx < kFullD * kFullD; idx += 256) wsh[idx] = w[idx];
+  for (int idx = threadIdx.x; idx < kFullD * kFullD / 4; idx += 256)
+    *(float4*)(wsh + 4 * idx) = *(const float4*)(w + 4 * idx);
   __syncthreads();
   float* mp = m_out + p * kFullD * kFullD;
   _Float16* hi = perm + p * 2 * kFullD * kFullD;
   _Float16* lo = hi + kFullD * kFullD;
-  for (int idx = threadIdx.x; idx < kFullD * kFullD; idx += 256) {
-    const int i = idx / kFullD, jj = idx % kFullD;
-    float acc = 0.f;
-    for (int e = 0; e < kFullD; ++e) acc = fmaf(wsh[e * kFullD + i], wsh[e * kFullD + jj], acc);
-    mp[idx] = acc;
-  }
-  for (int idx = threadIdx.x; idx < kFullD * kFullD; idx += 256) {
-    const int r = idx / kFullD, col = idx % kFullD;
+  for (int idx = threadIdx.x; idx < 8 * kFullD; idx += 256) {
+    const int r = r0 + idx / kFullD, col = idx % kFullD;
     const int c = r >> 4, i = r & 15;
     const int src = 32 * (c >> 1) + 8 * (i >> 2) + 4 * (c & 1) + (i & 3);
-    // the same sum in the same order as M[src][col] above
     float v = 0.f;
     for (int e = 0; e < kFullD; ++e) v = fmaf(wsh[e * kFullD + src], wsh[e * kFullD + col], v);
+    mp[src * kFullD + col] = v;
     const half_t h = (half_t)v;
-    hi[idx] = h;
-    lo[idx] = (half_t)(v - (float)h);
+    hi[r * kFullD + col] = h;
+    lo[r * kFullD + col] = (half_t)(v - (float)h);
   }
 }
 
 // M c for every codeword (fp32, tiled like selector_tables128_kernel: one
-// 256-thread block per (problem, stage, 64 codewords), M^T = M in LDS), the
+// 256-thread block per (problem, stage, 64 codewords), M^T = M in LDS and the
+// fp16 codewords beside it, so two blocks share a CU), the
 // selector norms |W c|^2 = c . M c as the -|c'|^2/2 plane, and four partial
 // maxima of |c'|^2 (the other twelve partial slots are zero).
 __global__ __launch_bounds__(256) void full_whiten_tables_kernel(const _Float16* __restrict__ tab16,
@@ -137,8 +135,8 @@ __global__ __launch_bounds__(256) void full_whiten_tables_kernel(const _Float16*
                                                                  float* __restrict__ ncmax_part, int64_t S) {
   constexpr int kKTile = 64;
   extern __shared__ __align__(16) float sm[];
-  float* mt = sm;                    // [e][i] = M[i][e] = M[e][i]
-  float* ct = sm + kFullD * kFullD;  // [e][k]
+  float* mt = sm;                                  // [e][i] = M[i][e] = M[e][i]
+  _Float16* ct = (_Float16*)(sm + kFullD * kFullD);  // [e][k], fp16 codewords (exact)
   __shared__ float red[4];
   const int64_t ps = blockIdx.x >> 2;
   const int part = blockIdx.x & 3;
@@ -151,7 +149,7 @@ __global__ __launch_bounds__(256) void full_whiten_tables_kernel(const _Float16*
   const _Float16* csrc = tab16 + (ps * kFullK + k0) * kFullD;
   for (int idx = tid; idx < kKTile * kFullD; idx += 256) {
     const int k = idx / kFullD, e = idx % kFullD;
-    ct[e * kKTile + k] = (float)csrc[k * kFullD + e];
+    ct[e * kKTile + k] = csrc[k * kFullD + e];
   }
   __syncthreads();
   const int tx = tid & 15, ty = tid >> 4;
@@ -161,10 +159,10 @@ __global__ __launch_bounds__(256) void full_whiten_tables_kernel(const _Float16*
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[jj][u] = 0.f;
   for (int e = 0; e < kFullD; ++e) {
-    const float4 c4 = *(const float4*)(ct + e * kKTile + 4 * ty);
+    const half4 c4 = *(const half4*)(ct + e * kKTile + 4 * ty);
     const float4 m0 = *(const float4*)(mt + e * kFullD + 8 * tx);
     const float4 m1 = *(const float4*)(mt + e * kFullD + 8 * tx + 4);
-    const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+    const float cv[4] = {(float)c4[0], (float)c4[1], (float)c4[2], (float)c4[3]};
     const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
@@ -181,7 +179,7 @@ __global__ __launch_bounds__(256) void full_whiten_tables_kernel(const _Float16*
     // |c'|^2 = c . (M c) over this thread's 8 dims, summed over the 16 tx lanes
     float nc = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) nc = fmaf(ct[(8 * tx + u) * kKTile + 4 * ty + jj], acc[jj][u], nc);
+    for (int u = 0; u < 8; ++u) nc = fmaf((float)ct[(8 * tx + u) * kKTile + 4 * ty + jj], acc[jj][u], nc);
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) nc += __shfl_xor(nc, off, 16);
     if (tx == 0) nhalf[ps * kFullK + k] = -0.5f * nc;
@@ -563,12 +561,13 @@ int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
     float* mc = (float*)rest;
     float* m_all = (float*)(rest + P * S * kWhMcBytes);
     _Float16* mperm = (_Float16*)(rest + P * S * kWhMcBytes + P * kWhMBytes);
-    hipLaunchKernelGGL(full_whiten_m_kernel, dim3((uint32_t)P), dim3(256), kFullD * kFullD * sizeof(float), stream,
-                       a.whiteners, m_all, mperm);
+    hipLaunchKernelGGL(full_whiten_m_kernel, dim3((uint32_t)(P * 16)), dim3(256), kFullD * kFullD * sizeof(float),
+                       stream, a.whiteners, m_all, mperm);
     JKV_CHECK_LAUNCH();
     // the whitened norms overwrite the raw ones in the plane and the maxima
     hipLaunchKernelGGL(full_whiten_tables_kernel, dim3((uint32_t)(P * S * 4)), dim3(256),
-                       (kFullD * kFullD + kFullD * 64) * sizeof(float), stream, tab16, m_all, mc, nhalf, ncmax, S);
+                       kFullD * kFullD * sizeof(float) + kFullD * 64 * sizeof(_Float16), stream, tab16, m_all, mc,
+                       nhalf, ncmax, S);
     JKV_CHECK_LAUNCH();
     f.mc = mc;
     f.mperm = mperm;

@@ -22,15 +22,17 @@
 // searches with the fp32 residual r = x - dec, carried as r_hi + r_lo (two
 // fp16 words, |r - r_hi - r_lo| <= 2^-22 |r|).  The accumulator starts at
 // -|c_i|^2/2 and gathers c_i.r_hi + c_i.r_lo over 4 + 4 K-steps of 32 dims
-// (stage 1: r = x, 4 steps); one fp32 subtraction then gives
-//   D''[i][j] = c_i.r - |c_i|^2/2 - (|r|^2 + delta)/2 - M = -(|r - c_i|^2 + delta)/2 - M.
-// Near-ties are far more common at d = 128 than at d = 8, so the key keeps the
-// whole mantissa: M is a power of two >= 2 (|r|^2 + max|c|^2 + delta) > 2 max_i
-// (|r - c_i|^2 + delta)/2, which puts every D'' of the row in the one binade
-// (-2M, -M).  Sign and exponent are then common to the row and key =
-// (bits(D'') << 9) | index orders by distance at 2^-23 M, ties to the lowest
-// index.  delta = 2^-8 (|r|^2 + max|c|^2) keeps every D'' below -M; M is a
-// per-row constant and never changes the order.
+// (stage 1: r = x, 4 steps) into a_i = c_i.r - |c_i|^2/2, and the distance
+// is |r|^2 - 2 a_i.  Near-ties are far more common at d = 128 than at d = 8,
+// so the key keeps the whole mantissa: with A >= |c||r| + |c|^2/2 >= |a_i|
+// for every codeword of the stage (max |c|^2 per stage, a 2^-8 margin for
+// rounding) and M a power of two in (2A, 4A], one fp32 subtraction gives
+//   D''[i][j] = a_i - 1.5 M  in the one binade (-2M, -M).
+// Sign and exponent are then common to the row and key = (bits(D'') << 9) |
+// index orders by distance at 2^-23 M, ties to the lowest index.  M is a
+// per-row constant and never changes the order; bounding by |c||r| rather
+// than by |r|^2 keeps the step small where codewords are small next to the
+// residual (the deep stages of a long residual chain).
 #include "encode_args.h"
 
 namespace jkv {
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
 
   // whitened state: u in the B-operand layout (dims 32kk + 8lg + e) and |r'|^2
   float u[4][8];
-  float rr_sel = 0.f;
+  float rr_sel = 0.f, rr0 = 0.f;
   if constexpr (WH) {
     // u = M x: output chunk c of 16 permuted rows, lane (lg, i) reads plane
     // row 16c + i (hi) and 128 + 16c + i (lo); element v lands on dim
@@ -423,6 +425,7 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) xu = fmaf((float)x[kk][e], u[kk][e], xu);
     rr_sel = lane_group_sum_f(xu);
+    rr0 = fmaxf(rr_sel, 0.f);
     __syncthreads();  // every wave is done with M before stage 1's table lands there
   }
 
@@ -470,15 +473,22 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
       }
     }
     if constexpr (WH) {
-      rr = fmaxf(rr_sel, 0.f);
+      // the tracked |r'|^2 drifts by a few fp32 roundings of |x'|^2 per stage:
+      // the bound below takes that much on top
+      rr = fmaxf(rr_sel, 0.f) + rr0 * 0x1p-14f;
     } else {
       rr = lane_group_sum_f(rr);
     }
+    // acc = c . r - |c|^2/2 and |acc| <= |c||r| + |c|^2/2 <= A for every
+    // codeword of the stage.  With M = 2^(e+2) for A (1 + 2^-8) in
+    // [2^e, 2^(e+1)), acc - 1.5 M lies in (-2M, -M), one binade whose
+    // mantissa orders the distances |r|^2 - 2 acc.  Leaving |r|^2 out of the
+    // bound keeps the step at 2^-21 A: at deep stages, where the codewords are
+    // small next to the residual, far finer than 2^-21 |r|^2.
     const float ncm = ncm_s[s];
-    const float delta = (rr + ncm) * 0x1p-8f;
-    // M = 2^(e+2) for rr + ncm + delta in [2^e, 2^(e+1))
-    const float M = __uint_as_float((__float_as_uint(rr + ncm + delta) & 0x7F800000u) + (2u << 23));
-    const float bm = (rr + delta) * 0.5f + M;
+    const float A = (sqrtf(rr * ncm) + 0.5f * ncm) * (1.f + 0x1p-8f);
+    const float M = __uint_as_float((__float_as_uint(A) & 0x7F800000u) + (2u << 23));
+    const float bm = 1.5f * M;
 
     const uint32_t best = (s == 0 && !WH) ? full_search<false>(tabA, nhA, bh, bl, bm, lg, j, dma)
                                           : full_search<true>(tabA, nhA, bh, bl, bm, lg, j, dma);

@@ -8,7 +8,7 @@ import torch
 import jointkv_amd as jkv
 from oracle import jointkv_oracle as ref
 
-from parity import assert_codes, assert_recon_rows
+from parity import assert_codes, assert_codes_with_exact_floor, assert_recon_rows, bruteforce_rvq_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -102,6 +102,7 @@ def test_residual_vq_generic_geometries(device, seed, dtype, dim, stages, cluste
     (1, 300, 2, (1, 2)),
     (2, 77, 4, (2, 4)),
     (1, 40, 16, (1, 8, 16)),
+    (1, 64, 32, (16, 32)),   # R32 (gsrq2): the 32-stage maximum
 ])
 def test_full_vector_residual_vq(device, batch, tokens, stages, prefixes):
     gen = _gen(700 + stages)
@@ -110,7 +111,7 @@ def test_full_vector_residual_vq(device, batch, tokens, stages, prefixes):
     print(f"full-vector encode B={batch} T={tokens} S={stages}", flush=True)
     exits, codes = jkv.hard_residual_vq_exits(states.to(device), tables.to(device), prefixes=prefixes)
     r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=prefixes, return_margins=True)
-    assert_codes(codes, r_codes, d1, d2)
+    assert_codes_with_exact_floor(codes, r_codes, d1, d2, *bruteforce_rvq_codes(states, tables))
     for depth in prefixes:
         rows = (codes.cpu().long()[..., :depth] == r_codes.long()[..., :depth]).all(-1)
         assert_recon_rows(exits[depth].cpu(), r_exits[depth].detach(), rows)
@@ -154,6 +155,7 @@ def test_whitened_search(device, seed):
     (2, 96, 4, (2, 4)),
     (2, 300, 16, (1, 8, 16)),
     (8, 512, 2, (1, 2)),
+    (2, 48, 32, (32,)),
 ])
 def test_whitened_search_full_vector(device, heads, tokens, stages, prefixes):
     # d = 128 assignment whitener (upper triangular, as GSRQ fitting leaves
@@ -168,7 +170,7 @@ def test_whitened_search_full_vector(device, heads, tokens, stages, prefixes):
                                               assignment_whiteners=w.to(device))
     r_exits, r_codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=prefixes,
                                                           assignment_whiteners=w, return_margins=True)
-    assert_codes(codes, r_codes, d1, d2)
+    assert_codes_with_exact_floor(codes, r_codes, d1, d2, *bruteforce_rvq_codes(states, tables, w))
     for depth in prefixes:
         rows = (codes.cpu().long()[..., :depth] == r_codes.long()[..., :depth]).all(-1)
         assert_recon_rows(exits[depth].cpu(), r_exits[depth].detach(), rows)

@@ -15,6 +15,7 @@ import torch
 
 from oracle import bruteforce as bf
 from oracle import jointkv_oracle as ref
+from parity import assert_codes_with_exact_floor, bruteforce_rvq_codes, compare_codes
 
 
 def _clear(d1: np.ndarray, d2: np.ndarray, margin: float) -> np.ndarray:
@@ -145,6 +146,31 @@ def test_whitened_search_matches_bruteforce_in_selector_space():
         ours = codes[0, h].numpy()
         clear0 = _clear(bd1[:, 0], bd2[:, 0], 1e-5)
         assert np.array_equal(ours[clear0, 0], bcodes[clear0, 0])
+
+
+def test_long_whitened_chain_oracle_flips_only_near_ties():
+    # 32 whitened full-vector stages (sigma 0.8^s): the fp32 oracle agrees with
+    # the float64 search on every code whose float64 margin is clear and flips
+    # only near-ties; this floor is what the device kernels are held to there
+    stages = 32
+    gen = torch.Generator().manual_seed(43 + stages)
+    states = ref.synthetic_states(gen, 1, 2, 48, 128)
+    tables = ref.synthetic_tables(gen, (2, stages, 256, 128), tuple(0.8 ** s for s in range(stages)), stage_axis=1)
+    w = torch.triu(torch.randn(2, 128, 128, generator=gen) * 0.1) + torch.eye(128)
+    _out, codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=(stages,), assignment_whiteners=w,
+                                                     return_margins=True)
+    exact, e1, e2 = bruteforce_rvq_codes(states, tables, w)
+    res = compare_codes(codes, exact, e1, e2)
+    assert res["clear_mismatches"] == 0 and 0.999 < res["agreement"] < 1.0
+    # the float64 search itself passes the floor check; a code moved at a
+    # clear float64 margin fails it
+    assert_codes_with_exact_floor(exact, codes, d1, d2, exact, e1, e2)
+    ratio = (e2 - e1) / e1
+    n = int(torch.nonzero(ratio[0, 0, :, 0] > 1e-2)[0, 0])
+    planted = exact.clone()
+    planted[0, 0, n, 0] = (planted[0, 0, n, 0] + 1) % 256
+    with pytest.raises(AssertionError):
+        assert_codes_with_exact_floor(planted, codes, d1, d2, exact, e1, e2)
 
 
 def test_grouped_residual_fold_matches_per_group_calls():

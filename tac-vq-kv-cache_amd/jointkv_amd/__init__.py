@@ -34,7 +34,20 @@ from .closed_loop_vq import (
     hard_residual_vq_exits,
 )
 from .cq_tac import ClosedLoopGroupedCQ, hard_grouped_cq
-from .packed_nested import pack_fixed_width, unpack_fixed_width
+from .packed_nested import (
+    PackedLayoutLedger,
+    PackedNestedKVCache,
+    PackedProgressiveStream,
+    estimate_block_shared_paired_progressive_layout,
+    estimate_layered_paired_progressive_layout,
+    estimate_paired_progressive_layout,
+    pack_fixed_width,
+    pack_paired_progressive_indices,
+    unpack_action_depths,
+    unpack_fixed_width,
+    unpack_paired_progressive_indices,
+    validate_packed_nested_cache,
+)
 from .uniform_depth_tac import ClosedLoopUniformResidualVQ
 
 __all__ = [
@@ -44,6 +57,9 @@ __all__ = [
     "ClosedLoopUniformResidualVQ",
     "DecodedWindowCache",
     "PackedCodeCache",
+    "PackedLayoutLedger",
+    "PackedNestedKVCache",
+    "PackedProgressiveStream",
     "QuantizedKV",
     "StorageLedger",
     "clip_codebook_gradients",
@@ -51,18 +67,25 @@ __all__ = [
     "decode_attention_window",
     "deploy_tables",
     "dynamic_bpa",
+    "estimate_block_shared_paired_progressive_layout",
+    "estimate_layered_paired_progressive_layout",
+    "estimate_paired_progressive_layout",
     "frozen_assignment_reconstruction",
     "hard_grouped_cq",
     "hard_grouped_residual_vq",
     "hard_residual_vq_exits",
     "pack_fixed_width",
+    "pack_paired_progressive_indices",
     "prefill_attention",
     "prefill_attention_from_codes",
     "paired_prefix_rates",
     "prefix_index_bits",
     "residual_vq_ledger",
     "sgd_step",
+    "unpack_action_depths",
     "unpack_fixed_width",
+    "unpack_paired_progressive_indices",
+    "validate_packed_nested_cache",
     "validate_stage_bits",
 ]
 

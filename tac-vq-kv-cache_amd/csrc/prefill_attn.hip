@@ -59,6 +59,13 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
+// max(a, b, c) in one instruction; the scores are never NaN
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // (a[e], b[e]) as one 32-bit word
 __device__ __forceinline__ uint32_t pair16(half8 a, half8 b, int e) {
   const half2v h = {a[e], b[e]};
@@ -211,9 +218,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     for (int rg = 0; rg < 2; ++rg) {
       float mx = -INFINITY;
       if (full) {
+        // two new scores per v_max3_f32 (fmaxf chains compile to twice as
+        // many instructions: each MFMA result is canonicalised first)
 #pragma unroll
-        for (int kg = 0; kg < 4; ++kg)
-          mx = fmaxf(fmaxf(mx, fmaxf(s[kg][rg][0], s[kg][rg][1])), fmaxf(s[kg][rg][2], s[kg][rg][3]));
+        for (int kg = 0; kg < 4; ++kg) {
+          mx = max3_f32(mx, s[kg][rg][0], s[kg][rg][1]);
+          mx = max3_f32(mx, s[kg][rg][2], s[kg][rg][3]);
+        }
       } else {
         const int64_t qrow = row0 + 16 * rg + ln;
 #pragma unroll

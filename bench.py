@@ -344,6 +344,58 @@ def vstep_workload(args, device):
     return {"ms_per_step": ms, "steps_per_s": 1e3 / ms}
 
 
+def adapter_workload(args, device):
+    """One decoder layer of the closed-loop attention adapter at config 5's
+    shape (batch 4, 2048 tokens, 8 kv heads; Mistral hidden 4096, 32 query
+    heads): projections, GSRQ-2 encode of K and V, prefill attention with its
+    row normaliser, o_proj, then backward of a synthetic upstream gradient
+    into the value tables (o_proj backward GEMM, HIP value gradient, HIP
+    scatter-add).  Random weights; the value-gradient kernel is also timed
+    alone."""
+
+    import torch
+    import jointkv_amd as jkv
+    from jointkv_amd import _ops
+    from jointkv_amd.closed_loop_attention import AttentionWeights, closed_loop_attention
+
+    batch, tokens, hidden_size, qh = 4, 2048, 4096, 32
+    gen = torch.Generator(device=device).manual_seed(8601)
+    hidden = (torch.randn(batch, tokens, hidden_size, generator=gen, device=device) * 0.5).half()
+    w = [(torch.randn(rows, hidden_size, generator=gen, device=device) / hidden_size ** 0.5).half()
+         for rows in (hidden_size, HEADS * HEAD_DIM, HEADS * HEAD_DIM, hidden_size)]
+    weights = AttentionWeights(*w)
+    shape = (HEADS, GROUPS, STAGES, CLUSTERS, GROUP_DIM)
+    ktab = make_tables(gen, shape, (1.0, 0.5), 2, device)
+    vtab = make_tables(gen, shape, (1.0, 0.5), 2, device)
+    codec = jkv.ClosedLoopUniformResidualVQ([ktab], [vtab], [None], depth=STAGES, dynamic_bpa=2.0).to(device)
+    upstream = (torch.randn(batch, tokens, hidden_size, generator=gen, device=device) * 1e-3 ** 0.5).half()
+
+    def step():
+        codec.value_tables[0].grad = None
+        out = closed_loop_attention(hidden, weights, codec, 0)
+        out.backward(upstream)
+
+    ms = timed(step, max(1, args.steps // 2), 1)
+    # the value-gradient kernel alone
+    q = torch.randn(batch, qh, tokens, HEAD_DIM, generator=gen, device=device).half()
+    k = torch.randn(batch, HEADS, tokens, HEAD_DIM, generator=gen, device=device).half()
+    v = torch.randn(batch, HEADS, tokens, HEAD_DIM, generator=gen, device=device).half()
+    d = torch.randn(batch, qh, tokens, HEAD_DIM, generator=gen, device=device).half()
+    starts = torch.zeros(batch, dtype=torch.int32, device=device)
+    lse = torch.empty(batch, qh, tokens, dtype=torch.float32, device=device)
+    _ops.prefill_attention(q, k, v, starts, window=4096, rope_theta=10000.0, max_position=tokens - 1, lse=lse)
+    launches = [lambda: _ops.prefill_attention_value_grad(q, k, d, lse, starts, window=4096, rope_theta=10000.0,
+                                                          max_position=tokens - 1)] * 8
+    dv_ms = per_launch_ms(launches)
+    flops = 4.0 * batch * qh * HEAD_DIM * tokens * (tokens + 1) / 2  # causal S recompute + Pᵀ dO
+    return {
+        "ms_per_layer_step": ms,
+        "value_grad_us": dv_ms * 1e3,
+        "value_grad_tflops": flops / (dv_ms / 1e3) / 1e12,
+        "value_grad_mfma_frac": flops / (dv_ms / 1e3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+    }
+
+
 def cpu_baseline(args):
     """The oracle (eager PyTorch restatement of the reference) on one layer's K
     over a bounded token sample, timed on this host; scaled to tokens/s of the
@@ -385,7 +437,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
-    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,cq2,full,cpu")
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,adapter,cq2,full,cpu")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
@@ -419,6 +471,9 @@ def main() -> int:
     if "vstep" not in skip:
         log("V-only step workload (config 5)")
         extras["v_only_step"] = vstep_workload(args, device)
+    if "adapter" not in skip:
+        log("closed-loop attention layer step (config 5 shape)")
+        extras["closed_loop_attention"] = adapter_workload(args, device)
     cpu = None
     if "cpu" not in skip:
         log("cpu baseline")

@@ -213,6 +213,9 @@ int jkv_decode_attention_window(const void* q, int64_t q_stride_b,
  *   start_positions  [B] int32 device
  *   rope_table  jkv_rope_table() output, rope_len > max position
  *   out      [B,QH,T,128] fp16 contiguous
+ *   lse      [B,QH,T] fp32 contiguous or NULL: each row's log-sum-exp of
+ *            its visible scores q.k/sqrt(128) (natural log), what the
+ *            backward jkv_prefill_attention_value_grad recomputes P from
  * Strides must be multiples of 8 elements and buffers 16-byte aligned.
  */
 int jkv_prefill_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -224,7 +227,34 @@ int jkv_prefill_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int64_t KVH, int64_t T, int64_t D,
                           const int32_t* start_positions, int64_t window,
                           const void* rope_table, int64_t rope_len, void* out,
-                          jkv_stream_t stream);
+                          float* lse, jkv_stream_t stream);
+
+/*
+ * Value gradient of jkv_prefill_attention: for every key s of the chunk,
+ *   d_value[b,kvh,s,:] = sum over the kv head's query heads h and rows t of
+ *                        P[b,h,t,s] * d_out[b,h,t,:]
+ * with P = exp(RoPE(q).RoPE(K̂) / sqrt(128) - lse[b,h,t]) under the same
+ * causal sliding-window mask.  The value leg of the SDPA backward that the
+ * reference's V-only calibration step runs (loss.backward() through the
+ * closed-loop attention of experiments/train_full_model_closed_loop_vq.py:
+ * 277-304, step at experiments_followup_mistral/train_mistral_v_only.py:
+ * 142-150); K tables and backbone are frozen there, so no query or key
+ * gradient is formed.
+ *   q, k     as for jkv_prefill_attention (pre-RoPE fp16)
+ *   d_out    [B,QH,T,128] fp16 gradient of the attention output
+ *   lse      [B,QH,T] fp32 from jkv_prefill_attention
+ *   d_value  [B,KVH,T,128] fp32 contiguous (written, not accumulated)
+ * QH / KVH must be 1, 2, 4 or 8.  Deterministic: the heads' partial sums are
+ * added in head order.
+ */
+int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                     int64_t q_stride_t, const void* k, int64_t k_stride_b,
+                                     int64_t k_stride_h, int64_t k_stride_t, const void* d_out,
+                                     int64_t d_stride_b, int64_t d_stride_h, int64_t d_stride_t,
+                                     const float* lse, int64_t B, int64_t QH, int64_t KVH, int64_t T,
+                                     int64_t D, const int32_t* start_positions, int64_t window,
+                                     const void* rope_table, int64_t rope_len, float* d_value,
+                                     jkv_stream_t stream);
 
 /*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of

@@ -471,6 +471,112 @@ def prefill_attention(
     return torch.cat(outs, dim=0)
 
 
+def _rotated_chunk(q, key_hat, start, window, theta, b):
+    tokens, head_dim = int(q.shape[2]), int(q.shape[3])
+    pos = torch.arange(tokens) + int(start)
+    c, s = rotary_cos_sin(pos, head_dim, theta)
+    qr = apply_rotary(q[b : b + 1], c[None, None], s[None, None])
+    kr = apply_rotary(key_hat[b : b + 1], c[None, None], s[None, None])
+    return qr, kr.repeat_interleave(q.shape[1] // key_hat.shape[1], dim=1), sliding_causal_mask(tokens, window)
+
+
+def prefill_lse(
+    q: torch.Tensor,
+    key_hat: torch.Tensor,
+    start_positions: Sequence[int],
+    *,
+    window: int = 4096,
+    theta: float = 10000.0,
+) -> torch.Tensor:
+    """Each row's natural log-sum-exp of its visible scores
+    RoPE(q).RoPE(K̂)/sqrt(D), fp32 on the fp16-rotated operands: the row
+    normaliser of :func:`prefill_attention`'s softmax.  [B,QH,T] fp32."""
+
+    out = []
+    for b in range(q.shape[0]):
+        qr, kr, mask = _rotated_chunk(q, key_hat, start_positions[b], window, theta, b)
+        scores = (qr.float() @ kr.float().transpose(-1, -2)) / math.sqrt(q.shape[-1])
+        out.append(torch.logsumexp(scores.masked_fill(~mask, float("-inf")), dim=-1))
+    return torch.cat(out, dim=0)
+
+
+def prefill_value_grad(
+    q: torch.Tensor,
+    key_hat: torch.Tensor,
+    value_hat: torch.Tensor,
+    d_out: torch.Tensor,
+    start_positions: Sequence[int],
+    *,
+    window: int = 4096,
+    theta: float = 10000.0,
+) -> torch.Tensor:
+    """dL/dV̂ of :func:`prefill_attention` for the output gradient ``d_out``
+    ([B,QH,T,D]): autograd through ``repeat_kv`` and SDPA in fp32, the value
+    leg of what the reference's ``loss.backward()`` forms through its
+    closed-loop attention (train_full_model_closed_loop_vq.py:277-304).
+    Returns fp32 [B,KVH,T,D]."""
+
+    grads = []
+    for b in range(q.shape[0]):
+        qr, kr, mask = _rotated_chunk(q, key_hat, start_positions[b], window, theta, b)
+        v = value_hat[b : b + 1].float().requires_grad_(True)
+        vr = v.repeat_interleave(q.shape[1] // key_hat.shape[1], dim=1)
+        out = F.scaled_dot_product_attention(qr.float(), kr.float(), vr, attn_mask=mask, dropout_p=0.0)
+        out.backward(d_out[b : b + 1].float())
+        grads.append(v.grad)
+    return torch.cat(grads, dim=0)
+
+
+def closed_loop_attention_value_step(
+    hidden: torch.Tensor,
+    weights: dict,
+    key_tables: torch.Tensor,
+    value_tables: torch.Tensor,
+    d_projected: torch.Tensor,
+    *,
+    depth: int,
+    key_whitener: torch.Tensor | None = None,
+    window: int = 4096,
+    theta: float = 10000.0,
+    head_dim: int = 128,
+):
+    """One layer of install_closed_loop_attention
+    (train_full_model_closed_loop_vq.py:219-337) followed by backward of a
+    given upstream gradient, as the V-only step runs it
+    (train_mistral_v_only.py:142-150): fp16 projections (fp32 accumulate,
+    one rounding), the codec's greedy residual VQ on raw K and V (K tables
+    frozen), RoPE, repeat_kv, masked SDPA, o_proj, then backward of
+    ``d_projected``.  Returns (projected fp16 [B,T,hidden], dL/d value tables
+    fp32 [KVH,S,K,D])."""
+
+    batch, tokens, _ = map(int, hidden.shape)
+    h32 = hidden.float()
+
+    def proj(w):
+        return (h32 @ w.float().T).half()
+
+    qh = weights["q"].shape[0] // head_dim
+    kvh = weights["k"].shape[0] // head_dim
+    query = proj(weights["q"]).view(batch, tokens, qh, head_dim).transpose(1, 2)
+    raw_key = proj(weights["k"]).view(batch, tokens, kvh, head_dim).transpose(1, 2)
+    raw_value = proj(weights["v"]).view(batch, tokens, kvh, head_dim).transpose(1, 2)
+    vt = value_tables.detach().clone().requires_grad_(True)
+    k_exits, _ = hard_residual_vq_exits(raw_key, key_tables.detach(), prefixes=(depth,),
+                                        assignment_whiteners=key_whitener)
+    v_exits, _ = hard_residual_vq_exits(raw_value, vt, prefixes=(depth,))
+    khat, vhat = k_exits[depth].detach(), v_exits[depth]
+    outs = []
+    for b in range(batch):
+        qr, kr, mask = _rotated_chunk(query, khat, 0, window, theta, b)
+        vr = vhat[b : b + 1].repeat_interleave(qh // kvh, dim=1)
+        att = F.scaled_dot_product_attention(qr.float(), kr.float(), vr.float(), attn_mask=mask, dropout_p=0.0)
+        outs.append(att.to(torch.float16))
+    out = torch.cat(outs, dim=0).transpose(1, 2).reshape(batch, tokens, qh * head_dim)
+    projected = out.float() @ weights["o"].float().T
+    projected.backward(d_projected.float())
+    return projected.detach().half(), vt.grad
+
+
 def attention_fp64(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
     """Textbook softmax(q k^T / sqrt(D)) v in fp64 (pin for the SDPA leg)."""
 

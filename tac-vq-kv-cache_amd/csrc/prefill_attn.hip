@@ -43,6 +43,7 @@ struct PrefillArgs {
   const _Float16* rope;  // [rope_len][2][64]: cos row, sin row
   int64_t rope_len;
   _Float16* out;  // [B,QH,T,D] contiguous
+  float* lse;     // [B,QH,T] natural-log row normaliser, or null
   int32_t heads_per_wg;  // HW: query heads per workgroup (min(NQ, 4))
   int32_t row_sets;      // 8 / HW: 32-row sets per head in a workgroup
   int32_t head_groups;   // NQ / HW
@@ -294,6 +295,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     const int64_t row = row0 + 16 * rg + ln;
     const float lt = lane_group_sum(l[rg]);
     if (row >= a.T) continue;
+    if (a.lse != nullptr && lg == 0) {
+      // log sum_s exp(q.k_s / sqrt(D)) = ln2 (m + log2 l), m in base-2 units
+      const float mu = m[rg] == -INFINITY ? 0.f : m[rg];
+      a.lse[(b * a.QH + head) * a.T + row] = (mu + log2f(lt)) * 0.6931471805599453f;
+    }
     const float inv = 1.0f / lt;
     _Float16* op = a.out + ((b * a.QH + head) * a.T + row) * kPD;
 #pragma unroll
@@ -314,7 +320,7 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                           int64_t k_sb, int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb,
                           int64_t v_sh, int64_t v_st, int64_t B, int64_t QH, int64_t KVH,
                           int64_t T, int64_t D, const int32_t* start_positions, int64_t window,
-                          const void* rope_table, int64_t rope_len, void* out,
+                          const void* rope_table, int64_t rope_len, void* out, float* lse,
                           jkv_stream_t stream_) {
   using namespace jkv;
   hipStream_t stream = (hipStream_t)stream_;
@@ -342,6 +348,7 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   a.rope = (const _Float16*)rope_table;
   a.rope_len = rope_len;
   a.out = (_Float16*)out;
+  a.lse = lse;
   a.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
   a.row_sets = 8 / a.heads_per_wg;
   a.head_groups = (int32_t)(NQ / a.heads_per_wg);

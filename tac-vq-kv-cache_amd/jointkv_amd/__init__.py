@@ -27,6 +27,7 @@ from .budget import (
     validate_stage_bits,
 )
 from .calibration import clip_codebook_gradients, sgd_step
+from .closed_loop_attention import AttentionWeights, closed_loop_attention, relative_trajectory_attention_mse
 from .closed_loop_vq import (
     QuantizedKV,
     frozen_assignment_reconstruction,
@@ -51,6 +52,7 @@ from .packed_nested import (
 from .uniform_depth_tac import ClosedLoopUniformResidualVQ
 
 __all__ = [
+    "AttentionWeights",
     "artifacts",
     "CacheGeometry",
     "ClosedLoopGroupedCQ",
@@ -63,6 +65,7 @@ __all__ = [
     "QuantizedKV",
     "StorageLedger",
     "clip_codebook_gradients",
+    "closed_loop_attention",
     "decode_attention",
     "decode_attention_window",
     "deploy_tables",
@@ -80,6 +83,7 @@ __all__ = [
     "prefill_attention_from_codes",
     "paired_prefix_rates",
     "prefix_index_bits",
+    "relative_trajectory_attention_mse",
     "residual_vq_ledger",
     "sgd_step",
     "unpack_action_depths",

@@ -353,6 +353,27 @@ def decode_attention_window(
     return out
 
 
+def _prefill_operands(q, key, value_or_grad, start_positions, what):
+    device = _lib.require_device(q, key, value_or_grad, start_positions)
+    for name, t in (("query", q), ("key", key), (what, value_or_grad)):
+        if t.dtype != torch.float16 or t.ndim != 4 or t.shape[-1] != 128 or t.stride(-1) != 1:
+            raise ValueError(f"prefill {name} must be fp16 [B,H,T,128] with a contiguous last axis")
+    batch, qheads, tokens, _dim = map(int, q.shape)
+    if key.shape[0] != batch or key.shape[2] != tokens:
+        raise ValueError("prefill query/key/value geometry differs")
+    kvheads = int(key.shape[1])
+    if qheads % kvheads:
+        raise ValueError("query heads must be a multiple of kv heads")
+    tensors = []
+    for t in (q, key, value_or_grad):
+        if any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
+            t = t.contiguous()
+        tensors.append(t)
+    if start_positions.dtype != torch.int32 or start_positions.shape != (batch,):
+        raise ValueError("start_positions must be int32 [B]")
+    return device, tensors, start_positions.contiguous(), (batch, qheads, kvheads, tokens)
+
+
 def prefill_attention(
     q: torch.Tensor,
     key: torch.Tensor,
@@ -362,40 +383,65 @@ def prefill_attention(
     window: int,
     rope_theta: float,
     max_position: int,
+    lse: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal sliding-window GQA attention of one prefill chunk.
 
     ``q[B,QH,T,128]``, ``key``/``value`` ``[B,KVH,T,128]`` fp16 pre-RoPE,
     ``start_positions[B]`` int32 (position of each row's first token) and
     ``max_position`` an upper bound of ``start + T - 1`` (sizes the rotary
-    table).  Returns ``[B,QH,T,128]`` fp16.
+    table).  Returns ``[B,QH,T,128]`` fp16.  With ``lse`` (fp32 ``[B,QH,T]``
+    contiguous) each row's log-sum-exp of its visible scores is written there
+    for :func:`prefill_attention_value_grad`.
     """
 
-    device = _lib.require_device(q, key, value, start_positions)
-    for name, t in (("query", q), ("key", key), ("value", value)):
-        if t.dtype != torch.float16 or t.ndim != 4 or t.shape[-1] != 128 or t.stride(-1) != 1:
-            raise ValueError(f"prefill {name} must be fp16 [B,H,T,128] with a contiguous last axis")
-    batch, qheads, tokens, dim = map(int, q.shape)
-    if key.shape != value.shape or key.shape[0] != batch or key.shape[2] != tokens:
+    if key.shape != value.shape:
         raise ValueError("prefill query/key/value geometry differs")
-    kvheads = int(key.shape[1])
-    if qheads % kvheads:
-        raise ValueError("query heads must be a multiple of kv heads")
-    tensors = []
-    for t in (q, key, value):
-        if any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
-            t = t.contiguous()
-        tensors.append(t)
-    q, key, value = tensors
-    if start_positions.dtype != torch.int32 or start_positions.shape != (batch,):
-        raise ValueError("start_positions must be int32 [B]")
-    start_positions = start_positions.contiguous()
+    device, (q, key, value), start_positions, (batch, qheads, kvheads, tokens) = _prefill_operands(
+        q, key, value, start_positions, "value")
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape != (batch, qheads, tokens)
+                            or not lse.is_contiguous() or lse.device != q.device):
+        raise ValueError("lse must be a contiguous fp32 [B,QH,T] tensor on the query's device")
     table = rope_table(device, rope_theta, int(max_position) + 1)
-    out = torch.empty((batch, qheads, tokens, dim), dtype=torch.float16, device=device)
+    out = torch.empty((batch, qheads, tokens, 128), dtype=torch.float16, device=device)
     code = _lib.load().jkv_prefill_attention(
         q.data_ptr(), *q.stride()[:3], key.data_ptr(), *key.stride()[:3], value.data_ptr(),
-        *value.stride()[:3], batch, qheads, kvheads, tokens, dim, start_positions.data_ptr(),
-        int(window), table.data_ptr(), int(table.shape[0]), out.data_ptr(), _lib.stream_handle(device),
+        *value.stride()[:3], batch, qheads, kvheads, tokens, 128, start_positions.data_ptr(),
+        int(window), table.data_ptr(), int(table.shape[0]), out.data_ptr(),
+        lse.data_ptr() if lse is not None else None, _lib.stream_handle(device),
     )
     _lib.check(code)
     return out
+
+
+def prefill_attention_value_grad(
+    q: torch.Tensor,
+    key: torch.Tensor,
+    d_out: torch.Tensor,
+    lse: torch.Tensor,
+    start_positions: torch.Tensor,
+    *,
+    window: int,
+    rope_theta: float,
+    max_position: int,
+) -> torch.Tensor:
+    """Gradient of :func:`prefill_attention` with respect to ``value``:
+    fp32 ``[B,KVH,T,128]`` from ``d_out`` (fp16 ``[B,QH,T,128]``) and the
+    forward's ``lse``."""
+
+    device, (q, key, d_out), start_positions, (batch, qheads, kvheads, tokens) = _prefill_operands(
+        q, key, d_out, start_positions, "output gradient")
+    if d_out.shape != q.shape:
+        raise ValueError("the output gradient must have the query's shape")
+    if lse.dtype != torch.float32 or lse.shape != (batch, qheads, tokens) or not lse.is_contiguous():
+        raise ValueError("lse must be a contiguous fp32 [B,QH,T] tensor")
+    table = rope_table(device, rope_theta, int(max_position) + 1)
+    d_value = torch.empty((batch, kvheads, tokens, 128), dtype=torch.float32, device=device)
+    code = _lib.load().jkv_prefill_attention_value_grad(
+        q.data_ptr(), *q.stride()[:3], key.data_ptr(), *key.stride()[:3], d_out.data_ptr(),
+        *d_out.stride()[:3], lse.data_ptr(), batch, qheads, kvheads, tokens, 128,
+        start_positions.data_ptr(), int(window), table.data_ptr(), int(table.shape[0]),
+        d_value.data_ptr(), _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return d_value

@@ -145,8 +145,39 @@ def prefill_attention(
 
     batch, _qh, tokens, _d = map(int, query.shape)
     starts, top = _start_tensor(start_positions, batch, tokens, query.device)
+    if torch.is_grad_enabled() and (query.requires_grad or key.requires_grad):
+        raise NotImplementedError(
+            "prefill attention differentiates only with respect to value (the V-only step freezes "
+            "the backbone and the K tables); detach query and key")
+    if torch.is_grad_enabled() and value.requires_grad:
+        return _PrefillAttention.apply(query, key, value, starts, window, rope_theta, top)
     return _ops.prefill_attention(query, key, value, starts, window=window, rope_theta=rope_theta,
                                   max_position=top)
+
+
+class _PrefillAttention(torch.autograd.Function):
+    """Prefill attention whose backward is the value leg of the SDPA
+    backward (HIP): the forward keeps each row's log-sum-exp, the backward
+    recomputes P from it and forms dV̂ = Pᵀ dO summed over the GQA group."""
+
+    @staticmethod
+    def forward(ctx, query, key, value, starts, window, rope_theta, top):
+        batch, qheads, tokens, _d = map(int, query.shape)
+        lse = torch.empty((batch, qheads, tokens), dtype=torch.float32, device=query.device)
+        out = _ops.prefill_attention(query, key, value, starts, window=window, rope_theta=rope_theta,
+                                     max_position=top, lse=lse)
+        ctx.save_for_backward(query, key, lse, starts)
+        ctx.params = (window, rope_theta, top, value.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        query, key, lse, starts = ctx.saved_tensors
+        window, rope_theta, top, dtype = ctx.params
+        d_value = _ops.prefill_attention_value_grad(query, key, d_out.to(torch.float16), lse, starts,
+                                                    window=window, rope_theta=rope_theta, max_position=top)
+        # the value's dtype, as SDPA's backward returns it (fp32 sum, one rounding)
+        return None, None, d_value.to(dtype), None, None, None, None
 
 
 def prefill_attention_from_codes(

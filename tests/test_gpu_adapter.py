@@ -1,0 +1,109 @@
+"""Closed-loop attention adapter on the MI355X: the prefill row normaliser,
+its HIP value gradient, and one layer's V-only step against the oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import jointkv_amd as jkv
+from jointkv_amd import _ops
+from jointkv_amd.attention import _start_tensor
+from jointkv_amd.closed_loop_attention import AttentionWeights, closed_loop_attention
+from oracle import jointkv_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+LSE_ATOL = 2e-3      # natural-log row normaliser, fp32 math on fp16 operands
+DV_RTOL = 3e-3       # dV̂ against fp32 autograd: P enters the MFMA as fp16 (2^-11)
+STEP_RTOL = 1e-2     # table gradients after fp16 projections, fp16 dO and fp16 dV̂
+
+
+def _case(seed, batch, qh, kvh, tokens):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, qh, tokens, 128, generator=gen).half()
+    k = torch.randn(batch, kvh, tokens, 128, generator=gen).half()
+    v = torch.randn(batch, kvh, tokens, 128, generator=gen).half()
+    d = torch.randn(batch, qh, tokens, 128, generator=gen).half()
+    return q, k, v, d
+
+
+@pytest.mark.parametrize("batch,qh,kvh,tokens,starts,window", [
+    (1, 32, 8, 200, (0,), 4096),        # Mistral GQA 4, window does not bind
+    (2, 8, 2, 301, (0, 5000), 64),      # window binds; ragged key blocks and row tiles
+    (1, 4, 4, 70, (17,), 4096),         # one query head per kv head
+    (1, 4, 2, 45, (3,), 4096),          # GQA 2
+    (1, 16, 2, 96, (0,), 4096),         # GQA 8
+    (1, 4, 1, 1, (9,), 4096),           # one token
+])
+def test_lse_and_value_grad_match_oracle(device, batch, qh, kvh, tokens, starts, window):
+    print(f"value grad B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)
+    q, k, v, d = _case(900 + tokens, batch, qh, kvh, tokens)
+    qd, kd, vd, dd = (t.to(device) for t in (q, k, v, d))
+    st, top = _start_tensor(list(starts), batch, tokens, qd.device)
+    lse = torch.empty(batch, qh, tokens, dtype=torch.float32, device=device)
+    out = _ops.prefill_attention(qd, kd, vd, st, window=window, rope_theta=10000.0, max_position=top, lse=lse)
+    # the forward is unchanged by asking for lse
+    assert torch.equal(out, jkv.prefill_attention(qd, kd, vd, list(starts), window=window))
+    lse_ref = ref.prefill_lse(q, k, starts, window=window)
+    err = float((lse.cpu() - lse_ref).abs().max())
+    assert err <= LSE_ATOL, f"lse max abs error {err}"
+    dv = _ops.prefill_attention_value_grad(qd, kd, dd, lse, st, window=window, rope_theta=10000.0,
+                                           max_position=top)
+    dv_ref = ref.prefill_value_grad(q, k, v, d, starts, window=window)
+    scale = float(dv_ref.abs().max())
+    err = float((dv.cpu() - dv_ref).abs().max())
+    print(f"  lse err {float((lse.cpu() - lse_ref).abs().max()):.2e}  dV err {err:.2e} of {scale:.2e}", flush=True)
+    assert err <= DV_RTOL * scale, f"dV max abs error {err} (scale {scale})"
+    # deterministic: a second call gives the same bits
+    again = _ops.prefill_attention_value_grad(qd, kd, dd, lse, st, window=window, rope_theta=10000.0,
+                                              max_position=top)
+    assert torch.equal(dv, again)
+
+
+def test_autograd_value_path_and_refusals(device):
+    q, k, v, d = _case(31, 1, 8, 2, 64)
+    qd, kd, dd = q.to(device), k.to(device), d.to(device)
+    vd = v.to(device).requires_grad_(True)
+    out = jkv.prefill_attention(qd, kd, vd, 0, window=4096)
+    out.backward(dd)
+    assert vd.grad.dtype == torch.float16
+    dv_ref = ref.prefill_value_grad(q, k, v, d, (0,), window=4096)
+    assert float((vd.grad.cpu().float() - dv_ref).abs().max()) <= DV_RTOL * float(dv_ref.abs().max())
+    with pytest.raises(NotImplementedError, match="value"):
+        jkv.prefill_attention(qd.clone().requires_grad_(True), kd, vd, 0)
+
+
+@pytest.mark.parametrize("tokens,stages,whitened", [(96, 2, False), (150, 4, True)])
+def test_closed_loop_attention_value_step(device, tokens, stages, whitened):
+    # a small decoder layer (4 query heads, 1 kv head, head_dim 128) with
+    # full-vector codebooks; synthetic hidden states and upstream gradient
+    print(f"adapter step T={tokens} S={stages} whitened={whitened}", flush=True)
+    gen = torch.Generator().manual_seed(77 + tokens)
+    hidden_size, kvh = 512, 1
+    hidden = (torch.randn(1, tokens, hidden_size, generator=gen) * 0.5).half()
+    w = {name: (torch.randn(rows, hidden_size, generator=gen) / hidden_size ** 0.5).half()
+         for name, rows in (("q", hidden_size), ("k", 128 * kvh), ("v", 128 * kvh), ("o", hidden_size))}
+    sig = tuple(0.8 ** s for s in range(stages))
+    ktab = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1) * 0.5
+    vtab = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1) * 0.5
+    whitener = (torch.triu(torch.randn(kvh, 128, 128, generator=gen) * 0.05) + torch.eye(128)) if whitened else None
+    d_proj = (torch.randn(1, tokens, hidden_size, generator=gen) * 0.1).half()
+
+    codec = jkv.ClosedLoopUniformResidualVQ([ktab], [vtab], [whitener], depth=stages, dynamic_bpa=1.0).to(device)
+    weights = AttentionWeights(*(w[n].to(device) for n in ("q", "k", "v", "o")))
+    projected, traj = closed_loop_attention(hidden.to(device), weights, codec, 0, trajectory_epsilon=1e-8)
+    projected.backward(d_proj.to(device))
+    grad = codec.value_tables[0].grad
+
+    expect_out, expect_grad = ref.closed_loop_attention_value_step(hidden, w, ktab, vtab, d_proj, depth=stages,
+                                                                   key_whitener=whitener)
+    out_err = float((projected.detach().cpu().float() - expect_out.float()).abs().max())
+    assert out_err <= 2e-3 + 2e-3 * float(expect_out.abs().max()), f"projected max abs error {out_err}"
+    rel = float((grad.cpu() - expect_grad).norm() / expect_grad.norm())
+    print(f"  projected err {out_err:.2e}  table-grad relative error {rel:.2e}", flush=True)
+    assert rel <= STEP_RTOL, f"value-table gradient relative error {rel}"
+    traj = float(traj.detach())
+    assert traj >= 0.0 and traj == traj
+    # the frozen K tables take no gradient
+    assert codec.key_tables[0].grad is None

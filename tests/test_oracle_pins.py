@@ -272,6 +272,35 @@ def test_synthetic_generator_is_reproducible():
     assert a.dtype == torch.float16 and float(big) < 0.2
 
 
+def test_prefill_lse_and_value_grad_against_fp64_closed_form():
+    # lse: exp(score - lse) over a row's visible keys sums to one and weights
+    # the fp64 rows of the attention oracle; dV̂[kvh, s] = sum over the group's
+    # heads h and rows t of P[h, t, s] dO[h, t] (the grouping, the mask and the
+    # transposition are what a slip here would break)
+    gen = torch.Generator().manual_seed(5)
+    T, window = 37, 9
+    q = torch.randn(2, 4, T, 128, generator=gen).half()
+    k = torch.randn(2, 2, T, 128, generator=gen).half()
+    v = torch.randn(2, 2, T, 128, generator=gen).half()
+    d_out = torch.randn(2, 4, T, 128, generator=gen).half()
+    starts = (0, 300)
+    lse = ref.prefill_lse(q, k, starts, window=window)
+    dv = ref.prefill_value_grad(q, k, v, d_out, starts, window=window)
+    mask = ref.sliding_causal_mask(T, window)
+    for b in range(2):
+        pos = torch.arange(T) + starts[b]
+        c, s = ref.rotary_cos_sin(pos, 128, 10000.0)
+        qr = ref.apply_rotary(q[b], c[None], s[None]).double()
+        kr = ref.apply_rotary(k[b], c[None], s[None]).double()
+        expect = torch.zeros(2, T, 128, dtype=torch.float64)
+        for hq in range(4):
+            scores = qr[hq] @ kr[hq // 2].T / math.sqrt(128)
+            p = torch.exp(scores - lse[b, hq].double()[:, None]) * mask
+            np.testing.assert_allclose(p.sum(-1).numpy(), 1.0, rtol=1e-5)
+            expect[hq // 2] += p.T @ d_out[b, hq].double()
+        np.testing.assert_allclose(dv[b].double().numpy(), expect.numpy(), rtol=1e-4, atol=1e-5)
+
+
 def test_prefill_oracle_against_fp64_rows_and_masks():
     # the window mask equals torch's is_causal when it does not bind, and each
     # output row equals fp64 textbook attention over its visible keys

@@ -244,8 +244,12 @@ int jkv_prefill_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *   d_out    [B,QH,T,128] fp16 gradient of the attention output
  *   lse      [B,QH,T] fp32 from jkv_prefill_attention
  *   d_value  [B,KVH,T,128] fp32 contiguous (written, not accumulated)
- * QH / KVH must be 1, 2, 4 or 8.  Deterministic: the heads' partial sums are
- * added in head order.
+ *   workspace  jkv_prefill_value_grad_workspace_bytes() bytes, 16-byte
+ *            aligned (may be NULL when that is 0): a key block's query rows
+ *            are split into runs that fill the device evenly, each writing
+ *            a partial slot that a second kernel adds up
+ * Deterministic: each key's sum runs over the heads, rows and runs in one
+ * fixed order.
  */
 int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                      int64_t q_stride_t, const void* k, int64_t k_stride_b,
@@ -254,7 +258,11 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
                                      const float* lse, int64_t B, int64_t QH, int64_t KVH, int64_t T,
                                      int64_t D, const int32_t* start_positions, int64_t window,
                                      const void* rope_table, int64_t rope_len, float* d_value,
-                                     jkv_stream_t stream);
+                                     void* workspace, int64_t workspace_bytes, jkv_stream_t stream);
+
+/* Workspace of jkv_prefill_attention_value_grad for this geometry (bytes;
+ * 0 when one run covers every key block's rows). */
+int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T, int64_t window);
 
 /*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of

@@ -9,20 +9,20 @@
 // 142-150 step): the K tables and the backbone are frozen there, so the query
 // and key gradients are not needed for the value tables.
 //
-// One workgroup of NQ waves per (batch row, kv head, block of 32 keys); wave
-// h is query head h of the group.  The block's rotated K̂ stays in registers
-// as MFMA B operands.  Per 32-row query tile, on v_mfma_f32_16x16x32_f16:
-//   S[row][key]    = Q K̂ᵀ          A = the wave's rotated q rows, B = K̂
+// One workgroup of 4 waves per (batch row, kv head, block of 128 keys); wave
+// w owns keys 32w..32w+31 of the block and keeps their rotated K̂ in registers
+// as MFMA B operands and their dV̂ in accumulators.  The workgroup walks
+// (32-row query tile, query head of the group) steps; each step's rotated q
+// rows ([row][dim]), dO transposed ([dim][row]) and lse land in LDS once,
+// double-buffered, and serve all four waves.  Per step and wave, on
+// v_mfma_f32_16x16x32_f16:
+//   S[row][key]    = Q K̂ᵀ      A = q rows from LDS, B = the wave's K̂
 //   P              = exp2(S log2e/sqrt(D) - lse log2e), masked, fp16
-//   dO in B order  = dO I           A = dO rows, B = identity columns: the
-//                                  MFMA output layout is the transpose of its
-//                                  A layout, so lane (dim j) ends up holding
-//                                  rows of dim j; exact, since every product
-//                                  is one fp16 value times 1
-//   dV̂[key][dim] += Pᵀ dO          A = P read straight off the S accumulators
-//                                  (two 16-row tiles interleaved into the 32
-//                                  contraction slots), B = the transposed dO
-// The heads' partial sums meet in LDS and are added in head order.
+//   dV̂[key][dim] += Pᵀ dO      A = P read straight off the S accumulators
+//                              (two 16-row tiles interleaved into the 32
+//                              contraction slots), B = dOᵀ rows from LDS in
+//                              the same slot order
+// Steps where none of a wave's keys is visible skip its arithmetic.
 #include <math.h>
 
 #include "jkv_common.h"
@@ -30,9 +30,14 @@
 
 namespace jkv {
 
-static const int kBD = 128;      // head dim
-static const int kBKeys = 32;    // keys per workgroup
-static const int kBRows = 32;    // query rows per tile
+static const int kBD = 128;            // head dim
+static const int kBKeys = 128;         // keys per workgroup (32 per wave)
+static const int kBRows = 32;          // query rows per step
+static const int kBThreads = 256;      // 4 waves
+static const int kQStride = kBD + 8;   // q tile row stride (halves): 272 B spreads rows over banks
+static const int kDStride = kBRows + 4;  // dOᵀ row stride (halves): 72 B, conflict-free b64 reads
+static const int kQTile = kBRows * kQStride;
+static const int kDTile = kBD * kDStride;
 
 struct ValueGradArgs {
   const _Float16* q;
@@ -47,24 +52,36 @@ struct ValueGradArgs {
   int64_t window;
   const _Float16* rope;
   int64_t rope_len;
-  float* dv;  // [B,KVH,T,D] fp32 contiguous
+  float* dv;  // [B,KVH,T,D] fp32 contiguous, or the chunk's partial slot
+  int32_t nq;
+  int32_t chunk_tiles;  // query tiles per workgroup (a key block's rows are split in chunks)
+  int64_t slot_stride;  // elements between the chunks' partial slots (0: one chunk)
 };
 
-template <int NQ>
-__global__ __launch_bounds__(64 * NQ) void prefill_value_grad_kernel(ValueGradArgs a) {
-  // partial sums of heads 1..NQ-1: [head-1][key][dim] fp32
-  extern __shared__ __align__(16) float part[];
-  const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+// (a[e], b[e]) as one 32-bit word
+__device__ __forceinline__ uint32_t pair_words(half8 a, half8 b, int e) {
+  const half2v h = {a[e], b[e]};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGradArgs a) {
+  __shared__ __align__(16) _Float16 q_lds[2][kQTile];
+  __shared__ __align__(16) _Float16 d_lds[2][kDTile];
+  __shared__ __align__(16) float l_lds[2][kBRows];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
+  const int NQ = a.nq;
   const int64_t nkb = ceil_div(a.T, kBKeys);
   // key blocks fastest: the blocks of one (batch row, kv head) share its q and
   // dO rows in one XCD's L2
   const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int chunk = blockIdx.y;  // which run of query tiles of the key block
   const int64_t kb = bid % (uint32_t)nkb;
   const int64_t kvh = (bid / (uint32_t)nkb) % (uint32_t)a.KVH;
   const int64_t b = bid / ((uint32_t)nkb * (uint32_t)a.KVH);
-  const int64_t head = kvh * NQ + h;
   const int64_t key0 = kb * kBKeys;
+  const int64_t kw0 = key0 + 32 * wave;  // this wave's first key
   const int64_t p0 = a.start[b];
   const float scale2 = 1.4426950408889634f / sqrtf((float)kBD);
   const int64_t rope_last = a.rope_len - 1;
@@ -73,12 +90,13 @@ __global__ __launch_bounds__(64 * NQ) void prefill_value_grad_kernel(ValueGradAr
   };
   const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
 
-  // ---- the block's rotated keys as B operands: kb_[kt][c] = dims
-  // [32c + 8lg, +8) of key 16kt + ln (chunks c and c+2 are rotary partners) ----
+  // ---- the wave's rotated keys as B operands: kop[kt][c] = dims
+  // [32c + 8lg, +8) of key kw0 + 16kt + ln (chunks c and c+2 are rotary
+  // partners) ----
   half8 kop[2][4];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
-    const int64_t key = key0 + 16 * kt + ln;
+    const int64_t key = kw0 + 16 * kt + ln;
     const bool ok = key < a.T;
     const _Float16* kp = a.k + b * a.ksb + kvh * a.ksh + (ok ? key : 0) * a.kst;
     const _Float16* tr = rope_row(p0 + (ok ? key : 0));
@@ -92,157 +110,222 @@ __global__ __launch_bounds__(64 * NQ) void prefill_value_grad_kernel(ValueGradAr
       kop[kt][c + 2] = ok ? r1 : zero8;
     }
   }
-  // identity columns: B operand lane (column ln, lg) holds contraction slots
-  // 8lg..8lg+7; ident[half] selects column ln of dims 16 half .. 16 half + 15
-  half8 ident[2];
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ident[hf][e] = (_Float16)(8 * lg + e == 16 * hf + ln ? 1.f : 0.f);
-
-  float4v acc[2][8];  // dV̂[key 16kt + 4lg + e][dim 16dt + ln]
+  float4v acc[2][8];  // dV̂[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  // query rows that see some key of the block: [key0, key0 + 31 + window)
+  // query rows that see some key of the block: [key0, key0 + 127 + window)
   int64_t rend = key0 + kBKeys - 1 + a.window;
   if (rend > a.T || rend < 0) rend = a.T;
-  const _Float16* qbase = a.q + b * a.qsb + head * a.qsh;
-  const _Float16* dbase = a.dout + b * a.dsb + head * a.dsh;
-  const float* lbase = a.lse + (b * a.QH + head) * a.T;
+  const int64_t all_tiles = ceil_div(rend - key0, kBRows);
+  const int64_t tile_lo = (int64_t)chunk * a.chunk_tiles;
+  int64_t ntiles = all_tiles - tile_lo;
+  if (ntiles > a.chunk_tiles) ntiles = a.chunk_tiles;
+  if (ntiles < 0) ntiles = 0;
+  const int64_t nsteps = ntiles * NQ;
 
-  for (int64_t r0 = key0; r0 < rend; r0 += kBRows) {
-    // ---- the tile's rotated q rows (A operands) and dO rows ----
-    half8 qa[2][4], da[2][4];
+  // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
+  // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
+  // dims [8*(tid/16), +8), stored transposed as (row, row+1) words.  A step
+  // (tile ft, head fh) is addressed as a uniform base plus per-thread offsets
+  // fixed for the whole loop ----
+  const int qr = tid >> 3, qp = tid & 7;
+  const int drp = tid & 15, ddb = tid >> 4;
+  const int64_t q_thr = (int64_t)qr * a.qst + 8 * qp;
+  const int64_t d_thr0 = (int64_t)(2 * drp) * a.dst + 8 * ddb;
+  const int64_t d_thr1 = d_thr0 + a.dst;
+  const _Float16* q_b = a.q + b * a.qsb + kvh * NQ * a.qsh;
+  const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
+  const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
+  struct StepRegs {
+    half8 q0, q1, cs, sn, d0, d1;
+    float l;
+  };
+  auto fetch = [&](int ft, int fh, StepRegs& r) {
+    const int64_t r0 = key0 + (tile_lo + ft) * kBRows;
+    const int64_t row = r0 + qr;
+    const bool ok = row < a.T;
+    const _Float16* qrow = ok ? q_b + fh * a.qsh + r0 * a.qst + q_thr : a.q;
+    r.q0 = *(const half8*)qrow;
+    r.q1 = *(const half8*)(qrow + 64);
+    r.q0 = ok ? r.q0 : zero8;
+    r.q1 = ok ? r.q1 : zero8;
+    load_trig8(rope_row(p0 + (ok ? row : 0)), 8 * qp, &r.cs, &r.sn);
+    const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
+    const bool ok0 = r0 + 2 * drp < a.T, ok1 = r0 + 2 * drp + 1 < a.T;
+    r.d0 = ok0 ? *(const half8*)(dstep + d_thr0) : zero8;
+    r.d1 = ok1 ? *(const half8*)(dstep + d_thr1) : zero8;
+    r.l = tid < kBRows && r0 + tid < a.T ? l_b[fh * a.T + r0 + tid] * 1.4426950408889634f : 0.f;
+  };
+  auto store = [&](const StepRegs& r, int buf) {
+    half8 r0, r1;
+    rope16(r.q0, r.q1, r.cs, r.sn, &r0, &r1);
+    _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
+    *(half8*)qd = r0;
+    *(half8*)(qd + 64) = r1;
+    _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
 #pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
-      const int64_t row = r0 + 16 * rg + ln;
-      const bool ok = row < a.T;
-      const _Float16* qp = qbase + (ok ? row : 0) * a.qst;
-      const _Float16* dp = dbase + (ok ? row : 0) * a.dst;
-      const _Float16* tr = rope_row(p0 + (ok ? row : 0));
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int d0 = 32 * c + 8 * lg;
-        half8 cs, sn, r0h, r1h;
-        load_trig8(tr, d0, &cs, &sn);
-        rope16(*(const half8*)(qp + d0), *(const half8*)(qp + d0 + 64), cs, sn, &r0h, &r1h);
-        qa[rg][c] = ok ? r0h : zero8;
-        qa[rg][c + 2] = ok ? r1h : zero8;
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) da[rg][c] = ok ? *(const half8*)(dp + 32 * c + 8 * lg) : zero8;
+    for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(r.d0, r.d1, e);
+    if (tid < kBRows) l_lds[buf][tid] = r.l;
+  };
+
+  // step s+1 waits in registers while s is computed and s+2 is in flight;
+  // steps run tile by tile, the group's heads within a tile
+  int ft = 0, fh = 0;  // the next step to fetch
+  auto advance = [&]() {
+    if (++fh == NQ) {
+      fh = 0;
+      ++ft;
     }
-    // lse (base 2) of the rows this lane's S elements belong to: 4lg + e, 16 + 4lg + e
-    float l2[2][4];
-#pragma unroll
-    for (int rg = 0; rg < 2; ++rg)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t row = r0 + 16 * rg + 4 * lg + e;
-        l2[rg][e] = row < a.T ? lbase[row] * 1.4426950408889634f : 0.f;
-      }
+  };
+  StepRegs nxt;
+  if (nsteps > 0) {
+    StepRegs r;
+    fetch(ft, fh, r);
+    advance();
+    if (nsteps > 1) {
+      fetch(ft, fh, nxt);
+      advance();
+    }
+    store(r, 0);
+  }
+  __syncthreads();
 
-    // ---- S[row][key] for 2 row tiles x 2 key tiles ----
-    float4v s[2][2];
-#pragma unroll
-    for (int rg = 0; rg < 2; ++rg)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          s[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rg][c], kop[kt][c], s[rg][kt], 0, 0, 0);
-      }
-    // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
-    // key0 + 16kt + ln.  pa[kt]: A operand of key 16kt + ln, contraction slot
-    // 8lg + e <-> row 4lg + e (e < 4), 16 + 4lg + e - 4 (e >= 4) ----
-    const bool full = r0 >= key0 + kBKeys - 1 && r0 + kBRows - 1 - key0 < a.window && r0 + kBRows <= a.T;
-    // masks in 32-bit offsets from the tile: row - key = base + 16rg + e - 16kt
-    const int base = (int)(r0 - key0) + 4 * lg - ln;
-    const int rows_left = (int)(a.T - r0 < kBRows ? a.T - r0 : kBRows);  // valid rows of the tile
-    const int keys_left = (int)(a.T - key0 < kBKeys ? a.T - key0 : kBKeys);
-    const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
-    half8 pa[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int rg = 0; rg < 2; ++rg)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float p = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][e], scale2, -l2[rg][e]));
-          if (!full) {
-            const int diff = base + 16 * rg + e - 16 * kt;
-            const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left && 16 * kt + ln < keys_left;
-            p = vis ? p : 0.f;
-          }
-          pa[kt][4 * rg + e] = (_Float16)p;
-        }
-    // ---- per 16-dim slice: dO in B order (db = rows {4lg+e, 16+4lg+e} of
-    // dim 16dt + ln), then dV̂ += Pᵀ dO for both key tiles ----
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      half8 db;
+  int ct = 0, ch = 0;  // the step being computed
+  for (int64_t step = 0; step < nsteps; ++step) {
+    const int buf = (int)(step & 1);
+    const bool more = step + 1 < nsteps;
+    StepRegs ahead;
+    if (step + 2 < nsteps) {
+      fetch(ft, fh, ahead);
+      advance();
+    }
+    const int64_t r0 = key0 + (tile_lo + ct) * kBRows;
+    // does any row of the step see any of this wave's keys?
+    const bool any = r0 + kBRows - 1 >= kw0 && r0 - (kw0 + 31) < a.window && kw0 < a.T;
+    if (any) {
+      const _Float16* ql = q_lds[buf];
+      const _Float16* dl = d_lds[buf];
+      // ---- S[row][key]: 2 row tiles x 2 key tiles ----
+      float4v sacc[2][2];
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg) {
-        const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[rg][dt >> 1], ident[dt & 1],
-                                                               float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        half8 qa[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) db[4 * rg + e] = (_Float16)t[e];
+        for (int c = 0; c < 4; ++c) qa[c] = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            sacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kop[kt][c], sacc[rg][kt], 0, 0, 0);
+        }
       }
+      // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
+      // kw0 + 16kt + ln; pa[kt] contraction slot 4rg + e (of lane group lg)
+      // <-> row 16rg + 4lg + e ----
+      const bool full = r0 >= kw0 + 31 && r0 + kBRows - 1 - kw0 < a.window && r0 + kBRows <= a.T;
+      const int base = (int)(r0 - kw0) + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
+      const int rows_left = (int)(a.T - r0 < kBRows ? a.T - r0 : kBRows);
+      const int keys_left = (int)(a.T - kw0 < 32 ? a.T - kw0 : 32);
+      const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
+      half8 pa[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-        acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
+      for (int rg = 0; rg < 2; ++rg) {
+        const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
+        const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
+            if (!full) {
+              const int diff = base + 16 * rg + e - 16 * kt;
+              const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
+                               16 * kt + ln < keys_left;
+              p = vis ? p : 0.f;
+            }
+            pa[kt][4 * rg + e] = (_Float16)p;
+          }
+      }
+      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
+      // {16+4lg..16+4lg+3} ----
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const _Float16* dr = dl + (16 * dt + ln) * kDStride + 4 * lg;
+        const half4 lo = *(const half4*)dr;
+        const half4 hi = *(const half4*)(dr + 16);
+        const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
+      }
+    }
+    // ---- the next step into the other buffer ----
+    if (more) store(nxt, buf ^ 1);
+    nxt = ahead;
+    __syncthreads();
+    if (++ch == NQ) {
+      ch = 0;
+      ++ct;
     }
   }
 
-  // ---- sum the heads in order (head 0 + head 1 + ...) and store ----
-  if (NQ > 1) {
-    if (h > 0) {
-      float* mine = part + (size_t)(h - 1) * kBKeys * kBD;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mine[(16 * kt + 4 * lg + e) * kBD + 16 * dt + ln] = acc[kt][dt][e];
-    }
-    __syncthreads();
-    if (h > 0) return;
-#pragma unroll 1
-    for (int o = 1; o < NQ; ++o) {
-      const float* other = part + (size_t)(o - 1) * kBKeys * kBD;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[kt][dt][e] += other[(16 * kt + 4 * lg + e) * kBD + 16 * dt + ln];
-    }
-  }
-  float* out = a.dv + ((b * a.KVH + kvh) * a.T) * kBD;
+  // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
+  // (a chunk with no rows still writes its slot: zeros)
+  float* out = a.dv + (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int64_t key = key0 + 16 * kt + 4 * lg + e;
+      const int64_t key = kw0 + 16 * kt + 4 * lg + e;
       if (key >= a.T) continue;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) out[key * kBD + 16 * dt + ln] = acc[kt][dt][e];
     }
 }
 
-template <int NQ>
-static void launch_value_grad(const ValueGradArgs& a, int64_t blocks, hipStream_t stream) {
-  const size_t lds = (size_t)(NQ - 1) * kBKeys * kBD * sizeof(float);
-  hipLaunchKernelGGL(prefill_value_grad_kernel<NQ>, dim3((uint32_t)blocks), dim3(64 * NQ), lds, stream, a);
+// dV̂ = the sum of the chunks' partial slots, in chunk order
+__global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ dv, int64_t n4,
+                                                                int64_t slot4, int chunks) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  float4 acc = ((const float4*)part)[i];
+  for (int c = 1; c < chunks; ++c) {
+    const float4 v = ((const float4*)part)[i + c * slot4];
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  ((float4*)dv)[i] = acc;
+}
+
+// query tiles per chunk and the number of chunks of the largest key block
+static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* chunks) {
+  int64_t rows = (int64_t)kBKeys - 1 + window;
+  if (rows > T || rows < 0) rows = T;
+  const int64_t tiles = ceil_div(rows, kBRows) + 1;  // + 1: a block's rows start inside a tile row
+  int64_t per = 16;
+  if (ceil_div(tiles, per) > 8) per = ceil_div(tiles, 8);
+  *chunk_tiles = (int)per;
+  *chunks = (int)ceil_div(tiles, per);
 }
 
 }  // namespace jkv
 
 extern "C" {
+
+int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T, int64_t window) {
+  using namespace jkv;
+  if (B <= 0 || KVH <= 0 || T <= 0 || window < 1) return 0;
+  int chunk_tiles, chunks;
+  value_grad_chunks(T, window, &chunk_tiles, &chunks);
+  return chunks > 1 ? (int64_t)chunks * B * KVH * T * kBD * (int64_t)sizeof(float) : 0;
+}
 
 int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                      int64_t q_stride_t, const void* k, int64_t k_stride_b,
@@ -251,14 +334,13 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
                                      const float* lse, int64_t B, int64_t QH, int64_t KVH, int64_t T,
                                      int64_t D, const int32_t* start_positions, int64_t window,
                                      const void* rope_table, int64_t rope_len, float* d_value,
-                                     jkv_stream_t stream_) {
+                                     void* workspace, int64_t workspace_bytes, jkv_stream_t stream_) {
   using namespace jkv;
   hipStream_t stream = (hipStream_t)stream_;
   JKV_CHECK_ARG(D == kBD, "prefill value gradient supports head_dim 128, got %lld", (long long)D);
   JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
   const int64_t NQ = QH / KVH;
-  JKV_CHECK_ARG(NQ == 1 || NQ == 2 || NQ == 4 || NQ == 8,
-                "query heads per kv head must be 1, 2, 4 or 8, got %lld", (long long)NQ);
+  JKV_CHECK_ARG(NQ <= 64, "at most 64 query heads per kv head, got %lld", (long long)NQ);
   JKV_CHECK_ARG(window >= 1, "window must be positive");
   if (B == 0 || T == 0) return JKV_OK;
   JKV_CHECK_ARG(q && k && d_out && lse && d_value && start_positions && rope_table, "null buffer");
@@ -279,16 +361,34 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
   a.window = window;
   a.rope = (const _Float16*)rope_table;
   a.rope_len = rope_len;
-  a.dv = d_value;
+  a.nq = (int32_t)NQ;
+  int chunk_tiles, chunks;
+  value_grad_chunks(T, window, &chunk_tiles, &chunks);
+  a.chunk_tiles = chunk_tiles;
+  const int64_t n = B * KVH * T * kBD;
+  if (chunks > 1) {
+    const int64_t need = jkv_prefill_value_grad_workspace_bytes(B, KVH, T, window);
+    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "value gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
+                  (long long)need);
+    JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
+    a.dv = (float*)workspace;
+    a.slot_stride = n;
+  } else {
+    a.dv = d_value;
+    a.slot_stride = 0;
+  }
   const int64_t blocks = ceil_div(T, kBKeys) * KVH * B;
   JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-  switch (NQ) {
-    case 1: launch_value_grad<1>(a, blocks, stream); break;
-    case 2: launch_value_grad<2>(a, blocks, stream); break;
-    case 4: launch_value_grad<4>(a, blocks, stream); break;
-    default: launch_value_grad<8>(a, blocks, stream); break;
-  }
+  hipLaunchKernelGGL(prefill_value_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
+                     stream, a);
   JKV_CHECK_LAUNCH();
+  if (chunks > 1) {
+    const int64_t n4 = n / 4;
+    hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
+                       (const float*)workspace, d_value, n4, n4, chunks);
+    JKV_CHECK_LAUNCH();
+  }
   return JKV_OK;
 }
 

@@ -437,11 +437,14 @@ def prefill_attention_value_grad(
         raise ValueError("lse must be a contiguous fp32 [B,QH,T] tensor")
     table = rope_table(device, rope_theta, int(max_position) + 1)
     d_value = torch.empty((batch, kvheads, tokens, 128), dtype=torch.float32, device=device)
-    code = _lib.load().jkv_prefill_attention_value_grad(
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_prefill_value_grad_workspace_bytes(batch, kvheads, tokens, int(window)))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    code = lib.jkv_prefill_attention_value_grad(
         q.data_ptr(), *q.stride()[:3], key.data_ptr(), *key.stride()[:3], d_out.data_ptr(),
         *d_out.stride()[:3], lse.data_ptr(), batch, qheads, kvheads, tokens, 128,
         start_positions.data_ptr(), int(window), table.data_ptr(), int(table.shape[0]),
-        d_value.data_ptr(), _lib.stream_handle(device),
+        d_value.data_ptr(), workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
     )
     _lib.check(code)
     return d_value

@@ -35,9 +35,12 @@ def _case(seed, batch, qh, kvh, tokens):
     (1, 4, 2, 45, (3,), 4096),          # GQA 2
     (1, 16, 2, 96, (0,), 4096),         # GQA 8
     (1, 4, 1, 1, (9,), 4096),           # one token
+    (1, 8, 2, 600, (0,), 4096),         # key blocks' rows split in two runs (workspace + reduce)
+    (1, 8, 2, 1030, (40,), 4096),       # three runs, ragged last tile
 ])
 def test_lse_and_value_grad_match_oracle(device, batch, qh, kvh, tokens, starts, window):
-    print(f"value grad B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)
+    ws = int(_ops._lib.load().jkv_prefill_value_grad_workspace_bytes(batch, kvh, tokens, window))
+    print(f"value grad B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window} ws={ws}", flush=True)
     q, k, v, d = _case(900 + tokens, batch, qh, kvh, tokens)
     qd, kd, vd, dd = (t.to(device) for t in (q, k, v, d))
     st, top = _start_tensor(list(starts), batch, tokens, qd.device)

@@ -251,10 +251,9 @@ def decode_workload(args, device):
     def step():
         # encode the new token's K and V straight into the cache slot, then attend
         for cache, (kt, vt, kt16, vt16) in zip(caches, tabs):
-            _ops.rvq_encode(knew, kt, groups=GROUPS, group_dim=GROUP_DIM, exits=(),
-                            codes_out=cache.key[:, :, slot : slot + 1])
-            _ops.rvq_encode(vnew, vt, groups=GROUPS, group_dim=GROUP_DIM, exits=(),
-                            codes_out=cache.value[:, :, slot : slot + 1])
+            _ops.rvq_encode_kv(knew, vnew, kt, vt, groups=GROUPS, group_dim=GROUP_DIM, exits=(),
+                               key_codes_out=cache.key[:, :, slot : slot + 1],
+                               value_codes_out=cache.value[:, :, slot : slot + 1])
             _ops.decode_attention(q, cache.key, cache.value, kt16, vt16, lengths, window=window,
                                   rope_theta=10000.0, max_length=window)
 

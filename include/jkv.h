@@ -78,6 +78,27 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B,
                    jkv_stream_t stream);
 
 /*
+ * A token's K and V through jkv_rvq_encode in one call: the codec forward
+ * encodes K then V with the same geometry (src/jointkv/uniform_depth_tac.py:
+ * 69-101 and cq_tac.py:117-192, per decode step at
+ * experiments_followup_mistral/evaluate_mistral_longbench.py:94-98).  Both
+ * share B/H/T/G/d/S/K, the state strides, the code strides and the exit
+ * depths; each has its own states, tables, codes and reconstructions.  With
+ * fp16 states, d in {4, 8}, K = 256 and S <= 2 both run in one launch (twice
+ * the workgroups of one, at the latency of one for decode-sized calls);
+ * other geometries run the two encodes in turn, sharing `workspace`.  No
+ * whitener (the K side's whitener needs jkv_rvq_encode).
+ */
+int jkv_rvq_encode_kv(const void* key_states, const void* value_states, int32_t states_dtype,
+                      int64_t B, int64_t H, int64_t T, int64_t G, int64_t d, int64_t stride_b,
+                      int64_t stride_h, int64_t stride_t, const float* key_tables,
+                      const float* value_tables, int64_t S, int64_t K, uint8_t* key_codes,
+                      uint8_t* value_codes, int64_t code_stride_b, int64_t code_stride_h,
+                      int64_t code_stride_t, int32_t n_exits, const int32_t* exit_depths,
+                      void* const* key_recon, void* const* value_recon, void* workspace,
+                      int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
  * Codes-to-vector reconstruction with given (frozen) codes:
  * out = dtype( sum_{s<depth} fp32(fp16(tables[h*G+g, s, code])) ).
  * Replaces frozen_assignment_u16_reconstruction

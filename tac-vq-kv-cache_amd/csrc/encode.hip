@@ -264,17 +264,29 @@ static const int kTiles = 4;                      // 16-row tiles per wave itera
 static const int kRowsPerWave = kTiles * 16;      // rows per wave iteration
 static const int kRowsPerIter = 4 * kRowsPerWave; // rows per workgroup iteration
 
-struct MfmaArgs {
+struct MfmaJob {
   EncodeArgs e;
   void* recon_depth[2];  // reconstruction at depth 1 / 2 (or null)
   int64_t rows_per_wg;
   int64_t n_chunks;      // row chunks per problem
 };
 
-template <int D, int S>
+// One launch runs one or two jobs of the same geometry (a token's K and V):
+// logical workgroups below `split` take job 0, the others job 1.
+struct MfmaArgs {
+  MfmaJob job[2];
+  int64_t split;
+};
+
+// PAIR: two jobs in the launch (a single-job launch keeps every argument at
+// a fixed kernarg offset)
+template <int D, int S, bool PAIR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void rvq_encode_mfma(MfmaArgs m) {
-  const EncodeArgs& a = m.e;
+  const uint32_t L0 = xcd_remap(blockIdx.x, gridDim.x);
+  const int jb = PAIR && (int64_t)L0 >= m.split ? 1 : 0;
+  const MfmaJob& mj = m.job[jb];
+  const EncodeArgs& a = mj.e;
   // slot groups with data (bias sits where the lanes read plane hi):
   // stage 1 [x, bias]; stage 2 d=8 [x, -c_1, bias], d=4 [[x,-c_1], bias]
   constexpr int kSgX = 0;
@@ -297,9 +309,9 @@ void rvq_encode_mfma(MfmaArgs m) {
   const int ln = lane & 15;
 
   // logical block: group fastest, then head, then row chunk
-  const uint32_t L = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t L = jb ? L0 - (uint32_t)m.split : L0;
   const int64_t P = a.H * a.G;
-  const bool active = (int64_t)L < P * m.n_chunks;
+  const bool active = (int64_t)L < P * mj.n_chunks;
   const int64_t g = active ? (int64_t)L % a.G : 0;
   const int64_t h = active ? ((int64_t)L / a.G) % a.H : 0;
   const int64_t chunk = active ? (int64_t)L / P : 0;
@@ -365,8 +377,8 @@ void rvq_encode_mfma(MfmaArgs m) {
   constexpr int kSgStride = kTiles * 16;  // half8 words between slot groups
 
   const int64_t rows = a.B * a.T;
-  const int64_t r_begin = chunk * m.rows_per_wg;
-  int64_t r_end = r_begin + m.rows_per_wg;
+  const int64_t r_begin = chunk * mj.rows_per_wg;
+  int64_t r_end = r_begin + mj.rows_per_wg;
   if (r_end > rows) r_end = rows;
   const _Float16* states = (const _Float16*)a.states;
   const int64_t Dfull = a.G * D;
@@ -599,7 +611,7 @@ void rvq_encode_mfma(MfmaArgs m) {
       // depth-(s+1) reconstruction fp16(fp32(c1) + fp32(c2)): the sum of two
       // fp16 words is exact in fp32 or, when it is not, too small to move the
       // fp16 rounding, so one fp16 add gives the same bits.
-      void* out = m.recon_depth[s];
+      void* out = mj.recon_depth[s];
       if (out != nullptr && valid) {
         const half8 dec = (s > 0) ? sub_h8(cw, negc1) : cw;
         _Float16* op = (_Float16*)out + oo;
@@ -637,24 +649,80 @@ static int launch_generic(const EncodeArgs& a, hipStream_t stream) {
   return JKV_OK;
 }
 
-template <int D, int S>
-static int launch_mfma(const EncodeArgs& e, hipStream_t stream) {
-  MfmaArgs m = {};
-  m.e = e;
-  for (int i = 0; i < e.n_exits; ++i) m.recon_depth[e.exit_depth[i] - 1] = e.recon[i];
+static MfmaJob mfma_job(const EncodeArgs& e) {
+  MfmaJob j = {};
+  j.e = e;
+  for (int i = 0; i < e.n_exits; ++i) j.recon_depth[e.exit_depth[i] - 1] = e.recon[i];
   const int64_t rows = e.B * e.T;
   const int64_t P = e.H * e.G;
   // rows per workgroup: amortise the codebook staging, fill 256 CUs x 4 WGs
   int64_t rpw = 4096;
   while (rpw > kRowsPerIter && P * ceil_div(rows, rpw) < 256 * 4) rpw >>= 1;
-  m.rows_per_wg = rpw;
-  m.n_chunks = ceil_div(rows, rpw);
-  int64_t nblocks = P * m.n_chunks;
+  j.rows_per_wg = rpw;
+  j.n_chunks = ceil_div(rows, rpw);
+  return j;
+}
+
+// one job, or two of the same geometry (second non-null) in one launch
+template <int D, int S>
+static int launch_mfma(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t stream) {
+  MfmaArgs m = {};
+  m.job[0] = mfma_job(e);
+  const int64_t per_job = e.H * e.G * m.job[0].n_chunks;
+  int64_t nblocks = per_job;
+  m.split = per_job;
+  if (e2 != nullptr) {
+    m.job[1] = mfma_job(*e2);
+    nblocks += per_job;
+  } else {
+    m.job[1] = m.job[0];
+  }
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < (int64_t)1 << 31, "grid too large");
-  hipLaunchKernelGGL((rvq_encode_mfma<D, S>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+  if (e2 == nullptr) {
+    m.split = nblocks;
+    hipLaunchKernelGGL((rvq_encode_mfma<D, S, false>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+  } else {
+    hipLaunchKernelGGL((rvq_encode_mfma<D, S, true>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+  }
   JKV_CHECK_LAUNCH();
   return JKV_OK;
+}
+
+template <int D, int S>
+static int launch_mfma(const EncodeArgs& e, hipStream_t stream) {
+  return launch_mfma<D, S>(e, nullptr, stream);
+}
+
+// Whether rvq_encode_mfma takes these arguments: fp16 states, d in {4, 8},
+// K = 256, S <= 2, no whitener, 16-byte aligned states and reconstructions,
+// and offsets that fit the kernel's 32-bit (24-bit for token strides)
+// arithmetic.
+static bool mfma_eligible(const EncodeArgs& a, int32_t states_dtype) {
+  const int64_t B = a.B, H = a.H, T = a.T, G = a.G, d = a.d, S = a.S;
+  const bool aligned16 = (((uintptr_t)a.states) % 16 == 0) && a.sb % 8 == 0 && a.sh % 8 == 0 && a.st % 8 == 0;
+  const bool codes_aligned =
+      (S == 1) || ((((uintptr_t)a.codes) % 2 == 0) && a.cb % 2 == 0 && a.ch % 2 == 0 && a.ct % 2 == 0);
+  bool recon_aligned = true, distinct_exits = true;
+  for (int e = 0; e < a.n_exits; ++e) {
+    if (a.recon[e] && ((uintptr_t)a.recon[e]) % 16 != 0) recon_aligned = false;
+    for (int f = 0; f < e; ++f)
+      if (a.exit_depth[e] == a.exit_depth[f]) distinct_exits = false;
+  }
+  const int64_t x_span = (B - 1) * a.sb + (H - 1) * a.sh + (T - 1) * a.st + G * d;
+  const int64_t c_span = (B - 1) * a.cb + (H - 1) * a.ch + (T - 1) * a.ct + G * S;
+  const bool offsets32 = a.sb >= 0 && a.sh >= 0 && a.st >= 0 && a.cb >= 0 && a.ch >= 0 && a.ct >= 0 &&
+                         x_span < ((int64_t)1 << 31) && c_span < ((int64_t)1 << 31) &&
+                         B * H * T * G * d < ((int64_t)1 << 31) && a.st < ((int64_t)1 << 24) &&
+                         a.ct < ((int64_t)1 << 24) && G * d < ((int64_t)1 << 24);
+  return offsets32 && states_dtype == JKV_F16 && a.whiteners == nullptr && a.K == 256 &&
+         (d == 8 || d == 4) && (S == 1 || S == 2) && aligned16 && codes_aligned && recon_aligned &&
+         distinct_exits && B * T < ((int64_t)1 << 31) && T < ((int64_t)1 << 31);
+}
+
+template <int D, int S>
+static int launch_mfma_pair_t(const EncodeArgs& k, const EncodeArgs& v, hipStream_t stream) {
+  return launch_mfma<D, S>(k, &v, stream);
 }
 
 }  // namespace jkv
@@ -707,8 +775,6 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
 
   const bool aligned16 = (((uintptr_t)states) % 16 == 0) && stride_b % 8 == 0 &&
                          stride_h % 8 == 0 && stride_t % 8 == 0;
-  const bool codes_aligned = (S == 1) || ((((uintptr_t)codes) % 2 == 0) && code_stride_b % 2 == 0 &&
-                                          code_stride_h % 2 == 0 && code_stride_t % 2 == 0);
   bool recon_aligned = true;
   for (int e = 0; e < n_exits; ++e)
     if (a.recon[e] && ((uintptr_t)a.recon[e]) % 16 != 0) recon_aligned = false;
@@ -716,20 +782,7 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
   for (int i = 0; i < n_exits; ++i)
     for (int j = 0; j < i; ++j)
       if (exit_depths[i] == exit_depths[j]) distinct_exits = false;
-  // the MFMA path addresses states, codes and reconstructions with 32-bit
-  // element offsets
-  const int64_t x_span = (B - 1) * stride_b + (H - 1) * stride_h + (T - 1) * stride_t + G * d;
-  const int64_t c_span = (B - 1) * code_stride_b + (H - 1) * code_stride_h + (T - 1) * code_stride_t + G * S;
-  // (and token strides below 2^24, for 24-bit multiplies)
-  const bool offsets32 = stride_b >= 0 && stride_h >= 0 && stride_t >= 0 && code_stride_b >= 0 &&
-                         code_stride_h >= 0 && code_stride_t >= 0 && x_span < ((int64_t)1 << 31) &&
-                         c_span < ((int64_t)1 << 31) && B * H * T * G * d < ((int64_t)1 << 31) &&
-                         stride_t < ((int64_t)1 << 24) && code_stride_t < ((int64_t)1 << 24) &&
-                         G * d < ((int64_t)1 << 24);
-  const bool fast = offsets32 && states_dtype == JKV_F16 && whiteners == nullptr && K == 256 &&
-                    (d == 8 || d == 4) && (S == 1 || S == 2) && aligned16 && codes_aligned &&
-                    recon_aligned && distinct_exits && B * T < ((int64_t)1 << 31) &&
-                    T < ((int64_t)1 << 31);
+  const bool fast = mfma_eligible(a, states_dtype);
   if (fast) {
     if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
     return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);
@@ -767,6 +820,54 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
     case JKV_BF16: return launch_generic<JKV_BF16>(a, stream);
     default: return launch_generic<JKV_F32>(a, stream);
   }
+}
+
+int jkv_rvq_encode_kv(const void* key_states, const void* value_states, int32_t states_dtype, int64_t B,
+                      int64_t H, int64_t T, int64_t G, int64_t d, int64_t stride_b, int64_t stride_h,
+                      int64_t stride_t, const float* key_tables, const float* value_tables, int64_t S,
+                      int64_t K, uint8_t* key_codes, uint8_t* value_codes, int64_t code_stride_b,
+                      int64_t code_stride_h, int64_t code_stride_t, int32_t n_exits,
+                      const int32_t* exit_depths, void* const* key_recon, void* const* value_recon,
+                      void* workspace, int64_t workspace_bytes, jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(B >= 0 && H > 0 && T >= 0 && G > 0 && d > 0 && S > 0 && K > 0, "invalid geometry");
+  JKV_CHECK_ARG(n_exits >= 0 && n_exits <= JKV_MAX_EXITS, "at most %d exits", JKV_MAX_EXITS);
+  if (B * T == 0) return JKV_OK;
+  JKV_CHECK_ARG(key_states && value_states && key_tables && value_tables && key_codes && value_codes,
+                "null buffer");
+  EncodeArgs ak = {};
+  ak.states = key_states;
+  ak.sb = stride_b; ak.sh = stride_h; ak.st = stride_t;
+  ak.B = B; ak.H = H; ak.T = T; ak.G = G; ak.d = d; ak.S = S; ak.K = K;
+  ak.tables = key_tables;
+  ak.codes = key_codes;
+  ak.cb = code_stride_b; ak.ch = code_stride_h; ak.ct = code_stride_t;
+  ak.n_exits = n_exits;
+  for (int e = 0; e < n_exits; ++e) {
+    JKV_CHECK_ARG(exit_depths[e] >= 1 && exit_depths[e] <= S, "exit depth outside the ladder");
+    ak.exit_depth[e] = exit_depths[e];
+    ak.recon[e] = key_recon ? key_recon[e] : nullptr;
+  }
+  EncodeArgs av = ak;
+  av.states = value_states;
+  av.tables = value_tables;
+  av.codes = value_codes;
+  for (int e = 0; e < n_exits; ++e) av.recon[e] = value_recon ? value_recon[e] : nullptr;
+  if (mfma_eligible(ak, states_dtype) && mfma_eligible(av, states_dtype)) {
+    if (d == 8) return S == 1 ? launch_mfma_pair_t<8, 1>(ak, av, stream) : launch_mfma_pair_t<8, 2>(ak, av, stream);
+    return S == 1 ? launch_mfma_pair_t<4, 1>(ak, av, stream) : launch_mfma_pair_t<4, 2>(ak, av, stream);
+  }
+  // other geometries: the two encodes one after the other on the stream
+  // (they may share the workspace: the second starts after the first)
+  const int rc = jkv_rvq_encode(key_states, states_dtype, B, H, T, G, d, stride_b, stride_h, stride_t,
+                                key_tables, S, K, nullptr, key_codes, code_stride_b, code_stride_h,
+                                code_stride_t, n_exits, exit_depths, key_recon, workspace, workspace_bytes,
+                                stream_);
+  if (rc != JKV_OK) return rc;
+  return jkv_rvq_encode(value_states, states_dtype, B, H, T, G, d, stride_b, stride_h, stride_t,
+                        value_tables, S, K, nullptr, value_codes, code_stride_b, code_stride_h, code_stride_t,
+                        n_exits, exit_depths, value_recon, workspace, workspace_bytes, stream_);
 }
 
 }  // extern "C"

@@ -78,6 +78,67 @@ def rvq_encode(
     return recon, codes
 
 
+def rvq_encode_kv(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_tables: torch.Tensor,
+    value_tables: torch.Tensor,
+    *,
+    groups: int,
+    group_dim: int,
+    exits: Sequence[int],
+    key_codes_out: torch.Tensor | None = None,
+    value_codes_out: torch.Tensor | None = None,
+):
+    """:func:`rvq_encode` of K and of V (same geometry, no whitener) in one
+    call; one launch on the grouped MFMA path.  Returns
+    ``(key_recon, key_codes, value_recon, value_codes)``."""
+
+    device = _lib.require_device(key, value, key_tables, value_tables)
+    if key.shape != value.shape or key.dtype != value.dtype or key_tables.shape != value_tables.shape:
+        raise ValueError("K and V must share their geometry")
+    batch, heads, tokens, dim = map(int, key.shape)
+    problems, stages, clusters, d = map(int, key_tables.shape)
+    if dim != groups * group_dim or d != group_dim or problems != heads * groups:
+        raise ValueError("state and table geometry differs")
+    for t in (key_tables, value_tables):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("encode tables must be contiguous fp32 masters")
+    if len(exits) > _lib.MAX_EXITS:
+        raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
+    key, strides = _encode_states_strides(key)
+    value, vstrides = _encode_states_strides(value)
+    if vstrides != strides:
+        key, strides = _encode_states_strides(key.contiguous())
+        value, vstrides = _encode_states_strides(value.contiguous())
+    codes = []
+    for out in (key_codes_out, value_codes_out):
+        if out is None:
+            out = torch.empty((batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device)
+        elif (out.dtype != torch.uint8 or tuple(out.shape) != (batch, heads, tokens, groups, stages)
+              or out.stride(-1) != 1 or out.stride(-2) != stages or out.device != device):
+            raise ValueError("codes_out must be uint8 [B,H,T,G,S] with a contiguous (G,S) block")
+        codes.append(out)
+    if codes[0].stride()[:3] != codes[1].stride()[:3]:
+        raise ValueError("K and V code outputs must share their strides")
+    recon_k = [torch.empty((batch, heads, tokens, dim), dtype=key.dtype, device=device) for _ in exits]
+    recon_v = [torch.empty((batch, heads, tokens, dim), dtype=key.dtype, device=device) for _ in exits]
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_rvq_encode_workspace_bytes(heads, groups, stages, clusters, d, 0))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
+    depth_arr = _lib.ptr_array(ctypes.c_int32, [int(e) for e in exits])
+    code = lib.jkv_rvq_encode_kv(
+        key.data_ptr(), value.data_ptr(), _lib.dtype_code(key.dtype), batch, heads, tokens, groups, d,
+        *strides, key_tables.data_ptr(), value_tables.data_ptr(), stages, clusters,
+        codes[0].data_ptr(), codes[1].data_ptr(), *codes[0].stride()[:3], len(exits), depth_arr,
+        _lib.ptr_array(ctypes.c_void_p, [r.data_ptr() for r in recon_k]),
+        _lib.ptr_array(ctypes.c_void_p, [r.data_ptr() for r in recon_v]),
+        _lib.ptr(workspace), ws_bytes, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return recon_k, codes[0], recon_v, codes[1]
+
+
 def rvq_decode(
     codes: torch.Tensor,
     tables: torch.Tensor,

@@ -270,10 +270,10 @@ class PackedCodeCache:
             raise ValueError("encode_append takes one token per sequence")
         slot = self._host_length % self.capacity
         groups = self.key.shape[3]
-        _ops.rvq_encode(key, key_tables, groups=groups, group_dim=group_dim, exits=(),
-                        codes_out=self.key[:, :, slot : slot + 1])
-        _ops.rvq_encode(value, value_tables, groups=groups, group_dim=group_dim, exits=(),
-                        codes_out=self.value[:, :, slot : slot + 1])
+        # K and V in one launch (one token per sequence is latency-bound)
+        _ops.rvq_encode_kv(key, value, key_tables, value_tables, groups=groups, group_dim=group_dim, exits=(),
+                           key_codes_out=self.key[:, :, slot : slot + 1],
+                           value_codes_out=self.value[:, :, slot : slot + 1])
         self._host_length += 1
         self.lengths.fill_(self._host_length)
 
@@ -358,10 +358,10 @@ class DecodedWindowCache:
             raise ValueError("encode_append takes one token per sequence")
         groups, stages = self.codes.key.shape[3], self.codes.key.shape[4]
         slot = self.codes.length % self.capacity
-        recon_k, _ = _ops.rvq_encode(key, key_tables, groups=groups, group_dim=group_dim, exits=(stages,),
-                                     codes_out=self.codes.key[:, :, slot : slot + 1])
-        recon_v, _ = _ops.rvq_encode(value, value_tables, groups=groups, group_dim=group_dim,
-                                     exits=(stages,), codes_out=self.codes.value[:, :, slot : slot + 1])
+        recon_k, _, recon_v, _ = _ops.rvq_encode_kv(
+            key, value, key_tables, value_tables, groups=groups, group_dim=group_dim, exits=(stages,),
+            key_codes_out=self.codes.key[:, :, slot : slot + 1],
+            value_codes_out=self.codes.value[:, :, slot : slot + 1])
         self.decoded_key[:, :, slot : slot + 1] = recon_k[0]
         self.decoded_value[:, :, slot : slot + 1] = recon_v[0]
         self.codes._host_length += 1

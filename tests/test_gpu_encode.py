@@ -232,3 +232,27 @@ def test_full_size_layer_properties(device):
     chosen = dist.gather(-1, codes[0, :, :64, :, 0].long().cpu()[..., None])[..., 0]
     best = dist.min(-1).values
     assert bool(((chosen - best) <= 1e-3 * best.clamp_min(1e-9)).all())
+
+
+@pytest.mark.parametrize("batch,tokens,groups,dim,stages,dtype,exits", [
+    (2, 300, 16, 8, 2, torch.float16, (1, 2)),     # G2: one paired launch
+    (16, 1, 32, 4, 1, torch.float16, (1,)),        # cq2, one token per sequence (the decode step)
+    (1, 70, 16, 8, 2, torch.float32, (2,)),        # fp32 states: the two encodes in turn
+    (1, 40, 1, 128, 4, torch.float16, (2, 4)),     # full-vector tables: in turn, shared workspace
+])
+def test_encode_kv_equals_two_encodes(device, batch, tokens, groups, dim, stages, dtype, exits):
+    from jointkv_amd import _ops
+
+    print(f"encode_kv B={batch} T={tokens} G={groups} d={dim} S={stages} {dtype}", flush=True)
+    gen = _gen(4242 + tokens)
+    k = ref.synthetic_states(gen, batch, 8, tokens, groups * dim).to(dtype).to(device)
+    v = ref.synthetic_states(gen, batch, 8, tokens, groups * dim).to(dtype).to(device)
+    sig = tuple(0.5 ** s for s in range(stages))
+    kt = ref.synthetic_tables(gen, (8 * groups, stages, 256, dim), sig, stage_axis=1).to(device)
+    vt = ref.synthetic_tables(gen, (8 * groups, stages, 256, dim), sig, stage_axis=1).to(device)
+    rk, ck, rv, cv = _ops.rvq_encode_kv(k, v, kt, vt, groups=groups, group_dim=dim, exits=exits)
+    ek, eck = _ops.rvq_encode(k, kt, groups=groups, group_dim=dim, exits=exits)
+    ev, ecv = _ops.rvq_encode(v, vt, groups=groups, group_dim=dim, exits=exits)
+    assert torch.equal(ck, eck) and torch.equal(cv, ecv)
+    for a, b in zip(rk + rv, ek + ev):
+        assert torch.equal(a, b)

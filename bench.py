@@ -387,11 +387,21 @@ def adapter_workload(args, device):
                                                           max_position=tokens - 1)] * 8
     dv_ms = per_launch_ms(launches)
     flops = 4.0 * batch * qh * HEAD_DIM * tokens * (tokens + 1) / 2  # causal S recompute + Pᵀ dO
+    # the full backward (query, key and value legs), as a lower layer of the
+    # trajectory needs it
+    out = _ops.prefill_attention(q, k, v, starts, window=4096, rope_theta=10000.0, max_position=tokens - 1,
+                                 lse=lse)
+    full = [lambda: _ops.prefill_attention_backward(q, k, v, out, d, lse, starts, window=4096, rope_theta=10000.0,
+                                                    max_position=tokens - 1)] * 4
+    bwd_ms = per_launch_ms(full)
+    bwd_flops = 4 * flops  # S recompute, dP, dS K̂ and dSᵀ Q, Pᵀ dO (the key leg recomputes S and dP)
     return {
         "ms_per_layer_step": ms,
         "value_grad_us": dv_ms * 1e3,
         "value_grad_tflops": flops / (dv_ms / 1e3) / 1e12,
         "value_grad_mfma_frac": flops / (dv_ms / 1e3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+        "full_backward_us": bwd_ms * 1e3,
+        "full_backward_tflops_algorithmic": 2.5 * flops / (bwd_ms / 1e3) / 1e12,
     }
 
 

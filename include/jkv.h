@@ -286,6 +286,50 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
 int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T, int64_t window);
 
 /*
+ * The full backward of jkv_prefill_attention (the SDPA backward under the
+ * reference's loss.backward() through its closed-loop attention,
+ * experiments/train_full_model_closed_loop_vq.py:277-304), for the gradients
+ * that are not NULL:
+ *   d_query [B,QH,T,128], d_key [B,KVH,T,128], d_value [B,KVH,T,128], fp32
+ *   contiguous, with respect to the PRE-RoPE q and K̂ (the rotary's transpose
+ *   is applied) and V̂; the key and value gradients are summed over the GQA
+ *   group.
+ * dS = P (dO V̂ᵀ - rowsum(dO * O)), dQ = dS K̂ / sqrt(128), dK = dSᵀ Q /
+ * sqrt(128), dV = Pᵀ dO, with P recomputed from the forward's lse.
+ *   out      the forward output [B,QH,T,128] fp16 (for rowsum(dO * O))
+ *   workspace  jkv_prefill_backward_workspace_bytes() bytes, 16-byte aligned
+ * Query heads per kv head: 1, 2 or a multiple of 4.  Deterministic.
+ */
+int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                                   const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                                   const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                                   const void* out, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_t,
+                                   const void* d_out, int64_t d_stride_b, int64_t d_stride_h,
+                                   int64_t d_stride_t, const float* lse, int64_t B, int64_t QH, int64_t KVH,
+                                   int64_t T, int64_t D, const int32_t* start_positions, int64_t window,
+                                   const void* rope_table, int64_t rope_len, float* d_query, float* d_key,
+                                   float* d_value, void* workspace, int64_t workspace_bytes,
+                                   jkv_stream_t stream);
+
+/* Workspace of jkv_prefill_attention_backward (bytes). */
+int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window);
+
+/*
+ * The key-gradient leg of jkv_prefill_attention_backward alone, given
+ * delta = rowsum(dO * O) [B,QH,T] fp32 (the backward computes it in its query
+ * leg).  Same buffers and workspace rule as jkv_prefill_attention_value_grad.
+ */
+int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                                   const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                                   const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                                   const void* d_out, int64_t d_stride_b, int64_t d_stride_h,
+                                   int64_t d_stride_t, const float* lse, const float* delta, int64_t B,
+                                   int64_t QH, int64_t KVH, int64_t T, int64_t D,
+                                   const int32_t* start_positions, int64_t window, const void* rope_table,
+                                   int64_t rope_len, float* d_key, void* workspace, int64_t workspace_bytes,
+                                   jkv_stream_t stream);
+
+/*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of
  * the 64 frequencies, then their sin):
  * angle = fp32(p) * inv_freq[i] in fp32, cos/sin in fp32 rounded to fp16 —

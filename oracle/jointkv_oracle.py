@@ -527,6 +527,42 @@ def prefill_value_grad(
     return torch.cat(grads, dim=0)
 
 
+def prefill_qk_grad(
+    q: torch.Tensor,
+    key_hat: torch.Tensor,
+    value_hat: torch.Tensor,
+    d_out: torch.Tensor,
+    start_positions: Sequence[int],
+    *,
+    window: int = 4096,
+    theta: float = 10000.0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """dL/dq and dL/dK̂ (pre-RoPE) of :func:`prefill_attention` for the output
+    gradient ``d_out``: autograd in fp32 through the rotary (the model's fp16
+    cos/sin), ``repeat_kv`` and SDPA, the query and key legs of the
+    reference's ``loss.backward()`` through its closed-loop attention
+    (train_full_model_closed_loop_vq.py:277-304).  Returns fp32
+    [B,QH,T,D] and [B,KVH,T,D]."""
+
+    head_dim = int(q.shape[-1])
+    groups = q.shape[1] // key_hat.shape[1]
+    mask = sliding_causal_mask(int(q.shape[2]), window)
+    dqs, dks = [], []
+    for b in range(q.shape[0]):
+        pos = torch.arange(q.shape[2]) + int(start_positions[b])
+        c, s = rotary_cos_sin(pos, head_dim, theta)
+        qf = q[b : b + 1].float().requires_grad_(True)
+        kf = key_hat[b : b + 1].float().requires_grad_(True)
+        qr = apply_rotary(qf, c.float()[None, None], s.float()[None, None])
+        kr = apply_rotary(kf, c.float()[None, None], s.float()[None, None]).repeat_interleave(groups, dim=1)
+        vr = value_hat[b : b + 1].float().repeat_interleave(groups, dim=1)
+        out = F.scaled_dot_product_attention(qr, kr, vr, attn_mask=mask, dropout_p=0.0)
+        out.backward(d_out[b : b + 1].float())
+        dqs.append(qf.grad)
+        dks.append(kf.grad)
+    return torch.cat(dqs, dim=0), torch.cat(dks, dim=0)
+
+
 def closed_loop_attention_value_step(
     hidden: torch.Tensor,
     weights: dict,
@@ -539,6 +575,7 @@ def closed_loop_attention_value_step(
     window: int = 4096,
     theta: float = 10000.0,
     head_dim: int = 128,
+    hidden_grad: bool = False,
 ):
     """One layer of install_closed_loop_attention
     (train_full_model_closed_loop_vq.py:219-337) followed by backward of a
@@ -547,10 +584,12 @@ def closed_loop_attention_value_step(
     one rounding), the codec's greedy residual VQ on raw K and V (K tables
     frozen), RoPE, repeat_kv, masked SDPA, o_proj, then backward of
     ``d_projected``.  Returns (projected fp16 [B,T,hidden], dL/d value tables
-    fp32 [KVH,S,K,D])."""
+    fp32 [KVH,S,K,D]), and with ``hidden_grad`` also dL/d hidden (through the
+    codec's straight-through edges to raw K and V and the attention's query
+    and key legs)."""
 
     batch, tokens, _ = map(int, hidden.shape)
-    h32 = hidden.float()
+    h32 = hidden.float().requires_grad_(hidden_grad)
 
     def proj(w):
         return (h32 @ w.float().T).half()
@@ -564,16 +603,23 @@ def closed_loop_attention_value_step(
     k_exits, _ = hard_residual_vq_exits(raw_key, key_tables.detach(), prefixes=(depth,),
                                         assignment_whiteners=key_whitener)
     v_exits, _ = hard_residual_vq_exits(raw_value, vt, prefixes=(depth,))
-    khat, vhat = k_exits[depth].detach(), v_exits[depth]
+    khat, vhat = (k_exits[depth] if hidden_grad else k_exits[depth].detach()), v_exits[depth]
     outs = []
     for b in range(batch):
-        qr, kr, mask = _rotated_chunk(query, khat, 0, window, theta, b)
+        pos = torch.arange(tokens)
+        c, s = rotary_cos_sin(pos, head_dim, theta)
+        qr = apply_rotary(query[b : b + 1].float(), c.float()[None, None], s.float()[None, None])
+        kr = apply_rotary(khat[b : b + 1].float(), c.float()[None, None], s.float()[None, None])
+        kr = kr.repeat_interleave(qh // kvh, dim=1)
+        mask = sliding_causal_mask(tokens, window)
         vr = vhat[b : b + 1].repeat_interleave(qh // kvh, dim=1)
-        att = F.scaled_dot_product_attention(qr.float(), kr.float(), vr.float(), attn_mask=mask, dropout_p=0.0)
+        att = F.scaled_dot_product_attention(qr, kr, vr.float(), attn_mask=mask, dropout_p=0.0)
         outs.append(att.to(torch.float16))
     out = torch.cat(outs, dim=0).transpose(1, 2).reshape(batch, tokens, qh * head_dim)
     projected = out.float() @ weights["o"].float().T
     projected.backward(d_projected.float())
+    if hidden_grad:
+        return projected.detach().half(), vt.grad, h32.grad
     return projected.detach().half(), vt.grad
 
 

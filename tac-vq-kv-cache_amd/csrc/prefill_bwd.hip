@@ -46,7 +46,10 @@ struct ValueGradArgs {
   int64_t ksb, ksh, kst;
   const _Float16* dout;
   int64_t dsb, dsh, dst;
-  const float* lse;  // [B,QH,T]
+  const _Float16* v;  // key gradient only: V̂ [B,KVH,T,D]
+  int64_t vsb, vsh, vst;
+  const float* lse;    // [B,QH,T]
+  const float* delta;  // key gradient only: rowsum(dO * O) [B,QH,T]
   int64_t B, QH, KVH, T;
   const int32_t* start;
   int64_t window;
@@ -287,6 +290,574 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
     }
 }
 
+// The same walk for dK̂ (DK = true) of the same attention; DK = false is the
+// value gradient again, kept as the template's reference instance (the value
+// gradient launches prefill_value_grad_kernel above, which the compiler
+// schedules with fewer waits: 522 against 626 us at the config-5 shape):
+//   dP = dO V̂ᵀ, dS = P (dP - delta_row), dK̂_rot += dSᵀ Q_rot / sqrt(D),
+// then the inverse rotary at the key's position.  There the staged dO rows
+// stay row-major (A operand of dP), the wave's V̂ rows join its K̂ as B
+// operands, and Q_rotᵀ for the last product comes from the q operands already
+// in registers by MFMAs against identity columns (exact).
+template <bool DK>
+__global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArgs a) {
+  __shared__ __align__(16) _Float16 q_lds[2][kQTile];
+  __shared__ __align__(16) _Float16 d_lds[2][kDTile];  // dOᵀ [dim][row], or dO rows when DK
+  __shared__ __align__(16) float l_lds[2][kBRows];
+  __shared__ __align__(16) float x_lds[2][kBRows];     // delta (DK)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int NQ = a.nq;
+  const int64_t nkb = ceil_div(a.T, kBKeys);
+  // key blocks fastest: the blocks of one (batch row, kv head) share its q and
+  // dO rows in one XCD's L2
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int chunk = blockIdx.y;  // which run of query tiles of the key block
+  const int64_t kb = bid % (uint32_t)nkb;
+  const int64_t kvh = (bid / (uint32_t)nkb) % (uint32_t)a.KVH;
+  const int64_t b = bid / ((uint32_t)nkb * (uint32_t)a.KVH);
+  const int64_t key0 = kb * kBKeys;
+  const int64_t kw0 = key0 + 32 * wave;  // this wave's first key
+  const int64_t p0 = a.start[b];
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kBD);
+  const int64_t rope_last = a.rope_len - 1;
+  auto rope_row = [&](int64_t pos) -> const _Float16* {
+    return a.rope + (pos < 0 ? 0 : (pos < rope_last ? pos : rope_last)) * kRopeRow;
+  };
+  const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  // ---- the wave's rotated keys as B operands: kop[kt][c] = dims
+  // [32c + 8lg, +8) of key kw0 + 16kt + ln (chunks c and c+2 are rotary
+  // partners) ----
+  half8 kop[2][4];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int64_t key = kw0 + 16 * kt + ln;
+    const bool ok = key < a.T;
+    const _Float16* kp = a.k + b * a.ksb + kvh * a.ksh + (ok ? key : 0) * a.kst;
+    const _Float16* tr = rope_row(p0 + (ok ? key : 0));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int d0 = 32 * c + 8 * lg;
+      half8 cs, sn, r0, r1;
+      load_trig8(tr, d0, &cs, &sn);
+      rope16(*(const half8*)(kp + d0), *(const half8*)(kp + d0 + 64), cs, sn, &r0, &r1);
+      kop[kt][c] = ok ? r0 : zero8;
+      kop[kt][c + 2] = ok ? r1 : zero8;
+    }
+  }
+  // DK: the wave's V̂ rows as B operands, same layout (no rotary), and the
+  // identity columns of the transposing MFMAs
+  half8 vop[2][4], ident[2];
+  if constexpr (DK) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int64_t key = kw0 + 16 * kt + ln;
+      const bool ok = key < a.T;
+      const _Float16* vp = a.v + b * a.vsb + kvh * a.vsh + (ok ? key : 0) * a.vst;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) vop[kt][c] = ok ? *(const half8*)(vp + 32 * c + 8 * lg) : zero8;
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ident[hf][e] = (_Float16)(8 * lg + e == 16 * hf + ln ? 1.f : 0.f);
+  }
+  float4v acc[2][8];  // d[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  // query rows that see some key of the block: [key0, key0 + 127 + window)
+  int64_t rend = key0 + kBKeys - 1 + a.window;
+  if (rend > a.T || rend < 0) rend = a.T;
+  const int64_t all_tiles = ceil_div(rend - key0, kBRows);
+  const int64_t tile_lo = (int64_t)chunk * a.chunk_tiles;
+  int64_t ntiles = all_tiles - tile_lo;
+  if (ntiles > a.chunk_tiles) ntiles = a.chunk_tiles;
+  if (ntiles < 0) ntiles = 0;
+  const int64_t nsteps = ntiles * NQ;
+
+  // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
+  // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
+  // dims [8*(tid/16), +8), stored transposed as (row, row+1) words.  A step
+  // (tile ft, head fh) is addressed as a uniform base plus per-thread offsets
+  // fixed for the whole loop ----
+  const int qr = tid >> 3, qp = tid & 7;
+  const int drp = tid & 15, ddb = tid >> 4;
+  const int64_t q_thr = (int64_t)qr * a.qst + 8 * qp;
+  const int64_t d_thr0 = (int64_t)(2 * drp) * a.dst + 8 * ddb;
+  const int64_t d_thr1 = d_thr0 + a.dst;
+  const _Float16* q_b = a.q + b * a.qsb + kvh * NQ * a.qsh;
+  const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
+  const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
+  struct StepRegs {
+    half8 q0, q1, cs, sn, d0, d1;
+    float l, x;
+  };
+  auto fetch = [&](int ft, int fh, StepRegs& r) {
+    const int64_t r0 = key0 + (tile_lo + ft) * kBRows;
+    const int64_t row = r0 + qr;
+    const bool ok = row < a.T;
+    const _Float16* qrow = ok ? q_b + fh * a.qsh + r0 * a.qst + q_thr : a.q;
+    r.q0 = *(const half8*)qrow;
+    r.q1 = *(const half8*)(qrow + 64);
+    r.q0 = ok ? r.q0 : zero8;
+    r.q1 = ok ? r.q1 : zero8;
+    load_trig8(rope_row(p0 + (ok ? row : 0)), 8 * qp, &r.cs, &r.sn);
+    const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
+    if constexpr (DK) {
+      // dO row qr, dims [8qp, +8) and [8qp + 64, +8), as the q rows
+      const _Float16* drow = ok ? dstep + (int64_t)qr * a.dst + 8 * qp : a.dout;
+      r.d0 = *(const half8*)drow;
+      r.d1 = *(const half8*)(drow + 64);
+      r.d0 = ok ? r.d0 : zero8;
+      r.d1 = ok ? r.d1 : zero8;
+      r.x = tid < kBRows && r0 + tid < a.T ? a.delta[(b * a.QH + kvh * NQ + fh) * a.T + r0 + tid] : 0.f;
+    } else {
+      const bool ok0 = r0 + 2 * drp < a.T, ok1 = r0 + 2 * drp + 1 < a.T;
+      r.d0 = ok0 ? *(const half8*)(dstep + d_thr0) : zero8;
+      r.d1 = ok1 ? *(const half8*)(dstep + d_thr1) : zero8;
+    }
+    r.l = tid < kBRows && r0 + tid < a.T ? l_b[fh * a.T + r0 + tid] * 1.4426950408889634f : 0.f;
+  };
+  auto store = [&](const StepRegs& r, int buf) {
+    half8 r0, r1;
+    rope16(r.q0, r.q1, r.cs, r.sn, &r0, &r1);
+    _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
+    *(half8*)qd = r0;
+    *(half8*)(qd + 64) = r1;
+    if constexpr (DK) {
+      _Float16* dd = d_lds[buf] + qr * kQStride + 8 * qp;
+      *(half8*)dd = r.d0;
+      *(half8*)(dd + 64) = r.d1;
+      if (tid < kBRows) x_lds[buf][tid] = r.x;
+    } else {
+      _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(r.d0, r.d1, e);
+    }
+    if (tid < kBRows) l_lds[buf][tid] = r.l;
+  };
+
+  // step s+1 waits in registers while s is computed and s+2 is in flight;
+  // steps run tile by tile, the group's heads within a tile
+  int ft = 0, fh = 0;  // the next step to fetch
+  auto advance = [&]() {
+    if (++fh == NQ) {
+      fh = 0;
+      ++ft;
+    }
+  };
+  StepRegs nxt;
+  if (nsteps > 0) {
+    StepRegs r;
+    fetch(ft, fh, r);
+    advance();
+    if (nsteps > 1) {
+      fetch(ft, fh, nxt);
+      advance();
+    }
+    store(r, 0);
+  }
+  __syncthreads();
+
+  int ct = 0, ch = 0;  // the step being computed
+  for (int64_t step = 0; step < nsteps; ++step) {
+    const int buf = (int)(step & 1);
+    const bool more = step + 1 < nsteps;
+    StepRegs ahead;
+    if (step + 2 < nsteps) {
+      fetch(ft, fh, ahead);
+      advance();
+    }
+    const int64_t r0 = key0 + (tile_lo + ct) * kBRows;
+    // does any row of the step see any of this wave's keys?
+    const bool any = r0 + kBRows - 1 >= kw0 && r0 - (kw0 + 31) < a.window && kw0 < a.T;
+    if (any) {
+      const _Float16* ql = q_lds[buf];
+      const _Float16* dl = d_lds[buf];
+      // ---- S[row][key]: 2 row tiles x 2 key tiles ----
+      float4v sacc[2][2];
+      // (DK keeps both row tiles' q operands for the transposes; the value
+      // gradient reads them one row tile at a time)
+      half8 qa[DK ? 2 : 1][4];
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg) {
+        half8 (&qr)[4] = qa[DK ? rg : 0];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qr[c] = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            sacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qr[c], kop[kt][c], sacc[rg][kt], 0, 0, 0);
+        }
+      }
+      // DK: dP[row][key] = dO V̂ᵀ (A = the staged dO rows)
+      float4v dpacc[2][2];
+      if constexpr (DK) {
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          half8 da[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) da[c] = *(const half8*)(dl + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            dpacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              dpacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[c], vop[kt][c], dpacc[rg][kt], 0, 0, 0);
+          }
+        }
+      }
+      // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
+      // kw0 + 16kt + ln; pa[kt] contraction slot 4rg + e (of lane group lg)
+      // <-> row 16rg + 4lg + e ----
+      const bool full = r0 >= kw0 + 31 && r0 + kBRows - 1 - kw0 < a.window && r0 + kBRows <= a.T;
+      const int base = (int)(r0 - kw0) + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
+      const int rows_left = (int)(a.T - r0 < kBRows ? a.T - r0 : kBRows);
+      const int keys_left = (int)(a.T - kw0 < 32 ? a.T - kw0 : 32);
+      const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
+      half8 pa[2];
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg) {
+        const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
+        const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
+        float x4[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (DK) {
+          const float4 d4 = *(const float4*)(&x_lds[buf][16 * rg + 4 * lg]);
+          x4[0] = d4.x; x4[1] = d4.y; x4[2] = d4.z; x4[3] = d4.w;
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
+            if (!full) {
+              const int diff = base + 16 * rg + e - 16 * kt;
+              const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
+                               16 * kt + ln < keys_left;
+              p = vis ? p : 0.f;
+            }
+            // DK: dS = P (dP - delta_row) in place of P
+            if constexpr (DK) p *= dpacc[rg][kt][e] - x4[e];
+            pa[kt][4 * rg + e] = (_Float16)p;
+          }
+      }
+      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
+      // {16+4lg..16+4lg+3}.  DK: dK̂_rot += dSᵀ Q_rot, B = Q_rotᵀ from the
+      // transposing MFMAs in the same slot order ----
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        half8 db;
+        if constexpr (DK) {
+#pragma unroll
+          for (int rg = 0; rg < 2; ++rg) {
+            const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[DK ? rg : 0][dt >> 1], ident[dt & 1],
+                                                                   float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) db[4 * rg + e] = (_Float16)t[e];
+          }
+        } else {
+          const _Float16* dr = dl + (16 * dt + ln) * kDStride + 4 * lg;
+          const half4 lo = *(const half4*)dr;
+          const half4 hi = *(const half4*)(dr + 16);
+          db = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
+      }
+    }
+    // ---- the next step into the other buffer ----
+    if (more) store(nxt, buf ^ 1);
+    nxt = ahead;
+    __syncthreads();
+    if (++ch == NQ) {
+      ch = 0;
+      ++ct;
+    }
+  }
+
+  // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
+  // (a chunk with no rows still writes its slot: zeros)
+  float* out = a.dv + (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t key = kw0 + 16 * kt + 4 * lg + e;
+      if (key >= a.T) continue;
+      if constexpr (DK) {
+        // 1/sqrt(D), then the rotary's transpose at the key's position:
+        // dims f and f + 64 (slices dt and dt + 4) are one rotation pair
+        const _Float16* tr = rope_row(p0 + key);
+        const float inv = 1.0f / sqrtf((float)kBD);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const int f = 16 * dt + ln;
+          const float c = (float)tr[f], sn = (float)tr[64 + f];
+          const float lo = acc[kt][dt][e] * inv, hi = acc[kt][dt + 4][e] * inv;
+          out[key * kBD + f] = lo * c + hi * sn;
+          out[key * kBD + 64 + f] = hi * c - lo * sn;
+        }
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) out[key * kBD + 16 * dt + ln] = acc[kt][dt][e];
+      }
+    }
+}
+
+// Query gradient of the same attention, and delta = rowsum(dO * O) that the
+// key gradient needs:
+//   dSᵀ = Pᵀ (dPᵀ - delta_row),  dPᵀ = V̂ dOᵀ,  dQ_rot += dS K̂_rot / sqrt(D),
+// then the rotary's transpose at the row's position.  One workgroup of 4
+// waves per (batch row, kv head, head group, block of query rows) and run of
+// 32-key tiles; wave w is query head w % HW of the group on rows
+// 32 (w / HW) .. + 31 of the block.  Its rotated q and its dO rows stay in
+// registers as B operands; each key tile's rotated K̂ rows and V̂ rows land in
+// LDS once for the four waves.  Per tile and wave, on v_mfma_f32_16x16x32_f16:
+//   Sᵀ[key][row] = K̂ Qᵀ and dPᵀ[key][row] = V̂ dOᵀ   (A = K̂ / V̂ rows from LDS)
+//   dS in A order read straight off the Sᵀ/dPᵀ accumulators (two 16-key
+//   tiles interleaved into the contraction slots)
+//   K̂ in B order from the same K̂ operands by MFMAs against identity columns
+//   dQ[row][dim] += dS K̂
+static const int kQKeys = 32;  // keys per tile
+
+struct QGradArgs {
+  ValueGradArgs g;
+  const _Float16* o;  // forward output [B,QH,T,D] fp16
+  int64_t osb, osh, ost;
+  float* delta;       // [B,QH,T] written
+  float* dq;          // [B,QH,T,D] fp32, or the run's partial slot
+  int32_t heads_per_wg, row_sets, head_groups;
+};
+
+__global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_) {
+  const ValueGradArgs& a = qa_.g;
+  __shared__ __align__(16) _Float16 k_lds[2][kQKeys * kQStride];
+  __shared__ __align__(16) _Float16 v_lds[2][kQKeys * kQStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int HW = qa_.heads_per_wg, RS = qa_.row_sets;
+  const int NQ = a.nq;
+  const int64_t block_rows = 32 * (int64_t)RS;
+  const int64_t nqb = ceil_div(a.T, block_rows);
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int chunk = blockIdx.y;
+  const int64_t qblk = bid % (uint32_t)nqb;
+  const int64_t yz = bid / (uint32_t)nqb;
+  const int64_t gy = a.KVH * qa_.head_groups;
+  const int64_t kvh = (yz % gy) / qa_.head_groups;
+  const int64_t hg = (yz % gy) % qa_.head_groups;
+  const int64_t b = yz / gy;
+  const int64_t head = kvh * NQ + hg * HW + wave % HW;
+  const int64_t wg_row0 = qblk * block_rows;
+  const int64_t row0 = wg_row0 + (wave / HW) * 32;  // the wave's first row
+  const int64_t p0 = a.start[b];
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kBD);
+  const int64_t rope_last = a.rope_len - 1;
+  auto rope_row = [&](int64_t pos) -> const _Float16* {
+    return a.rope + (pos < 0 ? 0 : (pos < rope_last ? pos : rope_last)) * kRopeRow;
+  };
+  const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  // ---- the wave's rotated q and dO rows as B operands (lane (row ln, lg):
+  // dims [32c + 8lg, +8)), its rows' lse (base 2) and delta ----
+  half8 qop[2][4], dop[2][4];
+  float l2[2], dl[2];
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg) {
+    const int64_t row = row0 + 16 * rg + ln;
+    const bool ok = row < a.T;
+    const _Float16* qp = a.q + b * a.qsb + head * a.qsh + (ok ? row : 0) * a.qst;
+    const _Float16* dp = a.dout + b * a.dsb + head * a.dsh + (ok ? row : 0) * a.dst;
+    const _Float16* op = qa_.o + b * qa_.osb + head * qa_.osh + (ok ? row : 0) * qa_.ost;
+    const _Float16* tr = rope_row(p0 + (ok ? row : 0));
+    float dsum = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int d0 = 32 * c + 8 * lg;
+      half8 cs, sn, r0, r1;
+      load_trig8(tr, d0, &cs, &sn);
+      rope16(*(const half8*)(qp + d0), *(const half8*)(qp + d0 + 64), cs, sn, &r0, &r1);
+      qop[rg][c] = ok ? r0 : zero8;
+      qop[rg][c + 2] = ok ? r1 : zero8;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const half8 dv = *(const half8*)(dp + 32 * c + 8 * lg);
+      const half8 ov = *(const half8*)(op + 32 * c + 8 * lg);
+      dop[rg][c] = ok ? dv : zero8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum = fmaf((float)dv[e], (float)ov[e], dsum);
+    }
+    dsum += __shfl_xor(dsum, 16);
+    dsum += __shfl_xor(dsum, 32);
+    dl[rg] = ok ? dsum : 0.f;
+    l2[rg] = ok ? a.lse[(b * a.QH + head) * a.T + row] * 1.4426950408889634f : 0.f;
+    if (ok && lg == 0 && chunk == 0) qa_.delta[(b * a.QH + head) * a.T + row] = dsum;
+  }
+  half8 ident[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ident[hf][e] = (_Float16)(8 * lg + e == 16 * hf + ln ? 1.f : 0.f);
+  float4v acc[2][8];  // dQ_rot[row 16rg + 4lg + e][dim 16dt + ln]
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[rg][dt] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  // ---- the key tiles the block's rows see: [wg_row0 - window + 1, wg_row1) ----
+  int64_t wg_row1 = wg_row0 + block_rows;
+  if (wg_row1 > a.T) wg_row1 = a.T;
+  int64_t kmin = wg_row0 - a.window + 1;
+  if (kmin < 0) kmin = 0;
+  const int64_t t_first = kmin / kQKeys;
+  const int64_t all_tiles = ceil_div(wg_row1, kQKeys) - t_first;
+  const int64_t tile_lo = (int64_t)chunk * a.chunk_tiles;
+  int64_t ntiles = all_tiles - tile_lo;
+  if (ntiles > a.chunk_tiles) ntiles = a.chunk_tiles;
+  if (ntiles < 0) ntiles = 0;
+
+  // ---- tile loaders: thread -> key tid/8, rotary chunk pair (p, p+8),
+  // p = tid%8: rotated K̂ and plain V̂ ----
+  const int kr = tid >> 3, kp = tid & 7;
+  const _Float16* kb_ = a.k + b * a.ksb + kvh * a.ksh;
+  const _Float16* vb_ = a.v + b * a.vsb + kvh * a.vsh;
+  struct TileRegs {
+    half8 k0, k1, v0, v1, cs, sn;
+  };
+  auto fetch = [&](int64_t tile, TileRegs& r) {
+    const int64_t key = (t_first + tile_lo + tile) * kQKeys + kr;
+    const bool ok = key < a.T;
+    const _Float16* kp_ = kb_ + (ok ? key : 0) * a.kst + 8 * kp;
+    const _Float16* vp_ = vb_ + (ok ? key : 0) * a.vst + 8 * kp;
+    r.k0 = ok ? *(const half8*)kp_ : zero8;
+    r.k1 = ok ? *(const half8*)(kp_ + 64) : zero8;
+    r.v0 = ok ? *(const half8*)vp_ : zero8;
+    r.v1 = ok ? *(const half8*)(vp_ + 64) : zero8;
+    load_trig8(rope_row(p0 + (ok ? key : 0)), 8 * kp, &r.cs, &r.sn);
+  };
+  auto store = [&](const TileRegs& r, int buf) {
+    half8 r0, r1;
+    rope16(r.k0, r.k1, r.cs, r.sn, &r0, &r1);
+    _Float16* kd = k_lds[buf] + kr * kQStride + 8 * kp;
+    *(half8*)kd = r0;
+    *(half8*)(kd + 64) = r1;
+    _Float16* vd = v_lds[buf] + kr * kQStride + 8 * kp;
+    *(half8*)vd = r.v0;
+    *(half8*)(vd + 64) = r.v1;
+  };
+  if (ntiles > 0) {
+    TileRegs r;
+    fetch(0, r);
+    store(r, 0);
+  }
+  __syncthreads();
+  const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
+
+  for (int64_t tile = 0; tile < ntiles; ++tile) {
+    const int buf = (int)(tile & 1);
+    const bool more = tile + 1 < ntiles;
+    TileRegs nxt;
+    if (more) fetch(tile + 1, nxt);
+    const int64_t key0 = (t_first + tile_lo + tile) * kQKeys;
+    const bool any = key0 <= row0 + 31 && row0 - (key0 + kQKeys - 1) < a.window;
+    if (any) {
+      const _Float16* kl = k_lds[buf];
+      const _Float16* vl = v_lds[buf];
+      // ---- Sᵀ and dPᵀ [key][row]: 2 key tiles x 2 row tiles ----
+      half8 ka[2][4];
+      float4v st[2][2], dpt[2][2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        half8 va[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          ka[kt][c] = *(const half8*)(kl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
+          va[c] = *(const half8*)(vl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
+        }
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          st[kt][rg] = float4v{0.f, 0.f, 0.f, 0.f};
+          dpt[kt][rg] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            st[kt][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][c], qop[rg][c], st[kt][rg], 0, 0, 0);
+            dpt[kt][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[c], dop[rg][c], dpt[kt][rg], 0, 0, 0);
+          }
+        }
+      }
+      // ---- dS, masked: element (kt, rg, e) is key key0 + 16kt + 4lg + e of
+      // row row0 + 16rg + ln; dsa[rg] contraction slot 4kt + e (of lane group
+      // lg) <-> key 16kt + 4lg + e ----
+      const bool full = key0 + kQKeys - 1 <= row0 && row0 + 31 - key0 < a.window && row0 + 32 <= a.T;
+      const int base = (int)(row0 - key0) + ln - 4 * lg;  // row - key = base + 16rg - 16kt - e
+      const int rows_left = (int)(a.T - row0 < 32 ? a.T - row0 : 32);
+      half8 dsa[2];
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(st[kt][rg][e], scale2, -l2[rg]));
+            if (!full) {
+              const int diff = base + 16 * rg - 16 * kt - e;
+              const bool vis = diff >= 0 && diff < win && 16 * rg + ln < rows_left;
+              p = vis ? p : 0.f;
+            }
+            dsa[rg][4 * kt + e] = (_Float16)(p * (dpt[kt][rg][e] - dl[rg]));
+          }
+      // ---- dQ += dS K̂: B = K̂ in B order (keys {4lg+e, 16+4lg+e} of dim
+      // 16dt + ln) from the identity MFMAs ----
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        half8 kbo;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][dt >> 1], ident[dt & 1],
+                                                                 float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) kbo[4 * kt + e] = (_Float16)t[e];
+        }
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg)
+          acc[rg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dsa[rg], kbo, acc[rg][dt], 0, 0, 0);
+      }
+    }
+    if (more) store(nxt, buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- 1/sqrt(D), the rotary's transpose at the row's position, store:
+  // lane holds dims 16dt + ln of rows row0 + 16rg + 4lg + e ----
+  float* out = qa_.dq + (int64_t)chunk * a.slot_stride + ((b * a.QH + head) * a.T) * kBD;
+  const float inv = 1.0f / sqrtf((float)kBD);
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t row = row0 + 16 * rg + 4 * lg + e;
+      if (row >= a.T) continue;
+      const _Float16* tr = rope_row(p0 + row);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int f = 16 * dt + ln;
+        const float c = (float)tr[f], sn = (float)tr[64 + f];
+        const float lo = acc[rg][dt][e] * inv, hi = acc[rg][dt + 4][e] * inv;
+        out[row * kBD + f] = lo * c + hi * sn;
+        out[row * kBD + 64 + f] = hi * c - lo * sn;
+      }
+    }
+}
+
 // dV̂ = the sum of the chunks' partial slots, in chunk order
 __global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dv, int64_t n4,
@@ -327,6 +898,72 @@ int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T
   return chunks > 1 ? (int64_t)chunks * B * KVH * T * kBD * (int64_t)sizeof(float) : 0;
 }
 
+}  // extern "C"
+
+namespace jkv {
+
+// shared by the value and key gradients: checks, the row runs, the launch and
+// the reduction of the runs' partial slots
+template <bool DK>
+static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[12], int nstrides,
+                          const void* rope_table, float* d_out_buf, void* workspace, int64_t workspace_bytes,
+                          hipStream_t stream) {
+  const int64_t B = a.B, QH = a.QH, KVH = a.KVH, T = a.T;
+  JKV_CHECK_ARG(D == kBD, "prefill gradients support head_dim 128, got %lld", (long long)D);
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
+  const int64_t NQ = QH / KVH;
+  JKV_CHECK_ARG(NQ <= 64, "at most 64 query heads per kv head, got %lld", (long long)NQ);
+  JKV_CHECK_ARG(a.window >= 1, "window must be positive");
+  if (B == 0 || T == 0) return JKV_OK;
+  JKV_CHECK_ARG(a.q && a.k && a.dout && a.lse && d_out_buf && a.start && rope_table, "null buffer");
+  JKV_CHECK_ARG(!DK || (a.v && a.delta), "null buffer");
+  JKV_CHECK_ARG(a.rope_len >= 1, "rotary table is empty");
+  for (int i = 0; i < nstrides; ++i)
+    JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");
+  JKV_CHECK_ARG(((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.dout | (uintptr_t)d_out_buf |
+                 (uintptr_t)(DK ? a.v : a.q)) % 16 == 0,
+                "prefill buffers must be 16-byte aligned");
+  a.rope = (const _Float16*)rope_table;
+  a.nq = (int32_t)NQ;
+  int chunk_tiles, chunks;
+  value_grad_chunks(T, a.window, &chunk_tiles, &chunks);
+  a.chunk_tiles = chunk_tiles;
+  const int64_t n = B * KVH * T * kBD;
+  if (chunks > 1) {
+    const int64_t need = (int64_t)chunks * n * (int64_t)sizeof(float);
+    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
+                  (long long)need);
+    JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
+    a.dv = (float*)workspace;
+    a.slot_stride = n;
+  } else {
+    a.dv = d_out_buf;
+    a.slot_stride = 0;
+  }
+  const int64_t blocks = ceil_div(T, kBKeys) * KVH * B;
+  JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
+  if constexpr (DK) {
+    hipLaunchKernelGGL(prefill_kv_grad_kernel<true>, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL(prefill_value_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
+                       stream, a);
+  }
+  JKV_CHECK_LAUNCH();
+  if (chunks > 1) {
+    const int64_t n4 = n / 4;
+    hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
+                       (const float*)workspace, d_out_buf, n4, n4, chunks);
+    JKV_CHECK_LAUNCH();
+  }
+  return JKV_OK;
+}
+
+}  // namespace jkv
+
+extern "C" {
+
 int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                      int64_t q_stride_t, const void* k, int64_t k_stride_b,
                                      int64_t k_stride_h, int64_t k_stride_t, const void* d_out,
@@ -336,21 +973,6 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
                                      const void* rope_table, int64_t rope_len, float* d_value,
                                      void* workspace, int64_t workspace_bytes, jkv_stream_t stream_) {
   using namespace jkv;
-  hipStream_t stream = (hipStream_t)stream_;
-  JKV_CHECK_ARG(D == kBD, "prefill value gradient supports head_dim 128, got %lld", (long long)D);
-  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
-  const int64_t NQ = QH / KVH;
-  JKV_CHECK_ARG(NQ <= 64, "at most 64 query heads per kv head, got %lld", (long long)NQ);
-  JKV_CHECK_ARG(window >= 1, "window must be positive");
-  if (B == 0 || T == 0) return JKV_OK;
-  JKV_CHECK_ARG(q && k && d_out && lse && d_value && start_positions && rope_table, "null buffer");
-  JKV_CHECK_ARG(rope_len >= 1, "rotary table is empty");
-  const int64_t strides[9] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h,
-                              k_stride_t, d_stride_b, d_stride_h, d_stride_t};
-  for (int i = 0; i < 9; ++i)
-    JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");
-  JKV_CHECK_ARG(((uintptr_t)q | (uintptr_t)k | (uintptr_t)d_out | (uintptr_t)d_value) % 16 == 0,
-                "prefill buffers must be 16-byte aligned");
   ValueGradArgs a = {};
   a.q = (const _Float16*)q; a.qsb = q_stride_b; a.qsh = q_stride_h; a.qst = q_stride_t;
   a.k = (const _Float16*)k; a.ksb = k_stride_b; a.ksh = k_stride_h; a.kst = k_stride_t;
@@ -359,35 +981,136 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
   a.B = B; a.QH = QH; a.KVH = KVH; a.T = T;
   a.start = start_positions;
   a.window = window;
-  a.rope = (const _Float16*)rope_table;
   a.rope_len = rope_len;
-  a.nq = (int32_t)NQ;
+  const int64_t strides[12] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h, k_stride_t,
+                               d_stride_b, d_stride_h, d_stride_t, 0, 0, 0};
+  return launch_kv_grad<false>(a, D, strides, 9, rope_table, d_value, workspace, workspace_bytes,
+                               (hipStream_t)stream_);
+}
+
+int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                                   const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                                   const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                                   const void* d_out, int64_t d_stride_b, int64_t d_stride_h,
+                                   int64_t d_stride_t, const float* lse, const float* delta, int64_t B,
+                                   int64_t QH, int64_t KVH, int64_t T, int64_t D,
+                                   const int32_t* start_positions, int64_t window, const void* rope_table,
+                                   int64_t rope_len, float* d_key, void* workspace, int64_t workspace_bytes,
+                                   jkv_stream_t stream_) {
+  using namespace jkv;
+  ValueGradArgs a = {};
+  a.q = (const _Float16*)q; a.qsb = q_stride_b; a.qsh = q_stride_h; a.qst = q_stride_t;
+  a.k = (const _Float16*)k; a.ksb = k_stride_b; a.ksh = k_stride_h; a.kst = k_stride_t;
+  a.v = (const _Float16*)v; a.vsb = v_stride_b; a.vsh = v_stride_h; a.vst = v_stride_t;
+  a.dout = (const _Float16*)d_out; a.dsb = d_stride_b; a.dsh = d_stride_h; a.dst = d_stride_t;
+  a.lse = lse;
+  a.delta = delta;
+  a.B = B; a.QH = QH; a.KVH = KVH; a.T = T;
+  a.start = start_positions;
+  a.window = window;
+  a.rope_len = rope_len;
+  const int64_t strides[12] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h, k_stride_t,
+                               v_stride_b, v_stride_h, v_stride_t, d_stride_b, d_stride_h, d_stride_t};
+  return launch_kv_grad<true>(a, D, strides, 12, rope_table, d_key, workspace, workspace_bytes,
+                              (hipStream_t)stream_);
+}
+
+int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window) {
+  using namespace jkv;
+  if (B <= 0 || QH <= 0 || KVH <= 0 || T <= 0 || window < 1) return 0;
   int chunk_tiles, chunks;
   value_grad_chunks(T, window, &chunk_tiles, &chunks);
-  a.chunk_tiles = chunk_tiles;
-  const int64_t n = B * KVH * T * kBD;
-  if (chunks > 1) {
-    const int64_t need = jkv_prefill_value_grad_workspace_bytes(B, KVH, T, window);
-    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                  "value gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
-                  (long long)need);
-    JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
-    a.dv = (float*)workspace;
-    a.slot_stride = n;
-  } else {
-    a.dv = d_value;
-    a.slot_stride = 0;
-  }
-  const int64_t blocks = ceil_div(T, kBKeys) * KVH * B;
-  JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-  hipLaunchKernelGGL(prefill_value_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
-                     stream, a);
-  JKV_CHECK_LAUNCH();
-  if (chunks > 1) {
-    const int64_t n4 = n / 4;
-    hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
-                       (const float*)workspace, d_value, n4, n4, chunks);
+  const int64_t delta = ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
+  return delta + (int64_t)chunks * B * QH * T * kBD * (int64_t)sizeof(float);
+}
+
+int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                                   const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                                   const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                                   const void* out, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_t,
+                                   const void* d_out, int64_t d_stride_b, int64_t d_stride_h,
+                                   int64_t d_stride_t, const float* lse, int64_t B, int64_t QH, int64_t KVH,
+                                   int64_t T, int64_t D, const int32_t* start_positions, int64_t window,
+                                   const void* rope_table, int64_t rope_len, float* d_query, float* d_key,
+                                   float* d_value, void* workspace, int64_t workspace_bytes,
+                                   jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(D == kBD, "prefill gradients support head_dim 128, got %lld", (long long)D);
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
+  JKV_CHECK_ARG(window >= 1, "window must be positive");
+  if (B == 0 || T == 0 || (!d_query && !d_key && !d_value)) return JKV_OK;
+  const int64_t need = jkv_prefill_backward_workspace_bytes(B, QH, KVH, T, window);
+  JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace) % 16 == 0,
+                "prefill backward needs %lld bytes of 16-byte aligned workspace", (long long)need);
+  const int64_t NQ = QH / KVH;
+  float* delta = (float*)workspace;
+  unsigned char* slots = (unsigned char*)workspace + ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
+  const int64_t slot_bytes = workspace_bytes - (slots - (unsigned char*)workspace);
+  ValueGradArgs g = {};
+  g.q = (const _Float16*)q; g.qsb = q_stride_b; g.qsh = q_stride_h; g.qst = q_stride_t;
+  g.k = (const _Float16*)k; g.ksb = k_stride_b; g.ksh = k_stride_h; g.kst = k_stride_t;
+  g.v = (const _Float16*)v; g.vsb = v_stride_b; g.vsh = v_stride_h; g.vst = v_stride_t;
+  g.dout = (const _Float16*)d_out; g.dsb = d_stride_b; g.dsh = d_stride_h; g.dst = d_stride_t;
+  g.lse = lse;
+  g.delta = delta;
+  g.B = B; g.QH = QH; g.KVH = KVH; g.T = T;
+  g.start = start_positions;
+  g.window = window;
+  g.rope_len = rope_len;
+  const int64_t strides[12] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h, k_stride_t,
+                               v_stride_b, v_stride_h, v_stride_t, d_stride_b, d_stride_h, d_stride_t};
+  // ---- dQ and delta: the query kernel; its runs are summed into d_query
+  // (they stay in the slots when only delta is wanted) ----
+  if (d_query || d_key) {
+    JKV_CHECK_ARG(q && k && v && out && d_out && lse && start_positions && rope_table && rope_len >= 1,
+                  "null buffer");
+    for (int i = 0; i < 12; ++i)
+      JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");
+    JKV_CHECK_ARG(o_stride_b % 8 == 0 && o_stride_h % 8 == 0 && o_stride_t % 8 == 0,
+                  "prefill strides must be multiples of 8 elements");
+    JKV_CHECK_ARG(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)d_out |
+                   (uintptr_t)(d_query ? d_query : (float*)slots)) % 16 == 0,
+                  "prefill buffers must be 16-byte aligned");
+    // four waves: head w % HW on rows 32 (w / HW) of the block
+    JKV_CHECK_ARG(NQ < 4 || NQ % 4 == 0, "query heads per kv head must be 1, 2 or a multiple of 4");
+    QGradArgs qa = {};
+    qa.g = g;
+    qa.g.rope = (const _Float16*)rope_table;
+    qa.g.nq = (int32_t)NQ;
+    qa.o = (const _Float16*)out; qa.osb = o_stride_b; qa.osh = o_stride_h; qa.ost = o_stride_t;
+    qa.delta = delta;
+    qa.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
+    qa.row_sets = 4 / qa.heads_per_wg;
+    qa.head_groups = (int32_t)(NQ / qa.heads_per_wg);
+    int chunk_tiles, chunks;
+    value_grad_chunks(T, window, &chunk_tiles, &chunks);
+    qa.g.chunk_tiles = chunk_tiles;
+    const int64_t n = B * QH * T * kBD;
+    JKV_CHECK_ARG(slot_bytes >= (int64_t)chunks * n * (int64_t)sizeof(float), "workspace too small");
+    const bool direct = chunks == 1 && d_query != nullptr;
+    qa.dq = direct ? d_query : (float*)slots;
+    qa.g.slot_stride = direct ? 0 : n;
+    const int64_t nqb = ceil_div(T, 32 * (int64_t)qa.row_sets);
+    const int64_t blocks = nqb * KVH * qa.head_groups * B;
+    JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
+    hipLaunchKernelGGL(prefill_q_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
+                       stream, qa);
     JKV_CHECK_LAUNCH();
+    if (!direct && d_query != nullptr) {
+      const int64_t n4 = n / 4;
+      hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
+                         (const float*)slots, d_query, n4, n4, chunks);
+      JKV_CHECK_LAUNCH();
+    }
+  }
+  if (d_key) {
+    const int rc = launch_kv_grad<true>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream);
+    if (rc != JKV_OK) return rc;
+  }
+  if (d_value) {
+    const int rc = launch_kv_grad<false>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream);
+    if (rc != JKV_OK) return rc;
   }
   return JKV_OK;
 }

@@ -78,6 +78,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
     ),
     "jkv_prefill_value_grad_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "jkv_prefill_attention_backward": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+         _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+         _vp, _i64, _vp],
+    ),
+    "jkv_prefill_backward_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "jkv_prefill_attention_key_grad": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+         _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
+    ),
     "jkv_rope_table": (ctypes.c_int, [_vp, _i64, _vp, _vp]),
     "jkv_f32_to_f16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
 }

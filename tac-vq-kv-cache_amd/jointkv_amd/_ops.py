@@ -475,6 +475,51 @@ def prefill_attention(
     return out
 
 
+def prefill_attention_backward(
+    q: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    out: torch.Tensor,
+    d_out: torch.Tensor,
+    lse: torch.Tensor,
+    start_positions: torch.Tensor,
+    *,
+    window: int,
+    rope_theta: float,
+    max_position: int,
+    need: tuple[bool, bool, bool] = (True, True, True),
+):
+    """Gradients of :func:`prefill_attention` with respect to the pre-RoPE
+    ``q``, ``key`` and ``value`` (fp32; ``None`` where ``need`` is False),
+    from the forward's ``out`` and ``lse`` and the output gradient."""
+
+    if key.shape != value.shape:
+        raise ValueError("prefill query/key/value geometry differs")
+    device, (q, key, value), start_positions, (batch, qheads, kvheads, tokens) = _prefill_operands(
+        q, key, value, start_positions, "value")
+    _d, (out, _k, d_out), _s, _g = _prefill_operands(out, key, d_out, start_positions, "output gradient")
+    if d_out.shape != q.shape or out.shape != q.shape:
+        raise ValueError("the output and its gradient must have the query's shape")
+    if lse.dtype != torch.float32 or lse.shape != (batch, qheads, tokens) or not lse.is_contiguous():
+        raise ValueError("lse must be a contiguous fp32 [B,QH,T] tensor")
+    table = rope_table(device, rope_theta, int(max_position) + 1)
+    grads = [torch.empty(shape, dtype=torch.float32, device=device) if want else None
+             for want, shape in zip(need, ((batch, qheads, tokens, 128), (batch, kvheads, tokens, 128),
+                                           (batch, kvheads, tokens, 128)))]
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_prefill_backward_workspace_bytes(batch, qheads, kvheads, tokens, int(window)))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    code = lib.jkv_prefill_attention_backward(
+        q.data_ptr(), *q.stride()[:3], key.data_ptr(), *key.stride()[:3], value.data_ptr(), *value.stride()[:3],
+        out.data_ptr(), *out.stride()[:3], d_out.data_ptr(), *d_out.stride()[:3], lse.data_ptr(),
+        batch, qheads, kvheads, tokens, 128, start_positions.data_ptr(), int(window), table.data_ptr(),
+        int(table.shape[0]), *[_lib.ptr(g) for g in grads], workspace.data_ptr(), ws_bytes,
+        _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return tuple(grads)
+
+
 def prefill_attention_value_grad(
     q: torch.Tensor,
     key: torch.Tensor,

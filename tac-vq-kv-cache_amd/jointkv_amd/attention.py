@@ -145,20 +145,18 @@ def prefill_attention(
 
     batch, _qh, tokens, _d = map(int, query.shape)
     starts, top = _start_tensor(start_positions, batch, tokens, query.device)
-    if torch.is_grad_enabled() and (query.requires_grad or key.requires_grad):
-        raise NotImplementedError(
-            "prefill attention differentiates only with respect to value (the V-only step freezes "
-            "the backbone and the K tables); detach query and key")
-    if torch.is_grad_enabled() and value.requires_grad:
+    if torch.is_grad_enabled() and (query.requires_grad or key.requires_grad or value.requires_grad):
         return _PrefillAttention.apply(query, key, value, starts, window, rope_theta, top)
     return _ops.prefill_attention(query, key, value, starts, window=window, rope_theta=rope_theta,
                                   max_position=top)
 
 
 class _PrefillAttention(torch.autograd.Function):
-    """Prefill attention whose backward is the value leg of the SDPA
-    backward (HIP): the forward keeps each row's log-sum-exp, the backward
-    recomputes P from it and forms dV̂ = Pᵀ dO summed over the GQA group."""
+    """Prefill attention with a HIP backward: the forward keeps each row's
+    log-sum-exp; the backward recomputes P from it.  Only the value is
+    needed: dV̂ = Pᵀ dO summed over the GQA group (the V-only step).  Query
+    or key too: the full backward (dS = P (dO V̂ᵀ - rowsum(dO O)), dQ = dS K̂,
+    dK̂ = dSᵀ Q, through the rotary's transpose)."""
 
     @staticmethod
     def forward(ctx, query, key, value, starts, window, rope_theta, top):
@@ -166,18 +164,29 @@ class _PrefillAttention(torch.autograd.Function):
         lse = torch.empty((batch, qheads, tokens), dtype=torch.float32, device=query.device)
         out = _ops.prefill_attention(query, key, value, starts, window=window, rope_theta=rope_theta,
                                      max_position=top, lse=lse)
-        ctx.save_for_backward(query, key, lse, starts)
-        ctx.params = (window, rope_theta, top, value.dtype)
+        ctx.save_for_backward(query, key, value, out, lse, starts)
+        ctx.params = (window, rope_theta, top)
         return out
 
     @staticmethod
     def backward(ctx, d_out):
-        query, key, lse, starts = ctx.saved_tensors
-        window, rope_theta, top, dtype = ctx.params
-        d_value = _ops.prefill_attention_value_grad(query, key, d_out.to(torch.float16), lse, starts,
-                                                    window=window, rope_theta=rope_theta, max_position=top)
-        # the value's dtype, as SDPA's backward returns it (fp32 sum, one rounding)
-        return None, None, d_value.to(dtype), None, None, None, None
+        query, key, value, out, lse, starts = ctx.saved_tensors
+        window, rope_theta, top = ctx.params
+        need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        d_out = d_out.to(torch.float16)
+        if need_q or need_k:
+            dq, dk, dv = _ops.prefill_attention_backward(
+                query, key, value, out, d_out, lse, starts, window=window, rope_theta=rope_theta,
+                max_position=top, need=(need_q, need_k, need_v))
+        else:
+            dq = dk = None
+            dv = _ops.prefill_attention_value_grad(query, key, d_out, lse, starts, window=window,
+                                                   rope_theta=rope_theta, max_position=top)
+        # each input's dtype, as SDPA's backward returns it (fp32 sums, one rounding)
+        return (dq.to(query.dtype) if dq is not None else None,
+                dk.to(key.dtype) if dk is not None else None,
+                dv.to(value.dtype) if (dv is not None and need_v) else None,
+                None, None, None, None)
 
 
 def prefill_attention_from_codes(

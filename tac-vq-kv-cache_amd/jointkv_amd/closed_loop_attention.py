@@ -12,10 +12,11 @@ prefill kernel, and ``loss.backward()`` reaches the value tables through
 its HIP value gradient (dV̂ = Pᵀ dO) and the codec's HIP scatter-add: the
 V-only step's real upstream gradient, rather than a synthetic dL/dV̂.
 
-Only the value path is differentiable: the V-only step freezes the backbone
-and the K tables, and the query/key legs of the attention backward (needed
-to carry the gradient into lower layers' hidden states) are not built, so
-``hidden`` must not require grad.
+The attention's backward is HIP too: the value leg alone when only the
+tables need gradients, the full backward (query and key legs through the
+rotary) when the hidden states require grad, so that stacked layers carry
+the gradient down to lower layers' value tables as the reference's 32-layer
+trajectory does.
 """
 
 from __future__ import annotations
@@ -78,9 +79,6 @@ def closed_loop_attention(
     ``trajectory_epsilon`` also the layer's trajectory-match loss against the
     same attention on raw K/V (train_full_model_closed_loop_vq.py:304-334)."""
 
-    if hidden.requires_grad and torch.is_grad_enabled():
-        raise NotImplementedError("closed-loop attention differentiates only into the value tables; "
-                                  "the hidden states must not require grad")
     batch, tokens, _ = map(int, hidden.shape)
     d = weights.head_dim
     query = F.linear(hidden, weights.q).view(batch, tokens, weights.query_heads, d).transpose(1, 2)

@@ -64,7 +64,7 @@ def test_lse_and_value_grad_match_oracle(device, batch, qh, kvh, tokens, starts,
     assert torch.equal(dv, again)
 
 
-def test_autograd_value_path_and_refusals(device):
+def test_autograd_value_path(device):
     q, k, v, d = _case(31, 1, 8, 2, 64)
     qd, kd, dd = q.to(device), k.to(device), d.to(device)
     vd = v.to(device).requires_grad_(True)
@@ -73,8 +73,30 @@ def test_autograd_value_path_and_refusals(device):
     assert vd.grad.dtype == torch.float16
     dv_ref = ref.prefill_value_grad(q, k, v, d, (0,), window=4096)
     assert float((vd.grad.cpu().float() - dv_ref).abs().max()) <= DV_RTOL * float(dv_ref.abs().max())
-    with pytest.raises(NotImplementedError, match="value"):
-        jkv.prefill_attention(qd.clone().requires_grad_(True), kd, vd, 0)
+
+
+@pytest.mark.parametrize("batch,qh,kvh,tokens,starts,window", [
+    (1, 32, 8, 200, (0,), 4096),        # Mistral GQA 4
+    (2, 8, 2, 301, (0, 5000), 64),      # window binds, later positions, ragged tiles
+    (1, 4, 4, 70, (17,), 4096),         # one query head per kv head
+    (1, 4, 2, 45, (3,), 4096),          # GQA 2
+    (1, 16, 2, 96, (0,), 4096),         # GQA 8: two head groups per kv head
+    (1, 8, 2, 600, (0,), 4096),         # rows and keys split in runs (workspace + reduce)
+])
+def test_full_backward_matches_oracle(device, batch, qh, kvh, tokens, starts, window):
+    print(f"backward B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)
+    q, k, v, d = _case(1900 + tokens, batch, qh, kvh, tokens)
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    out = jkv.prefill_attention(qd, kd, vd, list(starts), window=window)
+    out.backward(d.to(device))
+    dq_ref, dk_ref = ref.prefill_qk_grad(q, k, v, d, starts, window=window)
+    dv_ref = ref.prefill_value_grad(q, k, v, d, starts, window=window)
+    for name, got, want in (("dq", qd.grad, dq_ref), ("dk", kd.grad, dk_ref), ("dv", vd.grad, dv_ref)):
+        assert got.dtype == torch.float16
+        scale = float(want.abs().max())
+        err = float((got.cpu().float() - want).abs().max())
+        print(f"  {name} err {err:.2e} of {scale:.2e}", flush=True)
+        assert err <= DV_RTOL * scale + 1e-3, f"{name} max abs error {err} (scale {scale})"
 
 
 @pytest.mark.parametrize("tokens,stages,whitened", [(96, 2, False), (150, 4, True)])
@@ -110,3 +132,28 @@ def test_closed_loop_attention_value_step(device, tokens, stages, whitened):
     assert traj >= 0.0 and traj == traj
     # the frozen K tables take no gradient
     assert codec.key_tables[0].grad is None
+
+
+def test_closed_loop_attention_hidden_gradient(device):
+    # hidden states that require grad: the attention's query and key legs
+    # carry dL/d hidden down (as to a lower layer in the 32-layer trajectory)
+    gen = torch.Generator().manual_seed(515)
+    tokens, stages, hidden_size, kvh = 80, 2, 512, 1
+    hidden = (torch.randn(1, tokens, hidden_size, generator=gen) * 0.5).half()
+    w = {name: (torch.randn(rows, hidden_size, generator=gen) / hidden_size ** 0.5).half()
+         for name, rows in (("q", hidden_size), ("k", 128 * kvh), ("v", 128 * kvh), ("o", hidden_size))}
+    sig = tuple(0.8 ** s for s in range(stages))
+    ktab = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1) * 0.5
+    vtab = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1) * 0.5
+    d_proj = (torch.randn(1, tokens, hidden_size, generator=gen) * 0.1).half()
+    codec = jkv.ClosedLoopUniformResidualVQ([ktab], [vtab], [None], depth=stages, dynamic_bpa=1.0).to(device)
+    weights = AttentionWeights(*(w[n].to(device) for n in ("q", "k", "v", "o")))
+    hd = hidden.to(device).requires_grad_(True)
+    projected = closed_loop_attention(hd, weights, codec, 0)
+    projected.backward(d_proj.to(device))
+    _out, expect_grad, expect_hidden = ref.closed_loop_attention_value_step(
+        hidden, w, ktab, vtab, d_proj, depth=stages, hidden_grad=True)
+    rel_t = float((codec.value_tables[0].grad.cpu() - expect_grad).norm() / expect_grad.norm())
+    rel_h = float((hd.grad.cpu().float() - expect_hidden).norm() / expect_hidden.norm())
+    print(f"  table-grad relative error {rel_t:.2e}  hidden-grad relative error {rel_h:.2e}", flush=True)
+    assert rel_t <= STEP_RTOL and rel_h <= STEP_RTOL

@@ -301,6 +301,37 @@ def test_prefill_lse_and_value_grad_against_fp64_closed_form():
         np.testing.assert_allclose(dv[b].double().numpy(), expect.numpy(), rtol=1e-4, atol=1e-5)
 
 
+def test_prefill_qk_grad_against_fp64_closed_form():
+    # dS = P (dO V^T - rowsum(dO * O)); dq_rot = dS K_rot / sqrt(D) and
+    # dk_rot = dS^T Q_rot / sqrt(D) summed over the group; then the rotary's
+    # transpose: d_i = r_i cos + r_{i+64} sin, d_{i+64} = r_{i+64} cos - r_i sin
+    gen = torch.Generator().manual_seed(6)
+    T, window = 29, 11
+    q = torch.randn(1, 4, T, 128, generator=gen).half()
+    k = torch.randn(1, 2, T, 128, generator=gen).half()
+    v = torch.randn(1, 2, T, 128, generator=gen).half()
+    d_out = torch.randn(1, 4, T, 128, generator=gen).half()
+    dq, dk = ref.prefill_qk_grad(q, k, v, d_out, (70,), window=window)
+    pos = torch.arange(T) + 70
+    c, s = ref.rotary_cos_sin(pos, 128, 10000.0)
+    c, s = c.double(), s.double()
+    rot = lambda x: x * c + torch.cat((-x[..., 64:], x[..., :64]), -1) * s
+    unrot = lambda r: r * c + torch.cat((r[..., 64:], -r[..., :64]), -1) * s
+    mask = ref.sliding_causal_mask(T, window)
+    qr, kr = rot(q[0].double()), rot(k[0].double())
+    dk_rot = torch.zeros(2, T, 128, dtype=torch.float64)
+    for h in range(4):
+        scores = (qr[h] @ kr[h // 2].T / math.sqrt(128)).masked_fill(~mask, float("-inf"))
+        p = torch.softmax(scores, -1)
+        o = p @ v[0, h // 2].double()
+        dov = d_out[0, h].double()
+        ds = p * (dov @ v[0, h // 2].double().T - (dov * o).sum(-1, keepdim=True))
+        np.testing.assert_allclose(dq[0, h].double().numpy(), unrot(ds @ kr[h // 2] / math.sqrt(128)).numpy(),
+                                   rtol=1e-4, atol=1e-4)
+        dk_rot[h // 2] += ds.T @ qr[h] / math.sqrt(128)
+    np.testing.assert_allclose(dk[0].double().numpy(), unrot(dk_rot).numpy(), rtol=1e-4, atol=1e-4)
+
+
 def test_prefill_oracle_against_fp64_rows_and_masks():
     # the window mask equals torch's is_causal when it does not bind, and each
     # output row equals fp64 textbook attention over its visible keys

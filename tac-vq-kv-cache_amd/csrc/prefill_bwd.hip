@@ -300,7 +300,8 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
 // operands, and Q_rotᵀ for the last product comes from the q operands already
 // in registers by MFMAs against identity columns (exact).
 template <bool DK>
-__global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArgs a) {
+__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_kv_grad_kernel(ValueGradArgs a) {
   __shared__ __align__(16) _Float16 q_lds[2][kQTile];
   __shared__ __align__(16) _Float16 d_lds[2][kDTile];  // dOᵀ [dim][row], or dO rows when DK
   __shared__ __align__(16) float l_lds[2][kBRows];
@@ -394,8 +395,9 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
   const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
   const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
   struct StepRegs {
-    half8 q0, q1, cs, sn, d0, d1;
+    half8 q0, q1, d0, d1;
     float l, x;
+    int64_t pos;  // the q row's position (its trig row is read at store time)
   };
   auto fetch = [&](int ft, int fh, StepRegs& r) {
     const int64_t r0 = key0 + (tile_lo + ft) * kBRows;
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
     r.q1 = *(const half8*)(qrow + 64);
     r.q0 = ok ? r.q0 : zero8;
     r.q1 = ok ? r.q1 : zero8;
-    load_trig8(rope_row(p0 + (ok ? row : 0)), 8 * qp, &r.cs, &r.sn);
+    r.pos = p0 + (ok ? row : 0);
     const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
     if constexpr (DK) {
       // dO row qr, dims [8qp, +8) and [8qp + 64, +8), as the q rows
@@ -424,8 +426,9 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
     r.l = tid < kBRows && r0 + tid < a.T ? l_b[fh * a.T + r0 + tid] * 1.4426950408889634f : 0.f;
   };
   auto store = [&](const StepRegs& r, int buf) {
-    half8 r0, r1;
-    rope16(r.q0, r.q1, r.cs, r.sn, &r0, &r1);
+    half8 cs, sn, r0, r1;
+    load_trig8(rope_row(r.pos), 8 * qp, &cs, &sn);
+    rope16(r.q0, r.q1, cs, sn, &r0, &r1);
     _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
     *(half8*)qd = r0;
     *(half8*)(qd + 64) = r1;
@@ -451,12 +454,13 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
       ++ft;
     }
   };
+  // (DK: one step ahead only; its registers are needed elsewhere)
   StepRegs nxt;
   if (nsteps > 0) {
     StepRegs r;
     fetch(ft, fh, r);
     advance();
-    if (nsteps > 1) {
+    if (!DK && nsteps > 1) {
       fetch(ft, fh, nxt);
       advance();
     }
@@ -469,7 +473,12 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
     const int buf = (int)(step & 1);
     const bool more = step + 1 < nsteps;
     StepRegs ahead;
-    if (step + 2 < nsteps) {
+    if constexpr (DK) {
+      if (more) {
+        fetch(ft, fh, nxt);
+        advance();
+      }
+    } else if (step + 2 < nsteps) {
       fetch(ft, fh, ahead);
       advance();
     }
@@ -481,12 +490,10 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
       const _Float16* dl = d_lds[buf];
       // ---- S[row][key]: 2 row tiles x 2 key tiles ----
       float4v sacc[2][2];
-      // (DK keeps both row tiles' q operands for the transposes; the value
-      // gradient reads them one row tile at a time)
-      half8 qa[DK ? 2 : 1][4];
+      half8 qa[4];  // one row tile's q operands at a time
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg) {
-        half8 (&qr)[4] = qa[DK ? rg : 0];
+        half8 (&qr)[4] = qa;
 #pragma unroll
         for (int c = 0; c < 4; ++c) qr[c] = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
 #pragma unroll
@@ -557,7 +564,9 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
         if constexpr (DK) {
 #pragma unroll
           for (int rg = 0; rg < 2; ++rg) {
-            const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[DK ? rg : 0][dt >> 1], ident[dt & 1],
+            // the q operand again from LDS (cheaper than keeping both row tiles live)
+            const half8 qav = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * (dt >> 1) + 8 * lg);
+            const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(qav, ident[dt & 1],
                                                                    float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
             for (int e = 0; e < 4; ++e) db[4 * rg + e] = (_Float16)t[e];
@@ -575,7 +584,7 @@ __global__ __launch_bounds__(kBThreads) void prefill_kv_grad_kernel(ValueGradArg
     }
     // ---- the next step into the other buffer ----
     if (more) store(nxt, buf ^ 1);
-    nxt = ahead;
+    if constexpr (!DK) nxt = ahead;
     __syncthreads();
     if (++ch == NQ) {
       ch = 0;
@@ -649,7 +658,8 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
   const int64_t nqb = ceil_div(a.T, block_rows);
   const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
   const int chunk = blockIdx.y;
-  const int64_t qblk = bid % (uint32_t)nqb;
+  // longest key ranges first (later row blocks see more keys)
+  const int64_t qblk = nqb - 1 - (int64_t)(bid % (uint32_t)nqb);
   const int64_t yz = bid / (uint32_t)nqb;
   const int64_t gy = a.KVH * qa_.head_groups;
   const int64_t kvh = (yz % gy) / qa_.head_groups;
@@ -731,7 +741,8 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
   const _Float16* kb_ = a.k + b * a.ksb + kvh * a.ksh;
   const _Float16* vb_ = a.v + b * a.vsb + kvh * a.vsh;
   struct TileRegs {
-    half8 k0, k1, v0, v1, cs, sn;
+    half8 k0, k1, v0, v1;
+    int64_t key;
   };
   auto fetch = [&](int64_t tile, TileRegs& r) {
     const int64_t key = (t_first + tile_lo + tile) * kQKeys + kr;
@@ -742,11 +753,12 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
     r.k1 = ok ? *(const half8*)(kp_ + 64) : zero8;
     r.v0 = ok ? *(const half8*)vp_ : zero8;
     r.v1 = ok ? *(const half8*)(vp_ + 64) : zero8;
-    load_trig8(rope_row(p0 + (ok ? key : 0)), 8 * kp, &r.cs, &r.sn);
+    r.key = ok ? key : 0;
   };
   auto store = [&](const TileRegs& r, int buf) {
-    half8 r0, r1;
-    rope16(r.k0, r.k1, r.cs, r.sn, &r0, &r1);
+    half8 cs, sn, r0, r1;
+    load_trig8(rope_row(p0 + r.key), 8 * kp, &cs, &sn);
+    rope16(r.k0, r.k1, cs, sn, &r0, &r1);
     _Float16* kd = k_lds[buf] + kr * kQStride + 8 * kp;
     *(half8*)kd = r0;
     *(half8*)(kd + 64) = r1;
@@ -773,14 +785,13 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
       const _Float16* kl = k_lds[buf];
       const _Float16* vl = v_lds[buf];
       // ---- Sᵀ and dPᵀ [key][row]: 2 key tiles x 2 row tiles ----
-      half8 ka[2][4];
       float4v st[2][2], dpt[2][2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        half8 va[4];
+        half8 ka[4], va[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          ka[kt][c] = *(const half8*)(kl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
+          ka[c] = *(const half8*)(kl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
           va[c] = *(const half8*)(vl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
         }
 #pragma unroll
@@ -789,7 +800,7 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
           dpt[kt][rg] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            st[kt][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][c], qop[rg][c], st[kt][rg], 0, 0, 0);
+            st[kt][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], qop[rg][c], st[kt][rg], 0, 0, 0);
             dpt[kt][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[c], dop[rg][c], dpt[kt][rg], 0, 0, 0);
           }
         }
@@ -822,7 +833,9 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
         half8 kbo;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-          const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][dt >> 1], ident[dt & 1],
+          // the K̂ operand again from LDS (cheaper than keeping all eight live)
+          const half8 kav = *(const half8*)(kl + (16 * kt + ln) * kQStride + 32 * (dt >> 1) + 8 * lg);
+          const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(kav, ident[dt & 1],
                                                                  float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
           for (int e = 0; e < 4; ++e) kbo[4 * kt + e] = (_Float16)t[e];
@@ -1083,9 +1096,9 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
     qa.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
     qa.row_sets = 4 / qa.heads_per_wg;
     qa.head_groups = (int32_t)(NQ / qa.heads_per_wg);
-    int chunk_tiles, chunks;
-    value_grad_chunks(T, window, &chunk_tiles, &chunks);
-    qa.g.chunk_tiles = chunk_tiles;
+    // one run per row block: 32-row blocks are many, and the longest go first
+    const int chunks = 1;
+    qa.g.chunk_tiles = 0x7fffffff;
     const int64_t n = B * QH * T * kBD;
     JKV_CHECK_ARG(slot_bytes >= (int64_t)chunks * n * (int64_t)sizeof(float), "workspace too small");
     const bool direct = chunks == 1 && d_query != nullptr;

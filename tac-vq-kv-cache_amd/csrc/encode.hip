@@ -279,8 +279,13 @@ struct MfmaArgs {
 };
 
 // PAIR: two jobs in the launch (a single-job launch keeps every argument at
-// a fixed kernarg offset)
-template <int D, int S, bool PAIR>
+// a fixed kernarg offset).  WH (d = 4, one stage): a selector whitener F per
+// problem.  The search distance |F x - F c|^2 = x.Mx - 2 x.Mc + c.Mc with
+// M = F^T F (cq_tac.py:81-95), so the codeword plane holds M c as two fp16
+// words [Mc_hi | Mc_lo] against B slots [x | x] (x.Mc to 2^-22), the norm
+// plane holds c.Mc / 2, the row bias x.Mx, and the raw codeword rides in the
+// norm plane's upper half (its B slots are zero) for the reconstruction.
+template <int D, int S, bool PAIR, bool WH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void rvq_encode_mfma(MfmaArgs m) {
   const uint32_t L0 = xcd_remap(blockIdx.x, gridDim.x);
@@ -317,6 +322,23 @@ void rvq_encode_mfma(MfmaArgs m) {
   const int64_t chunk = active ? (int64_t)L / P : 0;
   const int64_t p = h * a.G + g;
 
+  // WH: M = F^T F of this problem, in every lane (the row norm x.Mx uses it)
+  float Mw[4][4];
+  if constexpr (WH) {
+    const float* F = a.whiteners + p * 16;
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = F[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc = fmaf(f[r * 4 + i], f[r * 4 + j], acc);
+        Mw[i][j] = acc;
+      }
+  }
   // ---- stage the fp16-deployed codebooks (one codeword per thread) ----
   half8 hi = half8{};
 #pragma unroll
@@ -336,14 +358,33 @@ void rvq_encode_mfma(MfmaArgs m) {
       for (int i = 0; i < 4; ++i) cw[i] = (half_t)f[i];
     }
     float nc = 0.f;
+    half8 lo;
+    if constexpr (WH) {
+      float mc[4];
 #pragma unroll
-    for (int i = 0; i < D; ++i) nc = fmaf((float)cw[i], (float)cw[i], nc);
+      for (int i = 0; i < 4; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = fmaf(Mw[i][j], (float)cw[j], acc);
+        mc[i] = acc;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nc = fmaf((float)cw[i], mc[i], nc);
+        const half_t mh = (half_t)mc[i];
+        lo[i] = mh;
+        lo[4 + i] = (half_t)(mc[i] - (float)mh);
+        hi[4 + i] = cw[i];  // the raw codeword (zero B slots)
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < D; ++i) nc = fmaf((float)cw[i], (float)cw[i], nc);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = cw[e % D];
+    }
     const float halfn = 0.5f * nc;
     const half_t nhi = (half_t)halfn;
     const half_t nlo = (half_t)(halfn - (float)nhi);
-    half8 lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) lo[e] = cw[e % D];
     hi[4 * s + 0] = nhi;
     hi[4 * s + 1] = nlo;
     hi[4 * s + 2] = (half_t)16.f;  // bias slots: 16 * (beta/16)_hi + 16 * (beta/16)_lo
@@ -435,6 +476,7 @@ void rvq_encode_mfma(MfmaArgs m) {
     locate(it, &xo, &co, &oo);
     if (D == 8) return *(const half8*)(states + xo);
     const half4 v = *(const half4*)(states + xo);
+    if constexpr (WH) return half8{v[0], v[1], v[2], v[3], v[0], v[1], v[2], v[3]};  // [x | x]
     return half8{v[0], v[1], v[2], v[3], (half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
   };
   // stage s's bias slots (-1, -1, -(beta/16) in two fp16 halves) in half s
@@ -575,7 +617,20 @@ void rvq_encode_mfma(MfmaArgs m) {
     const bool valid = locate(cur, &xo, &co, &oo);
 
     // stage-1 B rows of this lane's row: x, no previous codeword, bias
-    const float rr1 = dot2_acc(x, x);
+    float rr1;
+    if constexpr (WH) {
+      // |F x|^2 = x.Mx
+      rr1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mx = fmaf(Mw[i][j], (float)x[j], mx);
+        rr1 = fmaf((float)x[i], mx, rr1);
+      }
+    } else {
+      rr1 = dot2_acc(x, x);
+    }
     const float delta1 = (rr1 + ncmax[0]) * 0x1p-8f;
     bdst[kSgX * kSgStride] = x;  // d=4: [x, 0]
     bdst[kSgBias1 * kSgStride] = bias_slots(0, rr1, delta1);
@@ -596,6 +651,10 @@ void rvq_encode_mfma(MfmaArgs m) {
       const uint32_t kstar = kmin & 255u;
       code |= kstar << (8 * s);
       half8 cw = tab_lo[s][kstar];
+      if constexpr (WH) {
+        const half8 t = tab_hi[kstar];
+        cw = half8{t[4], t[5], t[6], t[7], t[4], t[5], t[6], t[7]};
+      }
       if (s + 1 < S) {
         // stage-2 B rows: -c_1 and the bias from |x - c_1|^2
         negc1 = -cw;
@@ -681,9 +740,16 @@ static int launch_mfma(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t st
   JKV_CHECK_ARG(nblocks < (int64_t)1 << 31, "grid too large");
   if (e2 == nullptr) {
     m.split = nblocks;
-    hipLaunchKernelGGL((rvq_encode_mfma<D, S, false>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+    if constexpr (D == 4 && S == 1) {
+      if (e.whiteners != nullptr) {
+        hipLaunchKernelGGL((rvq_encode_mfma<4, 1, false, true>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+        JKV_CHECK_LAUNCH();
+        return JKV_OK;
+      }
+    }
+    hipLaunchKernelGGL((rvq_encode_mfma<D, S, false, false>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
   } else {
-    hipLaunchKernelGGL((rvq_encode_mfma<D, S, true>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+    hipLaunchKernelGGL((rvq_encode_mfma<D, S, true, false>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
   }
   JKV_CHECK_LAUNCH();
   return JKV_OK;
@@ -783,6 +849,12 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
     for (int j = 0; j < i; ++j)
       if (exit_depths[i] == exit_depths[j]) distinct_exits = false;
   const bool fast = mfma_eligible(a, states_dtype);
+  // whitened grouped CQ at d = 4 (one stage): the same kernel with M = F^T F
+  EncodeArgs plain = a;
+  plain.whiteners = nullptr;
+  if (whiteners != nullptr && d == 4 && S == 1 && ((uintptr_t)whiteners) % 4 == 0 &&
+      mfma_eligible(plain, states_dtype))
+    return launch_mfma<4, 1>(a, stream);
   if (fast) {
     if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
     return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);

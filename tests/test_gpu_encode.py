@@ -256,3 +256,21 @@ def test_encode_kv_equals_two_encodes(device, batch, tokens, groups, dim, stages
     assert torch.equal(ck, eck) and torch.equal(cv, ecv)
     for a, b in zip(rk + rv, ek + ev):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("batch,tokens,seed", [(2, 300, 51), (4, 2048, 52), (16, 1, 53)])
+def test_whitened_grouped_cq_d4_on_mfma(device, batch, tokens, seed):
+    # the cq2 cell [8,32,256,4] with per-(head, group) selector whiteners: the
+    # MFMA kernel with M = F^T F (codes at clear margins exact, recon equal
+    # wherever codes agree)
+    print(f"whitened cq d=4 B={batch} T={tokens}", flush=True)
+    gen = _gen(seed)
+    states = ref.synthetic_states(gen, batch, 8, tokens)
+    books = ref.synthetic_tables(gen, (8, 32, 256, 4), (1.0,), stage_axis=0)
+    f = torch.eye(4) + 0.3 * torch.randn(8, 32, 4, 4, generator=gen)
+    out, codes = jkv.hard_grouped_cq(states.to(device), books.to(device), selector_whiteners=f.to(device))
+    r_out, r_codes, d1, d2 = ref.hard_grouped_cq(states, books, selector_whiteners=f, return_margins=True)
+    res = assert_codes(codes[..., None], r_codes[..., None], d1[..., None], d2[..., None])
+    rows = res["prefix_ok"].all(-1)
+    same = (codes.cpu() == r_codes).all(-1)
+    assert torch.equal(out.cpu()[same], r_out.detach()[same])

@@ -285,6 +285,9 @@ struct MfmaArgs {
 // words [Mc_hi | Mc_lo] against B slots [x | x] (x.Mc to 2^-22), the norm
 // plane holds c.Mc / 2, the row bias x.Mx, and the raw codeword rides in the
 // norm plane's upper half (its B slots are zero) for the reconstruction.
+// At d = 8 the stage's [x | x | bias] takes 20 slots, so it runs on the
+// 16x16x32 layout of the later stages: planes Mc_hi, Mc_lo and the raw
+// codeword, M in LDS.
 template <int D, int S, bool PAIR, bool WH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void rvq_encode_mfma(MfmaArgs m) {
@@ -296,10 +299,15 @@ void rvq_encode_mfma(MfmaArgs m) {
   // stage 1 [x, bias]; stage 2 d=8 [x, -c_1, bias], d=4 [[x,-c_1], bias]
   constexpr int kSgX = 0;
   constexpr int kSgC = (D == 8 && S > 1) ? 1 : 0;  // d=4: upper half of sg0
-  constexpr int kSgBias1 = 1;                       // stage 1 (K = 16)
+  // whitened d=8: stage 1 on K = 32 with slot groups [x, x, bias]
+  constexpr bool kWh8 = WH && D == 8;
+  static_assert(!WH || S == 1, "whitened search runs one stage");
+  constexpr int kSgBias1 = kWh8 ? 2 : 1;            // stage 1 (K = 16)
   constexpr int kSgBias = (D == 8) ? 2 : 1;         // later stages (K = 32)
-  constexpr int kSlotGroups = (D == 8 && S > 1) ? 3 : 2;
-  __shared__ half8 tab_lo[S][256];
+  constexpr int kSlotGroups = ((D == 8 && S > 1) || kWh8) ? 3 : 2;
+  constexpr int kPlanes = kWh8 ? 3 : S;             // Mc_hi, Mc_lo, raw codeword
+  __shared__ half8 tab_lo[kPlanes][256];
+  __shared__ float s_M[kWh8 ? 64 : 1];
   __shared__ half8 tab_hi[256];
   // per-wave B images [slot group][tile][row] plus one shared zero plane
   __shared__ half8 bimg[4][kSlotGroups][kTiles][16];
@@ -324,7 +332,18 @@ void rvq_encode_mfma(MfmaArgs m) {
 
   // WH: M = F^T F of this problem, in every lane (the row norm x.Mx uses it)
   float Mw[4][4];
-  if constexpr (WH) {
+  if constexpr (kWh8) {
+    // M = F^T F, one entry per thread of the first wave
+    if (tid < 64) {
+      const float* F = a.whiteners + p * 64;
+      const int i = tid >> 3, j = tid & 7;
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) acc = fmaf(F[r * 8 + i], F[r * 8 + j], acc);
+      s_M[tid] = acc;
+    }
+    __syncthreads();
+  } else if constexpr (WH) {
     const float* F = a.whiteners + p * 16;
     float f[16];
 #pragma unroll
@@ -359,7 +378,27 @@ void rvq_encode_mfma(MfmaArgs m) {
     }
     float nc = 0.f;
     half8 lo;
-    if constexpr (WH) {
+    if constexpr (kWh8) {
+      float mc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = fmaf(s_M[i * 8 + j], (float)cw[j], acc);
+        mc[i] = acc;
+      }
+      half8 mlo, raw;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        nc = fmaf((float)cw[i], mc[i], nc);
+        const half_t mh = (half_t)mc[i];
+        lo[i] = mh;
+        mlo[i] = (half_t)(mc[i] - (float)mh);
+        raw[i] = cw[i];
+      }
+      tab_lo[1][tid] = mlo;
+      tab_lo[2][tid] = raw;
+    } else if constexpr (WH) {
       float mc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -555,8 +594,7 @@ void rvq_encode_mfma(MfmaArgs m) {
 
   // Later stages on v_mfma_f32_16x16x32_f16 (20 slots): four 16-row tiles,
   // sixteen 16-codeword chunks.
-  auto stage_next = [&]() -> uint32_t {
-    constexpr int s = 1;
+  auto stage_next = [&](const half8* pl) -> uint32_t {
     half8 bop[kTiles];
 #pragma unroll
     for (int i = 0; i < kTiles; ++i) bop[i] = bsrc[i * 16];
@@ -565,7 +603,6 @@ void rvq_encode_mfma(MfmaArgs m) {
     uint32_t best[kTiles];
 #pragma unroll
     for (int i = 0; i < kTiles; ++i) best[i] = 0xFFFFFFFFu;
-    const half8* pl = (a_hi ? &tab_hi[0] : plane_lo + s * 256) + ln;
     // software pipeline: the MFMAs of chunk c+1 run while the keys of
     // chunk c are reduced
     half8 af_next = pl[0];
@@ -618,7 +655,16 @@ void rvq_encode_mfma(MfmaArgs m) {
 
     // stage-1 B rows of this lane's row: x, no previous codeword, bias
     float rr1;
-    if constexpr (WH) {
+    if constexpr (kWh8) {
+      rr1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaf(s_M[i * 8 + j], (float)x[j], mx);
+        rr1 = fmaf((float)x[i], mx, rr1);
+      }
+    } else if constexpr (WH) {
       // |F x|^2 = x.Mx
       rr1 = 0.f;
 #pragma unroll
@@ -633,6 +679,7 @@ void rvq_encode_mfma(MfmaArgs m) {
     }
     const float delta1 = (rr1 + ncmax[0]) * 0x1p-8f;
     bdst[kSgX * kSgStride] = x;  // d=4: [x, 0]
+    if constexpr (kWh8) bdst[1 * kSgStride] = x;
     bdst[kSgBias1 * kSgStride] = bias_slots(0, rr1, delta1);
     // x is consumed: the next iteration's row loads during this one
     if (more) x = load_x(nxt);
@@ -643,15 +690,18 @@ void rvq_encode_mfma(MfmaArgs m) {
     for (int s = 0; s < S; ++s) {
       wave_lds_sync();
       uint32_t kmin;
-      if (s == 0) {
+      if (s == 0 && !kWh8) {
         kmin = stage_first();
       } else {
-        kmin = stage_next();
+        // lane group lg reads plane lg (whitened d=8) or the stage's plane
+        kmin = stage_next((a_hi ? &tab_hi[0] : plane_lo + (kWh8 ? lg : s) * 256) + ln);
       }
       const uint32_t kstar = kmin & 255u;
       code |= kstar << (8 * s);
       half8 cw = tab_lo[s][kstar];
-      if constexpr (WH) {
+      if constexpr (kWh8) {
+        cw = tab_lo[2][kstar];
+      } else if constexpr (WH) {
         const half8 t = tab_hi[kstar];
         cw = half8{t[4], t[5], t[6], t[7], t[4], t[5], t[6], t[7]};
       }
@@ -740,9 +790,9 @@ static int launch_mfma(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t st
   JKV_CHECK_ARG(nblocks < (int64_t)1 << 31, "grid too large");
   if (e2 == nullptr) {
     m.split = nblocks;
-    if constexpr (D == 4 && S == 1) {
+    if constexpr (S == 1) {
       if (e.whiteners != nullptr) {
-        hipLaunchKernelGGL((rvq_encode_mfma<4, 1, false, true>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+        hipLaunchKernelGGL((rvq_encode_mfma<D, 1, false, true>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
         JKV_CHECK_LAUNCH();
         return JKV_OK;
       }
@@ -852,9 +902,9 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
   // whitened grouped CQ at d = 4 (one stage): the same kernel with M = F^T F
   EncodeArgs plain = a;
   plain.whiteners = nullptr;
-  if (whiteners != nullptr && d == 4 && S == 1 && ((uintptr_t)whiteners) % 4 == 0 &&
+  if (whiteners != nullptr && (d == 4 || d == 8) && S == 1 && ((uintptr_t)whiteners) % 4 == 0 &&
       mfma_eligible(plain, states_dtype))
-    return launch_mfma<4, 1>(a, stream);
+    return d == 4 ? launch_mfma<4, 1>(a, stream) : launch_mfma<8, 1>(a, stream);
   if (fast) {
     if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
     return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);

@@ -258,16 +258,17 @@ def test_encode_kv_equals_two_encodes(device, batch, tokens, groups, dim, stages
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("batch,tokens,seed", [(2, 300, 51), (4, 2048, 52), (16, 1, 53)])
-def test_whitened_grouped_cq_d4_on_mfma(device, batch, tokens, seed):
-    # the cq2 cell [8,32,256,4] with per-(head, group) selector whiteners: the
-    # MFMA kernel with M = F^T F (codes at clear margins exact, recon equal
-    # wherever codes agree)
-    print(f"whitened cq d=4 B={batch} T={tokens}", flush=True)
+@pytest.mark.parametrize("dim,batch,tokens,seed", [(4, 2, 300, 51), (4, 4, 2048, 52), (4, 16, 1, 53),
+                                                    (8, 2, 300, 54), (8, 1, 2048, 55), (8, 16, 1, 56)])
+def test_whitened_grouped_cq_on_mfma(device, dim, batch, tokens, seed):
+    # the cq2 cell [8,32,256,4] and the cq1 cell [8,16,256,8] with
+    # per-(head, group) selector whiteners: the MFMA kernel with M = F^T F
+    # (codes at clear margins exact, recon equal wherever codes agree)
+    print(f"whitened cq d={dim} B={batch} T={tokens}", flush=True)
     gen = _gen(seed)
     states = ref.synthetic_states(gen, batch, 8, tokens)
-    books = ref.synthetic_tables(gen, (8, 32, 256, 4), (1.0,), stage_axis=0)
-    f = torch.eye(4) + 0.3 * torch.randn(8, 32, 4, 4, generator=gen)
+    books = ref.synthetic_tables(gen, (8, 128 // dim, 256, dim), (1.0,), stage_axis=0)
+    f = torch.eye(dim) + 0.3 * torch.randn(8, 128 // dim, dim, dim, generator=gen)
     out, codes = jkv.hard_grouped_cq(states.to(device), books.to(device), selector_whiteners=f.to(device))
     r_out, r_codes, d1, d2 = ref.hard_grouped_cq(states, books, selector_whiteners=f, return_margins=True)
     res = assert_codes(codes[..., None], r_codes[..., None], d1[..., None], d2[..., None])

@@ -329,6 +329,17 @@ int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_
                                    int64_t rope_len, float* d_key, void* workspace, int64_t workspace_bytes,
                                    jkv_stream_t stream);
 
+/* fp32 nearest codeword of every row: states [H,N,D] and tables [H,K,D]
+ * contiguous fp32 (not deployed to fp16), D in 1..128; indices [H,N] int64
+ * receive argmin_k (|x|^2 + |c_k|^2) - 2 x.c_k, the lowest k on ties.
+ * Replaces `_nearest_indices` without whiteners
+ * (src/jointkv/nested_vq.py:178-215), the search of the offline multi-exit
+ * additive coordinate refinement (nested_vq.py:583-741).
+ */
+int jkv_nearest_f32(const float* states, int64_t H, int64_t N, int64_t D,
+                    const float* tables, int64_t K, int64_t* indices,
+                    jkv_stream_t stream);
+
 /*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of
  * the 64 frequencies, then their sin):

@@ -139,6 +139,26 @@ def rvq_encode_kv(
     return recon_k, codes[0], recon_v, codes[1]
 
 
+def nearest_f32(states: torch.Tensor, tables: torch.Tensor) -> torch.Tensor:
+    """Nearest fp32 codeword per row: ``states[H,N,D]``, ``tables[H,K,D]``
+    (fp32, D <= 128) -> int64 ``[H,N]`` (nested_vq.py:178-215 without
+    whiteners)."""
+
+    device = _lib.require_device(states, tables)
+    if states.ndim != 3 or tables.ndim != 3:
+        raise ValueError("nearest-neighbor inputs must have [H,N,D]/[H,K,D]")
+    heads, tokens, dim = map(int, states.shape)
+    if int(tables.shape[0]) != heads or int(tables.shape[2]) != dim:
+        raise ValueError("nearest-neighbor geometry differs")
+    states = states.detach().float().contiguous()
+    tables = tables.detach().float().contiguous()
+    out = torch.empty((heads, tokens), dtype=torch.int64, device=device)
+    _lib.check(_lib.load().jkv_nearest_f32(
+        states.data_ptr(), heads, tokens, dim, tables.data_ptr(), int(tables.shape[1]),
+        out.data_ptr(), _lib.stream_handle(device)))
+    return out
+
+
 def rvq_decode(
     codes: torch.Tensor,
     tables: torch.Tensor,

@@ -1,0 +1,141 @@
+"""Offline multi-exit additive coordinate refinement on the MI355X
+(src/jointkv/nested_vq.py:582-741, ``multi_exit_additive_coordinate_refinement``).
+
+Given greedy residual indices, a reverse sweep re-chooses one stage at a
+time with the others fixed.  For stage ``s`` the exits ``m`` that include it
+share one Euclidean target, ``old_word + sum_m w_m (x - recon_m) / sum_m w_m``,
+so the stage's new index is that target's nearest codeword and every step is
+non-increasing for the weighted multi-exit objective (nested_vq.py:596-604).
+
+The search is ``jkv_nearest_f32`` (fp32 tables, as the reference keeps them
+for this encoder, nested_vq.py:636-639); the target and reconstruction
+updates are elementwise tensor arithmetic in the reference's order.  Index
+layout and decoder are unchanged: the output indices decode with the same
+tables as the greedy ones.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Iterable, Sequence
+
+import torch
+
+from . import _ops
+
+
+def _gather_words(table: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+    """``[H,N]`` indices of one ``[H,K,D]`` table -> ``[H,N,D]`` (nested_vq.py:568-580)."""
+
+    return torch.gather(table, 1, indices.unsqueeze(-1).expand(-1, -1, table.shape[-1]))
+
+
+@torch.no_grad()
+def multi_exit_additive_coordinate_refinement(
+    states: torch.Tensor,
+    stage_tables: Sequence[torch.Tensor],
+    initial_indices: torch.Tensor,
+    *,
+    prefixes: Iterable[int],
+    exit_weights: Sequence[float],
+    sweeps: int = 1,
+    token_chunk_size: int = 4096,
+):
+    """Refine ``initial_indices`` ``[B,H,T,S]`` of ``states`` ``[B,H,T,D]``
+    against the exits in ``prefixes`` jointly.  Returns
+    ``({prefix: reconstruction [B,H,T,D] in states' dtype}, uint8 indices
+    [B,H,T,S], diagnostics)`` with the reference's diagnostics keys
+    (nested_vq.py:727-741).  ``token_chunk_size`` is validated as the
+    reference does; the HIP search needs no chunking."""
+
+    requested = tuple(sorted({int(prefix) for prefix in prefixes}))
+    weights = tuple(float(weight) for weight in exit_weights)
+    if states.ndim != 4 or not torch.isfinite(states).all():
+        raise ValueError("states must have finite [B,H,T,D] layout")
+    if not requested or requested[0] <= 0 or requested[-1] > len(stage_tables):
+        raise ValueError("prefixes must lie inside the materialized stages")
+    if len(weights) != len(requested) or any(not math.isfinite(w) or w < 0 for w in weights):
+        raise ValueError("one finite non-negative weight is required per exit")
+    if not any(w > 0 for w in weights):
+        raise ValueError("at least one exit weight must be positive")
+    if sweeps <= 0 or token_chunk_size <= 0:
+        raise ValueError("coordinate sweeps and token chunks must be positive")
+    batch, heads, tokens, dim = map(int, states.shape)
+    depth = requested[-1]
+    if tuple(initial_indices.shape) != (batch, heads, tokens, depth):
+        raise ValueError("initial indices differ from the requested stage geometry")
+    tables = [t.to(device=states.device, dtype=torch.float32).contiguous() for t in stage_tables[:depth]]
+    for stage, table in enumerate(tables):
+        if table.ndim != 3 or table.shape[0] != heads or table.shape[2] != dim:
+            raise ValueError(f"stage {stage} table geometry differs from states")
+        if not torch.isfinite(table).all():
+            raise ValueError(f"stage {stage} table is non-finite")
+
+    x = states.permute(1, 0, 2, 3).reshape(heads, batch * tokens, dim).float()
+    idx = initial_indices.permute(1, 0, 2, 3).reshape(heads, batch * tokens, depth).long().clone()
+    recon: dict[int, torch.Tensor] = {}
+    running = torch.zeros_like(x)
+    for stage, table in enumerate(tables):
+        col = idx[..., stage]
+        if int(col.min()) < 0 or int(col.max()) >= table.shape[1]:
+            raise ValueError(f"stage {stage} index is outside its codebook")
+        running.add_(_gather_words(table, col))
+        if stage + 1 in requested:
+            recon[stage + 1] = running.clone()
+
+    def objective():
+        per_exit = {str(p): float((x - recon[p]).square().mean().item()) for p in requested}
+        weighted = sum(w * per_exit[str(p)] for p, w in zip(requested, weights)) / sum(weights)
+        return weighted, per_exit
+
+    initial_objective, initial_per_exit = objective()
+    history = []
+    for sweep in range(sweeps):
+        changed: dict[str, float] = {}
+        for stage in range(depth - 1, -1, -1):
+            affected = [(p, w) for p, w in zip(requested, weights) if p > stage and w > 0]
+            weight_sum = sum(w for _p, w in affected)
+            if weight_sum <= 0:
+                raise ValueError(f"stage {stage} is not covered by a positive exit")
+            table = tables[stage]
+            old = idx[..., stage]
+            old_words = _gather_words(table, old)
+            target = old_words.clone()
+            residual = torch.zeros_like(target)
+            for p, w in affected:
+                residual.add_(x - recon[p], alpha=w)
+            target.add_(residual, alpha=1.0 / weight_sum)
+            new = _ops.nearest_f32(target, table)
+            changed[str(stage + 1)] = float(new.ne(old).float().mean().item())
+            delta = _gather_words(table, new) - old_words
+            for p, _w in affected:
+                recon[p].add_(delta)
+            idx[..., stage] = new
+        weighted, per_exit = objective()
+        history.append({
+            "sweep": sweep + 1,
+            "weighted_objective": weighted,
+            "per_exit_mse": per_exit,
+            "changed_fraction_by_stage": changed,
+            "mean_changed_fraction": sum(changed.values()) / len(changed),
+        })
+    final_objective, final_per_exit = objective()
+    outputs = {
+        p: r.reshape(heads, batch, tokens, dim).permute(1, 0, 2, 3).to(dtype=states.dtype).contiguous()
+        for p, r in recon.items()
+    }
+    refined = idx.reshape(heads, batch, tokens, depth).permute(1, 0, 2, 3).to(torch.uint8).contiguous()
+    diagnostics = {
+        "mode": "multi_exit_additive_coordinate",
+        "coordinate_order": "reverse",
+        "sweeps": sweeps,
+        "prefixes": list(requested),
+        "exit_weights": list(weights),
+        "initial_weighted_objective": initial_objective,
+        "final_weighted_objective": final_objective,
+        "relative_objective_change": final_objective / max(initial_objective, 1e-30) - 1.0,
+        "initial_per_exit_mse": initial_per_exit,
+        "final_per_exit_mse": final_per_exit,
+        "sweep_history": history,
+    }
+    return outputs, refined, diagnostics

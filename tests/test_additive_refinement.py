@@ -1,0 +1,148 @@
+"""Offline multi-exit additive coordinate refinement
+(src/jointkv/nested_vq.py:178-215, 583-741): the CPU oracle pinned by
+exhaustive search, the host function's argument checks, and the HIP nearest
+search and refinement against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import jointkv_amd as jkv
+from jointkv_amd import _ops
+from oracle import additive_oracle as ora
+
+
+def _problem(seed, batch, heads, tokens, dim, clusters, stages):
+    gen = torch.Generator().manual_seed(seed)
+    states = torch.randn(batch, heads, tokens, dim, generator=gen)
+    tables = [torch.randn(heads, clusters, dim, generator=gen) * (0.7 ** s) for s in range(stages)]
+    init = torch.randint(0, clusters, (batch, heads, tokens, stages), generator=gen)
+    return states, tables, init
+
+
+def _stage_objective(x, tabs, idx, stage, aff):
+    """float64 weighted objective of every candidate k for `stage` over the
+    exits in `aff`, the other stages at idx: [N, K]."""
+
+    n, k = x.shape[0], tabs[stage].shape[0]
+    out = np.zeros((n, k))
+    for p, w in aff:
+        base = np.zeros_like(x)
+        for j in range(p):
+            if j != stage:
+                base += tabs[j][idx[:, j]]
+        diff = (x - base)[:, None, :] - tabs[stage][None, :, :]
+        out += w * np.square(diff).sum(-1)
+    return out
+
+
+@pytest.mark.parametrize("prefixes,weights", [((1, 2, 3), (1.0, 0.5, 2.0)), ((2, 3), (0.0, 1.0)), ((3,), (1.0,))])
+def test_oracle_sweep_matches_exhaustive_search(prefixes, weights):
+    states, tables, init = _problem(7, 1, 2, 40, 6, 12, 3)
+    _out, idx, _hist, _init = ora.coordinate_refinement(states.numpy(), [t.numpy() for t in tables], init.numpy(),
+                                                        prefixes, weights, sweeps=1)
+    x_all = states.double().numpy()
+    tabs_all = [t.double().numpy() for t in tables]
+    checked = 0
+    for h in range(2):
+        x = x_all[0, h]
+        final = idx[0, h]
+        start = init.numpy()[0, h]
+        for stage in range(2, -1, -1):
+            aff = [(p, w) for p, w in zip(prefixes, weights) if p > stage and w > 0]
+            if not aff:
+                continue
+            # when stage is chosen: later stages final, earlier ones initial
+            state = np.concatenate([start[:, :stage], final[:, stage:]], axis=1)
+            obj = _stage_objective(x, [t[h] for t in tabs_all], state, stage, aff)
+            order = np.sort(obj, axis=1)
+            clear = (order[:, 1] - order[:, 0]) > 1e-4 * np.maximum(order[:, 0], 1e-6)
+            assert np.array_equal(obj.argmin(1)[clear], final[clear, stage]), f"stage {stage} head {h}"
+            checked += int(clear.sum())
+    assert checked > 150
+
+
+def test_oracle_objective_never_rises():
+    states, tables, init = _problem(11, 2, 2, 64, 8, 32, 4)
+    _out, _idx, hist, initial = ora.coordinate_refinement(states.numpy(), [t.numpy() for t in tables],
+                                                          init.numpy(), (1, 2, 4), (1.0, 1.0, 3.0), sweeps=3)
+    seq = [initial] + hist
+    assert all(b <= a * (1 + 1e-6) for a, b in zip(seq, seq[1:])), seq
+    assert seq[-1] < 0.9 * seq[0]
+
+
+def test_oracle_nearest_against_float64():
+    gen = torch.Generator().manual_seed(3)
+    x, c = torch.randn(300, 16, generator=gen), torch.randn(50, 16, generator=gen)
+    got = ora.nearest(x.numpy(), c.numpy())
+    d = torch.cdist(x.double(), c.double())
+    assert np.array_equal(got, d.argmin(1).numpy())
+    # ties go to the lowest index
+    assert ora.nearest(np.zeros((1, 4), np.float32), np.zeros((3, 4), np.float32))[0] == 0
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(prefixes=(), exit_weights=()), "prefixes must lie"),
+    (dict(prefixes=(4,), exit_weights=(1.0,)), "prefixes must lie"),
+    (dict(prefixes=(1, 2), exit_weights=(1.0,)), "one finite non-negative weight"),
+    (dict(prefixes=(1,), exit_weights=(0.0,)), "at least one exit weight"),
+    (dict(prefixes=(1,), exit_weights=(1.0,), sweeps=0), "sweeps and token chunks"),
+])
+def test_refinement_argument_errors(kwargs, match):
+    states, tables, init = _problem(1, 1, 2, 8, 4, 8, 3)
+    with pytest.raises(ValueError, match=match):
+        jkv.multi_exit_additive_coordinate_refinement(states, tables, init, **kwargs)
+
+
+def test_refinement_rejects_bad_indices():
+    states, tables, init = _problem(1, 1, 2, 8, 4, 8, 2)
+    with pytest.raises(ValueError, match="initial indices differ"):
+        jkv.multi_exit_additive_coordinate_refinement(states, tables, init[..., :1], prefixes=(2,),
+                                                      exit_weights=(1.0,))
+    init[0, 0, 0, 1] = 8
+    with pytest.raises(ValueError, match="outside its codebook"):
+        jkv.multi_exit_additive_coordinate_refinement(states, tables, init, prefixes=(2,), exit_weights=(1.0,))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,rows,dim,clusters", [(3, 1000, 128, 256), (2, 77, 7, 100), (1, 64, 128, 64)])
+def test_nearest_f32_matches_oracle(device, heads, rows, dim, clusters):
+    print(f"nearest H={heads} N={rows} D={dim} K={clusters}", flush=True)
+    gen = torch.Generator().manual_seed(rows + dim)
+    x = torch.randn(heads, rows, dim, generator=gen)
+    c = torch.randn(heads, clusters, dim, generator=gen)
+    got = _ops.nearest_f32(x.to(device), c.to(device)).cpu().numpy()
+    for h in range(heads):
+        want = ora.nearest(x[h].numpy(), c[h].numpy())
+        d = np.sort(torch.cdist(x[h].double(), c[h].double()).square().numpy(), axis=1)
+        clear = (d[:, 1] - d[:, 0]) > 1e-3 * d[:, 0]
+        assert np.array_equal(got[h][clear], want[clear])
+        assert (got[h] == want).mean() >= 0.9999
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,batch,tokens,sweeps", [(torch.float32, 2, 300, 2), (torch.float16, 1, 65, 1)])
+def test_refinement_matches_oracle(device, dtype, batch, tokens, sweeps):
+    print(f"refinement dtype={dtype} B={batch} T={tokens} sweeps={sweeps}", flush=True)
+    states, tables, init = _problem(23 + tokens, batch, 4, tokens, 128, 256, 3)
+    states = states.to(dtype)
+    prefixes, weights = (1, 2, 3), (1.0, 1.0, 2.0)
+    out, idx, diag = jkv.multi_exit_additive_coordinate_refinement(
+        states.to(device), [t.to(device) for t in tables], init.to(device), prefixes=prefixes,
+        exit_weights=weights, sweeps=sweeps)
+    r_out, r_idx, r_hist, r_init = ora.coordinate_refinement(states.float().numpy(), [t.numpy() for t in tables],
+                                                             init.numpy(), prefixes, weights, sweeps=sweeps)
+    assert idx.dtype == torch.uint8 and tuple(idx.shape) == (batch, 4, tokens, 3)
+    same = (idx.cpu().long().numpy() == r_idx).all(-1)
+    assert same.mean() >= 0.999, same.mean()
+    for p in prefixes:
+        assert out[p].dtype == dtype
+        err = np.abs(out[p].cpu().float().numpy() - r_out[p].astype(np.float32).astype(
+            np.float16 if dtype == torch.float16 else np.float32).astype(np.float32))[same].max()
+        assert err <= 1e-4, (p, err)
+    assert diag["final_weighted_objective"] == pytest.approx(r_hist[-1], rel=1e-4)
+    assert diag["initial_weighted_objective"] == pytest.approx(r_init, rel=1e-5)
+    assert diag["final_weighted_objective"] < diag["initial_weighted_objective"]
+    assert len(diag["sweep_history"]) == sweeps and diag["mode"] == "multi_exit_additive_coordinate"

@@ -340,6 +340,18 @@ int jkv_nearest_f32(const float* states, int64_t H, int64_t N, int64_t D,
                     const float* tables, int64_t K, int64_t* indices,
                     jkv_stream_t stream);
 
+/* The M (1..8, M < K) nearest fp32 codewords of every row, nearest first
+ * (equal distances in index order): states [H,N,D], tables [H,K,D] as for
+ * jkv_nearest_f32; excluded [H,N] int64 or NULL, one index per row left out
+ * of the search; indices [H,N,M] int64.  Replaces `_nearest_topk_indices`
+ * (src/jointkv/nested_vq.py:218-260), the shortlist search of the offline
+ * multi-exit additive block refinement (nested_vq.py:757-1001).
+ */
+int jkv_nearest_topk_f32(const float* states, int64_t H, int64_t N, int64_t D,
+                         const float* tables, int64_t K, int64_t M,
+                         const int64_t* excluded, int64_t* indices,
+                         jkv_stream_t stream);
+
 /*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of
  * the 64 frequencies, then their sin):

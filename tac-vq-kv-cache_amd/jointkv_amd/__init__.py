@@ -8,7 +8,7 @@ HIP kernels of ``libjkv.so``; there is no CPU fallback.
 """
 
 from . import _lib, artifacts
-from .additive_refinement import multi_exit_additive_coordinate_refinement
+from .additive_refinement import multi_exit_additive_block_refinement, multi_exit_additive_coordinate_refinement
 from .attention import (
     DecodedWindowCache,
     PackedCodeCache,
@@ -53,6 +53,7 @@ from .packed_nested import (
 from .uniform_depth_tac import ClosedLoopUniformResidualVQ
 
 __all__ = [
+    "multi_exit_additive_block_refinement",
     "multi_exit_additive_coordinate_refinement",
     "AttentionWeights",
     "artifacts",

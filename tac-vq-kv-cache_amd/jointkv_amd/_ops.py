@@ -159,6 +159,31 @@ def nearest_f32(states: torch.Tensor, tables: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def nearest_topk_f32(states: torch.Tensor, tables: torch.Tensor, candidates: int,
+                     excluded: torch.Tensor | None = None) -> torch.Tensor:
+    """The ``candidates`` nearest fp32 codewords per row, nearest first:
+    ``states[H,N,D]``, ``tables[H,K,D]``, optional ``excluded[H,N]`` ->
+    int64 ``[H,N,candidates]`` (nested_vq.py:218-260)."""
+
+    device = _lib.require_device(states, tables, excluded)
+    if states.ndim != 3 or tables.ndim != 3:
+        raise ValueError("nearest-neighbor inputs must have [H,N,D]/[H,K,D]")
+    heads, tokens, dim = map(int, states.shape)
+    if int(tables.shape[0]) != heads or int(tables.shape[2]) != dim:
+        raise ValueError("nearest-neighbor geometry differs")
+    if excluded is not None:
+        if tuple(excluded.shape) != (heads, tokens):
+            raise ValueError("excluded indices must have [H,N] layout")
+        excluded = excluded.to(torch.int64).contiguous()
+    states = states.detach().float().contiguous()
+    tables = tables.detach().float().contiguous()
+    out = torch.empty((heads, tokens, int(candidates)), dtype=torch.int64, device=device)
+    _lib.check(_lib.load().jkv_nearest_topk_f32(
+        states.data_ptr(), heads, tokens, dim, tables.data_ptr(), int(tables.shape[1]), int(candidates),
+        None if excluded is None else excluded.data_ptr(), out.data_ptr(), _lib.stream_handle(device)))
+    return out
+
+
 def rvq_decode(
     codes: torch.Tensor,
     tables: torch.Tensor,

@@ -146,3 +146,103 @@ def test_refinement_matches_oracle(device, dtype, batch, tokens, sweeps):
     assert diag["initial_weighted_objective"] == pytest.approx(r_init, rel=1e-5)
     assert diag["final_weighted_objective"] < diag["initial_weighted_objective"]
     assert len(diag["sweep_history"]) == sweeps and diag["mode"] == "multi_exit_additive_coordinate"
+
+
+def test_oracle_topk_against_float64_sort():
+    gen = torch.Generator().manual_seed(5)
+    x, c = torch.randn(200, 12, generator=gen), torch.randn(40, 12, generator=gen)
+    excl = torch.randint(0, 40, (200,), generator=gen).numpy()
+    got = ora.nearest_topk(x.numpy(), c.numpy(), 5, excl)
+    d = torch.cdist(x.double(), c.double()).numpy()
+    d[np.arange(200), excl] = np.inf
+    assert np.array_equal(got, np.argsort(d, axis=1, kind="stable")[:, :5])
+    assert not (got == excl[:, None]).any()
+
+
+def test_block_oracle_with_full_shortlist_is_the_exhaustive_pair_optimum():
+    # two stages, one block; a shortlist of every codeword makes the block
+    # step the joint optimum over all K^2 pairs
+    states, tables, init = _problem(9, 1, 2, 30, 5, 6, 2)
+    prefixes, weights = (1, 2), (1.0, 2.0)
+    _out, idx, hist, initial = ora.block_refinement(states.numpy(), [t.numpy() for t in tables], init.numpy(),
+                                                    prefixes, weights, sweeps=1, shortlist=6)
+    assert hist[0] <= initial
+    checked = 0
+    for h in range(2):
+        x = states[0, h].double().numpy()
+        t0, t1 = tables[0][h].double().numpy(), tables[1][h].double().numpy()
+        e1 = np.square(x[:, None, :] - t0[None]).sum(-1)                               # [N, K]
+        e2 = np.square(x[:, None, None, :] - t0[None, :, None] - t1[None, None]).sum(-1)  # [N, K, K]
+        cost = (weights[0] * e1[:, :, None] + weights[1] * e2).reshape(len(x), -1)
+        order = np.sort(cost, axis=1)
+        clear = (order[:, 1] - order[:, 0]) > 1e-4 * np.maximum(order[:, 0], 1e-6)
+        best = cost.argmin(1)
+        assert np.array_equal((best // 6)[clear], idx[0, h, clear, 0])
+        assert np.array_equal((best % 6)[clear], idx[0, h, clear, 1])
+        checked += int(clear.sum())
+    assert checked > 40
+
+
+def test_block_oracle_objective_never_rises():
+    states, tables, init = _problem(13, 1, 2, 30, 8, 16, 3)
+    _out, _idx, hist, initial = ora.block_refinement(states.numpy(), [t.numpy() for t in tables], init.numpy(),
+                                                     (1, 2, 3), (1.0, 1.0, 2.0), sweeps=2, shortlist=3)
+    seq = [initial] + hist
+    assert all(b <= a * (1 + 1e-6) for a, b in zip(seq, seq[1:])), seq
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(prefixes=(1,), exit_weights=(1.0,)), "requires at least two stages"),
+    (dict(prefixes=(2,), exit_weights=(1.0,), shortlist_size=1), "invalid block-refinement"),
+    (dict(prefixes=(2,), exit_weights=(1.0,), shortlist_size=9), "cannot support the requested shortlist"),
+])
+def test_block_refinement_argument_errors(kwargs, match):
+    states, tables, init = _problem(1, 1, 2, 8, 4, 8, 2)
+    if kwargs["prefixes"] == (1,):
+        init = init[..., :1]
+    with pytest.raises(ValueError, match=match):
+        jkv.multi_exit_additive_block_refinement(states, tables, init, **kwargs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,rows,dim,clusters,m,exclude", [(2, 500, 128, 256, 3, True), (1, 70, 9, 40, 8, False),
+                                                                (2, 64, 128, 64, 1, True)])
+def test_nearest_topk_f32_matches_float64(device, heads, rows, dim, clusters, m, exclude):
+    print(f"topk H={heads} N={rows} D={dim} K={clusters} M={m} exclude={exclude}", flush=True)
+    gen = torch.Generator().manual_seed(rows + m)
+    x = torch.randn(heads, rows, dim, generator=gen)
+    c = torch.randn(heads, clusters, dim, generator=gen)
+    excl = torch.randint(0, clusters, (heads, rows), generator=gen) if exclude else None
+    got = _ops.nearest_topk_f32(x.to(device), c.to(device), m,
+                                excluded=None if excl is None else excl.to(device)).cpu().numpy()
+    agree = 0
+    for h in range(heads):
+        want = ora.nearest_topk(x[h].numpy(), c[h].numpy(), m, None if excl is None else excl[h].numpy())
+        d = torch.cdist(x[h].double(), c[h].double()).square().numpy()
+        if excl is not None:
+            d[np.arange(rows), excl[h].numpy()] = np.inf
+        ds = np.sort(d, axis=1)[:, :m + 1]
+        clear = ((ds[:, 1:] - ds[:, :-1]) > 1e-3 * ds[:, :1]).all(1)
+        assert np.array_equal(got[h][clear], np.argsort(d, axis=1, kind="stable")[clear, :m])
+        agree += int((got[h] == want).all(1).sum())
+    assert agree >= 0.999 * heads * rows
+
+
+@pytest.mark.gpu
+def test_block_refinement_matches_oracle(device):
+    print("block refinement H=2 T=100 D=128 K=64 S=3", flush=True)
+    states, tables, init = _problem(31, 1, 2, 100, 128, 64, 3)
+    prefixes, weights = (1, 2, 3), (1.0, 1.0, 2.0)
+    out, idx, diag = jkv.multi_exit_additive_block_refinement(
+        states.to(device), [t.to(device) for t in tables], init.to(device), prefixes=prefixes,
+        exit_weights=weights, sweeps=1, shortlist_size=4, token_chunk_size=64)
+    r_out, r_idx, r_hist, r_init = ora.block_refinement(states.numpy(), [t.numpy() for t in tables], init.numpy(),
+                                                        prefixes, weights, sweeps=1, shortlist=4)
+    same = (idx.cpu().long().numpy() == r_idx).all(-1)
+    assert same.mean() >= 0.99, same.mean()
+    for p in prefixes:
+        err = np.abs(out[p].cpu().numpy() - r_out[p])[same].max()
+        assert err <= 1e-4, (p, err)
+    assert diag["final_weighted_objective"] == pytest.approx(r_hist[-1], rel=1e-3)
+    assert diag["final_weighted_objective"] <= diag["initial_weighted_objective"]
+    assert diag["mode"] == "multi_exit_additive_block" and len(diag["sweep_history"][0]["blocks"]) == 2

@@ -160,9 +160,11 @@ def multi_exit_additive_block_refinement(
     ``shortlist_size - 1`` nearest other codewords of its coordinate target
     (``jkv_nearest_topk_f32``); the ``shortlist_size^2`` products are scored
     with the exact weighted error of every affected exit and the lowest wins,
-    the old pair first on ties.  Rows are scored ``token_chunk_size`` at a
-    time, as the reference does, to bound the ``[H,n,L,L,D]`` score
-    temporaries."""
+    the old pair first on ties.  Rows are independent, so the row chunks
+    only bound the ``[H,n,L,L,D]`` fp32 score temporaries: at least
+    ``token_chunk_size`` rows are scored at a time, and more while those
+    temporaries stay within 512 MiB (the reference's 512-row default would
+    otherwise leave the sweep bound by per-chunk launch overhead)."""
 
     requested = tuple(sorted({int(prefix) for prefix in prefixes}))
     weights = tuple(float(weight) for weight in exit_weights)
@@ -216,14 +218,15 @@ def multi_exit_additive_block_refinement(
     history = []
     total = x.shape[1]
     L = shortlist_size
+    rows_per_chunk = max(token_chunk_size, (512 << 20) // (4 * heads * L * L * dim))
     for sweep in range(sweeps):
         blocks = []
         for first in range(depth - 2, -1, -1):
             pair = (first, first + 1)
             affected = [(p, w) for p, w in zip(requested, weights) if p > first and w > 0]
             changed = [0, 0]
-            for start in range(0, total, token_chunk_size):
-                stop = min(total, start + token_chunk_size)
+            for start in range(0, total, rows_per_chunk):
+                stop = min(total, start + rows_per_chunk)
                 xc = x[:, start:stop]
                 olds = [idx[:, start:stop, s] for s in pair]
                 old_words = [_gather_words(tables[s], o) for s, o in zip(pair, olds)]

@@ -455,7 +455,7 @@ def main() -> int:
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the hot path has no multi-GPU leg "
-              "(per-head sharding needs no exchange; see DESIGN.md)", file=sys.stderr)
+              "(its kv heads shard across GPUs with no exchange between them)", file=sys.stderr)
         return 2
     import torch
 

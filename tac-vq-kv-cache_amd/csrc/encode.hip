@@ -264,19 +264,6 @@ static const int kTiles = 4;                      // 16-row tiles per wave itera
 static const int kRowsPerWave = kTiles * 16;      // rows per wave iteration
 static const int kRowsPerIter = 4 * kRowsPerWave; // rows per workgroup iteration
 
-struct MfmaJob {
-  EncodeArgs e;
-  void* recon_depth[2];  // reconstruction at depth 1 / 2 (or null)
-  int64_t rows_per_wg;
-  int64_t n_chunks;      // row chunks per problem
-};
-
-// One launch runs one or two jobs of the same geometry (a token's K and V):
-// logical workgroups below `split` take job 0, the others job 1.
-struct MfmaArgs {
-  MfmaJob job[2];
-  int64_t split;
-};
 
 // PAIR: two jobs in the launch (a single-job launch keeps every argument at
 // a fixed kernarg offset).  WH (d = 4, one stage): a selector whitener F per
@@ -836,11 +823,6 @@ static bool mfma_eligible(const EncodeArgs& a, int32_t states_dtype) {
          distinct_exits && B * T < ((int64_t)1 << 31) && T < ((int64_t)1 << 31);
 }
 
-template <int D, int S>
-static int launch_mfma_pair_t(const EncodeArgs& k, const EncodeArgs& v, hipStream_t stream) {
-  return launch_mfma<D, S>(k, &v, stream);
-}
-
 }  // namespace jkv
 
 extern "C" {
@@ -905,10 +887,7 @@ int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t 
   if (whiteners != nullptr && (d == 4 || d == 8) && S == 1 && ((uintptr_t)whiteners) % 4 == 0 &&
       mfma_eligible(plain, states_dtype))
     return d == 4 ? launch_mfma<4, 1>(a, stream) : launch_mfma<8, 1>(a, stream);
-  if (fast) {
-    if (d == 8) return S == 1 ? launch_mfma<8, 1>(a, stream) : launch_mfma<8, 2>(a, stream);
-    return S == 1 ? launch_mfma<4, 1>(a, stream) : launch_mfma<4, 2>(a, stream);
-  }
+  if (fast) return launch_grouped(a, nullptr, stream);
   // full-vector codebooks on MFMA (fp16-deployed tables in the workspace),
   // plain or whitened
   const bool full = states_dtype == JKV_F16 && d == 128 && K == 256 && S <= 32 && aligned16 &&
@@ -976,10 +955,7 @@ int jkv_rvq_encode_kv(const void* key_states, const void* value_states, int32_t 
   av.tables = value_tables;
   av.codes = value_codes;
   for (int e = 0; e < n_exits; ++e) av.recon[e] = value_recon ? value_recon[e] : nullptr;
-  if (mfma_eligible(ak, states_dtype) && mfma_eligible(av, states_dtype)) {
-    if (d == 8) return S == 1 ? launch_mfma_pair_t<8, 1>(ak, av, stream) : launch_mfma_pair_t<8, 2>(ak, av, stream);
-    return S == 1 ? launch_mfma_pair_t<4, 1>(ak, av, stream) : launch_mfma_pair_t<4, 2>(ak, av, stream);
-  }
+  if (mfma_eligible(ak, states_dtype) && mfma_eligible(av, states_dtype)) return launch_grouped(ak, &av, stream);
   // other geometries: the two encodes one after the other on the stream
   // (they may share the workspace: the second starts after the first)
   const int rc = jkv_rvq_encode(key_states, states_dtype, B, H, T, G, d, stride_b, stride_h, stride_t,

@@ -26,4 +26,24 @@ int64_t full_workspace_bytes(int64_t P, int64_t S);
 int64_t full_wh_workspace_bytes(int64_t P, int64_t S);  // with an assignment whitener
 int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream);
 
+// Grouped encode on MFMA (d in {4, 8}, K = 256, S <= 2, fp16 states): one job
+// is one encode call; a launch runs one or two jobs of the same geometry (a
+// token's K and V).  Logical workgroups below `split` take job 0.
+struct MfmaJob {
+  EncodeArgs e;
+  void* recon_depth[2];  // reconstruction at depth 1 / 2 (or null)
+  int64_t rows_per_wg;
+  int64_t n_chunks;      // row chunks per problem
+};
+struct MfmaArgs {
+  MfmaJob job[2];
+  int64_t split;
+};
+
+// Rows a workgroup encodes per iteration (4 waves x 64 rows).
+static const int kGroupedRowsPerIter = 256;
+
+// Unwhitened grouped encode (encode_grouped.hip); e2 = second job or null.
+int launch_grouped(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t stream);
+
 }  // namespace jkv

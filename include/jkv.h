@@ -330,8 +330,10 @@ int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_
                                    jkv_stream_t stream);
 
 /* fp32 nearest codeword of every row: states [H,N,D] and tables [H,K,D]
- * contiguous fp32 (not deployed to fp16), D in 1..128; indices [H,N] int64
- * receive argmin_k (|x|^2 + |c_k|^2) - 2 x.c_k, the lowest k on ties.
+ * contiguous fp32 (not deployed to fp16), D in 1..128, N below 2^30 rows
+ * per head (one 256-thread block per 64 rows; larger N returns JKV_EINVAL);
+ * indices [H,N] int64 receive argmin_k (|x|^2 + |c_k|^2) - 2 x.c_k, the
+ * lowest k on ties.
  * Replaces `_nearest_indices` without whiteners
  * (src/jointkv/nested_vq.py:178-215), the search of the offline multi-exit
  * additive coordinate refinement (nested_vq.py:583-741).

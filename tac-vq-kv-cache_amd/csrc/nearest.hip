@@ -304,7 +304,11 @@ extern "C" int jkv_nearest_f32(const float* states, int64_t H, int64_t N, int64_
   JKV_CHECK_ARG(D > 0 && D <= kNrMaxD, "nearest-codeword dimension must lie in 1..%d (got %lld)",
                 kNrMaxD, (long long)D);
   JKV_CHECK_ARG(H <= 65535, "at most 65535 heads per call (got %lld)", (long long)H);
-  JKV_CHECK_ARG(K < ((int64_t)1 << 31) && N < ((int64_t)1 << 37), "nearest-codeword size too large");
+  JKV_CHECK_ARG(K < ((int64_t)1 << 31), "nearest-codeword size too large");
+  // one 256-thread block per 64 rows: the grid's x extent counts work items
+  JKV_CHECK_ARG(ceil_div(N, (int64_t)kNrRows) * 256 < ((int64_t)1 << 32),
+                "at most %lld rows per head (got %lld)", (long long)(kNrRows * ((((int64_t)1 << 32) - 1) / 256)),
+                (long long)N);
   if (N == 0) return JKV_OK;
   JKV_CHECK_ARG(states && tables && indices, "null buffer");
   NearestArgs a = {states, tables, indices, H, N, D, K};
@@ -326,7 +330,11 @@ extern "C" int jkv_nearest_topk_f32(const float* states, int64_t H, int64_t N, i
   JKV_CHECK_ARG(M >= 1 && M <= 8, "top-k candidate count must lie in 1..8 (got %lld)", (long long)M);
   JKV_CHECK_ARG(M < K, "top-k candidate count must lie in [1, cardinality)");
   JKV_CHECK_ARG(H <= 65535, "at most 65535 heads per call (got %lld)", (long long)H);
-  JKV_CHECK_ARG(K < ((int64_t)1 << 31) && N < ((int64_t)1 << 37), "nearest-codeword size too large");
+  JKV_CHECK_ARG(K < ((int64_t)1 << 31), "nearest-codeword size too large");
+  // one 256-thread block per 64 rows: the grid's x extent counts work items
+  JKV_CHECK_ARG(ceil_div(N, (int64_t)kNrRows) * 256 < ((int64_t)1 << 32),
+                "at most %lld rows per head (got %lld)", (long long)(kNrRows * ((((int64_t)1 << 32) - 1) / 256)),
+                (long long)N);
   if (N == 0) return JKV_OK;
   JKV_CHECK_ARG(states && tables && indices, "null buffer");
   NearestArgs a = {states, tables, indices, H, N, D, K};

@@ -20,7 +20,12 @@ def compare_codes(ours: torch.Tensor, expect: torch.Tensor, d1: torch.Tensor, d2
 
     ours = ours.cpu().long()
     expect = expect.cpu().long()
-    ratio = (d2.cpu().double() - d1.cpu().double()) / d1.cpu().double().clamp_min(1e-30)
+    d1 = d1.cpu().double()
+    d2 = d2.cpu().double()
+    # relative to d1, floored at 1e-4 d2: fp32 cancellation in |r|^2+|c|^2-2r.c
+    # can leave a near-exact best match at d1 <= 0, and that match is still
+    # clearly ahead of a second-best distance far above zero
+    ratio = (d2 - d1) / torch.maximum(d1, 1e-4 * d2.abs()).clamp_min(1e-30)
     stages = ours.shape[-1]
     prefix_ok = torch.ones(ours.shape[:-1], dtype=torch.bool)
     judged = equal = clear_bad = 0

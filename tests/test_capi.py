@@ -146,3 +146,15 @@ def test_product_rejects_host_tensors_loudly():
     tables = torch.randn(2, 1, 256, 8)
     with pytest.raises(ValueError, match="HIP"):
         jkv.hard_residual_vq_exits(states, tables, prefixes=(1,))
+
+
+def test_nearest_rejects_rows_beyond_the_grid_before_touching_the_device():
+    # one 256-thread block per 64 rows: 2^30 rows would need a 2^32-item grid
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(16)
+    for name, extra in (("jkv_nearest_f32", []), ("jkv_nearest_topk_f32", [ctypes.c_int64(2), ctypes.c_void_p(0)])):
+        fn = getattr(lib, name)
+        args = [dummy, ctypes.c_int64(1), ctypes.c_int64(1 << 30), ctypes.c_int64(8), dummy, ctypes.c_int64(256)]
+        args += extra + [dummy, ctypes.c_void_p(0)]
+        assert fn(*args) == _lib.JKV_EINVAL
+        assert b"rows per head" in lib.jkv_last_error()

@@ -36,6 +36,7 @@ def _expect(q, kc, vc, kt, vt, length, window, cap):
 
 @pytest.mark.parametrize("batch,qh,kvh,groups,stages,d,length,window,cap", [
     (2, 32, 8, 16, 2, 8, 4096, 4096, 4096),   # config 4 geometry, full window
+    (16, 32, 8, 16, 2, 8, 4096, 4096, 4096),  # config 4 exactly: batch 16 (the benchmarked block mapping)
     (1, 8, 2, 16, 2, 8, 300, 4096, 4096),     # short prefix
     (1, 8, 2, 16, 2, 8, 5000, 4096, 4096),    # window slides, ring buffer wraps
     (1, 4, 4, 32, 1, 4, 700, 512, 512),       # cq2 codes, MHA group of 1

@@ -22,6 +22,17 @@ def _clear(d1: np.ndarray, d2: np.ndarray, margin: float) -> np.ndarray:
     return (d2 - d1) > margin * np.maximum(d1, 1e-30)
 
 
+def _assert_margins_track(d1, d2, bd1, bd2, rows):
+    """The oracle's fp32 best and second-best distances equal the float64
+    brute force's on the given rows (where the codes up to this stage match):
+    the second-best distance decides which codes must be bit-exact, so a slip
+    in it (e.g. the best distance returned twice) must not go unseen."""
+
+    d1, d2 = np.asarray(d1, dtype=np.float64), np.asarray(d2, dtype=np.float64)
+    np.testing.assert_allclose(d1[rows], bd1[rows], rtol=1e-3, atol=1e-4)
+    np.testing.assert_allclose(d2[rows], bd2[rows], rtol=1e-3, atol=1e-4)
+
+
 @pytest.mark.parametrize("seed,dim,clusters", [(1, 3, 4), (2, 4, 16), (3, 8, 256), (4, 4, 256)])
 def test_nearest_search_matches_fp64_bruteforce(seed, dim, clusters):
     gen = torch.Generator().manual_seed(seed)
@@ -47,10 +58,27 @@ def test_residual_stages_match_fp64_bruteforce_hierarchically():
         for s in range(3):
             clear = _clear(bd1[:, s], bd2[:, s], 1e-5) & matched
             assert np.array_equal(ours[clear, s], bcodes[clear, s])
+            # best and second-best distances of stage s, where stages < s matched
+            _assert_margins_track(d1[0, h, :, s].numpy(), d2[0, h, :, s].numpy(), bd1[:, s], bd2[:, s], matched)
             matched &= ours[:, s] == bcodes[:, s]
         assert matched.mean() > 0.98
-        # the oracle's own fp32 margins track the fp64 ones
-        np.testing.assert_allclose(d1[0, h].numpy()[matched], bd1[matched], rtol=1e-3, atol=1e-4)
+
+
+def test_margin_pin_catches_a_second_best_slip():
+    # plant the slip in the oracle's output: the best distance returned as the
+    # second best (vals[..., 0] for vals[..., 1]) must fail the pin
+    gen = torch.Generator().manual_seed(12)
+    states = ref.synthetic_states(gen, 1, 1, 150, 8, outliers=1)
+    tables = ref.synthetic_tables(gen, (1, 2, 64, 8), (1.0, 0.5), stage_axis=1)
+    _out, codes, d1, d2 = ref.hard_residual_vq_exits(states, tables, prefixes=(2,), return_margins=True)
+    bcodes, bd1, bd2 = bf.rvq_encode(states[0, 0].double().numpy(), tables[0].double().numpy())
+    rows = codes[0, 0, :, 0].numpy() == bcodes[:, 0]
+    _assert_margins_track(d1[0, 0, :, 0].numpy(), d2[0, 0, :, 0].numpy(), bd1[:, 0], bd2[:, 0], rows)
+    with pytest.raises(AssertionError):
+        _assert_margins_track(d1[0, 0, :, 0].numpy(), d1[0, 0, :, 0].numpy(), bd1[:, 0], bd2[:, 0], rows)
+    # and the clear-margin rule then judges no code at all: the check it feeds
+    # would be switched off
+    assert compare_codes(codes, codes, d1, d1)["clear_mismatches"] == 0
 
 
 def test_exits_equal_decode_of_codes_and_fp16_codewords():
@@ -129,6 +157,9 @@ def test_grouped_cq_matches_bruteforce_and_identity_whitener():
             ours = codes[:, h, :, g].reshape(-1).numpy()
             clear = _clear(bd1[:, 0], bd2[:, 0], 1e-5)
             assert np.array_equal(ours[clear], bcodes[clear, 0])
+            same = ours == bcodes[:, 0]
+            _assert_margins_track(d1[:, h, :, g].reshape(-1).numpy(), d2[:, h, :, g].reshape(-1).numpy(),
+                                  bd1[:, 0], bd2[:, 0], same)
     recon = books.half().float()[torch.arange(2)[None, :, None, None], torch.arange(8)[None, None, None, :], codes.long()]
     torch.testing.assert_close(out.float(), recon.reshape(2, 2, 64, 32), rtol=0, atol=0)
 
@@ -357,3 +388,17 @@ def test_prefill_oracle_against_fp64_rows_and_masks():
                     row = bf.attention_row(qr[hq, t].double().numpy(), kr[hq // 2, lo : t + 1].double().numpy(),
                                            v[b, hq // 2, lo : t + 1].double().numpy())
                     np.testing.assert_allclose(out[b, hq, t].float().numpy(), row, atol=2e-3)
+
+
+def test_clear_margin_rule_judges_near_zero_best_distances():
+    # a best distance rounded to <= 0 by fp32 cancellation is still a clear
+    # winner against a second best far above zero: a different code there fails
+    ours = torch.tensor([[1], [2], [3]])
+    expect = torch.tensor([[1], [5], [3]])
+    d1 = torch.tensor([[1.0], [-1e-6], [2.0]])
+    d2 = torch.tensor([[2.0], [0.5], [2.0000001]])
+    res = compare_codes(ours, expect, d1, d2)
+    assert res["clear_mismatches"] == 1
+    # a true near-tie stays exempt
+    res = compare_codes(torch.tensor([[4]]), torch.tensor([[3]]), torch.tensor([[2.0]]), torch.tensor([[2.0000001]]))
+    assert res["clear_mismatches"] == 0

@@ -201,6 +201,32 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b,
                          int64_t workspace_bytes, jkv_stream_t stream);
 
 /*
+ * Allocation-free variant of jkv_decode_attention.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and errors as jkv_decode_attention without the
+ * workspace: the split partials go to a file-scope device array of the
+ * library (one per GPU, jkv_decode_noalloc_max_workspace_bytes() = 16 MiB,
+ * held until the process ends).  Calls that need more partial space than
+ * that (jkv_decode_workspace_bytes(B, QH, 128, window) above the maximum)
+ * return JKV_EINVAL.  The array is looked up on the first call on each
+ * device (the current HIP device); no call allocates or frees memory.  Every
+ * call on a device shares that device's array: calls that overlap on one
+ * GPU (two streams, two threads) race and must be serialised by the caller.
+ */
+int64_t jkv_decode_noalloc_max_workspace_bytes(void);
+int jkv_decode_attention_noalloc(const void* q, int64_t q_stride_b,
+                                 int64_t q_stride_h, const uint8_t* k_codes,
+                                 const uint8_t* v_codes, int64_t code_stride_b,
+                                 int64_t code_stride_h, int64_t cap,
+                                 const void* k_tables, const void* v_tables,
+                                 int64_t B, int64_t QH, int64_t KVH, int64_t G,
+                                 int64_t d, int64_t S, int64_t K,
+                                 const int32_t* lengths, int64_t window,
+                                 const void* rope_table, int64_t rope_len,
+                                 void* out, jkv_stream_t stream);
+
+/*
  * Decode attention over a decoded fp16 K̂/V̂ window, the reference's own
  * decode path (evaluate_mistral_longbench.py:112-122 over LayerCache's
  * decoded_key/decoded_value, :44-70), for codecs whose codewords do not fit

@@ -10,6 +10,8 @@
 //  * softmax over the split in fp32; P.V̂ accumulates in fp32 on the VALU;
 //  * the split's unnormalised (max, sum, out) go to a workspace that
 //    decode_combine folds into fp16 outputs.
+#include <mutex>
+
 #include "jkv_common.h"
 #include "rotary.h"
 
@@ -884,15 +886,18 @@ int64_t jkv_decode_workspace_bytes(int64_t B, int64_t QH, int64_t D, int64_t win
   return B * QH * ns * (D + 2) * (int64_t)sizeof(float);
 }
 
-int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                         const uint8_t* k_codes, const uint8_t* v_codes, int64_t code_stride_b,
-                         int64_t code_stride_h, int64_t cap, const void* k_tables,
-                         const void* v_tables, int64_t B, int64_t QH, int64_t KVH, int64_t G,
-                         int64_t d, int64_t S, int64_t K, const int32_t* lengths, int64_t window,
+}  // extern "C"
+
+namespace jkv {
+
+// Packed-code decode with the split partials in `workspace`; the C entry
+// points below pass the caller's buffer or the library's static scratch.
+static int decode_packed(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* k_codes,
+                         const uint8_t* v_codes, int64_t code_stride_b, int64_t code_stride_h, int64_t cap,
+                         const void* k_tables, const void* v_tables, int64_t B, int64_t QH, int64_t KVH,
+                         int64_t G, int64_t d, int64_t S, int64_t K, const int32_t* lengths, int64_t window,
                          const void* rope_table, int64_t rope_len, void* out, void* workspace,
-                         int64_t workspace_bytes, jkv_stream_t stream_) {
-  using namespace jkv;
-  hipStream_t stream = (hipStream_t)stream_;
+                         int64_t workspace_bytes, hipStream_t stream) {
   JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && QH % KVH == 0, "invalid head geometry");
   JKV_CHECK_ARG(G * d == kHeadDim, "decode attention supports head_dim 128 (got %lld)",
                 (long long)(G * d));
@@ -940,6 +945,76 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   JKV_DEC(128, 1) JKV_DEC(128, 2) JKV_DEC(128, 4) JKV_DEC(128, 8)
 #undef JKV_DEC
   return set_error(JKV_ENOTSUP, "unsupported decode geometry");
+}
+
+// Allocation-free decode (jkv_decode_attention_noalloc): the split partials
+// live in this file-scope array, one copy per GPU, held until the process
+// ends.  Host code never passes the array's name to a kernel (on the host it
+// is a stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, once per device with that device current, and is kept
+// in g_scratch_ptr.
+static const int64_t kNoAllocScratchBytes = (int64_t)16 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+static const int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (looked up on first use).
+static int current_scratch(void** ptr) {
+  int dev = -1;
+  JKV_CHECK_HIP(hipGetDevice(&dev));
+  JKV_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device ordinal %d outside 0..%d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    JKV_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    JKV_CHECK_ARG(p != nullptr, "scratch symbol has no device address");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return JKV_OK;
+}
+
+}  // namespace jkv
+
+extern "C" {
+
+int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                         const uint8_t* k_codes, const uint8_t* v_codes, int64_t code_stride_b,
+                         int64_t code_stride_h, int64_t cap, const void* k_tables,
+                         const void* v_tables, int64_t B, int64_t QH, int64_t KVH, int64_t G,
+                         int64_t d, int64_t S, int64_t K, const int32_t* lengths, int64_t window,
+                         const void* rope_table, int64_t rope_len, void* out, void* workspace,
+                         int64_t workspace_bytes, jkv_stream_t stream) {
+  return jkv::decode_packed(q, q_stride_b, q_stride_h, k_codes, v_codes, code_stride_b, code_stride_h, cap,
+                            k_tables, v_tables, B, QH, KVH, G, d, S, K, lengths, window, rope_table, rope_len,
+                            out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int64_t jkv_decode_noalloc_max_workspace_bytes(void) { return jkv::kNoAllocScratchBytes; }
+
+int jkv_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const uint8_t* k_codes, const uint8_t* v_codes, int64_t code_stride_b,
+                                 int64_t code_stride_h, int64_t cap, const void* k_tables,
+                                 const void* v_tables, int64_t B, int64_t QH, int64_t KVH, int64_t G,
+                                 int64_t d, int64_t S, int64_t K, const int32_t* lengths, int64_t window,
+                                 const void* rope_table, int64_t rope_len, void* out,
+                                 jkv_stream_t stream) {
+  using namespace jkv;
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && window > 0, "invalid head geometry");
+  const int64_t need = jkv_decode_workspace_bytes(B, QH, kHeadDim, window);
+  JKV_CHECK_ARG(need <= kNoAllocScratchBytes,
+                "allocation-free decode attention holds at most %lld bytes of split partials; "
+                "B=%lld, QH=%lld, window=%lld need %lld (use jkv_decode_attention with a workspace)",
+                (long long)kNoAllocScratchBytes, (long long)B, (long long)QH, (long long)window, (long long)need);
+  if (B == 0) return JKV_OK;
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc != JKV_OK) return rc;
+  return decode_packed(q, q_stride_b, q_stride_h, k_codes, v_codes, code_stride_b, code_stride_h, cap, k_tables,
+                       v_tables, B, QH, KVH, G, d, S, K, lengths, window, rope_table, rope_len, out, ws,
+                       kNoAllocScratchBytes, (hipStream_t)stream);
 }
 
 int jkv_decode_attention_window(const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -381,6 +381,37 @@ int jkv_nearest_topk_f32(const float* states, int64_t H, int64_t N, int64_t D,
                          jkv_stream_t stream);
 
 /*
+ * One sliding-pair step of the offline multi-exit additive block refinement:
+ * replaces the Cartesian scoring and update of one (stage, stage+1) block of
+ * `multi_exit_additive_block_refinement` (src/jointkv/nested_vq.py:838-958).
+ *   states     [H][N][D] fp32 rows x
+ *   recon      [n_recon][H][N][D] fp32 reconstruction of each exit, updated
+ *              in place for the n_exits exits listed
+ *   exit_slots, exit_weights, exit_has_second  (host arrays, n_exits <= 32):
+ *              the weighted exits that contain the first stage, their
+ *              weight and whether they also contain the second stage
+ *   first_table [H][K1][D], second_table [H][K2][D] fp32 codebooks
+ *   first_shortlist, second_shortlist  [H][N][L] int64 (1 <= L <= 9): entry
+ *              0 is the current index, the rest its alternatives, each in
+ *              [0, K)
+ *   first_out, second_out  [H][N] int64: the chosen indices
+ * The pair (i, j) minimises sum_m w_m |(x - r_m) + c1[cur1] + s_m c2[cur2]
+ * - c1[i] - s_m c2[j]|^2 (s_m = exit m contains the second stage), the
+ * lowest i*L + j (the current pair first) on equal cost; each listed
+ * reconstruction then moves by the chosen words' changes, first stage first.
+ */
+int jkv_pair_block_select(const float* states, float* recon, int64_t n_recon,
+                          int64_t H, int64_t N, int64_t D, int32_t n_exits,
+                          const int32_t* exit_slots, const float* exit_weights,
+                          const int32_t* exit_has_second,
+                          const float* first_table, const float* second_table,
+                          int64_t K1, int64_t K2,
+                          const int64_t* first_shortlist,
+                          const int64_t* second_shortlist, int64_t L,
+                          int64_t* first_out, int64_t* second_out,
+                          jkv_stream_t stream);
+
+/*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of
  * the 64 frequencies, then their sin):
  * angle = fp32(p) * inv_freq[i] in fp32, cos/sin in fp32 rounded to fp16 —

@@ -56,6 +56,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_i32, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _vp, _i32, _vp, _i64, _vp],
     ),
+    "jkv_pair_block_select": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp,
+         _vp],
+    ),
     "jkv_sumsq": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
     "jkv_scale_sgd": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _f32, _vp]),
     "jkv_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),

@@ -118,7 +118,8 @@ def hard_residual_vq_exits(
     soft_backward_beta: float = 0.0,
     deterministic_backward: bool = False,
 ) -> tuple[dict[int, torch.Tensor], torch.Tensor]:
-    """Encode hard residual-VQ indices and return differentiable exits.
+    """Greedy residual VQ of every head vector through all S stages in one
+    HIP launch, with straight-through exits at the requested depths.
 
     Same contract as closed_loop_vq.py:235-410: ``states[B,H,T,D]``,
     ``tables[H,S,K,D]`` (fp32 masters; search and decode use their fp16

@@ -26,10 +26,13 @@ def hard_grouped_cq(
     straight_through_states: bool = True,
     deterministic_backward: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Exact hard CQ roundtrip for ``[B,H,T,D]`` and ``[H,G,K,S]``.
+    """Grouped composite quantization of states ``[B,H,T,D]`` against
+    codebooks ``[H,G,K,S]`` (cq_tac.py:33-114): every S-wide channel group of
+    a vector picks its nearest fp16-deployed codeword in one HIP launch.
 
     Returns (reconstruction ``[B,H,T,D]`` in ``states.dtype``, codes
-    ``[B,H,T,G]`` uint8).  ``token_chunk_size`` is validated only.
+    ``[B,H,T,G]`` uint8).  ``token_chunk_size`` is validated only; the kernel
+    needs no row chunks.
     """
 
     if states.ndim != 4 or codebooks.ndim != 4:
@@ -74,7 +77,8 @@ def _is_identity(whitener: torch.Tensor) -> bool:
 
 
 class ClosedLoopGroupedCQ(nn.Module):
-    """All-layer hard CQ codec with frozen K and trainable V centroids.
+    """Per-layer grouped-CQ codec: K codebooks are frozen buffers of the
+    calibration, V codebooks are the trainable fp32 masters.
 
     Same constructor, buffers, parameters and forward contract as
     cq_tac.py:117-192.  An identity selector whitener (the default the

@@ -18,7 +18,8 @@ from .closed_loop_vq import QuantizedKV, hard_grouped_residual_vq, hard_residual
 
 
 class ClosedLoopUniformResidualVQ(nn.Module):
-    """Literal hard uniform residual VQ with value-only task adaptation."""
+    """Per-layer residual-VQ codec at one fixed depth: every stage of every
+    K and V head vector is coded (hard), and only the V tables train."""
 
     def __init__(
         self,

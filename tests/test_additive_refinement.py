@@ -246,3 +246,86 @@ def test_block_refinement_matches_oracle(device):
     assert diag["final_weighted_objective"] == pytest.approx(r_hist[-1], rel=1e-3)
     assert diag["final_weighted_objective"] <= diag["initial_weighted_objective"]
     assert diag["mode"] == "multi_exit_additive_block" and len(diag["sweep_history"][0]["blocks"]) == 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("block", [False, True])
+def test_zero_weight_exit_keeps_its_initial_reconstruction(device, block):
+    # only weighted exits move (nested_vq.py:711-716, :945-948): exit 2 of
+    # weight 0 keeps the decode of the initial indices while its stages change
+    print(f"zero-weight exit, block={block}", flush=True)
+    states, tables, init = _problem(41, 1, 2, 120, 16, 32, 3)
+    prefixes, weights = (1, 2, 3), (1.0, 0.0, 2.0)
+    args = (states.to(device), [t.to(device) for t in tables], init.to(device))
+    if block:
+        out, idx, diag = jkv.multi_exit_additive_block_refinement(*args, prefixes=prefixes, exit_weights=weights,
+                                                                  shortlist_size=3)
+        r_out, r_idx, r_hist, _ = ora.block_refinement(states.numpy(), [t.numpy() for t in tables], init.numpy(),
+                                                       prefixes, weights, shortlist=3)
+    else:
+        out, idx, diag = jkv.multi_exit_additive_coordinate_refinement(*args, prefixes=prefixes, exit_weights=weights)
+        r_out, r_idx, r_hist, _ = ora.coordinate_refinement(states.numpy(), [t.numpy() for t in tables],
+                                                            init.numpy(), prefixes, weights)
+    same = (idx.cpu().long().numpy() == r_idx).all(-1)
+    assert same.mean() >= 0.99
+    assert (idx.cpu().long() != init).any(), "the sweep moved no index"
+    initial_decode = sum(tables[s][torch.arange(2)[None, :, None], init[..., s]] for s in range(2)).permute(0, 1, 2, 3)
+    torch.testing.assert_close(out[2].cpu(), initial_decode, rtol=0, atol=1e-6)
+    for p in (1, 3):
+        assert np.abs(out[p].cpu().numpy() - r_out[p])[same].max() <= 1e-4
+    assert diag["final_weighted_objective"] == pytest.approx(r_hist[-1], rel=1e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("block", [False, True])
+def test_token_chunk_size_changes_nothing(device, block):
+    # rows are independent and no step materialises per-chunk temporaries, so
+    # the chunk size (validated, as the reference's) must not move a bit
+    print(f"chunk independence, block={block}", flush=True)
+    states, tables, init = _problem(43, 1, 2, 200, 32, 64, 3)
+    runs = []
+    for chunk in (1, 64, 4096):
+        args = (states.to(device), [t.to(device) for t in tables], init.to(device))
+        fn = jkv.multi_exit_additive_block_refinement if block else jkv.multi_exit_additive_coordinate_refinement
+        out, idx, diag = fn(*args, prefixes=(1, 2, 3), exit_weights=(1.0, 1.0, 2.0), sweeps=2, token_chunk_size=chunk)
+        runs.append((out, idx, diag["final_weighted_objective"]))
+    for out, idx, obj in runs[1:]:
+        assert torch.equal(idx, runs[0][1])
+        for p in (1, 2, 3):
+            assert torch.equal(out[p], runs[0][0][p])
+        assert obj == runs[0][2]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dim,clusters,shortlist", [(7, 40, 4), (128, 64, 9), (16, 256, 2)])
+def test_block_refinement_kernel_paths_match_oracle(device, dim, clusters, shortlist):
+    # odd D takes the scalar scoring loop, shortlist 9 gives lanes two pairs
+    print(f"block kernel D={dim} K={clusters} L={shortlist}", flush=True)
+    states, tables, init = _problem(47 + dim, 1, 2, 90, dim, clusters, 3)
+    prefixes, weights = (2, 3), (1.0, 3.0)
+    out, idx, diag = jkv.multi_exit_additive_block_refinement(
+        states.to(device), [t.to(device) for t in tables], init.to(device), prefixes=prefixes, exit_weights=weights,
+        shortlist_size=shortlist)
+    r_out, r_idx, r_hist, r_init = ora.block_refinement(states.numpy(), [t.numpy() for t in tables], init.numpy(),
+                                                        prefixes, weights, shortlist=shortlist)
+    same = (idx.cpu().long().numpy() == r_idx).all(-1)
+    assert same.mean() >= 0.98, same.mean()
+    for p in prefixes:
+        assert np.abs(out[p].cpu().numpy() - r_out[p])[same].max() <= 1e-4
+    assert diag["final_weighted_objective"] <= diag["initial_weighted_objective"] * (1 + 1e-6)
+    assert diag["final_weighted_objective"] == pytest.approx(r_hist[-1], rel=1e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("block", [False, True])
+def test_refinement_leaves_its_inputs_alone(device, block):
+    # batch 1 makes the permuted index view contiguous: the sweep must still
+    # work on a copy of the caller's indices (and states, tables)
+    states, tables, init = _problem(53, 1, 2, 64, 16, 32, 2)
+    args = [states.to(device), [t.to(device) for t in tables], init.to(device)]
+    before = [args[0].clone(), [t.clone() for t in args[1]], args[2].clone()]
+    fn = jkv.multi_exit_additive_block_refinement if block else jkv.multi_exit_additive_coordinate_refinement
+    _out, idx, _diag = fn(*args, prefixes=(1, 2), exit_weights=(1.0, 1.0))
+    assert (idx.cpu().long() != init).any()
+    assert torch.equal(args[0], before[0]) and torch.equal(args[2], before[2])
+    assert all(torch.equal(a, b) for a, b in zip(args[1], before[1]))

@@ -405,10 +405,36 @@ def adapter_workload(args, device):
     }
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_seconds(fn, runs: int = 3) -> float:
+    fn()  # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
 def cpu_baseline(args):
-    """The oracle (eager PyTorch restatement of the reference) on one layer's K
-    over a bounded token sample, timed on this host; scaled to tokens/s of the
-    full 32-layer x {K,V} workload."""
+    """The oracle (eager PyTorch restatement of the reference's op sequence)
+    timed on this host with every core, median of 3 after a warm-up.
+
+    Headline (config 2): one (layer, K) tensor over a bounded token sample,
+    scaled to tokens/s of the full 32-layer x {K,V} workload.  Alongside:
+    config 1 at full size (grouped CQ of one layer's K and V,
+    cq_tac.py:33-114) and one config-4 decode layer at batch 16 (decode the
+    codes, RoPE, repeat_kv, SDPA: evaluate_mistral_longbench.py:112-122),
+    scaled x32 layers."""
 
     import torch
     from oracle import jointkv_oracle as ref
@@ -419,24 +445,71 @@ def cpu_baseline(args):
     tokens = args.cpu_tokens
     states = ref.synthetic_states(gen, 1, HEADS, tokens)
     tables = ref.synthetic_tables(gen, (HEADS, GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), stage_axis=2)
-    ref.grouped_residual_vq(states[:, :, :64], tables, prefixes=(2,))  # warm-up
-    runs = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        with torch.no_grad():
-            ref.grouped_residual_vq(states, tables, prefixes=(2,))
-        runs.append(time.perf_counter() - t0)
-    sec = sorted(runs)[1]
+    with torch.no_grad():
+        sec = _median_seconds(lambda: ref.grouped_residual_vq(states, tables, prefixes=(2,)))
     # one (layer, K) tensor of `tokens` tokens took `sec`; a full token needs 64 such
     per_token = sec / tokens * (2 * LAYERS)
+
+    # config 1: cq1 K and V of one layer at full size, token_chunk_size 64
+    gen1 = torch.Generator().manual_seed(8601)
+    k1 = ref.synthetic_states(gen1, 1, HEADS, 2048)
+    v1 = ref.synthetic_states(gen1, 1, HEADS, 2048)
+    books = ref.synthetic_tables(gen1, (HEADS, GROUPS, CLUSTERS, GROUP_DIM), (1.0,), stage_axis=0)
+    with torch.no_grad():
+        sec1 = _median_seconds(lambda: (ref.hard_grouped_cq(k1, books), ref.hard_grouped_cq(v1, books)))
+
+    # config 4: one decode layer, B16, 32 query / 8 kv heads, 4096 cached tokens
+    gen4 = torch.Generator().manual_seed(8601)
+    b4, window = 16, 4096
+    q = torch.randn(b4, 32, 1, HEAD_DIM, generator=gen4).half()
+    kc = torch.randint(0, CLUSTERS, (b4, HEADS, window, GROUPS, STAGES), generator=gen4, dtype=torch.uint8)
+    vc = torch.randint(0, CLUSTERS, (b4, HEADS, window, GROUPS, STAGES), generator=gen4, dtype=torch.uint8)
+    kt = ref.synthetic_tables(gen4, (HEADS * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), stage_axis=1)
+    vt = ref.synthetic_tables(gen4, (HEADS * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), stage_axis=1)
+    pos = torch.arange(window)
+
+    def decode_layer():
+        khat = ref.frozen_decode(kc, kt, STAGES, torch.float16)
+        vhat = ref.frozen_decode(vc, vt, STAGES, torch.float16)
+        return ref.decode_attention(q, khat, vhat, window - 1, pos)
+
+    with torch.no_grad():
+        sec4 = _median_seconds(decode_layer)
     return {
         "value": 1.0 / per_token,
         "unit": "tokens/s",
         "cores": int(torch.get_num_threads()),
         "kind": "port",
         "sample": f"oracle grouped_residual_vq (reference op sequence, token_chunk_size=1024) on one "
-                  f"(layer,K) tensor [1,8,{tokens},128], median of 3, scaled x64 tensors per token",
+                  f"(layer,K) tensor [1,8,{tokens},128], median of 3 after a warm-up, scaled x64 tensors per token",
+        "host": {"cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+                 "torch_threads": int(torch.get_num_threads()), "torch": torch.__version__},
+        "config1_full": {"ms_per_layer_kv": sec1 * 1e3,
+                         "sample": "oracle hard_grouped_cq of K and V [1,8,2048,128], codebooks [8,16,256,8], "
+                                   "token_chunk_size 64, full size, median of 3"},
+        "config4_decode": {"us_per_step": sec4 * LAYERS * 1e6, "ms_per_layer": sec4 * 1e3,
+                           "sample": "oracle frozen_decode (K and V, G2 codes [16,8,4096,16,2]) + rotary + "
+                                     "repeat_kv + SDPA for q [16,32,1,128], one layer, median of 3, scaled x32"},
     }
+
+
+def cq1_workload(args, device):
+    """Config 1 on the GPU: cq1 (16 groups x 8 dims, 256 codewords) K and V
+    of one layer [1,8,2048,128], as the codec forward encodes them."""
+
+    import torch
+    from jointkv_amd import _ops
+
+    gen = torch.Generator(device=device).manual_seed(8601)
+    k = make_states(gen, 1, HEADS, 2048, device)
+    v = make_states(gen, 1, HEADS, 2048, device)
+    books = make_tables(gen, (HEADS * GROUPS, 1, CLUSTERS, GROUP_DIM), (1.0,), 1, device)
+    launches = [lambda: _ops.rvq_encode(k, books, groups=GROUPS, group_dim=GROUP_DIM, exits=(1,)),
+                lambda: _ops.rvq_encode(v, books, groups=GROUPS, group_dim=GROUP_DIM, exits=(1,))]
+    for fn in launches:
+        fn()
+    us = per_launch_ms(launches * 50) * 1e3
+    return {"us_per_layer_kv": 2 * us, "us_per_tensor": us}
 
 
 def main() -> int:
@@ -446,7 +519,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
-    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,adapter,cq2,full,cpu")
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,adapter,cq1,cq2,full,cpu")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
@@ -465,6 +538,9 @@ def main() -> int:
     enc = encode_workload(args, device)
     log(f"encode: {enc['ms_per_step']:.3f} ms/step")
     extras = {}
+    if "cq1" not in skip:
+        log("cq1 workload (config 1)")
+        extras["cq1_encode"] = cq1_workload(args, device)
     if "cq2" not in skip:
         log("cq2 workload (config 3)")
         extras["cq2_encode"] = cq2_workload(args, device)
@@ -513,7 +589,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
             "traffic": measured_traffic(ROOT / "profiles" / "rvq_encode_mfma_g2_config2.md"),
-            "kernel": "rvq_encode_mfma<8,2>",
+            "kernel": "rvq_encode_grouped<8,2>",
             "avg_launch_us": enc["avg_launch_ms"] * 1e3,
             "algorithmic_flop_per_launch": enc["flops_per_launch"],
             "algorithmic_bytes_per_launch": enc["bytes_per_launch"],

@@ -236,6 +236,128 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
   }
 }
 
+// fp16 gradients with 8-dim groups (the G2 / cq1 geometry): one block of
+// 1024 threads owns every stage's bins of one (head, group) over a chunk of
+// rows, so each row's 16-byte gradient slice is read once and feeds all
+// stages (bins [S][K][9] of exact 64-bit fixed point in LDS).  Row
+// addresses advance by the block stride without a division per row.
+// Logical blocks run group, chunk, head from fastest to slowest: the groups
+// of one row range share its 256-byte rows in one XCD's L2.
+template <int S>
+__global__ __launch_bounds__(1024) void scatter_group8_kernel(ScatterArgs a) {
+  constexpr int D = 8, U = 4, kPad = D + 1;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  long long* bins = (long long*)lds_raw;  // [S][K][kPad]
+  __shared__ uint32_t nonfinite;
+  const int K = (int)a.K;
+  const uint32_t G = (uint32_t)a.G;
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t g = bid % G;
+  const uint32_t chunk = (bid / G) % (uint32_t)a.n_chunks;
+  const uint32_t h = bid / (G * (uint32_t)a.n_chunks);
+  const uint32_t p = h * G + g;
+  for (int i = threadIdx.x; i < S * K * kPad; i += blockDim.x) bins[i] = 0;
+  if (threadIdx.x == 0) nonfinite = 0u;
+  __syncthreads();
+
+  // rows [r0, r1) of this chunk; offsets fit 32 bits (host-checked)
+  const uint32_t rows = (uint32_t)(a.B * a.T), T32 = (uint32_t)a.T;
+  const uint32_t r0 = chunk * (uint32_t)a.rows_per_chunk;
+  const uint32_t r1 = min(r0 + (uint32_t)a.rows_per_chunk, rows);
+  const uint32_t Dfull = G * D;
+  const uint32_t gstride_t = Dfull, gstride_b = (uint32_t)a.H * T32 * Dfull;
+  const uint32_t gbase = h * T32 * Dfull + g * D;
+  const int64_t cbase = (int64_t)h * a.ch + (int64_t)g * S;
+  const uint32_t step = blockDim.x;
+  // this thread's first row as (b, t); later rows advance by `step`
+  uint32_t row = r0 + threadIdx.x;
+  uint32_t b = row / T32, t = row - b * T32;
+  auto advance = [&]() {
+    row += step;
+    if (T32 >= step) {
+      t += step;
+      if (t >= T32) { t -= T32; ++b; }
+    } else {
+      b = row / T32;
+      t = row - b * T32;
+    }
+  };
+  uint32_t bad = 0u;
+  while (row < r1) {
+    uint32_t goff[U];
+    int64_t coff[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ok[u] = row < r1;
+      goff[u] = ok[u] ? b * gstride_b + gbase + t * gstride_t : gbase;
+      coff[u] = ok[u] ? (int64_t)b * a.cb + cbase + (int64_t)t * a.ct : cbase;
+      advance();
+    }
+    uint32_t code[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < S; ++s) code[u][s] = a.codes[coff[u] + s];
+    // each exit's slice goes straight into the bins of the stages it covers
+    // (exact integer sums, so the order of the additions does not matter)
+    for (int e = 0; e < a.n_exits; ++e) {
+      long long x[U][D];
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_slice<JKV_F16, D>(a.grads[e], goff[u], x[u], bad);
+      const int depth = a.exit_depth[e];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!ok[u]) continue;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if (s >= depth) continue;
+          long long* bin = bins + (s * K + (int)code[u][s]) * kPad;
+#pragma unroll
+          for (int i = 0; i < D; ++i) lds_add(&bin[i], x[u][i]);
+        }
+      }
+    }
+  }
+  if (bad) atomicOr(&nonfinite, 1u);
+  __syncthreads();
+
+  const int64_t d = a.d;
+  if (nonfinite) {
+    // a slice holds inf or nan: fp32 sums with global atomics give the IEEE
+    // outcome (exit sums in exit order, as grad_sum)
+    for (uint32_t rr = r0 + threadIdx.x; rr < r1; rr += step) {
+      const uint32_t bb = rr / T32, tt = rr - bb * T32;
+      const int64_t off = (int64_t)bb * gstride_b + gbase + (int64_t)tt * gstride_t;
+      const int64_t co = (int64_t)bb * a.cb + cbase + (int64_t)tt * a.ct;
+      for (int s = 0; s < S; ++s) {
+        float* dst = a.grad_tables + (((int64_t)p * S + s) * K + a.codes[co + s]) * d;
+        for (int i = 0; i < D; ++i) {
+          float acc = 0.f;
+          for (int e = 0; e < a.n_exits; ++e)
+            if (a.exit_depth[e] > s) acc += Elem<JKV_F16>::load(a.grads[e], off + i);
+          if (acc != 0.f || acc != acc) atomicAdd(&dst[i], acc);
+        }
+      }
+    }
+    if (a.n_chunks > 1) {
+      long long* part = (long long*)a.partials + (((int64_t)chunk * a.H * a.G + p) * S) * K * d;
+      for (int i = threadIdx.x; i < S * K * D; i += blockDim.x) part[i] = 0;
+    }
+    return;
+  }
+  for (int i = threadIdx.x; i < S * K * D; i += blockDim.x) {
+    const int s = i / (K * D), k = (i / D) % K, c = i % D;
+    const long long v = bins[(s * K + k) * kPad + c];
+    const int64_t o = (((int64_t)p * S + s) * K + k) * d + c;
+    if (a.n_chunks == 1) {
+      a.grad_tables[o] += fixed_to_float(v);
+    } else {
+      ((long long*)a.partials)[(int64_t)chunk * a.H * a.G * S * K * d + o] = v;
+    }
+  }
+}
+
 // grad[p, ...] += sum over chunks of the per-chunk partials: an exact integer
 // sum for fixed-point partials, else an fp32 sum in chunk order.
 template <typename Acc>
@@ -317,6 +439,7 @@ static const int64_t kDetRowsPerChunk = 256;
 struct BinsPlan {
   bool ok;
   bool fixed;      // exact 64-bit fixed-point bins (fp16 gradients)
+  bool group8;     // scatter_group8_kernel: every stage of an 8-dim group per block
   int32_t slice;   // dims per block (D): 8 or 4, dividing d
   int64_t chunks;  // row chunks (power of two)
   size_t lds;      // dynamic LDS bytes per block
@@ -325,13 +448,28 @@ struct BinsPlan {
 
 static BinsPlan bins_plan(int64_t B, int64_t T, int64_t H, int64_t G, int64_t d, int64_t S,
                           int64_t K, int32_t grad_dtype) {
-  BinsPlan r = {false, false, 0, 1, 0, 0};
+  BinsPlan r = {false, false, false, 0, 1, 0, 0};
   const int64_t rows = B * T;
   if (d % 4 != 0 || rows >= ((int64_t)1 << 31)) return r;
   r.slice = d % 8 == 0 ? 8 : 4;
   // fixed point: |bin| < rows * 8 exits * 2^40 must stay below 2^63
   r.fixed = grad_dtype == JKV_F16 && rows <= ((int64_t)1 << 20);
   const int64_t acc_bytes = r.fixed ? 8 : 4;
+  // every stage of an 8-dim group in one block: 32-bit offsets over the
+  // gradient rows (B*H*T*G*8 elements) and the code records
+  r.group8 = r.fixed && d == 8 && S <= 4 && K <= 256 && B * H * T * G * d < ((int64_t)1 << 31);
+  if (r.group8) {
+    const int64_t blocks = H * G;
+    int64_t chunks = 1;
+    while (blocks * chunks < JKV_SCATTER_TARGET_BLOCKS &&
+           ceil_div(rows, chunks * 2) >= JKV_SCATTER_MIN_ROWS)
+      chunks *= 2;
+    r.ok = true;
+    r.chunks = chunks;
+    r.lds = (size_t)(S * K * (d + 1) * acc_bytes);
+    r.workspace = chunks > 1 ? chunks * H * G * S * K * d * acc_bytes : 0;
+    return r;
+  }
   const int64_t blocks = H * G * S * (d / r.slice);
   if (blocks >= ((int64_t)1 << 24)) return r;
   int64_t chunks = 1;
@@ -383,7 +521,27 @@ static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) 
   for (int e = 0; e < a.n_exits; ++e) aligned = aligned && ((uintptr_t)a.grads[e] % align == 0);
   JKV_CHECK_ARG(aligned || !deterministic,
                 "deterministic scatter needs gradient buffers aligned to 8 (or 4) elements");
-  if (plan.ok && aligned) {
+  if (plan.ok && aligned && plan.group8) {
+    a.n_chunks = plan.chunks;
+    a.rows_per_chunk = ceil_div(rows, plan.chunks);
+    int64_t nblocks = P * plan.chunks;
+    const dim3 grid((uint32_t)nblocks);
+    switch (a.S) {
+      case 1: hipLaunchKernelGGL(scatter_group8_kernel<1>, grid, dim3(1024), plan.lds, stream, a); break;
+      case 2: hipLaunchKernelGGL(scatter_group8_kernel<2>, grid, dim3(1024), plan.lds, stream, a); break;
+      case 3: hipLaunchKernelGGL(scatter_group8_kernel<3>, grid, dim3(1024), plan.lds, stream, a); break;
+      default: hipLaunchKernelGGL(scatter_group8_kernel<4>, grid, dim3(1024), plan.lds, stream, a); break;
+    }
+    JKV_CHECK_LAUNCH();
+    if (a.n_chunks > 1) {
+      const int64_t per_chunk = P * a.S * a.K * a.d;
+      hipLaunchKernelGGL(scatter_chunk_reduce_kernel<long long>, dim3((uint32_t)ceil_div(per_chunk, 256)),
+                         dim3(256), 0, stream, a, per_chunk);
+      JKV_CHECK_LAUNCH();
+    }
+    return JKV_OK;
+  }
+  if (plan.ok && aligned && !plan.group8) {
     a.n_chunks = plan.chunks;
     a.rows_per_chunk = ceil_div(rows, plan.chunks);
     const dim3 grid((uint32_t)(P * a.S * (a.d / plan.slice) * plan.chunks));

@@ -85,6 +85,7 @@ def hard_residual_vq_exits(
     token_chunk_size: int = 1024,
     straight_through_states: bool = True,
     return_margins: bool = False,
+    forced_codes: torch.Tensor | None = None,
 ):
     """Greedy residual VQ exactly as src/jointkv/closed_loop_vq.py:235-410.
 
@@ -96,6 +97,13 @@ def hard_residual_vq_exits(
     straight-through edge (:408).  Autograd reaches the fp32 masters through
     ``torch.gather`` (:376-381).  With ``return_margins`` also returns the
     best and second-best fp32 search distances per (B,H,T,S).
+
+    ``forced_codes`` [B,H,T,S] (test use: another implementation's choices)
+    makes every stage reconstruct and subtract the forced codeword instead
+    of its own pick, so that a near-tie resolved the other way does not
+    change the rest of the chain; the returned codes and margins are still
+    this search's own, made on the forced chain's residuals, which is what
+    judging the other implementation's choice stage by stage needs.
     """
 
     batch, heads, tokens, dim = map(int, states.shape)
@@ -121,18 +129,20 @@ def hard_residual_vq_exits(
     for s in range(stages):
         table_s = search_tables[:, s]
         with torch.no_grad():
-            idx = nearest_indices(search_rows, table_s, token_chunk_size=token_chunk_size)
+            idx = own = nearest_indices(search_rows, table_s, token_chunk_size=token_chunk_size)
             if return_margins:
                 b1, b2 = distances_top2(search_rows, table_s, token_chunk_size=token_chunk_size)
                 d1[..., s] = b1.reshape(heads, batch, tokens).permute(1, 0, 2)
                 d2[..., s] = b2.reshape(heads, batch, tokens).permute(1, 0, 2)
+            if forced_codes is not None:
+                idx = forced_codes[..., s].permute(1, 0, 2).reshape(heads, batch * tokens).long()
         chosen = torch.gather(deployed[:, s].float(), 1, idx[..., None].expand(-1, -1, dim))
         decoded = decoded + chosen
         with torch.no_grad():
             raw.sub_(chosen.detach())
             if assignment_whiteners is not None:
                 search_rows.sub_(torch.gather(table_s, 1, idx[..., None].expand(-1, -1, dim)))
-            codes[..., s] = idx.reshape(heads, batch, tokens).permute(1, 0, 2).to(torch.uint8)
+            codes[..., s] = own.reshape(heads, batch, tokens).permute(1, 0, 2).to(torch.uint8)
         if s + 1 in requested:
             out = decoded.reshape(heads, batch, tokens, dim).permute(1, 0, 2, 3).contiguous().to(states.dtype)
             if straight_through_states:
@@ -151,12 +161,14 @@ def grouped_residual_vq(
     token_chunk_size: int = 1024,
     straight_through_states: bool = True,
     return_margins: bool = False,
+    forced_codes: torch.Tensor | None = None,
 ):
     """Grouped residual VQ via the reference's own call on folded heads.
 
     states [B,H,T,G*d], tables [H,G,S,K,d]: fold (head, group) into the head
     axis, call :func:`hard_residual_vq_exits` (the reference operator), and
-    unfold: codes [B,H,T,G,S], exits [B,H,T,G*d].
+    unfold: codes [B,H,T,G,S], exits [B,H,T,G*d].  ``forced_codes``
+    [B,H,T,G,S]: as in :func:`hard_residual_vq_exits`.
     """
 
     batch, heads, tokens, dim = map(int, states.shape)
@@ -171,6 +183,8 @@ def grouped_residual_vq(
         token_chunk_size=token_chunk_size,
         straight_through_states=straight_through_states,
         return_margins=return_margins,
+        forced_codes=None if forced_codes is None else forced_codes.permute(0, 1, 3, 2, 4).reshape(
+            batch, heads * groups, tokens, stages),
     )
     outputs, codes = res[0], res[1]
 
@@ -563,6 +577,78 @@ def prefill_qk_grad(
     return torch.cat(dqs, dim=0), torch.cat(dks, dim=0)
 
 
+def closed_loop_attention_layer(
+    hidden: torch.Tensor,
+    weights: dict,
+    key_tables: torch.Tensor,
+    value_tables: torch.Tensor,
+    *,
+    depth: int,
+    key_whitener: torch.Tensor | None = None,
+    window: int = 4096,
+    theta: float = 10000.0,
+    head_dim: int = 128,
+    key_grad: bool = True,
+    quantize: bool = True,
+    forced_codes: tuple | None = None,
+):
+    """Forward of one layer of install_closed_loop_attention
+    (train_full_model_closed_loop_vq.py:219-337) under autograd: fp16
+    projections of ``hidden`` (fp32 accumulate, one rounding), the codec's
+    greedy residual VQ on raw K and V (``key_tables`` frozen; full-vector
+    ``[KVH,S,K,D]`` or grouped ``[KVH,G,S,K,d]`` tables), RoPE, repeat_kv,
+    masked SDPA rounded to fp16, and o_proj in fp32.  ``value_tables`` may
+    require grad; with ``key_grad`` the quantized key keeps its
+    straight-through edge to ``hidden``.  Returns (projected fp32 [B,T,hidden],
+    key search, value search), each search the list [codes, best distance,
+    second-best distance] per stage.  ``forced_codes`` (key codes, value
+    codes) makes the chains follow another implementation's choices (see
+    :func:`hard_residual_vq_exits`).  ``quantize=False`` attends over the raw
+    K/V (the unadapted layer; searches None)."""
+
+    batch, tokens, _ = map(int, hidden.shape)
+    h32 = hidden.float()
+
+    def proj(w):
+        return (h32 @ w.float().T).half()
+
+    qh = weights["q"].shape[0] // head_dim
+    kvh = weights["k"].shape[0] // head_dim
+    query = proj(weights["q"]).view(batch, tokens, qh, head_dim).transpose(1, 2)
+    raw_key = proj(weights["k"]).view(batch, tokens, kvh, head_dim).transpose(1, 2)
+    raw_value = proj(weights["v"]).view(batch, tokens, kvh, head_dim).transpose(1, 2)
+    forced_k, forced_v = (None, None) if forced_codes is None else forced_codes
+    if not quantize:
+        k_exits, k_codes, v_exits, v_codes = {depth: raw_key}, None, {depth: raw_value}, None
+    elif key_tables.ndim == 5:
+        if key_whitener is not None:
+            raise ValueError("the oracle's grouped tables take no whitener")
+        k_exits, *k_codes = grouped_residual_vq(raw_key, key_tables.detach(), prefixes=(depth,),
+                                                return_margins=True, forced_codes=forced_k)
+        v_exits, *v_codes = grouped_residual_vq(raw_value, value_tables, prefixes=(depth,), return_margins=True,
+                                                forced_codes=forced_v)
+    else:
+        k_exits, *k_codes = hard_residual_vq_exits(raw_key, key_tables.detach(), prefixes=(depth,),
+                                                   assignment_whiteners=key_whitener, return_margins=True,
+                                                   forced_codes=forced_k)
+        v_exits, *v_codes = hard_residual_vq_exits(raw_value, value_tables, prefixes=(depth,), return_margins=True,
+                                                   forced_codes=forced_v)
+    khat, vhat = (k_exits[depth] if key_grad else k_exits[depth].detach()), v_exits[depth]
+    outs = []
+    for b in range(batch):
+        pos = torch.arange(tokens)
+        c, s = rotary_cos_sin(pos, head_dim, theta)
+        qr = apply_rotary(query[b : b + 1].float(), c.float()[None, None], s.float()[None, None])
+        kr = apply_rotary(khat[b : b + 1].float(), c.float()[None, None], s.float()[None, None])
+        kr = kr.repeat_interleave(qh // kvh, dim=1)
+        mask = sliding_causal_mask(tokens, window)
+        vr = vhat[b : b + 1].repeat_interleave(qh // kvh, dim=1)
+        att = F.scaled_dot_product_attention(qr, kr, vr.float(), attn_mask=mask, dropout_p=0.0)
+        outs.append(att.to(torch.float16))
+    out = torch.cat(outs, dim=0).transpose(1, 2).reshape(batch, tokens, qh * head_dim)
+    return out.float() @ weights["o"].float().T, k_codes, v_codes
+
+
 def closed_loop_attention_value_step(
     hidden: torch.Tensor,
     weights: dict,
@@ -580,47 +666,121 @@ def closed_loop_attention_value_step(
     """One layer of install_closed_loop_attention
     (train_full_model_closed_loop_vq.py:219-337) followed by backward of a
     given upstream gradient, as the V-only step runs it
-    (train_mistral_v_only.py:142-150): fp16 projections (fp32 accumulate,
-    one rounding), the codec's greedy residual VQ on raw K and V (K tables
-    frozen), RoPE, repeat_kv, masked SDPA, o_proj, then backward of
-    ``d_projected``.  Returns (projected fp16 [B,T,hidden], dL/d value tables
-    fp32 [KVH,S,K,D]), and with ``hidden_grad`` also dL/d hidden (through the
-    codec's straight-through edges to raw K and V and the attention's query
-    and key legs)."""
+    (train_mistral_v_only.py:142-150).  Returns (projected fp16
+    [B,T,hidden], dL/d value tables fp32 [KVH,S,K,D]), and with
+    ``hidden_grad`` also dL/d hidden (through the codec's straight-through
+    edges to raw K and V and the attention's query and key legs)."""
 
-    batch, tokens, _ = map(int, hidden.shape)
     h32 = hidden.float().requires_grad_(hidden_grad)
-
-    def proj(w):
-        return (h32 @ w.float().T).half()
-
-    qh = weights["q"].shape[0] // head_dim
-    kvh = weights["k"].shape[0] // head_dim
-    query = proj(weights["q"]).view(batch, tokens, qh, head_dim).transpose(1, 2)
-    raw_key = proj(weights["k"]).view(batch, tokens, kvh, head_dim).transpose(1, 2)
-    raw_value = proj(weights["v"]).view(batch, tokens, kvh, head_dim).transpose(1, 2)
     vt = value_tables.detach().clone().requires_grad_(True)
-    k_exits, _ = hard_residual_vq_exits(raw_key, key_tables.detach(), prefixes=(depth,),
-                                        assignment_whiteners=key_whitener)
-    v_exits, _ = hard_residual_vq_exits(raw_value, vt, prefixes=(depth,))
-    khat, vhat = (k_exits[depth] if hidden_grad else k_exits[depth].detach()), v_exits[depth]
-    outs = []
-    for b in range(batch):
-        pos = torch.arange(tokens)
-        c, s = rotary_cos_sin(pos, head_dim, theta)
-        qr = apply_rotary(query[b : b + 1].float(), c.float()[None, None], s.float()[None, None])
-        kr = apply_rotary(khat[b : b + 1].float(), c.float()[None, None], s.float()[None, None])
-        kr = kr.repeat_interleave(qh // kvh, dim=1)
-        mask = sliding_causal_mask(tokens, window)
-        vr = vhat[b : b + 1].repeat_interleave(qh // kvh, dim=1)
-        att = F.scaled_dot_product_attention(qr, kr, vr.float(), attn_mask=mask, dropout_p=0.0)
-        outs.append(att.to(torch.float16))
-    out = torch.cat(outs, dim=0).transpose(1, 2).reshape(batch, tokens, qh * head_dim)
-    projected = out.float() @ weights["o"].float().T
+    projected, _kc, _vc = closed_loop_attention_layer(
+        h32, weights, key_tables, vt, depth=depth, key_whitener=key_whitener, window=window, theta=theta,
+        head_dim=head_dim, key_grad=hidden_grad)
     projected.backward(d_projected.float())
     if hidden_grad:
         return projected.detach().half(), vt.grad, h32.grad
     return projected.detach().half(), vt.grad
+
+
+def rms_norm(hidden: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Mistral's RMSNorm (transformers 4.45.1 MistralRMSNorm, third-party;
+    restated): fp32 x * rsqrt(mean(x^2) + eps), cast to fp16, times the fp16
+    weight (one fp16 rounding)."""
+
+    x = hidden.float()
+    x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return (weight.float() * x.half().float()).half()
+
+
+def causal_loss(logits: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """Mean next-token cross-entropy (train_full_model_closed_loop_vq.py:359-364)."""
+
+    return F.cross_entropy(logits[:, :-1].float().reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1),
+                           reduction="mean")
+
+
+def stack_logits(
+    tokens: torch.Tensor,
+    stack: dict,
+    key_tables: Sequence[torch.Tensor] | None,
+    value_tables: Sequence[torch.Tensor] | None,
+    *,
+    depth: int = 1,
+    window: int = 4096,
+    theta: float = 10000.0,
+    eps: float = 1e-5,
+    head_dim: int = 128,
+    quantize: bool = True,
+    forced_codes: Sequence[tuple] | None = None,
+):
+    """Logits fp16 [B,T,V] of a Mistral-shaped decoder stack under autograd,
+    every layer's attention through :func:`closed_loop_attention_layer`.
+
+    ``stack``: ``embed [V,hidden]``, ``final_norm [hidden]``, ``lm_head
+    [V,hidden]`` and ``layers``, each a dict of ``input_norm``,
+    ``post_attention_norm``, attention ``q k v o`` and MLP ``gate up down``
+    (fp16, ``[out,in]``).  Each decoder layer is Mistral's pre-norm block
+    (transformers 4.45.1 MistralDecoderLayer, third-party; restated):
+    h += o_proj(attention(norm(h))); h += down(silu(gate(norm(h))) * up(norm(h))),
+    every fp16 op rounded once.  ``quantize=False`` runs the unadapted model
+    (tables unused).  ``forced_codes``: per layer, (key codes, value codes)
+    for :func:`closed_loop_attention_layer`.  Returns the logits and each
+    layer's (key search, value search)."""
+
+    h = stack["embed"][tokens]
+    codes = []
+    for layer, w in enumerate(stack["layers"]):
+        x = rms_norm(h, w["input_norm"], eps)
+        projected, kc, vc = closed_loop_attention_layer(
+            x, w, key_tables[layer] if quantize else None, value_tables[layer] if quantize else None,
+            depth=depth, window=window, theta=theta, head_dim=head_dim, quantize=quantize,
+            forced_codes=None if forced_codes is None else forced_codes[layer])
+        codes.append((kc, vc))
+        h = (h.float() + projected.half().float()).half()
+        x = rms_norm(h, w["post_attention_norm"], eps).float()
+        gate = (x @ w["gate"].float().T).half()
+        up = (x @ w["up"].float().T).half()
+        act = (F.silu(gate.float()).half().float() * up.float()).half()
+        h = (h.float() + (act.float() @ w["down"].float().T).half().float()).half()
+    h = rms_norm(h, stack["final_norm"], eps)
+    return (h.float() @ stack["lm_head"].float().T).half(), codes
+
+
+def v_only_stack_step(
+    tokens: torch.Tensor,
+    stack: dict,
+    key_tables: Sequence[torch.Tensor],
+    value_tables: Sequence[torch.Tensor],
+    *,
+    depth: int,
+    lr: float = 0.001,
+    maximum_norm: float = 1.0,
+    window: int = 4096,
+    theta: float = 10000.0,
+    eps: float = 1e-5,
+    head_dim: int = 128,
+    forced_codes: Sequence[tuple] | None = None,
+) -> dict:
+    """One V-only calibration step over a Mistral-shaped decoder stack, in the
+    order of train_mistral_v_only.py:143-153: :func:`stack_logits` with every
+    layer's attention routed through the codec (install_closed_loop_attention),
+    the causal loss, backward, the per_layer_kv clip at ``maximum_norm`` and
+    SGD at ``lr``.  Returns the loss, the value-table gradients before
+    clipping, the clip record, the updated tables and each layer's (key
+    search, value search).  ``forced_codes``: as in :func:`stack_logits`."""
+
+    kts = [t.detach().float().clone() for t in key_tables]
+    vts = [torch.nn.Parameter(t.detach().float().clone()) for t in value_tables]
+    logits, codes = stack_logits(tokens, stack, kts, vts, depth=depth, window=window, theta=theta, eps=eps,
+                                 head_dim=head_dim, forced_codes=forced_codes)
+    loss = causal_loss(logits, tokens)
+    loss.backward()
+    grads = [p.grad.detach().clone() for p in vts]
+    keys = [torch.nn.Parameter(t, requires_grad=False) for t in kts]
+    clip = clip_codebook_gradients(keys, vts, maximum_norm=maximum_norm, mode="per_layer_kv")
+    torch.optim.SGD(vts, lr=lr).step()
+    return {"loss": float(loss.detach()), "grads": grads, "clip": clip,
+            "value_tables": [p.detach() for p in vts], "codes": codes}
 
 
 def attention_fp64(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:

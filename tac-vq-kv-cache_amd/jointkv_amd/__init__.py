@@ -51,16 +51,20 @@ from .packed_nested import (
     validate_packed_nested_cache,
 )
 from .uniform_depth_tac import ClosedLoopUniformResidualVQ
+from .v_only import ClosedLoopRunContext, DecoderStack, causal_loss, run_loss, v_only_step
 
 __all__ = [
     "multi_exit_additive_block_refinement",
     "multi_exit_additive_coordinate_refinement",
     "AttentionWeights",
     "artifacts",
+    "causal_loss",
     "CacheGeometry",
     "ClosedLoopGroupedCQ",
+    "ClosedLoopRunContext",
     "ClosedLoopUniformResidualVQ",
     "DecodedWindowCache",
+    "DecoderStack",
     "PackedCodeCache",
     "PackedLayoutLedger",
     "PackedNestedKVCache",
@@ -88,12 +92,14 @@ __all__ = [
     "prefix_index_bits",
     "relative_trajectory_attention_mse",
     "residual_vq_ledger",
+    "run_loss",
     "sgd_step",
     "unpack_action_depths",
     "unpack_fixed_width",
     "unpack_paired_progressive_indices",
     "validate_packed_nested_cache",
     "validate_stage_bits",
+    "v_only_step",
 ]
 
 

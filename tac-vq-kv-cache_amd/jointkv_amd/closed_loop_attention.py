@@ -73,11 +73,14 @@ def closed_loop_attention(
     window: int = MISTRAL_WINDOW,
     rope_theta: float = MISTRAL_ROPE_THETA,
     trajectory_epsilon: float | None = None,
+    rate_records: list | None = None,
 ):
     """The quantized attention of ``layer`` over ``hidden`` ``[B,T,hidden]``
     fp16.  Returns the projected output ``[B,T,hidden]``, and with
     ``trajectory_epsilon`` also the layer's trajectory-match loss against the
-    same attention on raw K/V (train_full_model_closed_loop_vq.py:304-334)."""
+    same attention on raw K/V (train_full_model_closed_loop_vq.py:304-334).
+    A codec that returns projected depths has one rate record per request
+    appended to ``rate_records`` (train_full_model_closed_loop_vq.py:261-273)."""
 
     batch, tokens, _ = map(int, hidden.shape)
     d = weights.head_dim
@@ -85,6 +88,18 @@ def closed_loop_attention(
     raw_key = F.linear(hidden, weights.k).view(batch, tokens, weights.kv_heads, d).transpose(1, 2)
     raw_value = F.linear(hidden, weights.v).view(batch, tokens, weights.kv_heads, d).transpose(1, 2)
     quantized = codec(layer, raw_key, raw_value, mode=mode)
+    if quantized.projected_depths is not None and rate_records is not None:
+        depths = quantized.projected_depths
+        for request, ledger in enumerate(depths.ledgers):
+            rate_records.append({
+                "layer": layer,
+                "request": request,
+                "total_bits": ledger.total_bits,
+                "physical_effective_bits": ledger.physical_effective_bits,
+                "low_blocks": depths.low_blocks_per_request[request],
+                "anchor_blocks": depths.anchor_blocks_per_request[request],
+                "high_blocks": depths.high_blocks_per_request[request],
+            })
     out = prefill_attention(query, quantized.key, quantized.value, start_positions,
                             window=window, rope_theta=rope_theta)
     projected = F.linear(out.transpose(1, 2).contiguous().view(batch, tokens, -1), weights.o)

@@ -588,7 +588,7 @@ def main() -> int:
             "peak": MFMA_FP16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
-            "traffic": measured_traffic(ROOT / "profiles" / "rvq_encode_mfma_g2_config2.md"),
+            "traffic": measured_traffic(ROOT / "profiles" / "rvq_encode_grouped_g2_config2.md"),
             "kernel": "rvq_encode_grouped<8,2>",
             "avg_launch_us": enc["avg_launch_ms"] * 1e3,
             "algorithmic_flop_per_launch": enc["flops_per_launch"],

@@ -148,19 +148,36 @@ void rvq_encode_grouped(MfmaArgs m) {
   const uint32_t out_bstride = (uint32_t)a.H * T32 * Dfull;  // reconstructions are contiguous
   const uint32_t head_o = h * T32 * Dfull + g * D;
 
+  // a wave's 64-row slab: first row `at` = (batch b0, token t0), wave-uniform
   struct Iter {
-    uint32_t at, xb, cb, ob;
+    uint32_t at, b0, t0, xb, cb, ob;
     bool fast;
+  };
+  auto finish = [&](Iter& it) {
+    it.fast = it.t0 + kRowsPerWave <= T32 && it.at + kRowsPerWave <= r_end;
+    it.xb = it.b0 * (uint32_t)a.sb + head_x + it.t0 * (uint32_t)a.st;
+    it.cb = it.b0 * (uint32_t)a.cb + head_c + it.t0 * (uint32_t)a.ct;
+    it.ob = it.b0 * out_bstride + head_o + it.t0 * Dfull;
   };
   auto plan = [&](uint32_t at) {
     Iter it;
     it.at = at;
-    const uint32_t b0 = at / T32;
-    const uint32_t t0 = at - b0 * T32;
-    it.fast = t0 + kRowsPerWave <= T32 && at + kRowsPerWave <= r_end;
-    it.xb = b0 * (uint32_t)a.sb + head_x + t0 * (uint32_t)a.st;
-    it.cb = b0 * (uint32_t)a.cb + head_c + t0 * (uint32_t)a.ct;
-    it.ob = b0 * out_bstride + head_o + t0 * Dfull;
+    it.b0 = at / T32;
+    it.t0 = at - it.b0 * T32;
+    finish(it);
+    return it;
+  };
+  // the slab kGroupedRowsPerIter rows on, without a division
+  auto advance = [&](const Iter& c) {
+    Iter it;
+    it.at = c.at + kGroupedRowsPerIter;
+    it.b0 = c.b0;
+    it.t0 = c.t0 + kGroupedRowsPerIter;
+    while (it.t0 >= T32) {
+      it.t0 -= T32;
+      ++it.b0;
+    }
+    finish(it);
     return it;
   };
   // offsets of this lane's row; false for a row past the range (its offsets
@@ -365,7 +382,7 @@ void rvq_encode_grouped(MfmaArgs m) {
 
   for (; base < r_end; base += kGroupedRowsPerIter) {
     const bool more = base + kGroupedRowsPerIter < r_end;
-    const Iter nxt = plan(base + kGroupedRowsPerIter);
+    const Iter nxt = advance(cur);
     uint32_t xo, co, oo;
     const bool valid = locate(cur, &xo, &co, &oo);
 

@@ -787,6 +787,377 @@ __global__ __launch_bounds__(kLdsThreads) void decode_lds_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-table decode at group dim 8 (GSRQ / grouped CQ, S <= 2): one
+// 512-thread workgroup (8 waves) per (kv head, batch row, split of up to
+// 2048 visible tokens).  The kv head's fp16 tables ([16][S][256][8],
+// 128 KiB at G2) sit in LDS; the split's code records stream through LDS in
+// 256-token chunks, one 32-key block per wave.
+//   K phase  as decode_lds_kernel: per 16-key tile a lane rebuilds 32 dims of
+//            one key from 16-byte codeword gathers, rotates them with the
+//            reference's fp16 rotary, and four v_mfma_f32_16x16x32_f16 give
+//            Sᵀ = K̂ Qᵀ for the GQA group;
+//   V phase  the MFMA A operand V̂ᵀ (16 dims x 32 keys) is gathered straight
+//            from the codeword tables with ds_read_b64_tr_b16: in each 16-lane
+//            block, lane 4j + e receives element e of the 8-byte pieces that
+//            the block's lanes j, j+4, j+8, j+12 address, so when lane
+//            4i + j of block b addresses dims 16t + 4j..+3 of key 4b + i (and
+//            then of key 16 + 4b + i), lane w of block b holds dim 16t + w of
+//            the keys the P operand of block b carries.  The stage words are
+//            added in fp16 after the read (one rounding, as the reference's
+//            fp16(c1 + c2)); no staging tile, no per-key transposes.
+// The split's (max, sum, out) go to decode_combine_kernel.
+
+static const int kG8Threads = 512;
+static const int kG8Waves = kG8Threads / 64;
+static const int kG8Chunk = 256;       // tokens per chunk: one 32-key block per wave
+static const int kG8MaxSplit = 2048;   // eight chunks
+static const int kG8Plane = kLdsK * 16;  // bytes of one (group, stage) table: 256 words x 8 fp16
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+// transposing LDS read of the 8-byte piece at LDS byte address addr (see above)
+__device__ __forceinline__ half4 lds_read_tr(uint32_t addr) {
+  return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(size_t)addr));
+}
+
+// rope16 on packed pairs: (x * cos) + (rotate_half(x) * sin), every
+// operation rounded to fp16, written pair by pair so that the subtraction
+// becomes a v_pk_mul_f16 with a negated operand plus a v_pk_add_f16
+// (fp16(b * -s) = -fp16(b * s)), with no separate sign flips
+#pragma clang fp contract(off)
+__device__ __forceinline__ void rope16_pk(half8 a, half8 b, half8 c, half8 s, half8* ra, half8* rb) {
+  const uint4 A = __builtin_bit_cast(uint4, a), B = __builtin_bit_cast(uint4, b);
+  const uint4 C = __builtin_bit_cast(uint4, c), Sn = __builtin_bit_cast(uint4, s);
+  const uint32_t av[4] = {A.x, A.y, A.z, A.w}, bv[4] = {B.x, B.y, B.z, B.w};
+  const uint32_t cv[4] = {C.x, C.y, C.z, C.w}, sv[4] = {Sn.x, Sn.y, Sn.z, Sn.w};
+  uint32_t x[4], y[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const half2v ap = __builtin_bit_cast(half2v, av[p]), bp = __builtin_bit_cast(half2v, bv[p]);
+    const half2v cp = __builtin_bit_cast(half2v, cv[p]), sp = __builtin_bit_cast(half2v, sv[p]);
+    x[p] = __builtin_bit_cast(uint32_t, ap * cp - bp * sp);
+    y[p] = __builtin_bit_cast(uint32_t, bp * cp + ap * sp);
+  }
+  *ra = __builtin_bit_cast(half8, uint4{x[0], x[1], x[2], x[3]});
+  *rb = __builtin_bit_cast(half8, uint4{y[0], y[1], y[2], y[3]});
+}
+#pragma clang fp contract(on)
+
+template <int NQ, int S>
+__global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  constexpr int tab_bytes = 16 * S * kG8Plane;
+  constexpr int kSlots = kG8MaxSplit / kG8Chunk;
+  constexpr int kCb = 16 * S;  // code bytes per token
+  unsigned char* tab = dyn;
+  uint8_t* cbuf = dyn + tab_bytes;                      // [chunk][kCb]
+  float* red = (float*)(cbuf + kG8Chunk * kCb);         // [2][waves][NQ]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  // logical block: split fastest, then batch row, then kv head
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t split = bid % (uint32_t)a.n_splits;
+  const int64_t b = (bid / (uint32_t)a.n_splits) % (uint32_t)a.B;
+  const int64_t kvh = bid / ((uint32_t)a.n_splits * (uint32_t)a.B);
+  const int64_t L = a.lengths[b];
+  const int64_t n_vis = L < a.window ? L : a.window;
+  const int64_t t0 = L - n_vis + split * a.split_tokens;
+  int64_t t1 = t0 + a.split_tokens;
+  if (t1 > L) t1 = L;
+  const int ntok = t1 > t0 ? (int)(t1 - t0) : 0;
+  const int nchunks = (ntok + kG8Chunk - 1) / kG8Chunk;
+  const int64_t cbase = b * a.csb + kvh * a.csh;
+  const uint32_t cap = (uint32_t)a.cap;
+  const uint32_t slot0 = (uint32_t)(t0 % a.cap);
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kHeadDim);  // log2(e)/sqrt(D)
+  const int64_t rope_last = a.rope_len - 1;
+  auto rope_row = [&](int64_t pos) -> const _Float16* {
+    return a.rope + (pos < rope_last ? pos : rope_last) * kRopeRow;
+  };
+  // one 16-byte piece of chunk c's code records: token i = tid*16/kCb.  A
+  // slot past the split's tokens gets the split's first record, so every
+  // rebuilt vector is one the reference also forms (its score is masked and
+  // its weight is 0)
+  constexpr int pieces = kG8Chunk * kCb / 16;
+  auto fetch_codes = [&](const uint8_t* codes, int c) -> uint4 {
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (tid < pieces) {
+      const int i = tid * 16 / kCb, part = tid * 16 % kCb;
+      const int t = c * kG8Chunk + i;
+      uint32_t slot = slot0 + (uint32_t)(t < ntok ? t : 0);
+      if (slot >= cap) slot -= cap;
+      v = *(const uint4*)(codes + cbase + (int64_t)slot * kCb + part);
+    }
+    return v;
+  };
+  auto store_codes = [&](uint4 v) {
+    if (tid < pieces) *(uint4*)(cbuf + tid * 16) = v;
+  };
+  // tables global -> LDS directly, 8 KiB per workgroup-wide step; the
+  // workgroups of one kv head start at different slices
+  const int rot = (int)(bid % ((uint32_t)a.n_splits * (uint32_t)a.B));
+  auto load_tables = [&](const _Float16* src_tab) {
+    const uint4* src = (const uint4*)((const unsigned char*)src_tab + kvh * (int64_t)tab_bytes);
+    uint4* dst = (uint4*)tab;
+    constexpr int n = tab_bytes / 16;
+    static_assert(n % kG8Threads == 0, "tables are whole 8 KiB slices");
+    constexpr int per = n / kG8Threads;
+#pragma unroll
+    for (int u = 0; u < per; ++u) {
+      const int uu = (u + rot) % per;
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(src + tid + uu * kG8Threads),
+          (void __attribute__((address_space(3)))*)(dst + uu * kG8Threads + wave * 64), 16, 0, 0);
+    }
+  };
+  // rotary rows of one 16-key tile (key positions past the split clamp to a
+  // real row; their scores are masked).  Positions and row offsets fit 32
+  // bits (the table has rope_len < 2^24 rows of 128 halves: host-checked).
+  const uint32_t pos0 = (uint32_t)t0, rlast = (uint32_t)rope_last;
+  auto fetch_trig = [&](int c, int tl, half8 (&tg)[4]) {
+    const int tk = c * kG8Chunk + 32 * wave + 16 * tl + ln;
+    uint32_t pos = pos0 + (uint32_t)(tk < ntok ? tk : 0);
+    pos = pos < rlast ? pos : rlast;
+    const _Float16* tr = a.rope + pos * (uint32_t)kRopeRow;
+    load_trig8(tr, 8 * lg, &tg[0], &tg[1]);
+    load_trig8(tr, 32 + 8 * lg, &tg[2], &tg[3]);
+  };
+
+  // ---- K tables and the first chunk's records into LDS; later chunks'
+  // records wait in registers ----
+  load_tables(a.kt);
+  if (nchunks > 0) store_codes(fetch_codes(a.kc, 0));
+  // ---- rotated queries at position L-1: B operand, column ln = head ----
+  const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 qb[4];
+  {
+    const int64_t head = kvh * NQ + (ln < NQ ? ln : 0);
+    const _Float16* qp = a.q + b * a.qsb + head * a.qsh;
+    const _Float16* tr = rope_row(L > 0 ? L - 1 : 0);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int d0 = 32 * c + 8 * lg;
+      half8 x0, x1, cs, sn, r0, r1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x0[e] = qp[d0 + e];
+        x1[e] = qp[d0 + 64 + e];
+      }
+      load_trig8(tr, d0, &cs, &sn);
+      rope16_pk(x0, x1, cs, sn, &r0, &r1);
+      qb[c] = ln < NQ ? r0 : zero8;
+      qb[c + 2] = ln < NQ ? r1 : zero8;
+    }
+  }
+  half8 trig[4];
+  fetch_trig(0, 0, trig);
+  __builtin_amdgcn_s_waitcnt(0);  // the tables' direct-to-LDS loads have landed
+  __syncthreads();
+  // the next chunk's records wait in a register while a chunk is scored
+  uint4 knext = 1 < nchunks ? fetch_codes(a.kc, 1) : uint4{0u, 0u, 0u, 0u};
+
+  // ---- K phase.  Lane (key ln of a 16-key tile, lane group lg) owns 8-dim
+  // chunks 4q+lg (q = 0..3) = MFMA contraction slice q; chunks lg/lg+8 and
+  // lg+4/lg+12 are rotary partners.  sc[c][tl][e]: score of key 4lg+e of
+  // tile tl of the wave's block in chunk c, for head ln ----
+  // byte offsets of chunk lg's tables (chunks 8 + lg .. through a second base,
+  // so that every gather's constant part fits the instruction's offset)
+  const uint32_t kgrp = (uint32_t)lg * S * kG8Plane;
+  const uint32_t kgrp_hi = kgrp + 8u * S * kG8Plane;
+  float4v sc[kSlots][2];
+#pragma unroll
+  for (int c = 0; c < kSlots; ++c) {
+    sc[c][0] = float4v{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+    sc[c][1] = sc[c][0];
+    if (c >= nchunks) continue;
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl) {
+      uint32_t wrec[kCb / 4];
+      read_record<kCb>(cbuf + (32 * wave + 16 * tl + ln) * kCb, wrec);
+      // the next tile's rotary rows go out now
+      half8 tnext[4];
+      if (tl == 0) {
+        fetch_trig(c, 1, tnext);
+      } else {
+        fetch_trig(c + 1 < kSlots ? c + 1 : c, 0, tnext);
+      }
+      uint32_t cc[4];
+      record_codes<8, S>(wrec, lg, cc);
+      half8 g[4][S];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+          g[q][st] = *(const half8*)(tab + (q < 2 ? kgrp : kgrp_hi) + (uint32_t)(4 * (q & 1) * S + st) * kG8Plane +
+                                     (__builtin_amdgcn_ubfe(cc[q], 8u * st, 8u) << 4));
+      __builtin_amdgcn_sched_barrier(0);
+      half8 k[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) k[q] = S == 2 ? g[q][0] + g[q][S - 1] : g[q][0];
+      half8 r[4];
+      rope16_pk(k[0], k[2], trig[0], trig[1], &r[0], &r[2]);
+      rope16_pk(k[1], k[3], trig[2], trig[3], &r[1], &r[3]);
+      float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[q], qb[q], acc, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = c * kG8Chunk + 32 * wave + 16 * tl + 4 * lg + e;
+        sc[c][tl][e] = (ln < NQ && key < ntok) ? acc[e] * scale2 : -__builtin_inff();
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) trig[u] = tnext[u];
+    }
+    __syncthreads();  // chunk c's records are consumed
+    if (c + 1 < nchunks) {
+      store_codes(knext);
+      if (c + 2 < nchunks) knext = fetch_codes(a.kc, c + 2);
+    }
+    __syncthreads();
+  }
+
+  // every wave is done with the K tables: the V tables and the first chunk
+  // of V records load while the softmax runs
+  load_tables(a.vt);
+  uint4 vnext = nchunks > 0 ? fetch_codes(a.vc, 0) : uint4{0u, 0u, 0u, 0u};
+
+  // ---- split max and exp-sum per head (lanes ln < NQ carry head ln) ----
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int c = 0; c < kSlots; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fmaxf(sc[c][0][e], sc[c][1][e]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (lg == 0 && ln < NQ) red[wave * NQ + ln] = mx;
+  __syncthreads();
+  float mh[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < kG8Waves; ++w) m = fmaxf(m, red[w * NQ + h]);
+    mh[h] = m;
+  }
+  float m_lane = 0.f;
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) m_lane = ln == h ? mh[h] : m_lane;
+  const float m_use = m_lane == -__builtin_inff() ? 0.f : m_lane;
+  half8 pf[kSlots];
+  float lsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < kSlots; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pa = __builtin_amdgcn_exp2f(sc[c][0][e] - m_use);
+      const float pb = __builtin_amdgcn_exp2f(sc[c][1][e] - m_use);
+      lsum += pa + pb;
+      pf[c][e] = (_Float16)pa;
+      pf[c][e + 4] = (_Float16)pb;
+    }
+  }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (lg == 0 && ln < NQ) red[kG8Waves * NQ + wave * NQ + ln] = lsum;
+  __syncthreads();
+  float lh[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kG8Waves; ++w) l += red[kG8Waves * NQ + w * NQ + h];
+    lh[h] = l;
+  }
+
+  // ---- the V tables have landed; the first chunk of V records into LDS ----
+  if (nchunks > 0) store_codes(vnext);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  vnext = 1 < nchunks ? fetch_codes(a.vc, 1) : uint4{0u, 0u, 0u, 0u};
+
+  // ---- V phase.  As a source of the transposing reads, lane 4i + j of lane
+  // group lg addresses, for keys 4lg + i and 16 + 4lg + i of the wave's
+  // block, dims 4j..4j+3 of each 16-dim slice t: group 2t + (j >> 1), half
+  // j & 1.  As an MFMA A lane (dim ln of slice t, keys of lane group lg) it
+  // receives what the P operand of the same lane group weights ----
+  const int si = ln >> 2, sj = ln & 3;
+  // LDS byte addresses (the table area starts the dynamic allocation)
+  const uint32_t vlane = (uint32_t)(size_t)(const void __attribute__((address_space(3)))*)tab +
+                         (uint32_t)(sj >> 1) * S * kG8Plane + (uint32_t)(sj & 1) * 8u;
+  const uint32_t vlane_hi = vlane + 8u * S * kG8Plane;  // slices 4..7 (groups 8..15)
+  // record bits of this lane's group parity: S = 2: group 2t + jh sits at
+  // bits 16 jh + 8 s of dword t; S = 1: bits 8 (2 (t & 1) + jh) of dword t / 2
+  const uint32_t jsh = (uint32_t)(sj >> 1) * (S == 2 ? 16u : 8u);
+  float4v o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < kSlots; ++c) {
+    if (c >= nchunks) continue;
+    uint32_t wa[kCb / 4], wb[kCb / 4];
+    read_record<kCb>(cbuf + (32 * wave + 4 * lg + si) * kCb, wa);
+    read_record<kCb>(cbuf + (32 * wave + 16 + 4 * lg + si) * kCb, wb);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      // the lane's codes of group 2dt + (sj >> 1), stage st, as byte offsets
+      // of their words (code * 16) plus the lane's piece
+      uint32_t ra[S], rb[S];
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        const uint32_t wa_ = S == 2 ? wa[dt] : wa[dt >> 1];
+        const uint32_t wb_ = S == 2 ? wb[dt] : wb[dt >> 1];
+        const uint32_t off = jsh + (S == 2 ? 8u * st : 16u * (dt & 1));
+        const uint32_t base = dt < 4 ? vlane : vlane_hi;
+        ra[st] = (__builtin_amdgcn_ubfe(wa_, off, 8u) << 4) + base;
+        rb[st] = (__builtin_amdgcn_ubfe(wb_, off, 8u) << 4) + base;
+      }
+      const uint32_t plane = (uint32_t)(2 * (dt & 3) * S) * kG8Plane;
+      half4 va = lds_read_tr(ra[0] + plane);
+      half4 vb = lds_read_tr(rb[0] + plane);
+      if constexpr (S == 2) {
+        va = va + lds_read_tr(ra[1] + plane + kG8Plane);
+        vb = vb + lds_read_tr(rb[1] + plane + kG8Plane);
+      }
+      const uint4 w = uint4{__builtin_bit_cast(uint2, va).x, __builtin_bit_cast(uint2, va).y,
+                            __builtin_bit_cast(uint2, vb).x, __builtin_bit_cast(uint2, vb).y};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w), pf[c], o[dt], 0, 0, 0);
+    }
+    __syncthreads();  // chunk c's records are consumed
+    if (c + 1 < nchunks) {
+      store_codes(vnext);
+      if (c + 2 < nchunks) vnext = fetch_codes(a.vc, c + 2);
+    }
+    __syncthreads();
+  }
+
+  // ---- workgroup sum of the waves' Oᵀ (lane (head ln, lg) holds dims
+  // 16dt + 4lg + e) and the split's partial ----
+  float* o_red = (float*)dyn;  // [waves][NQ][128], in the table area
+  if (ln < NQ) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o_red[(wave * NQ + ln) * kHeadDim + 16 * dt + 4 * lg + e] = o[dt][e];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < NQ * kHeadDim; idx += kG8Threads) {
+    const int h = idx / kHeadDim, i = idx % kHeadDim;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kG8Waves; ++w) v += o_red[(w * NQ + h) * kHeadDim + i];
+    const int64_t qh = kvh * NQ + h;
+    a.ws_o[((b * a.QH + qh) * a.n_splits + split) * kHeadDim + i] = v;
+    if (i == 0) {
+      float* ml = a.ws_ml + ((b * a.QH + qh) * a.n_splits + split) * 2;
+      ml[0] = ntok > 0 ? mh[h] * 0.6931471805599453f : -__builtin_inff();
+      ml[1] = ntok > 0 ? lh[h] : 0.f;
+    }
+  }
+}
+
 // out[b,qh,:] = sum_s o_s e^{m_s-M} / sum_s l_s e^{m_s-M}
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
   const int64_t bq = blockIdx.x;  // b*QH + qh
@@ -838,12 +1209,39 @@ static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int
   return w < kLdsMaxSplit ? w : kLdsMaxSplit;
 }
 
+// Dynamic LDS of decode_g8_kernel: tables, one chunk of code records, the
+// reductions.
+static int64_t g8_lds_bytes(int64_t S, int64_t nq) {
+  return 16 * S * kG8Plane + kG8Chunk * 16 * S + 2 * kG8Waves * nq * 4;
+}
+
+// Tokens per split of decode_g8_kernel (0: the geometry does not fit).
+static int64_t g8_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int64_t window) {
+  if (G != 16 || S < 1 || S > 2 || K != kLdsK) return 0;
+  if (g8_lds_bytes(S, nq) > kMaxLds) return 0;
+  if (kG8Waves * nq * kHeadDim * 4 > 16 * S * kG8Plane) return 0;  // partials fit the table area
+  const int64_t w = ceil_div(window, kG8Chunk) * kG8Chunk;
+  return w < kG8MaxSplit ? w : kG8MaxSplit;
+}
+
 template <int D, int NQ>
 static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
   const int64_t split = lds_ok && D != 128 && D != 0 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
+  const int64_t g8_split = lds_ok && D == 8 ? g8_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
   if constexpr (D == 128 || D == 0) {
     hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
                        dim3(256), 0, stream, a);
+  } else if (D == 8 && g8_split > 0) {
+    a.split_tokens = (int32_t)g8_split;
+    a.n_splits = (int32_t)ceil_div(a.window, g8_split);
+    a.ws_ml = a.ws_o + a.B * a.QH * a.n_splits * kHeadDim;
+    const size_t lds = (size_t)g8_lds_bytes(a.S, NQ);
+    const dim3 grid((uint32_t)(a.KVH * a.B * a.n_splits));
+    if (a.S == 2) {
+      hipLaunchKernelGGL((decode_g8_kernel<NQ, 2>), grid, dim3(kG8Threads), lds, stream, a);
+    } else {
+      hipLaunchKernelGGL((decode_g8_kernel<NQ, 1>), grid, dim3(kG8Threads), lds, stream, a);
+    }
   } else if (split > 0) {
     a.split_tokens = (int32_t)split;
     a.n_splits = (int32_t)ceil_div(a.window, split);

@@ -41,6 +41,8 @@ def _expect(q, kc, vc, kt, vt, length, window, cap):
     (1, 8, 2, 16, 2, 8, 5000, 4096, 4096),    # window slides, ring buffer wraps
     (1, 4, 4, 32, 1, 4, 700, 512, 512),       # cq2 codes, MHA group of 1
     (1, 16, 2, 16, 1, 8, 257, 4096, 4096),    # cq1 codes, GQA 8
+    (1, 2, 2, 16, 2, 8, 1000, 4096, 4096),    # one query head per kv head at d = 8
+    (2, 4, 2, 16, 1, 8, 1500, 512, 1024),     # GQA 2, one stage, window of two 256-token chunks, ring wraps
     (1, 8, 2, 16, 3, 8, 600, 4096, 4096),     # three stages: the generic split kernel
     (1, 8, 2, 1, 4, 128, 600, 4096, 4096),    # full-vector codebooks, 4 stages (codewords from L2)
     (2, 32, 8, 1, 16, 128, 700, 256, 512),    # full-vector R16 geometry, sliding window, ring wraps

@@ -248,8 +248,17 @@ def decode_workload(args, device):
     lengths = torch.full((batch,), window, dtype=torch.int32, device=device)
     slot = (window - 1) % window
 
+    knew3, vnew3 = knew[:, :, 0], vnew[:, :, 0]
+
     def step():
-        # encode the new token's K and V straight into the cache slot, then attend
+        # one launch per layer encodes the new token's K and V into its cache
+        # slot and attends over the window with it
+        for cache, (_kt, _vt, kt16, vt16) in zip(caches, tabs):
+            _ops.decode_attention(q, cache.key, cache.value, kt16, vt16, lengths, window=window,
+                                  rope_theta=10000.0, max_length=window, key_new=knew3, value_new=vnew3)
+
+    def step_unfused():
+        # the same step with the encode as its own launch
         for cache, (kt, vt, kt16, vt16) in zip(caches, tabs):
             _ops.rvq_encode_kv(knew, vnew, kt, vt, groups=GROUPS, group_dim=GROUP_DIM, exits=(),
                                key_codes_out=cache.key[:, :, slot : slot + 1],
@@ -258,6 +267,7 @@ def decode_workload(args, device):
                                   rope_theta=10000.0, max_length=window)
 
     ms = timed(step, args.steps, args.warmup)
+    unfused_ms = timed(step_unfused, args.steps, 1)
     # attention kernels alone
     def attn_only():
         for cache, (_kt, _vt, kt16, vt16) in zip(caches, tabs):
@@ -272,6 +282,7 @@ def decode_workload(args, device):
     bytes_per_layer = 2 * batch * kvh * window * GROUPS * STAGES + 2 * kvh * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 2 + 2 * batch * qh * HEAD_DIM * 2
     return {
         "us_per_step": ms * 1e3,
+        "us_per_step_encode_separate": unfused_ms * 1e3,
         "attention_us_per_step": attn_ms * 1e3,
         "attention_kernels_us_per_layer": attn_layer_ms * 1e3,
         "hbm_bytes_per_step": bytes_per_layer * LAYERS,

@@ -201,6 +201,38 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b,
                          int64_t workspace_bytes, jkv_stream_t stream);
 
 /*
+ * One decode step with the new token's append fused in: the greedy residual
+ * codes of the raw K and V of the token at position lengths[b]-1 (the
+ * codec call and LayerCache.append of evaluate_mistral_longbench.py:94-98)
+ * are computed inside the attention launch from the tables it stages
+ * anyway, written to slot (lengths[b]-1) % cap of k_codes / v_codes, and
+ * attended over with the rest of the window (:112-122).
+ *   k_new, v_new  [B,KVH,128] fp16 raw (pre-RoPE) head vectors, element
+ *            strides new_stride_b / new_stride_h, rows 16-byte aligned
+ *   the codes: fp16(tables) searched stage by stage on the fp32 residual,
+ *            lowest index on ties; codes equal the reference's wherever its
+ *            best/second-best margin is clear (the same rule as
+ *            jkv_rvq_encode); rows with lengths[b] = 0 append nothing
+ * Other arguments as jkv_decode_attention.  Serves d = 8, G = 16, S in
+ * {1, 2}, K = 256 with 16-byte aligned codes and tables (the GSRQ-1/2 and
+ * grouped-CQ caches); other geometries return JKV_ENOTSUP (encode with
+ * jkv_rvq_encode_kv, then call jkv_decode_attention).
+ */
+int jkv_decode_attention_append(const void* q, int64_t q_stride_b,
+                                int64_t q_stride_h, const void* k_new,
+                                const void* v_new, int64_t new_stride_b,
+                                int64_t new_stride_h, uint8_t* k_codes,
+                                uint8_t* v_codes, int64_t code_stride_b,
+                                int64_t code_stride_h, int64_t cap,
+                                const void* k_tables, const void* v_tables,
+                                int64_t B, int64_t QH, int64_t KVH, int64_t G,
+                                int64_t d, int64_t S, int64_t K,
+                                const int32_t* lengths, int64_t window,
+                                const void* rope_table, int64_t rope_len,
+                                void* out, void* workspace,
+                                int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
  * Allocation-free variant of jkv_decode_attention.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -40,6 +40,14 @@ struct DecodeArgs {
   float* ws_o;   // [B,QH,n_splits,D]
   float* ws_ml;  // [B,QH,n_splits,2]
   _Float16* out;
+  // decode with append (decode_g8_kernel<..., true>): the raw fp16 K/V of
+  // the token at position lengths[b]-1, [B][KVH][128] with element strides,
+  // encoded into slot (lengths[b]-1) % cap of kc_out/vc_out (= kc/vc)
+  const _Float16* knew;
+  const _Float16* vnew;
+  int64_t nsb, nsh;
+  uint8_t* kc_out;
+  uint8_t* vc_out;
 };
 
 
@@ -845,7 +853,72 @@ __device__ __forceinline__ void rope16_pk(half8 a, half8 b, half8 c, half8 s, ha
 }
 #pragma clang fp contract(on)
 
-template <int NQ, int S>
+// Greedy residual search of one raw fp16 head vector over the kv head's
+// fp16 tables in LDS ([16][S][256][8], 4 KiB per (group, stage)): wave w
+// takes groups 2w and 2w + 1, lane l codewords l, l + 64, l + 128, l + 192.
+// Stage s scores ||c||^2 - 2 r.c, the reference's expanded distance
+// ||r||^2 + ||c||^2 - 2 r.c less the row's constant ||r||^2, with r the
+// residual x - c_1 - ... taken in its exact split x.c - c_1.c - ...: every
+// product is fp16 x fp16 into an fp32 v_dot2 sum.  Keys keep the score's
+// order-preserving bits with the index in the low byte, so the lowest score
+// wins and, within 2^-16 of it, the lowest index.  The code record [16][S]
+// goes to rec (LDS) and out (global).
+template <int S>
+__device__ __forceinline__ void encode_new_token(const unsigned char* tab, const _Float16* x, uint8_t* rec,
+                                                 uint8_t* out, int wave, int lane) {
+  auto dot8 = [](half8 p, half8 q, float acc) {
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const half2v u = {p[e], p[e + 1]}, v = {q[e], q[e + 1]};
+      acc = __builtin_amdgcn_fdot2(u, v, acc, false);
+    }
+    return acc;
+  };
+  const half8 xv[2] = {*(const half8*)(x + 16 * wave), *(const half8*)(x + 16 * wave + 8)};
+  half8 negc[2][S];  // negated words of the stages chosen so far
+#pragma unroll
+  for (int st = 0; st < S; ++st) {
+    uint32_t best[2] = {~0u, ~0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = lane + 64 * j;
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const int g = 2 * wave + gi;
+        const half8 c = *(const half8*)(tab + (g * S + st) * kG8Plane + k * 16);
+        float rc = dot8(xv[gi], c, 0.f);
+#pragma unroll
+        for (int p = 0; p < st; ++p) rc = dot8(negc[gi][p], c, rc);
+        const float score = fmaf(-2.f, rc, dot8(c, c, 0.f));
+        const uint32_t u = __float_as_uint(score);
+        const uint32_t ord = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);  // monotonic in the score
+        const uint32_t key = (ord & ~0xffu) | (uint32_t)k;
+        best[gi] = key < best[gi] ? key : best[gi];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const uint32_t other = __shfl_xor(best[gi], off, 64);
+        best[gi] = other < best[gi] ? other : best[gi];
+      }
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int g = 2 * wave + gi;
+      const int code = (int)(best[gi] & 0xffu);
+      const uint4 w = *(const uint4*)(tab + (g * S + st) * kG8Plane + code * 16);
+      negc[gi][st] = __builtin_bit_cast(half8, uint4{w.x ^ 0x80008000u, w.y ^ 0x80008000u, w.z ^ 0x80008000u,
+                                                     w.w ^ 0x80008000u});
+      if (lane == 0) {
+        rec[g * S + st] = (uint8_t)code;
+        out[g * S + st] = (uint8_t)code;
+      }
+    }
+  }
+}
+
+template <int NQ, int S, bool APPEND>
 __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char dyn[];
   constexpr int tab_bytes = 16 * S * kG8Plane;
@@ -854,6 +927,7 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   unsigned char* tab = dyn;
   uint8_t* cbuf = dyn + tab_bytes;                      // [chunk][kCb]
   float* red = (float*)(cbuf + kG8Chunk * kCb);         // [2][waves][NQ]
+  uint8_t* newrec = (uint8_t*)(red + 2 * kG8Waves * NQ);  // [kCb] code record of the appended token
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
@@ -874,6 +948,12 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   const uint32_t slot0 = (uint32_t)(t0 % a.cap);
   const float scale2 = 1.4426950408889634f / sqrtf((float)kHeadDim);  // log2(e)/sqrt(D)
   const int64_t rope_last = a.rope_len - 1;
+  // the split holding position L-1 encodes the appended token; its record
+  // replaces the ring slot's old bytes when its chunk is staged
+  const bool owner = APPEND && ntok > 0 && t1 == L;
+  const int new_i = ntok - 1;  // its index in the split
+  const int new_c = new_i / kG8Chunk, new_at = new_i % kG8Chunk;
+  const int64_t new_slot = cbase + ((L - 1) % a.cap) * kCb;
   auto rope_row = [&](int64_t pos) -> const _Float16* {
     return a.rope + (pos < rope_last ? pos : rope_last) * kRopeRow;
   };
@@ -893,8 +973,16 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     }
     return v;
   };
-  auto store_codes = [&](uint4 v) {
-    if (tid < pieces) *(uint4*)(cbuf + tid * 16) = v;
+  auto store_codes = [&](uint4 v, int c) {
+    if (tid < pieces) {
+      if (owner && c == new_c && tid * 16 / kCb == new_at) v = *(const uint4*)(newrec + tid * 16 % kCb);
+      *(uint4*)(cbuf + tid * 16) = v;
+    }
+  };
+  // after the appended token's encode: its record into an already staged chunk 0
+  auto patch_chunk0 = [&]() {
+    if (owner && new_c == 0 && tid < kCb / 16)
+      *(uint4*)(cbuf + new_at * kCb + tid * 16) = *(const uint4*)(newrec + tid * 16);
   };
   // tables global -> LDS directly, 8 KiB per workgroup-wide step; the
   // workgroups of one kv head start at different slices
@@ -929,7 +1017,7 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   // ---- K tables and the first chunk's records into LDS; later chunks'
   // records wait in registers ----
   load_tables(a.kt);
-  if (nchunks > 0) store_codes(fetch_codes(a.kc, 0));
+  if (nchunks > 0) store_codes(fetch_codes(a.kc, 0), owner ? -1 : 0);  // the owner patches after its encode
   // ---- rotated queries at position L-1: B operand, column ln = head ----
   const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 qb[4];
@@ -956,6 +1044,14 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   fetch_trig(0, 0, trig);
   __builtin_amdgcn_s_waitcnt(0);  // the tables' direct-to-LDS loads have landed
   __syncthreads();
+  if constexpr (APPEND) {
+    if (owner) {
+      encode_new_token<S>(tab, a.knew + b * a.nsb + kvh * a.nsh, newrec, a.kc_out + new_slot, wave, lane);
+      __syncthreads();
+      patch_chunk0();
+      __syncthreads();
+    }
+  }
   // the next chunk's records wait in a register while a chunk is scored
   uint4 knext = 1 < nchunks ? fetch_codes(a.kc, 1) : uint4{0u, 0u, 0u, 0u};
 
@@ -993,6 +1089,8 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
         for (int st = 0; st < S; ++st)
           g[q][st] = *(const half8*)(tab + (q < 2 ? kgrp : kgrp_hi) + (uint32_t)(4 * (q & 1) * S + st) * kG8Plane +
                                      (__builtin_amdgcn_ubfe(cc[q], 8u * st, 8u) << 4));
+      // every gather of the tile is in flight before the first sum (left to
+      // itself the scheduler interleaves the tiles and waits more)
       __builtin_amdgcn_sched_barrier(0);
       half8 k[4];
 #pragma unroll
@@ -1013,7 +1111,7 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     }
     __syncthreads();  // chunk c's records are consumed
     if (c + 1 < nchunks) {
-      store_codes(knext);
+      store_codes(knext, c + 1);
       if (c + 2 < nchunks) knext = fetch_codes(a.kc, c + 2);
     }
     __syncthreads();
@@ -1073,9 +1171,17 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   }
 
   // ---- the V tables have landed; the first chunk of V records into LDS ----
-  if (nchunks > 0) store_codes(vnext);
+  if (nchunks > 0 && !(owner && new_c == 0)) store_codes(vnext, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if constexpr (APPEND) {
+    if (owner) {
+      encode_new_token<S>(tab, a.vnew + b * a.nsb + kvh * a.nsh, newrec, a.vc_out + new_slot, wave, lane);
+      __syncthreads();
+      if (new_c == 0) store_codes(vnext, 0);
+      __syncthreads();
+    }
+  }
   vnext = 1 < nchunks ? fetch_codes(a.vc, 1) : uint4{0u, 0u, 0u, 0u};
 
   // ---- V phase.  As a source of the transposing reads, lane 4i + j of lane
@@ -1127,7 +1233,7 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     }
     __syncthreads();  // chunk c's records are consumed
     if (c + 1 < nchunks) {
-      store_codes(vnext);
+      store_codes(vnext, c + 1);
       if (c + 2 < nchunks) vnext = fetch_codes(a.vc, c + 2);
     }
     __syncthreads();
@@ -1212,7 +1318,7 @@ static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int
 // Dynamic LDS of decode_g8_kernel: tables, one chunk of code records, the
 // reductions.
 static int64_t g8_lds_bytes(int64_t S, int64_t nq) {
-  return 16 * S * kG8Plane + kG8Chunk * 16 * S + 2 * kG8Waves * nq * 4;
+  return 16 * S * kG8Plane + kG8Chunk * 16 * S + 2 * kG8Waves * nq * 4 + 32;
 }
 
 // Tokens per split of decode_g8_kernel (0: the geometry does not fit).
@@ -1225,7 +1331,7 @@ static int64_t g8_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int6
 }
 
 template <int D, int NQ>
-static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
+static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream, bool append = false) {
   const int64_t split = lds_ok && D != 128 && D != 0 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
   const int64_t g8_split = lds_ok && D == 8 ? g8_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
   if constexpr (D == 128 || D == 0) {
@@ -1238,10 +1344,21 @@ static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream) {
     const size_t lds = (size_t)g8_lds_bytes(a.S, NQ);
     const dim3 grid((uint32_t)(a.KVH * a.B * a.n_splits));
     if (a.S == 2) {
-      hipLaunchKernelGGL((decode_g8_kernel<NQ, 2>), grid, dim3(kG8Threads), lds, stream, a);
+      if (append) {
+        hipLaunchKernelGGL((decode_g8_kernel<NQ, 2, true>), grid, dim3(kG8Threads), lds, stream, a);
+      } else {
+        hipLaunchKernelGGL((decode_g8_kernel<NQ, 2, false>), grid, dim3(kG8Threads), lds, stream, a);
+      }
     } else {
-      hipLaunchKernelGGL((decode_g8_kernel<NQ, 1>), grid, dim3(kG8Threads), lds, stream, a);
+      if (append) {
+        hipLaunchKernelGGL((decode_g8_kernel<NQ, 1, true>), grid, dim3(kG8Threads), lds, stream, a);
+      } else {
+        hipLaunchKernelGGL((decode_g8_kernel<NQ, 1, false>), grid, dim3(kG8Threads), lds, stream, a);
+      }
     }
+  } else if (append) {
+    return set_error(JKV_ENOTSUP, "decode with append needs group dim 8, 16 groups, 1-2 stages, 256 codewords "
+                                  "and 16-byte aligned codes and tables");
   } else if (split > 0) {
     a.split_tokens = (int32_t)split;
     a.n_splits = (int32_t)ceil_div(a.window, split);
@@ -1295,7 +1412,10 @@ static int decode_packed(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
                          const void* k_tables, const void* v_tables, int64_t B, int64_t QH, int64_t KVH,
                          int64_t G, int64_t d, int64_t S, int64_t K, const int32_t* lengths, int64_t window,
                          const void* rope_table, int64_t rope_len, void* out, void* workspace,
-                         int64_t workspace_bytes, hipStream_t stream) {
+                         int64_t workspace_bytes, hipStream_t stream, const void* k_new = nullptr,
+                         const void* v_new = nullptr, int64_t new_stride_b = 0, int64_t new_stride_h = 0) {
+  const bool append = k_new != nullptr || v_new != nullptr;
+  JKV_CHECK_ARG(!append || (k_new != nullptr && v_new != nullptr), "append needs both the new K and the new V");
   JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && QH % KVH == 0, "invalid head geometry");
   JKV_CHECK_ARG(G * d == kHeadDim, "decode attention supports head_dim 128 (got %lld)",
                 (long long)(G * d));
@@ -1332,12 +1452,23 @@ static int decode_packed(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   a.ws_o = (float*)workspace;
   a.ws_ml = a.ws_o + B * QH * a.n_splits * kHeadDim;
   a.out = (_Float16*)out;
+  if (append) {
+    JKV_CHECK_ARG(((uintptr_t)k_new % 16 == 0) && ((uintptr_t)v_new % 16 == 0) && new_stride_b % 8 == 0 &&
+                      new_stride_h % 8 == 0,
+                  "appended K/V rows must be 16-byte aligned");
+    a.knew = (const _Float16*)k_new;
+    a.vnew = (const _Float16*)v_new;
+    a.nsb = new_stride_b;
+    a.nsh = new_stride_h;
+    a.kc_out = const_cast<uint8_t*>(k_codes);
+    a.vc_out = const_cast<uint8_t*>(v_codes);
+  }
   // LDS-table kernel: code records and tables copied in 16-byte pieces
   const bool lds_ok = ((uintptr_t)k_codes % 16 == 0) && ((uintptr_t)v_codes % 16 == 0) &&
                       code_stride_b % 16 == 0 && code_stride_h % 16 == 0 &&
                       ((uintptr_t)k_tables % 16 == 0) && ((uintptr_t)v_tables % 16 == 0);
 #define JKV_DEC(DD, NN) \
-  if (d == DD && nq == NN) return launch_decode<DD, NN>(a, lds_ok, stream);
+  if (d == DD && nq == NN) return launch_decode<DD, NN>(a, lds_ok, stream, append);
   JKV_DEC(8, 1) JKV_DEC(8, 2) JKV_DEC(8, 4) JKV_DEC(8, 8)
   JKV_DEC(4, 1) JKV_DEC(4, 2) JKV_DEC(4, 4) JKV_DEC(4, 8)
   JKV_DEC(128, 1) JKV_DEC(128, 2) JKV_DEC(128, 4) JKV_DEC(128, 8)
@@ -1388,6 +1519,20 @@ int jkv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   return jkv::decode_packed(q, q_stride_b, q_stride_h, k_codes, v_codes, code_stride_b, code_stride_h, cap,
                             k_tables, v_tables, B, QH, KVH, G, d, S, K, lengths, window, rope_table, rope_len,
                             out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int jkv_decode_attention_append(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                const void* v_new, int64_t new_stride_b, int64_t new_stride_h, uint8_t* k_codes,
+                                uint8_t* v_codes, int64_t code_stride_b, int64_t code_stride_h, int64_t cap,
+                                const void* k_tables, const void* v_tables, int64_t B, int64_t QH, int64_t KVH,
+                                int64_t G, int64_t d, int64_t S, int64_t K, const int32_t* lengths,
+                                int64_t window, const void* rope_table, int64_t rope_len, void* out,
+                                void* workspace, int64_t workspace_bytes, jkv_stream_t stream) {
+  if (B > 0) JKV_CHECK_ARG(k_new != nullptr && v_new != nullptr, "null buffer");
+  return jkv::decode_packed(q, q_stride_b, q_stride_h, k_codes, v_codes, code_stride_b, code_stride_h, cap,
+                            k_tables, v_tables, B, QH, KVH, G, d, S, K, lengths, window, rope_table, rope_len,
+                            out, workspace, workspace_bytes, (hipStream_t)stream, B > 0 ? k_new : nullptr,
+                            B > 0 ? v_new : nullptr, new_stride_b, new_stride_h);
 }
 
 int64_t jkv_decode_noalloc_max_workspace_bytes(void) { return jkv::kNoAllocScratchBytes; }

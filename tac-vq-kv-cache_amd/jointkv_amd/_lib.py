@@ -69,6 +69,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
     ),
+    "jkv_decode_attention_append": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
+    ),
     "jkv_decode_noalloc_max_workspace_bytes": (_i64, []),
     "jkv_decode_attention_noalloc": (
         ctypes.c_int,

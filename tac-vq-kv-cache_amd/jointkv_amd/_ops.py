@@ -349,6 +349,8 @@ def decode_attention(
     window: int,
     rope_theta: float,
     max_length: int | None = None,
+    key_new: torch.Tensor | None = None,
+    value_new: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One decode step of GQA attention straight from the packed code cache.
 
@@ -356,7 +358,10 @@ def decode_attention(
     deployed tables ``[KVH*G,S,K,d]``, ``lengths[B]`` int32 (cache length
     including the new token).  ``max_length`` bounds ``lengths`` (the rotary
     table is sized from it); when omitted it is read from the device, which
-    synchronises.  Returns ``[B,QH,D]`` fp16.
+    synchronises.  With ``key_new``/``value_new`` (``[B,KVH,128]`` fp16, the
+    raw K/V of the token at position ``lengths[b]-1``) the same launch
+    encodes that token into its ring slot first (``jkv_decode_attention_append``;
+    d = 8 caches).  Returns ``[B,QH,D]`` fp16.
     """
 
     device = _lib.require_device(q, key_codes, value_codes, key_tables16, value_tables16, lengths)
@@ -394,13 +399,31 @@ def decode_attention(
     out = torch.empty((batch, qheads, dim), dtype=torch.float16, device=device)
     ws_bytes = int(lib.jkv_decode_workspace_bytes(batch, qheads, dim, span))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-    code = lib.jkv_decode_attention(
-        q.data_ptr(), q.stride(0), q.stride(1), key_codes.data_ptr(), value_codes.data_ptr(),
-        key_codes.stride(0), key_codes.stride(1), cap, key_tables16.data_ptr(),
-        value_tables16.data_ptr(), batch, qheads, kvheads, groups, d, stages, clusters,
-        lengths.data_ptr(), span, table.data_ptr(), int(table.shape[0]), out.data_ptr(),
-        workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
-    )
+    if key_new is None and value_new is None:
+        code = lib.jkv_decode_attention(
+            q.data_ptr(), q.stride(0), q.stride(1), key_codes.data_ptr(), value_codes.data_ptr(),
+            key_codes.stride(0), key_codes.stride(1), cap, key_tables16.data_ptr(),
+            value_tables16.data_ptr(), batch, qheads, kvheads, groups, d, stages, clusters,
+            lengths.data_ptr(), span, table.data_ptr(), int(table.shape[0]), out.data_ptr(),
+            workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
+        )
+    else:
+        if key_new is None or value_new is None:
+            raise ValueError("append needs both the new key and the new value")
+        _lib.require_device(key_new, value_new)
+        for t in (key_new, value_new):
+            if t.dtype != torch.float16 or tuple(t.shape) != (batch, kvheads, dim) or t.stride(-1) != 1:
+                raise ValueError("appended K/V must be fp16 [B,KVH,128] with a contiguous last axis")
+        if key_new.stride() != value_new.stride():
+            raise ValueError("appended K and V need identical strides")
+        code = lib.jkv_decode_attention_append(
+            q.data_ptr(), q.stride(0), q.stride(1), key_new.data_ptr(), value_new.data_ptr(),
+            key_new.stride(0), key_new.stride(1), key_codes.data_ptr(), value_codes.data_ptr(),
+            key_codes.stride(0), key_codes.stride(1), cap, key_tables16.data_ptr(),
+            value_tables16.data_ptr(), batch, qheads, kvheads, groups, d, stages, clusters,
+            lengths.data_ptr(), span, table.data_ptr(), int(table.shape[0]), out.data_ptr(),
+            workspace.data_ptr(), ws_bytes, _lib.stream_handle(device),
+        )
     _lib.check(code)
     return out
 

@@ -53,6 +53,8 @@ def decode_attention(
     window: int = MISTRAL_WINDOW,
     rope_theta: float = MISTRAL_ROPE_THETA,
     max_length: int | None = None,
+    key_new: torch.Tensor | None = None,
+    value_new: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention output for one new token per sequence.
 
@@ -62,7 +64,12 @@ def decode_attention(
     including the new one, so the query sits at position ``lengths[b]-1``
     and sees the last ``min(window, lengths[b])`` positions (the reference's
     ``LayerCache.visible``).  ``max_length`` (an upper bound of ``lengths``)
-    avoids a device read.  Returns ``[B,QH,1,D]`` (or ``[B,QH,D]``) fp16.
+    avoids a device read.  With ``key_new``/``value_new`` (the raw
+    ``[B,KVH,1,D]`` or ``[B,KVH,D]`` fp16 K/V of the token at position
+    ``lengths[b]-1``) the launch first encodes that token into its ring slot
+    (the codec call and ``LayerCache.append`` of
+    evaluate_mistral_longbench.py:94-98, fused; group dim 8 caches).
+    Returns ``[B,QH,1,D]`` (or ``[B,QH,D]``) fp16.
     """
 
     squeeze = query.ndim == 3
@@ -72,9 +79,13 @@ def decode_attention(
         stages = key_codes.shape[-1] // groups
         key_codes = key_codes.unflatten(-1, (groups, stages))
         value_codes = value_codes.unflatten(-1, (groups, stages))
+    if key_new is not None and key_new.ndim == 4:
+        key_new = key_new.reshape(key_new.shape[0], key_new.shape[1], key_new.shape[-1])
+    if value_new is not None and value_new.ndim == 4:
+        value_new = value_new.reshape(value_new.shape[0], value_new.shape[1], value_new.shape[-1])
     out = _ops.decode_attention(
         q, key_codes, value_codes, key_tables16, value_tables16, lengths,
-        window=window, rope_theta=rope_theta, max_length=max_length,
+        window=window, rope_theta=rope_theta, max_length=max_length, key_new=key_new, value_new=value_new,
     )
     return out if squeeze else out.unsqueeze(2)
 
@@ -285,6 +296,23 @@ class PackedCodeCache:
                            value_codes_out=self.value[:, :, slot : slot + 1])
         self._host_length += 1
         self.lengths.fill_(self._host_length)
+
+    def attend_append(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                      key_tables16: torch.Tensor, value_tables16: torch.Tensor, *,
+                      window: int = MISTRAL_WINDOW, rope_theta: float = MISTRAL_ROPE_THETA) -> torch.Tensor:
+        """One decode step in one launch: encode the new token's raw K/V
+        (``[B,KVH,1,128]`` fp16) with the fp16 deployed tables
+        ``[KVH*G,S,K,8]`` into the next slot and attend over the window
+        (evaluate_mistral_longbench.py:94-122).  Returns ``[B,QH,1,128]``
+        (or ``[B,QH,128]`` for a 3-D query)."""
+
+        if (key.ndim == 4 and key.shape[2] != 1) or (value.ndim == 4 and value.shape[2] != 1):
+            raise ValueError("attend_append takes one token per sequence")
+        self._host_length += 1
+        self.lengths.fill_(self._host_length)
+        return decode_attention(query, self.key, self.value, key_tables16, value_tables16, self.lengths,
+                                window=window, rope_theta=rope_theta, max_length=self._host_length,
+                                key_new=key, value_new=value)
 
     def payload_bytes(self) -> int:
         visible = min(self._host_length, self.capacity)

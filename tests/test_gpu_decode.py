@@ -8,6 +8,7 @@ import torch
 
 import jointkv_amd as jkv
 from oracle import jointkv_oracle as ref
+from parity import compare_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -57,6 +58,65 @@ def test_decode_matches_oracle(device, batch, qh, kvh, groups, stages, d, length
     expect = _expect(q, kc, vc, kt, vt, length, window, cap)
     err = float((out.cpu().float() - expect.float()).abs().max())
     assert err <= ATOL, f"max abs error {err}"
+
+
+@pytest.mark.parametrize("batch,qh,kvh,stages,lengths,window,cap", [
+    (2, 32, 8, 2, (4096, 4096), 4096, 4096),    # config 4 geometry: the new token closes split 2
+    (3, 8, 2, 2, (1, 257, 5000), 4096, 4096),   # first token; chunk 1's first key; ring wrap
+    (2, 16, 2, 1, (600, 2049), 4096, 4096),     # one stage, GQA 8; the new token opens split 2
+    (2, 4, 2, 2, (513, 700), 512, 1024),        # window of two chunks, partial last chunk
+])
+def test_decode_append_matches_encode_then_decode(device, batch, qh, kvh, stages, lengths, window, cap):
+    # the fused step encodes the new token into its slot and attends with it
+    print(f"decode append B={batch} QH={qh} KVH={kvh} S={stages} lengths={lengths} win={window}", flush=True)
+    q, kc, vc, kt, vt = _case(sum(lengths) + qh, batch, qh, kvh, 16, stages, 8, 0, cap)
+    gen = torch.Generator().manual_seed(4242 + sum(lengths))
+    knew = ref.synthetic_states(gen, batch, kvh, 1)
+    vnew = ref.synthetic_states(gen, batch, kvh, 1)
+    lens = torch.tensor(lengths, dtype=torch.int32)
+    kc_d, vc_d = kc.to(device), vc.to(device)
+    kt16, vt16 = kt.half().to(device), vt.half().to(device)
+    out = jkv.decode_attention(q.to(device), kc_d, vc_d, kt16, vt16, lens.to(device), window=window,
+                               key_new=knew.to(device), value_new=vnew.to(device))
+    kc_got, vc_got = kc_d.cpu(), vc_d.cpu()
+    slots = [(int(L) - 1) % cap for L in lengths]
+    # only the new tokens' slots changed
+    keep = torch.ones(batch, cap, dtype=torch.bool)
+    for b, sl in enumerate(slots):
+        keep[b, sl] = False
+    assert torch.equal(kc_got.permute(0, 2, 1, 3, 4)[keep], kc.permute(0, 2, 1, 3, 4)[keep])
+    assert torch.equal(vc_got.permute(0, 2, 1, 3, 4)[keep], vc.permute(0, 2, 1, 3, 4)[keep])
+    # the written codes are the codec's greedy search of the raw vectors
+    for raw, tabs, got in ((knew, kt, kc_got), (vnew, vt, vc_got)):
+        _o, want, d1, d2 = ref.grouped_residual_vq(raw, tabs.reshape(kvh, 16, stages, 256, 8), prefixes=(stages,),
+                                                   return_margins=True)
+        ours = torch.stack([got[b, :, slots[b]] for b in range(batch)])[:, :, None]
+        verdict = compare_codes(ours, want, d1, d2)
+        assert verdict["clear_mismatches"] == 0 and verdict["agreement"] >= 0.999, verdict["agreement"]
+    # the attention equals the plain decode over the updated cache, bit for bit,
+    # and the oracle's decode of it within ATOL
+    again = jkv.decode_attention(q.to(device), kc_got.to(device), vc_got.to(device), kt16, vt16, lens.to(device),
+                                 window=window)
+    assert torch.equal(out, again)
+    for b, L in enumerate(lengths):
+        e = _expect(q[b : b + 1], kc_got[b : b + 1], vc_got[b : b + 1], kt, vt, int(L), window, cap)
+        err = float((out[b : b + 1].cpu().float() - e.float()).abs().max())
+        assert err <= ATOL, f"row {b} length {L}: {err}"
+
+
+def test_decode_append_entry_point_limits(device):
+    # geometries the fused step does not serve are refused, not mis-served
+    q, kc, vc, kt, vt = _case(3, 1, 8, 2, 32, 1, 4, 0, 512)
+    knew = torch.zeros(1, 2, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="group dim 8"):
+        jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device), vt.half().to(device),
+                             torch.tensor([5], dtype=torch.int32, device=device), window=512,
+                             key_new=knew.to(device), value_new=knew.to(device))
+    q, kc, vc, kt, vt = _case(3, 1, 8, 2, 16, 2, 8, 0, 512)
+    with pytest.raises(ValueError, match="both"):
+        jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device), vt.half().to(device),
+                             torch.tensor([5], dtype=torch.int32, device=device), window=512,
+                             key_new=knew.to(device))
 
 
 def test_ragged_lengths_and_cache_append(device):

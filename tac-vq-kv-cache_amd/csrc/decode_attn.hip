@@ -923,10 +923,10 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char dyn[];
   constexpr int tab_bytes = 16 * S * kG8Plane;
   constexpr int kSlots = kG8MaxSplit / kG8Chunk;
-  constexpr int kCb = 16 * S;  // code bytes per token
+  constexpr int kCb = 16 * S;    // code bytes per token
+  constexpr int kCw = kCb / 4;   // as dwords
   unsigned char* tab = dyn;
-  uint8_t* cbuf = dyn + tab_bytes;                      // [chunk][kCb]
-  float* red = (float*)(cbuf + kG8Chunk * kCb);         // [2][waves][NQ]
+  float* red = (float*)(dyn + tab_bytes);                 // [2][waves][NQ]
   uint8_t* newrec = (uint8_t*)(red + 2 * kG8Waves * NQ);  // [kCb] code record of the appended token
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -949,40 +949,39 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   const float scale2 = 1.4426950408889634f / sqrtf((float)kHeadDim);  // log2(e)/sqrt(D)
   const int64_t rope_last = a.rope_len - 1;
   // the split holding position L-1 encodes the appended token; its record
-  // replaces the ring slot's old bytes when its chunk is staged
+  // takes the place of the ring slot's old bytes when its key is rebuilt
   const bool owner = APPEND && ntok > 0 && t1 == L;
   const int new_i = ntok - 1;  // its index in the split
-  const int new_c = new_i / kG8Chunk, new_at = new_i % kG8Chunk;
+  const int new_c = new_i / kG8Chunk;
   const int64_t new_slot = cbase + ((L - 1) % a.cap) * kCb;
   auto rope_row = [&](int64_t pos) -> const _Float16* {
     return a.rope + (pos < rope_last ? pos : rope_last) * kRopeRow;
   };
-  // one 16-byte piece of chunk c's code records: token i = tid*16/kCb.  A
-  // slot past the split's tokens gets the split's first record, so every
-  // rebuilt vector is one the reference also forms (its score is masked and
-  // its weight is 0)
-  constexpr int pieces = kG8Chunk * kCb / 16;
-  auto fetch_codes = [&](const uint8_t* codes, int c) -> uint4 {
-    uint4 v = {0u, 0u, 0u, 0u};
-    if (tid < pieces) {
-      const int i = tid * 16 / kCb, part = tid * 16 % kCb;
-      const int t = c * kG8Chunk + i;
-      uint32_t slot = slot0 + (uint32_t)(t < ntok ? t : 0);
-      if (slot >= cap) slot -= cap;
-      v = *(const uint4*)(codes + cbase + (int64_t)slot * kCb + part);
-    }
-    return v;
-  };
-  auto store_codes = [&](uint4 v, int c) {
-    if (tid < pieces) {
-      if (owner && c == new_c && tid * 16 / kCb == new_at) v = *(const uint4*)(newrec + tid * 16 % kCb);
-      *(uint4*)(cbuf + tid * 16) = v;
+  // The code record of key k of the split, straight from the ring (each lane
+  // loads the record of the key it rebuilds; the four lanes of a key share
+  // the cache line).  Keys past the split read the split's first record, so
+  // every rebuilt vector is one the reference also forms (its score is masked
+  // and its weight is 0).
+  auto load_rec = [&](const uint8_t* codes, int k, uint32_t (&w)[kCw]) {
+    uint32_t slot = slot0 + (uint32_t)(k < ntok ? k : 0);
+    if (slot >= cap) slot -= cap;
+    const uint4* p = (const uint4*)(codes + cbase + (int64_t)slot * kCb);
+#pragma unroll
+    for (int i = 0; i < kCb / 16; ++i) {
+      const uint4 v = p[i];
+      w[4 * i] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
     }
   };
-  // after the appended token's encode: its record into an already staged chunk 0
-  auto patch_chunk0 = [&]() {
-    if (owner && new_c == 0 && tid < kCb / 16)
-      *(uint4*)(cbuf + new_at * kCb + tid * 16) = *(const uint4*)(newrec + tid * 16);
+  // the appended token's record (LDS) for the lane whose key it is
+  auto splice_new = [&](int k, uint32_t (&w)[kCw]) {
+    uint32_t nw[kCw];
+    read_record<kCb>(newrec, nw);
+    const bool mine = k == new_i;
+#pragma unroll
+    for (int i = 0; i < kCw; ++i) w[i] = mine ? nw[i] : w[i];
   };
   // tables global -> LDS directly, 8 KiB per workgroup-wide step; the
   // workgroups of one kv head start at different slices
@@ -1014,10 +1013,12 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     load_trig8(tr, 32 + 8 * lg, &tg[2], &tg[3]);
   };
 
-  // ---- K tables and the first chunk's records into LDS; later chunks'
-  // records wait in registers ----
+  // ---- K tables into LDS; the first chunk's records and rotary rows load
+  // beside them ----
   load_tables(a.kt);
-  if (nchunks > 0) store_codes(fetch_codes(a.kc, 0), owner ? -1 : 0);  // the owner patches after its encode
+  uint32_t rk[2][kCw];  // the records of the wave's two tiles in the current chunk
+#pragma unroll
+  for (int tl = 0; tl < 2; ++tl) load_rec(a.kc, 32 * wave + 16 * tl + ln, rk[tl]);
   // ---- rotated queries at position L-1: B operand, column ln = head ----
   const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 qb[4];
@@ -1048,17 +1049,14 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     if (owner) {
       encode_new_token<S>(tab, a.knew + b * a.nsb + kvh * a.nsh, newrec, a.kc_out + new_slot, wave, lane);
       __syncthreads();
-      patch_chunk0();
-      __syncthreads();
     }
   }
-  // the next chunk's records wait in a register while a chunk is scored
-  uint4 knext = 1 < nchunks ? fetch_codes(a.kc, 1) : uint4{0u, 0u, 0u, 0u};
 
-  // ---- K phase.  Lane (key ln of a 16-key tile, lane group lg) owns 8-dim
-  // chunks 4q+lg (q = 0..3) = MFMA contraction slice q; chunks lg/lg+8 and
-  // lg+4/lg+12 are rotary partners.  sc[c][tl][e]: score of key 4lg+e of
-  // tile tl of the wave's block in chunk c, for head ln ----
+  // ---- K phase, no barriers: each wave streams its own keys' records.
+  // Lane (key ln of a 16-key tile, lane group lg) owns 8-dim chunks 4q+lg
+  // (q = 0..3) = MFMA contraction slice q; chunks lg/lg+8 and lg+4/lg+12 are
+  // rotary partners.  sc[c][tl][e]: score of key 4lg+e of tile tl of the
+  // wave's block in chunk c, for head ln ----
   // byte offsets of chunk lg's tables (chunks 8 + lg .. through a second base,
   // so that every gather's constant part fits the instruction's offset)
   const uint32_t kgrp = (uint32_t)lg * S * kG8Plane;
@@ -1069,19 +1067,28 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     sc[c][0] = float4v{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
     sc[c][1] = sc[c][0];
     if (c >= nchunks) continue;
+    // the next chunk's records go out now
+    uint32_t rn[2][kCw];
+    const int cn = c + 1 < kSlots ? c + 1 : c;
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl) load_rec(a.kc, cn * kG8Chunk + 32 * wave + 16 * tl + ln, rn[tl]);
+    if constexpr (APPEND) {
+      if (owner && c == new_c) {
+#pragma unroll
+        for (int tl = 0; tl < 2; ++tl) splice_new(c * kG8Chunk + 32 * wave + 16 * tl + ln, rk[tl]);
+      }
+    }
 #pragma unroll
     for (int tl = 0; tl < 2; ++tl) {
-      uint32_t wrec[kCb / 4];
-      read_record<kCb>(cbuf + (32 * wave + 16 * tl + ln) * kCb, wrec);
       // the next tile's rotary rows go out now
       half8 tnext[4];
       if (tl == 0) {
         fetch_trig(c, 1, tnext);
       } else {
-        fetch_trig(c + 1 < kSlots ? c + 1 : c, 0, tnext);
+        fetch_trig(cn, 0, tnext);
       }
       uint32_t cc[4];
-      record_codes<8, S>(wrec, lg, cc);
+      record_codes<8, S>(rk[tl], lg, cc);
       half8 g[4][S];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -1109,18 +1116,23 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) trig[u] = tnext[u];
     }
-    __syncthreads();  // chunk c's records are consumed
-    if (c + 1 < nchunks) {
-      store_codes(knext, c + 1);
-      if (c + 2 < nchunks) knext = fetch_codes(a.kc, c + 2);
-    }
-    __syncthreads();
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+      for (int i = 0; i < kCw; ++i) rk[tl][i] = rn[tl][i];
   }
 
-  // every wave is done with the K tables: the V tables and the first chunk
-  // of V records load while the softmax runs
+  // every wave is done with the K tables (and the appended K record): the V
+  // tables and the first chunk's V records load while the softmax runs
+  __syncthreads();
   load_tables(a.vt);
-  uint4 vnext = nchunks > 0 ? fetch_codes(a.vc, 0) : uint4{0u, 0u, 0u, 0u};
+  // the lane's two V keys of each chunk (as a source of the transposing
+  // reads): 4lg + si and 16 + 4lg + si of the wave's block
+  const int si = ln >> 2, sj = ln & 3;
+  const int vkey = 32 * wave + 4 * lg + si;
+  uint32_t rva[kCw], rvb[kCw];
+  load_rec(a.vc, vkey, rva);
+  load_rec(a.vc, vkey + 16, rvb);
 
   // ---- split max and exp-sum per head (lanes ln < NQ carry head ln) ----
   float mx = -__builtin_inff();
@@ -1170,26 +1182,21 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
     lh[h] = l;
   }
 
-  // ---- the V tables have landed; the first chunk of V records into LDS ----
-  if (nchunks > 0 && !(owner && new_c == 0)) store_codes(vnext, 0);
+  // ---- the V tables have landed ----
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if constexpr (APPEND) {
     if (owner) {
       encode_new_token<S>(tab, a.vnew + b * a.nsb + kvh * a.nsh, newrec, a.vc_out + new_slot, wave, lane);
       __syncthreads();
-      if (new_c == 0) store_codes(vnext, 0);
-      __syncthreads();
     }
   }
-  vnext = 1 < nchunks ? fetch_codes(a.vc, 1) : uint4{0u, 0u, 0u, 0u};
 
-  // ---- V phase.  As a source of the transposing reads, lane 4i + j of lane
-  // group lg addresses, for keys 4lg + i and 16 + 4lg + i of the wave's
-  // block, dims 4j..4j+3 of each 16-dim slice t: group 2t + (j >> 1), half
-  // j & 1.  As an MFMA A lane (dim ln of slice t, keys of lane group lg) it
-  // receives what the P operand of the same lane group weights ----
-  const int si = ln >> 2, sj = ln & 3;
+  // ---- V phase, no barriers.  As a source of the transposing reads, lane
+  // 4i + j of lane group lg addresses, for keys 4lg + i and 16 + 4lg + i of
+  // the wave's block, dims 4j..4j+3 of each 16-dim slice t: group 2t + (j >> 1),
+  // half j & 1.  As an MFMA A lane (dim ln of slice t, keys of lane group lg)
+  // it receives what the P operand of the same lane group weights ----
   // LDS byte addresses (the table area starts the dynamic allocation)
   const uint32_t vlane = (uint32_t)(size_t)(const void __attribute__((address_space(3)))*)tab +
                          (uint32_t)(sj >> 1) * S * kG8Plane + (uint32_t)(sj & 1) * 8u;
@@ -1203,9 +1210,16 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
 #pragma unroll
   for (int c = 0; c < kSlots; ++c) {
     if (c >= nchunks) continue;
-    uint32_t wa[kCb / 4], wb[kCb / 4];
-    read_record<kCb>(cbuf + (32 * wave + 4 * lg + si) * kCb, wa);
-    read_record<kCb>(cbuf + (32 * wave + 16 + 4 * lg + si) * kCb, wb);
+    uint32_t na[kCw], nb[kCw];
+    const int cn = c + 1 < kSlots ? c + 1 : c;
+    load_rec(a.vc, cn * kG8Chunk + vkey, na);
+    load_rec(a.vc, cn * kG8Chunk + vkey + 16, nb);
+    if constexpr (APPEND) {
+      if (owner && c == new_c) {
+        splice_new(c * kG8Chunk + vkey, rva);
+        splice_new(c * kG8Chunk + vkey + 16, rvb);
+      }
+    }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       // the lane's codes of group 2dt + (sj >> 1), stage st, as byte offsets
@@ -1213,8 +1227,8 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
       uint32_t ra[S], rb[S];
 #pragma unroll
       for (int st = 0; st < S; ++st) {
-        const uint32_t wa_ = S == 2 ? wa[dt] : wa[dt >> 1];
-        const uint32_t wb_ = S == 2 ? wb[dt] : wb[dt >> 1];
+        const uint32_t wa_ = S == 2 ? rva[dt] : rva[dt >> 1];
+        const uint32_t wb_ = S == 2 ? rvb[dt] : rvb[dt >> 1];
         const uint32_t off = jsh + (S == 2 ? 8u * st : 16u * (dt & 1));
         const uint32_t base = dt < 4 ? vlane : vlane_hi;
         ra[st] = (__builtin_amdgcn_ubfe(wa_, off, 8u) << 4) + base;
@@ -1231,16 +1245,16 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
                             __builtin_bit_cast(uint2, vb).x, __builtin_bit_cast(uint2, vb).y};
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w), pf[c], o[dt], 0, 0, 0);
     }
-    __syncthreads();  // chunk c's records are consumed
-    if (c + 1 < nchunks) {
-      store_codes(vnext, c + 1);
-      if (c + 2 < nchunks) vnext = fetch_codes(a.vc, c + 2);
+#pragma unroll
+    for (int i = 0; i < kCw; ++i) {
+      rva[i] = na[i];
+      rvb[i] = nb[i];
     }
-    __syncthreads();
   }
 
   // ---- workgroup sum of the waves' Oᵀ (lane (head ln, lg) holds dims
   // 16dt + 4lg + e) and the split's partial ----
+  __syncthreads();  // every wave is done with the V tables
   float* o_red = (float*)dyn;  // [waves][NQ][128], in the table area
   if (ln < NQ) {
 #pragma unroll
@@ -1318,7 +1332,7 @@ static int64_t lds_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int
 // Dynamic LDS of decode_g8_kernel: tables, one chunk of code records, the
 // reductions.
 static int64_t g8_lds_bytes(int64_t S, int64_t nq) {
-  return 16 * S * kG8Plane + kG8Chunk * 16 * S + 2 * kG8Waves * nq * 4 + 32;
+  return 16 * S * kG8Plane + 2 * kG8Waves * nq * 4 + 32;
 }
 
 // Tokens per split of decode_g8_kernel (0: the geometry does not fit).

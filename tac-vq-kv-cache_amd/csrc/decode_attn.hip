@@ -853,6 +853,21 @@ __device__ __forceinline__ void rope16_pk(half8 a, half8 b, half8 c, half8 s, ha
 }
 #pragma clang fp contract(on)
 
+// Minimum of v over the wave, wave-uniform: within each 16-lane row by DPP
+// (quad swaps, half-row and row mirrors), then across the four rows through
+// lane reads; no LDS round trips.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return min(min(r0, r1), min(r2, r3));
+}
+
 // Greedy residual search of one raw fp16 head vector over the kv head's
 // fp16 tables in LDS ([16][S][256][8], 4 KiB per (group, stage)): wave w
 // takes groups 2w and 2w + 1, lane l codewords l, l + 64, l + 128, l + 192.
@@ -897,12 +912,7 @@ __device__ __forceinline__ void encode_new_token(const unsigned char* tab, const
       }
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-      for (int gi = 0; gi < 2; ++gi) {
-        const uint32_t other = __shfl_xor(best[gi], off, 64);
-        best[gi] = other < best[gi] ? other : best[gi];
-      }
+    for (int gi = 0; gi < 2; ++gi) best[gi] = wave_min_u32(best[gi]);
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       const int g = 2 * wave + gi;

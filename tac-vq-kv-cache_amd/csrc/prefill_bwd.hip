@@ -25,6 +25,8 @@
 // Steps where none of a wave's keys is visible skip its arithmetic.
 #include <math.h>
 
+#include <type_traits>
+
 #include "jkv_common.h"
 #include "rotary.h"
 
@@ -57,9 +59,37 @@ struct ValueGradArgs {
   int64_t rope_len;
   float* dv;  // [B,KVH,T,D] fp32 contiguous, or the chunk's partial slot
   int32_t nq;
-  int32_t chunk_tiles;  // query tiles per workgroup (a key block's rows are split in chunks)
+  int32_t chunk_tiles;  // query tiles per chunk (the query rows are split in chunks of tiles)
   int64_t slot_stride;  // elements between the chunks' partial slots (0: one chunk)
+  int32_t slots;        // partial slots (grid rows) of the key-block kernels
 };
+
+// The 32-row query tiles (absolute: tile t holds rows 32t..32t+31) that the
+// workgroup of key block key0 in grid row y walks, top tile first.  The rows
+// that see some key of the block are [key0, key0 + 127 + window) within
+// [0, T): tiles [tf, tl].  The query rows are split in absolute chunks of
+// `per` tiles; a block meets at most `slots` consecutive chunks, and chunk c
+// runs in grid row c mod slots, so the workgroups that walk one chunk for the
+// blocks of a (batch row, kv head) sit side by side in the grid and read each
+// q/dO tile at about the same time.
+struct TileRun {
+  int64_t top, n;
+};
+__host__ __device__ inline void block_tiles(int64_t key0, int64_t T, int64_t window, int64_t* tf, int64_t* tl) {
+  int64_t rend = key0 + kBKeys - 1 + window;
+  if (rend > T || rend < 0) rend = T;
+  *tf = key0 / kBRows;
+  *tl = (rend - 1) / kBRows;
+}
+__device__ inline TileRun tile_run(int64_t key0, int64_t T, int64_t window, int64_t per, int slots, int y) {
+  int64_t tf, tl;
+  block_tiles(key0, T, window, &tf, &tl);
+  const int64_t c_lo = tf / per;
+  const int64_t c = c_lo + ((int64_t)y - c_lo % slots + slots) % slots;
+  const int64_t lo = tf > c * per ? tf : c * per;
+  const int64_t hi = tl < c * per + per - 1 ? tl : c * per + per - 1;
+  return TileRun{hi, hi >= lo ? hi - lo + 1 : 0};
+}
 
 // (a[e], b[e]) as one 32-bit word
 __device__ __forceinline__ uint32_t pair_words(half8 a, half8 b, int e) {
@@ -72,14 +102,15 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
   __shared__ __align__(16) _Float16 d_lds[2][kDTile];
   __shared__ __align__(16) float l_lds[2][kBRows];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the step tests below branch on it
   const int ln = lane & 15, lg = lane >> 4;
   const int NQ = a.nq;
   const int64_t nkb = ceil_div(a.T, kBKeys);
   // key blocks fastest: the blocks of one (batch row, kv head) share its q and
   // dO rows in one XCD's L2
   const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int chunk = blockIdx.y;  // which run of query tiles of the key block
+  const int chunk = blockIdx.y;  // grid row: the chunk of query tiles (chunk index mod slots)
   const int64_t kb = bid % (uint32_t)nkb;
   const int64_t kvh = (bid / (uint32_t)nkb) % (uint32_t)a.KVH;
   const int64_t b = bid / ((uint32_t)nkb * (uint32_t)a.KVH);
@@ -119,15 +150,11 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  // query rows that see some key of the block: [key0, key0 + 127 + window)
-  int64_t rend = key0 + kBKeys - 1 + a.window;
-  if (rend > a.T || rend < 0) rend = a.T;
-  const int64_t all_tiles = ceil_div(rend - key0, kBRows);
-  const int64_t tile_lo = (int64_t)chunk * a.chunk_tiles;
-  int64_t ntiles = all_tiles - tile_lo;
-  if (ntiles > a.chunk_tiles) ntiles = a.chunk_tiles;
-  if (ntiles < 0) ntiles = 0;
-  const int64_t nsteps = ntiles * NQ;
+  // this workgroup's query tiles, top first (none: no slot to write)
+  const TileRun run = tile_run(key0, a.T, a.window, a.chunk_tiles, a.slots, chunk);
+  if (run.n == 0) return;
+  const int64_t t_top = run.top;
+  const int64_t nsteps = run.n * NQ;
 
   // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
   // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
@@ -142,25 +169,28 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
   const _Float16* q_b = a.q + b * a.qsb + kvh * NQ * a.qsh;
   const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
   const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
+  // Every load of a step is unconditional: rows past the end read the step's
+  // first row (a step's first row is always in range).  A select right after
+  // a load, or a load inside a branch, would make the wave wait for this
+  // step's whole prefetch where it is issued; the P mask gives those rows
+  // weight 0, so their values are never used.
   struct StepRegs {
     half8 q0, q1, cs, sn, d0, d1;
     float l;
   };
+  const int lrow = tid < kBRows ? tid : 0;
   auto fetch = [&](int ft, int fh, StepRegs& r) {
-    const int64_t r0 = key0 + (tile_lo + ft) * kBRows;
+    const int64_t r0 = (t_top - ft) * kBRows;
     const int64_t row = r0 + qr;
     const bool ok = row < a.T;
-    const _Float16* qrow = ok ? q_b + fh * a.qsh + r0 * a.qst + q_thr : a.q;
+    const _Float16* qrow = q_b + fh * a.qsh + r0 * a.qst + (ok ? q_thr : 8 * qp);
     r.q0 = *(const half8*)qrow;
     r.q1 = *(const half8*)(qrow + 64);
-    r.q0 = ok ? r.q0 : zero8;
-    r.q1 = ok ? r.q1 : zero8;
-    load_trig8(rope_row(p0 + (ok ? row : 0)), 8 * qp, &r.cs, &r.sn);
+    load_trig8(rope_row(p0 + (ok ? row : r0)), 8 * qp, &r.cs, &r.sn);
     const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
-    const bool ok0 = r0 + 2 * drp < a.T, ok1 = r0 + 2 * drp + 1 < a.T;
-    r.d0 = ok0 ? *(const half8*)(dstep + d_thr0) : zero8;
-    r.d1 = ok1 ? *(const half8*)(dstep + d_thr1) : zero8;
-    r.l = tid < kBRows && r0 + tid < a.T ? l_b[fh * a.T + r0 + tid] * 1.4426950408889634f : 0.f;
+    r.d0 = *(const half8*)(dstep + (r0 + 2 * drp < a.T ? d_thr0 : 8 * ddb));
+    r.d1 = *(const half8*)(dstep + (r0 + 2 * drp + 1 < a.T ? d_thr1 : 8 * ddb));
+    r.l = l_b[fh * a.T + r0 + (tid < kBRows && r0 + tid < a.T ? lrow : 0)];
   };
   auto store = [&](const StepRegs& r, int buf) {
     half8 r0, r1;
@@ -171,11 +201,13 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
     _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
 #pragma unroll
     for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(r.d0, r.d1, e);
-    if (tid < kBRows) l_lds[buf][tid] = r.l;
+    if (tid < kBRows) l_lds[buf][tid] = r.l * 1.4426950408889634f;
   };
 
   // step s+1 waits in registers while s is computed and s+2 is in flight;
-  // steps run tile by tile, the group's heads within a tile
+  // steps run tile by tile, the group's heads within a tile.  The two steps
+  // ahead alternate between two register sets, so that no load result is
+  // copied (a copy would wait for its load where it stands)
   int ft = 0, fh = 0;  // the next step to fetch
   auto advance = [&]() {
     if (++fh == NQ) {
@@ -183,13 +215,13 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
       ++ft;
     }
   };
-  StepRegs nxt;
+  StepRegs ra, rb;
   if (nsteps > 0) {
     StepRegs r;
     fetch(ft, fh, r);
     advance();
     if (nsteps > 1) {
-      fetch(ft, fh, nxt);
+      fetch(ft, fh, ra);
       advance();
     }
     store(r, 0);
@@ -197,15 +229,16 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
   __syncthreads();
 
   int ct = 0, ch = 0;  // the step being computed
-  for (int64_t step = 0; step < nsteps; ++step) {
+  // stage step + 1 from `nxt` (its buffer was freed by the last barrier);
+  // load step + 2 into `ahead`; compute step `step`
+  auto run_step = [&](int64_t step, StepRegs& ahead, const StepRegs& nxt) {
     const int buf = (int)(step & 1);
-    const bool more = step + 1 < nsteps;
-    StepRegs ahead;
+    if (step + 1 < nsteps) store(nxt, buf ^ 1);
     if (step + 2 < nsteps) {
       fetch(ft, fh, ahead);
       advance();
     }
-    const int64_t r0 = key0 + (tile_lo + ct) * kBRows;
+    const int64_t r0 = (t_top - ct) * kBRows;
     // does any row of the step see any of this wave's keys?
     const bool any = r0 + kBRows - 1 >= kw0 && r0 - (kw0 + 31) < a.window && kw0 < a.T;
     if (any) {
@@ -234,50 +267,68 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
       const int rows_left = (int)(a.T - r0 < kBRows ? a.T - r0 : kBRows);
       const int keys_left = (int)(a.T - kw0 < 32 ? a.T - kw0 : 32);
       const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
-      half8 pa[2];
-#pragma unroll
-      for (int rg = 0; rg < 2; ++rg) {
-        const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
-        const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
-            if (!full) {
-              const int diff = base + 16 * rg + e - 16 * kt;
-              const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
-                               16 * kt + ln < keys_left;
-              p = vis ? p : 0.f;
-            }
-            pa[kt][4 * rg + e] = (_Float16)p;
-          }
-      }
-      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
-      // {16+4lg..16+4lg+3} ----
+      // the dOᵀ operands of the second product go out now, under the
+      // exponentials (left alone, the reads sink next to their products)
+      half8 db[8];
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const _Float16* dr = dl + (16 * dt + ln) * kDStride + 4 * lg;
         const half4 lo = *(const half4*)dr;
         const half4 hi = *(const half4*)(dr + 16);
-        const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        db[dt] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // (rows past T hold the step's first row and keys past T zeros: the
+      // mask zeroes their weights by selection, so no product reads them)
+      half8 pa[2];
+      auto make_p = [&](auto masked_tag) {
+        constexpr bool masked = decltype(masked_tag)::value;
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
+          const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
+              if constexpr (masked) {
+                const int diff = base + 16 * rg + e - 16 * kt;
+                const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
+                                 16 * kt + ln < keys_left;
+                p = vis ? p : 0.f;
+              }
+              pa[kt][4 * rg + e] = (_Float16)p;
+            }
+        }
+      };
+      // a uniform branch: the steps away from the diagonal and the ends pay
+      // for no mask
+      if (full) {
+        make_p(std::false_type{});
+      } else {
+        make_p(std::true_type{});
+      }
+      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
+      // {16+4lg..16+4lg+3} ----
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
-          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
-      }
+          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db[dt], acc[kt][dt], 0, 0, 0);
     }
-    // ---- the next step into the other buffer ----
-    if (more) store(nxt, buf ^ 1);
-    nxt = ahead;
     __syncthreads();
     if (++ch == NQ) {
       ch = 0;
       ++ct;
     }
+  };
+  for (int64_t step = 0; step < nsteps; step += 2) {
+    run_step(step, rb, ra);
+    if (step + 1 < nsteps) run_step(step + 1, ra, rb);
   }
 
   // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
-  // (a chunk with no rows still writes its slot: zeros)
   float* out = a.dv + (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
@@ -314,7 +365,7 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
   // key blocks fastest: the blocks of one (batch row, kv head) share its q and
   // dO rows in one XCD's L2
   const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int chunk = blockIdx.y;  // which run of query tiles of the key block
+  const int chunk = blockIdx.y;  // grid row: the chunk of query tiles (chunk index mod slots)
   const int64_t kb = bid % (uint32_t)nkb;
   const int64_t kvh = (bid / (uint32_t)nkb) % (uint32_t)a.KVH;
   const int64_t b = bid / ((uint32_t)nkb * (uint32_t)a.KVH);
@@ -371,15 +422,11 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  // query rows that see some key of the block: [key0, key0 + 127 + window)
-  int64_t rend = key0 + kBKeys - 1 + a.window;
-  if (rend > a.T || rend < 0) rend = a.T;
-  const int64_t all_tiles = ceil_div(rend - key0, kBRows);
-  const int64_t tile_lo = (int64_t)chunk * a.chunk_tiles;
-  int64_t ntiles = all_tiles - tile_lo;
-  if (ntiles > a.chunk_tiles) ntiles = a.chunk_tiles;
-  if (ntiles < 0) ntiles = 0;
-  const int64_t nsteps = ntiles * NQ;
+  // this workgroup's query tiles, top first (none: no slot to write)
+  const TileRun run = tile_run(key0, a.T, a.window, a.chunk_tiles, a.slots, chunk);
+  if (run.n == 0) return;
+  const int64_t t_top = run.top;
+  const int64_t nsteps = run.n * NQ;
 
   // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
   // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
@@ -394,55 +441,61 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
   const _Float16* q_b = a.q + b * a.qsb + kvh * NQ * a.qsh;
   const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
   const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
+  // Every load of a step is unconditional (rows past the end read the step's
+  // first row, which is always in range) and the zero fill happens in
+  // store(): a select right after a load, or a load inside a branch, would
+  // make the wave wait for the whole prefetch where it is issued.
   struct StepRegs {
     half8 q0, q1, d0, d1;
     float l, x;
     int64_t pos;  // the q row's position (its trig row is read at store time)
+    bool ok, ok0, ok1, lok;
   };
+  const int lrow = tid < kBRows ? tid : 0;
   auto fetch = [&](int ft, int fh, StepRegs& r) {
-    const int64_t r0 = key0 + (tile_lo + ft) * kBRows;
+    const int64_t r0 = (t_top - ft) * kBRows;
     const int64_t row = r0 + qr;
-    const bool ok = row < a.T;
-    const _Float16* qrow = ok ? q_b + fh * a.qsh + r0 * a.qst + q_thr : a.q;
+    r.ok = row < a.T;
+    const _Float16* qrow = q_b + fh * a.qsh + r0 * a.qst + (r.ok ? q_thr : 8 * qp);
     r.q0 = *(const half8*)qrow;
     r.q1 = *(const half8*)(qrow + 64);
-    r.q0 = ok ? r.q0 : zero8;
-    r.q1 = ok ? r.q1 : zero8;
-    r.pos = p0 + (ok ? row : 0);
+    r.pos = p0 + (r.ok ? row : r0);
     const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
+    r.lok = tid < kBRows && r0 + tid < a.T;
+    const int64_t lr = r0 + (r.lok ? lrow : 0);
     if constexpr (DK) {
       // dO row qr, dims [8qp, +8) and [8qp + 64, +8), as the q rows
-      const _Float16* drow = ok ? dstep + (int64_t)qr * a.dst + 8 * qp : a.dout;
+      const _Float16* drow = dstep + (r.ok ? (int64_t)qr * a.dst : 0) + 8 * qp;
       r.d0 = *(const half8*)drow;
       r.d1 = *(const half8*)(drow + 64);
-      r.d0 = ok ? r.d0 : zero8;
-      r.d1 = ok ? r.d1 : zero8;
-      r.x = tid < kBRows && r0 + tid < a.T ? a.delta[(b * a.QH + kvh * NQ + fh) * a.T + r0 + tid] : 0.f;
+      r.x = a.delta[(b * a.QH + kvh * NQ + fh) * a.T + lr];
     } else {
-      const bool ok0 = r0 + 2 * drp < a.T, ok1 = r0 + 2 * drp + 1 < a.T;
-      r.d0 = ok0 ? *(const half8*)(dstep + d_thr0) : zero8;
-      r.d1 = ok1 ? *(const half8*)(dstep + d_thr1) : zero8;
+      r.ok0 = r0 + 2 * drp < a.T;
+      r.ok1 = r0 + 2 * drp + 1 < a.T;
+      r.d0 = *(const half8*)(dstep + (r.ok0 ? d_thr0 : 8 * ddb));
+      r.d1 = *(const half8*)(dstep + (r.ok1 ? d_thr1 : 8 * ddb));
     }
-    r.l = tid < kBRows && r0 + tid < a.T ? l_b[fh * a.T + r0 + tid] * 1.4426950408889634f : 0.f;
+    r.l = l_b[fh * a.T + lr];
   };
   auto store = [&](const StepRegs& r, int buf) {
     half8 cs, sn, r0, r1;
     load_trig8(rope_row(r.pos), 8 * qp, &cs, &sn);
-    rope16(r.q0, r.q1, cs, sn, &r0, &r1);
+    rope16(r.ok ? r.q0 : zero8, r.ok ? r.q1 : zero8, cs, sn, &r0, &r1);
     _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
     *(half8*)qd = r0;
     *(half8*)(qd + 64) = r1;
     if constexpr (DK) {
       _Float16* dd = d_lds[buf] + qr * kQStride + 8 * qp;
-      *(half8*)dd = r.d0;
-      *(half8*)(dd + 64) = r.d1;
-      if (tid < kBRows) x_lds[buf][tid] = r.x;
+      *(half8*)dd = r.ok ? r.d0 : zero8;
+      *(half8*)(dd + 64) = r.ok ? r.d1 : zero8;
+      if (tid < kBRows) x_lds[buf][tid] = r.lok ? r.x : 0.f;
     } else {
+      const half8 d0 = r.ok0 ? r.d0 : zero8, d1 = r.ok1 ? r.d1 : zero8;
       _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(r.d0, r.d1, e);
+      for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(d0, d1, e);
     }
-    if (tid < kBRows) l_lds[buf][tid] = r.l;
+    if (tid < kBRows) l_lds[buf][tid] = r.lok ? r.l * 1.4426950408889634f : 0.f;
   };
 
   // step s+1 waits in registers while s is computed and s+2 is in flight;
@@ -482,7 +535,7 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
       fetch(ft, fh, ahead);
       advance();
     }
-    const int64_t r0 = key0 + (tile_lo + ct) * kBRows;
+    const int64_t r0 = (t_top - ct) * kBRows;
     // does any row of the step see any of this wave's keys?
     const bool any = r0 + kBRows - 1 >= kw0 && r0 - (kw0 + 31) < a.window && kw0 < a.T;
     if (any) {
@@ -593,7 +646,6 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
   }
 
   // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
-  // (a chunk with no rows still writes its slot: zeros)
   float* out = a.dv + (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
@@ -871,15 +923,21 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
     }
 }
 
-// dV̂ = the sum of the chunks' partial slots, in chunk order
+// dV̂ (or dK̂) = the sum of the partial slots of the chunks that the key's
+// block meets, in chunk order.  Rows [*, T, 128] fp32, as float4.
 __global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dv, int64_t n4,
-                                                                int64_t slot4, int chunks) {
+                                                                int64_t slot4, int slots, int64_t T,
+                                                                int64_t window, int64_t per) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
-  float4 acc = ((const float4*)part)[i];
-  for (int c = 1; c < chunks; ++c) {
-    const float4 v = ((const float4*)part)[i + c * slot4];
+  const int64_t key = (i / (kBD / 4)) % T;
+  int64_t tf, tl;
+  block_tiles(key - key % kBKeys, T, window, &tf, &tl);
+  const int64_t c_lo = tf / per, c_hi = tl / per;
+  float4 acc = ((const float4*)part)[i + (c_lo % slots) * slot4];
+  for (int64_t c = c_lo + 1; c <= c_hi; ++c) {
+    const float4 v = ((const float4*)part)[i + (c % slots) * slot4];
     acc.x += v.x;
     acc.y += v.y;
     acc.z += v.z;
@@ -888,15 +946,19 @@ __global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __r
   ((float4*)dv)[i] = acc;
 }
 
-// query tiles per chunk and the number of chunks of the largest key block
-static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* chunks) {
+// Tiles per chunk and partial slots of the key-block kernels: chunks of 16
+// tiles, or of an eighth of the longest block's rows when that is more; the
+// slots are the most chunks one block meets.
+static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* slots) {
   int64_t rows = (int64_t)kBKeys - 1 + window;
   if (rows > T || rows < 0) rows = T;
-  const int64_t tiles = ceil_div(rows, kBRows) + 1;  // + 1: a block's rows start inside a tile row
+  const int64_t span = ceil_div(rows, kBRows);  // tiles of the longest block (blocks start on a tile)
   int64_t per = 16;
-  if (ceil_div(tiles, per) > 8) per = ceil_div(tiles, 8);
+  if (ceil_div(span, per) > 8) per = ceil_div(span, 8);
+  const int64_t all = ceil_div(ceil_div(T, kBRows), per);
+  const int64_t most = ceil_div(span - 1, per) + 1;
   *chunk_tiles = (int)per;
-  *chunks = (int)ceil_div(tiles, per);
+  *slots = (int)(all < most ? all : most);
 }
 
 }  // namespace jkv
@@ -941,6 +1003,7 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   int chunk_tiles, chunks;
   value_grad_chunks(T, a.window, &chunk_tiles, &chunks);
   a.chunk_tiles = chunk_tiles;
+  a.slots = chunks;
   const int64_t n = B * KVH * T * kBD;
   if (chunks > 1) {
     const int64_t need = (int64_t)chunks * n * (int64_t)sizeof(float);
@@ -967,7 +1030,7 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   if (chunks > 1) {
     const int64_t n4 = n / 4;
     hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
-                       (const float*)workspace, d_out_buf, n4, n4, chunks);
+                       (const float*)workspace, d_out_buf, n4, n4, chunks, T, a.window, (int64_t)chunk_tiles);
     JKV_CHECK_LAUNCH();
   }
   return JKV_OK;
@@ -1096,26 +1159,19 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
     qa.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
     qa.row_sets = 4 / qa.heads_per_wg;
     qa.head_groups = (int32_t)(NQ / qa.heads_per_wg);
-    // one run per row block: 32-row blocks are many, and the longest go first
-    const int chunks = 1;
+    // one run per row block (32-row blocks are many, and the longest go
+    // first), written straight to d_query, or to the slot area when only
+    // delta is wanted
     qa.g.chunk_tiles = 0x7fffffff;
     const int64_t n = B * QH * T * kBD;
-    JKV_CHECK_ARG(slot_bytes >= (int64_t)chunks * n * (int64_t)sizeof(float), "workspace too small");
-    const bool direct = chunks == 1 && d_query != nullptr;
-    qa.dq = direct ? d_query : (float*)slots;
-    qa.g.slot_stride = direct ? 0 : n;
+    JKV_CHECK_ARG(d_query != nullptr || slot_bytes >= n * (int64_t)sizeof(float), "workspace too small");
+    qa.dq = d_query != nullptr ? d_query : (float*)slots;
+    qa.g.slot_stride = 0;
     const int64_t nqb = ceil_div(T, 32 * (int64_t)qa.row_sets);
     const int64_t blocks = nqb * KVH * qa.head_groups * B;
     JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-    hipLaunchKernelGGL(prefill_q_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
-                       stream, qa);
+    hipLaunchKernelGGL(prefill_q_grad_kernel, dim3((uint32_t)blocks), dim3(kBThreads), 0, stream, qa);
     JKV_CHECK_LAUNCH();
-    if (!direct && d_query != nullptr) {
-      const int64_t n4 = n / 4;
-      hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
-                         (const float*)slots, d_query, n4, n4, chunks);
-      JKV_CHECK_LAUNCH();
-    }
   }
   if (d_key) {
     const int rc = launch_kv_grad<true>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream);

@@ -37,6 +37,7 @@ def _case(seed, batch, qh, kvh, tokens):
     (1, 4, 1, 1, (9,), 4096),           # one token
     (1, 8, 2, 600, (0,), 4096),         # key blocks' rows split in two runs (workspace + reduce)
     (1, 8, 2, 1030, (40,), 4096),       # three runs, ragged last tile
+    (1, 8, 2, 1500, (0,), 256),         # window binds over many tiles: blocks meet chunks that wrap the slots
 ])
 def test_lse_and_value_grad_match_oracle(device, batch, qh, kvh, tokens, starts, window):
     ws = int(_ops._lib.load().jkv_prefill_value_grad_workspace_bytes(batch, kvh, tokens, window))
@@ -82,6 +83,7 @@ def test_autograd_value_path(device):
     (1, 4, 2, 45, (3,), 4096),          # GQA 2
     (1, 16, 2, 96, (0,), 4096),         # GQA 8: two head groups per kv head
     (1, 8, 2, 600, (0,), 4096),         # rows and keys split in runs (workspace + reduce)
+    (1, 8, 2, 1500, (0,), 256),         # window binds over many tiles: chunks wrap the slots
 ])
 def test_full_backward_matches_oracle(device, batch, qh, kvh, tokens, starts, window):
     print(f"backward B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)

@@ -17,6 +17,8 @@
 // with an online softmax in fp32 (base-2 exponent, scale folded in).
 #include <math.h>
 
+#include <type_traits>
+
 #include "jkv_common.h"
 #include "rotary.h"
 
@@ -49,23 +51,25 @@ struct PrefillArgs {
   int32_t head_groups;   // NQ / HW
 };
 
+// max / sum of v over lanes l, l^16, l^32, l^48 (the four lane groups of one
+// MFMA row) with the gfx950 row-swap permutes: VALU only, no LDS round trip.
+// permlane16_swap(v, v) gives (v of the even row, v of the odd row) of each
+// row pair in every lane; permlane32_swap(v, v) the same for the two halves.
 __device__ __forceinline__ float lane_group_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float lane_group_sum(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// max(a, b, c) in one instruction; the scores are never NaN
-__device__ __forceinline__ float max3_f32(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
+// max(a, b, c); the compiler forms v_max3_f32 from it
+__device__ __forceinline__ float max3_f32(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 // (a[e], b[e]) as one 32-bit word
 __device__ __forceinline__ uint32_t pair16(half8 a, half8 b, int e) {
@@ -77,7 +81,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   __shared__ __align__(16) _Float16 k_lds[2][kKTile];
   __shared__ __align__(16) _Float16 v_lds[2][kVTile];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the tile tests below branch on it
   const int ln = lane & 15, lg = lane >> 4;
   const int HW = a.heads_per_wg, RS = a.row_sets;
   const int64_t block_rows = 32 * (int64_t)RS;
@@ -147,31 +152,50 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
 
   // Tile loaders.  K̂: thread -> key tid/8, 8-dim chunk pair (p, p+8), p =
   // tid%8, rotated before it is stored.  V̂: thread -> key pair tid%32, dims
-  // [8*(tid/32), +8), stored transposed as (key, key+1) words.
+  // [8*(tid/32), +8), stored transposed as (key, key+1) words.  Every load
+  // (the rotary rows too) is unconditional and its result untouched until
+  // store(), so the wave waits for a tile's loads only after the current
+  // tile's products: keys past T read the tile's first key (always in range)
+  // and the mask gives them weight 0.
   const int kk = tid >> 3, kpart = tid & 7;
   const int vkp = tid & 31, vdb = tid >> 5;
   struct TileRegs {
-    half8 k0, k1, v0, v1;
+    half8 k0, k1, v0, v1, cs, sn;
   };
+  // A tile's loads are a uniform base plus per-thread 32-bit offsets fixed
+  // for the whole walk (offsets within one (batch row, kv head) slice fit 32
+  // bits: host-checked); a key past T, or past the rotary table, takes the
+  // offset of the tile's last valid one.
+  const uint32_t k_off = (uint32_t)(kk * a.kst + 8 * kpart);
+  const uint32_t v_off0 = (uint32_t)(2 * vkp * a.vst + 8 * vdb), v_off1 = v_off0 + (uint32_t)a.vst;
+  const uint32_t t_off = (uint32_t)(kk * kRopeRow + 8 * kpart);
   auto fetch = [&](int64_t tile, TileRegs& r) {
-    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int64_t key = tile * kPKT + kk;
-    const bool ok = key < a.T;
-    const _Float16* kp = kbase + (ok ? key : 0) * a.kst + 8 * kpart;
-    r.k0 = ok ? *(const half8*)kp : zero;
-    r.k1 = ok ? *(const half8*)(kp + 64) : zero;
-    const int64_t vk0 = tile * kPKT + 2 * vkp;
-    const bool ok0 = vk0 < a.T, ok1 = vk0 + 1 < a.T;
-    const _Float16* vp = vbase + 8 * vdb;
-    r.v0 = ok0 ? *(const half8*)(vp + vk0 * a.vst) : zero;
-    r.v1 = ok1 ? *(const half8*)(vp + (vk0 + 1) * a.vst) : zero;
+    const int64_t first = tile * kPKT;  // < T for every tile walked
+    int64_t last = a.T - 1 - first;     // the tile's last valid key, relative
+    if (last > kPKT - 1) last = kPKT - 1;
+    int64_t pos = p0 + first;           // rotary row of the tile's first key
+    if (pos > a.rope_len - 1) pos = a.rope_len - 1;
+    if (pos < 0) pos = 0;
+    int64_t tlast = a.rope_len - 1 - pos;  // keys past it use the table's last row
+    if (tlast > last) tlast = last;
+    const _Float16* kt = kbase + first * a.kst;
+    const _Float16* vt = vbase + first * a.vst;
+    const _Float16* tt = a.rope + pos * kRopeRow;
+    const uint32_t lk = (uint32_t)last, lt = (uint32_t)tlast;
+    const uint32_t ko = (uint32_t)kk <= lk ? k_off : (uint32_t)(last * a.kst + 8 * kpart);
+    const uint32_t to = (uint32_t)kk <= lt ? t_off : (uint32_t)(tlast * kRopeRow + 8 * kpart);
+    r.k0 = *(const half8*)(kt + ko);
+    r.k1 = *(const half8*)(kt + ko + 64);
+    r.cs = *(const half8*)(tt + to);
+    r.sn = *(const half8*)(tt + to + 64);
+    const uint32_t vo0 = (uint32_t)(2 * vkp) <= lk ? v_off0 : (uint32_t)(8 * vdb);
+    const uint32_t vo1 = (uint32_t)(2 * vkp + 1) <= lk ? v_off1 : (uint32_t)(8 * vdb);
+    r.v0 = *(const half8*)(vt + vo0);
+    r.v1 = *(const half8*)(vt + vo1);
   };
-  auto store = [&](int64_t tile, const TileRegs& r, int buf) {
-    const int64_t key = tile * kPKT + kk;
-    const _Float16* tr = rope_row(p0 + (key < a.T ? key : 0));
-    half8 cs, sn, r0, r1;
-    load_trig8(tr, 8 * kpart, &cs, &sn);
-    rope16(r.k0, r.k1, cs, sn, &r0, &r1);
+  auto store = [&](const TileRegs& r, int buf) {
+    half8 r0, r1;
+    rope16(r.k0, r.k1, r.cs, r.sn, &r0, &r1);
     _Float16* kd = k_lds[buf] + kk * kKStride + 8 * kpart;
     *(half8*)kd = r0;
     *(half8*)(kd + 64) = r1;
@@ -183,7 +207,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   if (tile0 < tile1) {
     TileRegs r;
     fetch(tile0, r);
-    store(tile0, r, 0);
+    store(r, 0);
   }
   __syncthreads();
 
@@ -215,61 +239,77 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     // rescaled when some row's reference maximum moves ----
     const bool full = key0 + kPKT - 1 <= row0 && row0 + 31 - key0 < a.window && key0 + kPKT <= a.T;
     half8 pf[2][2];
+    float alpha[2];
+    // the whole softmax in two versions under one uniform branch, so that the
+    // unmasked tiles carry none of the mask's work or register copies
+    auto softmax = [&](auto masked_tag) {
+      constexpr bool masked = decltype(masked_tag)::value;
 #pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
-      float mx = -INFINITY;
-      if (full) {
-        // two new scores per v_max3_f32 (fmaxf chains compile to twice as
-        // many instructions: each MFMA result is canonicalised first)
+      for (int rg = 0; rg < 2; ++rg) {
+        float mx = -INFINITY;
+        if constexpr (!masked) {
+          // two new scores per v_max3_f32
 #pragma unroll
-        for (int kg = 0; kg < 4; ++kg) {
-          mx = max3_f32(mx, s[kg][rg][0], s[kg][rg][1]);
-          mx = max3_f32(mx, s[kg][rg][2], s[kg][rg][3]);
+          for (int kg = 0; kg < 4; ++kg) {
+            mx = max3_f32(mx, s[kg][rg][0], s[kg][rg][1]);
+            mx = max3_f32(mx, s[kg][rg][2], s[kg][rg][3]);
+          }
+        } else {
+          // row - key of element (kg, e) = d0 - 16 kg - e; key - key0 < keys_left
+          // (rows and keys < T < 2^31: host-checked)
+          const int d0 = (int)(row0 + 16 * rg + ln - key0) - 4 * lg;
+          const int keys_left = (int)(a.T - key0 < kPKT ? a.T - key0 : kPKT);
+          const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
+#pragma unroll
+          for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int diff = d0 - 16 * kg - e;
+              const bool vis = diff >= 0 && diff < win && 16 * kg + 4 * lg + e < keys_left;
+              const float v = vis ? s[kg][rg][e] : -INFINITY;
+              s[kg][rg][e] = v;
+              mx = fmaxf(mx, v);
+            }
         }
-      } else {
-        const int64_t qrow = row0 + 16 * rg + ln;
+        mx = lane_group_max(mx) * scale2;
+        // the reference maximum only moves when the row maximum passes it by
+        // more than 8 (so p < 2^8 and the output rescale is rare); o and l
+        // share it, so o / l is unchanged
+        const float m_new = mx > m[rg] + 8.f ? mx : m[rg];
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        alpha[rg] = __builtin_amdgcn_exp2f(m[rg] - m_use);
+        m[rg] = m_new;
+        float pr[16];
 #pragma unroll
         for (int kg = 0; kg < 4; ++kg)
 #pragma unroll
+          for (int e = 0; e < 4; ++e) pr[4 * kg + e] = __builtin_amdgcn_exp2f(fmaf(s[kg][rg][e], scale2, -m_use));
+        // the tile's row sum as a tree (four adds deep, not sixteen)
+        float t8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t8[i] = pr[2 * i] + pr[2 * i + 1];
+        const float psum = ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
+        l[rg] = l[rg] * alpha[rg] + psum;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int64_t key = key0 + 16 * kg + 4 * lg + e;
-            const int64_t diff = qrow - key;
-            const bool vis = diff >= 0 && diff < a.window && key < a.T;
-            const float v = vis ? s[kg][rg][e] : -INFINITY;
-            s[kg][rg][e] = v;
-            mx = fmaxf(mx, v);
+            pf[rg][kp][e] = (_Float16)pr[4 * (2 * kp) + e];
+            pf[rg][kp][e + 4] = (_Float16)pr[4 * (2 * kp + 1) + e];
           }
       }
-      mx = lane_group_max(mx) * scale2;
-      // the reference maximum only moves when the row maximum passes it by
-      // more than 8 (so p < 2^8 and the output rescale is rare); o and l
-      // share it, so o / l is unchanged
-      const float m_new = mx > m[rg] + 8.f ? mx : m[rg];
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m[rg] - m_use);
-      m[rg] = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int kg = 0; kg < 4; ++kg)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[kg][rg][e], scale2, -m_use));
-          s[kg][rg][e] = p;
-          psum += p;
-        }
-      l[rg] = l[rg] * alpha + psum;
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[rg][dt] *= alpha;
-      }
-#pragma unroll
-      for (int kp = 0; kp < 2; ++kp)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pf[rg][kp][e] = (_Float16)s[2 * kp][rg][e];
-          pf[rg][kp][e + 4] = (_Float16)s[2 * kp + 1][rg][e];
-        }
+    };
+    if (full) {
+      softmax(std::false_type{});
+    } else {
+      softmax(std::true_type{});
     }
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg)
+      if (__any(alpha[rg] != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[rg][dt] *= alpha[rg];
+      }
     // ---- Oᵀ += V̂ᵀ Pᵀ: contraction slot 8lg+e <-> key 32kp + 4lg + e (e < 4),
     //      32kp + 16 + 4lg + e - 4 (e >= 4) ----
 #pragma unroll
@@ -285,7 +325,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       }
     }
     // ---- the next tile into the other buffer ----
-    if (more) store(tile + 1, nxt, buf ^ 1);
+    if (more) store(nxt, buf ^ 1);
     __syncthreads();
   }
 
@@ -330,6 +370,8 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   const int64_t NQ = QH / KVH;
   JKV_CHECK_ARG((NQ & (NQ - 1)) == 0, "query heads per kv head must be a power of two");
   JKV_CHECK_ARG(window >= 1, "window must be positive");
+  JKV_CHECK_ARG(T < ((int64_t)1 << 31), "prefill chunk too long");
+  JKV_CHECK_ARG(T * (k_st > v_st ? k_st : v_st) < ((int64_t)1 << 31), "prefill K/V rows too far apart");
   if (B == 0 || T == 0) return JKV_OK;
   JKV_CHECK_ARG(q && k && v && out && start_positions && rope_table, "null buffer");
   JKV_CHECK_ARG(rope_len >= 1, "rotary table is empty");

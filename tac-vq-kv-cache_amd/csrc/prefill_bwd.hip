@@ -358,7 +358,8 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
   __shared__ __align__(16) float l_lds[2][kBRows];
   __shared__ __align__(16) float x_lds[2][kBRows];     // delta (DK)
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the step tests below branch on it
   const int ln = lane & 15, lg = lane >> 4;
   const int NQ = a.nq;
   const int64_t nkb = ceil_div(a.T, kBKeys);
@@ -583,30 +584,40 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
       const int keys_left = (int)(a.T - kw0 < 32 ? a.T - kw0 : 32);
       const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
       half8 pa[2];
+      auto make_p = [&](auto masked_tag) {
+        constexpr bool masked = decltype(masked_tag)::value;
 #pragma unroll
-      for (int rg = 0; rg < 2; ++rg) {
-        const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
-        const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
-        float x4[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (DK) {
-          const float4 d4 = *(const float4*)(&x_lds[buf][16 * rg + 4 * lg]);
-          x4[0] = d4.x; x4[1] = d4.y; x4[2] = d4.z; x4[3] = d4.w;
-        }
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
-            if (!full) {
-              const int diff = base + 16 * rg + e - 16 * kt;
-              const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
-                               16 * kt + ln < keys_left;
-              p = vis ? p : 0.f;
-            }
-            // DK: dS = P (dP - delta_row) in place of P
-            if constexpr (DK) p *= dpacc[rg][kt][e] - x4[e];
-            pa[kt][4 * rg + e] = (_Float16)p;
+        for (int rg = 0; rg < 2; ++rg) {
+          const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
+          const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
+          float x4[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (DK) {
+            const float4 d4 = *(const float4*)(&x_lds[buf][16 * rg + 4 * lg]);
+            x4[0] = d4.x; x4[1] = d4.y; x4[2] = d4.z; x4[3] = d4.w;
           }
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
+              if constexpr (masked) {
+                const int diff = base + 16 * rg + e - 16 * kt;
+                const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
+                                 16 * kt + ln < keys_left;
+                p = vis ? p : 0.f;
+              }
+              // DK: dS = P (dP - delta_row) in place of P
+              if constexpr (DK) p *= dpacc[rg][kt][e] - x4[e];
+              pa[kt][4 * rg + e] = (_Float16)p;
+            }
+        }
+      };
+      // a uniform branch: the steps away from the diagonal and the ends pay
+      // for no mask
+      if (full) {
+        make_p(std::false_type{});
+      } else {
+        make_p(std::true_type{});
       }
       // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
       // {16+4lg..16+4lg+3}.  DK: dK̂_rot += dSᵀ Q_rot, B = Q_rotᵀ from the
@@ -702,7 +713,8 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
   const ValueGradArgs& a = qa_.g;
   __shared__ __align__(16) _Float16 k_lds[2][kQKeys * kQStride];
   __shared__ __align__(16) _Float16 v_lds[2][kQKeys * kQStride];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the tile tests below branch on it
   const int ln = lane & 15, lg = lane >> 4;
   const int HW = qa_.heads_per_wg, RS = qa_.row_sets;
   const int NQ = a.nq;
@@ -792,25 +804,28 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
   const int kr = tid >> 3, kp = tid & 7;
   const _Float16* kb_ = a.k + b * a.ksb + kvh * a.ksh;
   const _Float16* vb_ = a.v + b * a.vsb + kvh * a.vsh;
+  // Every load of a tile (the rotary rows too) is unconditional and left
+  // untouched until store(): keys past T read the tile's first key (always in
+  // range; causality masks them for every row).  A select right after a load
+  // would make the wave wait for the whole prefetch where it is issued.
   struct TileRegs {
-    half8 k0, k1, v0, v1;
-    int64_t key;
+    half8 k0, k1, v0, v1, cs, sn;
   };
   auto fetch = [&](int64_t tile, TileRegs& r) {
-    const int64_t key = (t_first + tile_lo + tile) * kQKeys + kr;
-    const bool ok = key < a.T;
-    const _Float16* kp_ = kb_ + (ok ? key : 0) * a.kst + 8 * kp;
-    const _Float16* vp_ = vb_ + (ok ? key : 0) * a.vst + 8 * kp;
-    r.k0 = ok ? *(const half8*)kp_ : zero8;
-    r.k1 = ok ? *(const half8*)(kp_ + 64) : zero8;
-    r.v0 = ok ? *(const half8*)vp_ : zero8;
-    r.v1 = ok ? *(const half8*)(vp_ + 64) : zero8;
-    r.key = ok ? key : 0;
+    const int64_t first = (t_first + tile_lo + tile) * kQKeys;
+    const int64_t key = first + kr;
+    const int64_t kk_ = key < a.T ? key : first;
+    const _Float16* kp_ = kb_ + kk_ * a.kst + 8 * kp;
+    const _Float16* vp_ = vb_ + kk_ * a.vst + 8 * kp;
+    r.k0 = *(const half8*)kp_;
+    r.k1 = *(const half8*)(kp_ + 64);
+    r.v0 = *(const half8*)vp_;
+    r.v1 = *(const half8*)(vp_ + 64);
+    load_trig8(rope_row(p0 + kk_), 8 * kp, &r.cs, &r.sn);
   };
   auto store = [&](const TileRegs& r, int buf) {
-    half8 cs, sn, r0, r1;
-    load_trig8(rope_row(p0 + r.key), 8 * kp, &cs, &sn);
-    rope16(r.k0, r.k1, cs, sn, &r0, &r1);
+    half8 r0, r1;
+    rope16(r.k0, r.k1, r.cs, r.sn, &r0, &r1);
     _Float16* kd = k_lds[buf] + kr * kQStride + 8 * kp;
     *(half8*)kd = r0;
     *(half8*)(kd + 64) = r1;
@@ -864,20 +879,30 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
       const int base = (int)(row0 - key0) + ln - 4 * lg;  // row - key = base + 16rg - 16kt - e
       const int rows_left = (int)(a.T - row0 < 32 ? a.T - row0 : 32);
       half8 dsa[2];
+      auto make_ds = [&](auto masked_tag) {
+        constexpr bool masked = decltype(masked_tag)::value;
 #pragma unroll
-      for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < 2; ++rg)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(st[kt][rg][e], scale2, -l2[rg]));
-            if (!full) {
-              const int diff = base + 16 * rg - 16 * kt - e;
-              const bool vis = diff >= 0 && diff < win && 16 * rg + ln < rows_left;
-              p = vis ? p : 0.f;
+            for (int e = 0; e < 4; ++e) {
+              float p = __builtin_amdgcn_exp2f(fmaf(st[kt][rg][e], scale2, -l2[rg]));
+              if constexpr (masked) {
+                const int diff = base + 16 * rg - 16 * kt - e;
+                const bool vis = diff >= 0 && diff < win && 16 * rg + ln < rows_left;
+                p = vis ? p : 0.f;
+              }
+              dsa[rg][4 * kt + e] = (_Float16)(p * (dpt[kt][rg][e] - dl[rg]));
             }
-            dsa[rg][4 * kt + e] = (_Float16)(p * (dpt[kt][rg][e] - dl[rg]));
-          }
+      };
+      // a uniform branch: the tiles away from the diagonal and the ends pay
+      // for no mask
+      if (full) {
+        make_ds(std::false_type{});
+      } else {
+        make_ds(std::true_type{});
+      }
       // ---- dQ += dS K̂: B = K̂ in B order (keys {4lg+e, 16+4lg+e} of dim
       // 16dt + ln) from the identity MFMAs ----
 #pragma unroll

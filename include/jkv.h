@@ -309,6 +309,33 @@ int jkv_prefill_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           float* lse, jkv_stream_t stream);
 
 /*
+ * jkv_prefill_attention over a chunk given as codes: the same attention, with
+ * each K̂/V̂ tile rebuilt from uint8 codes while it loads (16-byte codeword
+ * gathers from the fp16 deployed tables, fp16 of the fp32 stage sum), so K̂
+ * and V̂ are never written to memory.  Replaces the decode-then-attend of the
+ * quantized prefill branch (experiments_followup_mistral/
+ * evaluate_mistral_longbench.py:101-111 with the codec's reconstruction of
+ * src/jointkv/closed_loop_vq.py:298-300); output and lse are bit-identical
+ * to jkv_rvq_decode at depth S followed by jkv_prefill_attention.
+ *   q        as for jkv_prefill_attention
+ *   k_codes, v_codes  uint8 [B,KVH,T,G,S] with byte strides (b, h, t) shared
+ *            by both, the (G,S) block contiguous; even strides and addresses
+ *   k_tables, v_tables  fp16 deployed tables [KVH*G][S][K][d] contiguous
+ *   G, d, S, K  16, 8, 1 or 2, 256 (other geometries: JKV_ENOTSUP, for the
+ *            jkv_rvq_decode + jkv_prefill_attention path)
+ *   start_positions, window, rope_table, rope_len, out, lse  as for
+ *            jkv_prefill_attention
+ */
+int jkv_prefill_attention_codes(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                int64_t q_stride_t, const uint8_t* k_codes, const uint8_t* v_codes,
+                                int64_t code_stride_b, int64_t code_stride_h, int64_t code_stride_t,
+                                const void* k_tables, const void* v_tables, int64_t B, int64_t QH,
+                                int64_t KVH, int64_t T, int64_t G, int64_t d, int64_t S, int64_t K,
+                                const int32_t* start_positions, int64_t window,
+                                const void* rope_table, int64_t rope_len, void* out, float* lse,
+                                jkv_stream_t stream);
+
+/*
  * Value gradient of jkv_prefill_attention: for every key s of the chunk,
  *   d_value[b,kvh,s,:] = sum over the kv head's query heads h and rows t of
  *                        P[b,h,t,s] * d_out[b,h,t,:]

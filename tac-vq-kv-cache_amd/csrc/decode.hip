@@ -3,32 +3,88 @@
 
 namespace jkv {
 
-// One thread per (row, group, dimension).  out[b,h,t,g*d+i] =
-// dtype( sum_{s<depth} fp32(fp16(C[h*G+g, s, code_s, i])) ), in stage order.
-template <int DT>
-__global__ __launch_bounds__(256) void rvq_decode_kernel(
-    const uint8_t* __restrict__ codes, int64_t cb, int64_t ch, int64_t ct, int64_t B,
-    int64_t H, int64_t T, int64_t G, int64_t d, const float* __restrict__ tables, int64_t S,
-    int64_t K, int32_t depth, void* __restrict__ out) {
-  const int64_t D = G * d;
-  const int64_t n = B * H * T * D;
-  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= n) return;
-  const int64_t col = idx % D;
-  const int64_t bht = idx / D;
-  const int64_t t = bht % T;
-  const int64_t bh = bht / T;
-  const int64_t h = bh % H;
-  const int64_t b = bh / H;
-  const int64_t g = col / d, i = col % d;
-  const uint8_t* cp = codes + b * cb + h * ch + t * ct + g * S;
-  const int64_t p = h * G + g;
-  float acc = 0.f;
-  for (int s = 0; s < depth; ++s) {
-    int64_t k = cp[s];
-    acc += deploy16(tables[((p * S + s) * K + k) * d + i]);
+struct RvqDecodeArgs {
+  const uint8_t* codes;
+  int64_t cb, ch, ct;  // code byte strides (b, h, t); the (G,S) block contiguous
+  int64_t BH, H;
+  int32_t T, G, d, S, K, depth;
+  const float* tables;  // [H*G][S][K][d] fp32 masters
+  void* out;            // [B,H,T,G*d] contiguous
+};
+
+// CW consecutive outputs from fp32 sums
+template <int DT, int CW>
+__device__ __forceinline__ void store_chunk(void* out, int64_t i, const float* v) {
+  if constexpr (CW == 1) {
+    Elem<DT>::store(out, i, v[0]);
+  } else if constexpr (DT == JKV_F16) {
+    typedef _Float16 hv __attribute__((ext_vector_type(CW)));
+    hv h;
+#pragma unroll
+    for (int e = 0; e < CW; ++e) h[e] = (_Float16)v[e];
+    *(hv*)((_Float16*)out + i) = h;
+  } else if constexpr (DT == JKV_F32) {
+#pragma unroll
+    for (int e = 0; e < CW; e += 4) *(float4*)((float*)out + i + e) = float4{v[e], v[e + 1], v[e + 2], v[e + 3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < CW; ++e) Elem<DT>::store(out, i + e, v[e]);
   }
-  Elem<DT>::store(out, idx, acc);
+}
+
+// One thread per (row, group): the group's code bytes, then per chunk of CW
+// dimensions each stage's codeword read as fp32 (16-byte loads for CW >= 4),
+// rounded to fp16 and back (the deployed table), summed in fp32 in stage
+// order and stored as CW consecutive outputs:
+//   out[b,h,t,g*d+i] = dtype( sum_{s<depth} fp32(fp16(C[h*G+g, s, code_s, i])) ).
+// Grid: x over the (row, group) items of one (batch, head) slice, y over the
+// slices.
+template <int DT, int CW>
+__global__ __launch_bounds__(256) void rvq_decode_kernel(RvqDecodeArgs a) {
+  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t n = (uint32_t)a.T * (uint32_t)a.G;
+  if (item >= n) return;
+  const uint32_t t = item / (uint32_t)a.G, g = item % (uint32_t)a.G;
+  const int64_t D = (int64_t)a.G * a.d;
+  for (int64_t bh = blockIdx.y; bh < a.BH; bh += gridDim.y) {
+    const int64_t b = bh / a.H, h = bh % a.H;
+    const uint8_t* cp = a.codes + b * a.cb + h * a.ch + t * a.ct + g * a.S;
+    const float* tab = a.tables + (h * a.G + g) * (int64_t)a.S * a.K * a.d;
+    const int64_t o = (bh * a.T + t) * D + (int64_t)g * a.d;
+    const int depth = a.depth;
+    for (int i = 0; i < a.d; i += CW) {
+      float acc[CW];
+#pragma unroll
+      for (int e = 0; e < CW; ++e) acc[e] = 0.f;
+      for (int s = 0; s < depth; ++s) {
+        const float* w = tab + ((int64_t)s * a.K + cp[s]) * a.d + i;
+        if constexpr (CW == 1) {
+          acc[0] += deploy16(w[0]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < CW; e += 4) {
+            const float4 x = *(const float4*)(w + e);
+            acc[e] += deploy16(x.x);
+            acc[e + 1] += deploy16(x.y);
+            acc[e + 2] += deploy16(x.z);
+            acc[e + 3] += deploy16(x.w);
+          }
+        }
+      }
+      store_chunk<DT, CW>(a.out, o + i, acc);
+    }
+  }
+}
+
+template <int DT>
+static void launch_decode(const RvqDecodeArgs& a, int cw, dim3 grid, hipStream_t stream) {
+  if (cw == 8) {
+    hipLaunchKernelGGL((rvq_decode_kernel<DT, 8>), grid, dim3(256), 0, stream, a);
+  } else if (cw == 4) {
+    hipLaunchKernelGGL((rvq_decode_kernel<DT, 4>), grid, dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((rvq_decode_kernel<DT, 1>), grid, dim3(256), 0, stream, a);
+  }
 }
 
 }  // namespace jkv
@@ -42,28 +98,31 @@ extern "C" int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b, int64
   JKV_CHECK_ARG(B >= 0 && H > 0 && T >= 0 && G > 0 && d > 0 && S > 0 && K > 0 && K <= 256,
                 "invalid decode geometry");
   JKV_CHECK_ARG(depth >= 1 && depth <= S, "decode depth outside the ladder");
+  JKV_CHECK_ARG(T * G < ((int64_t)1 << 31) && S <= 65536 && d <= 65536, "decode slice too large");
   const int64_t n = B * H * T * G * d;
   if (n == 0) return JKV_OK;
   JKV_CHECK_ARG(codes && tables && out, "null buffer");
-  dim3 grid((uint32_t)ceil_div(n, 256));
+  if (out_dtype != JKV_F16 && out_dtype != JKV_BF16 && out_dtype != JKV_F32)
+    return set_error(JKV_EINVAL, "unknown output dtype %d", out_dtype);
+  RvqDecodeArgs a;
+  a.codes = codes; a.cb = code_stride_b; a.ch = code_stride_h; a.ct = code_stride_t;
+  a.BH = B * H; a.H = H;
+  a.T = (int32_t)T; a.G = (int32_t)G; a.d = (int32_t)d; a.S = (int32_t)S; a.K = (int32_t)K; a.depth = depth;
+  a.tables = tables;
+  a.out = out;
+  // vector chunks when every table row and output chunk is 16-byte aligned
+  // (fp32 rows) and the output chunk is aligned to its own width
+  const size_t esize = out_dtype == JKV_F32 ? 4 : 2;
+  auto aligned = [&](int cw) {
+    return d % cw == 0 && (uintptr_t)tables % 16 == 0 && (uintptr_t)out % (cw * esize) == 0;
+  };
+  const int cw = aligned(8) ? 8 : aligned(4) ? 4 : 1;
+  const int64_t slices = B * H;
+  const dim3 grid((uint32_t)ceil_div(T * G, 256), (uint32_t)(slices < 65535 ? slices : 65535));
   switch (out_dtype) {
-    case JKV_F16:
-      hipLaunchKernelGGL(rvq_decode_kernel<JKV_F16>, grid, dim3(256), 0, stream, codes,
-                         code_stride_b, code_stride_h, code_stride_t, B, H, T, G, d, tables, S, K,
-                         depth, out);
-      break;
-    case JKV_BF16:
-      hipLaunchKernelGGL(rvq_decode_kernel<JKV_BF16>, grid, dim3(256), 0, stream, codes,
-                         code_stride_b, code_stride_h, code_stride_t, B, H, T, G, d, tables, S, K,
-                         depth, out);
-      break;
-    case JKV_F32:
-      hipLaunchKernelGGL(rvq_decode_kernel<JKV_F32>, grid, dim3(256), 0, stream, codes,
-                         code_stride_b, code_stride_h, code_stride_t, B, H, T, G, d, tables, S, K,
-                         depth, out);
-      break;
-    default:
-      return set_error(JKV_EINVAL, "unknown output dtype %d", out_dtype);
+    case JKV_F16: launch_decode<JKV_F16>(a, cw, grid, stream); break;
+    case JKV_BF16: launch_decode<JKV_BF16>(a, cw, grid, stream); break;
+    default: launch_decode<JKV_F32>(a, cw, grid, stream); break;
   }
   JKV_CHECK_LAUNCH();
   return JKV_OK;

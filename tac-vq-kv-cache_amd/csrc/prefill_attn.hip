@@ -49,7 +49,18 @@ struct PrefillArgs {
   int32_t heads_per_wg;  // HW: query heads per workgroup (min(NQ, 4))
   int32_t row_sets;      // 8 / HW: 32-row sets per head in a workgroup
   int32_t head_groups;   // NQ / HW
+  // codes instead of K̂/V̂ rows (prefill_attn_kernel<CS>, CS = stages): uint8
+  // records [B,KVH,T,16,CS] with byte strides and the fp16 deployed tables
+  // [KVH*16][CS][256][8]
+  const uint8_t* kc;
+  const uint8_t* vc;
+  int64_t csb, csh, cst;
+  const _Float16* kt16;
+  const _Float16* vt16;
 };
+
+static const int kPCodeGroups = 16;  // codes path: 16 groups of 8 dims, 256 codewords
+static const int kPCodewords = 256;
 
 // max / sum of v over lanes l, l^16, l^32, l^48 (the four lane groups of one
 // MFMA row) with the gfx950 row-swap permutes: VALU only, no LDS round trip.
@@ -77,6 +88,11 @@ __device__ __forceinline__ uint32_t pair16(half8 a, half8 b, int e) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// CS = 0: the chunk's fp16 K̂/V̂ rows.  CS = 1, 2: K̂/V̂ rebuilt from uint8
+// codes while each tile loads (codes -> 16-byte codeword gathers from the
+// L2-resident fp16 tables -> fp16 stage sum, the codec's reconstruction), so
+// K̂ and V̂ are never written to memory.
+template <int CS>
 __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
   __shared__ __align__(16) _Float16 k_lds[2][kKTile];
   __shared__ __align__(16) _Float16 v_lds[2][kVTile];
@@ -147,66 +163,133 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   if (kmin < 0) kmin = 0;
   const int64_t tile0 = kmin / kPKT;
   const int64_t tile1 = ceil_div(wg_row1, kPKT);
-  const _Float16* kbase = a.k + b * a.ksb + kvh * a.ksh;
-  const _Float16* vbase = a.v + b * a.vsb + kvh * a.vsh;
+  const _Float16* kbase = CS == 0 ? a.k + b * a.ksb + kvh * a.ksh : nullptr;
+  const _Float16* vbase = CS == 0 ? a.v + b * a.vsb + kvh * a.vsh : nullptr;
 
   // Tile loaders.  K̂: thread -> key tid/8, 8-dim chunk pair (p, p+8), p =
   // tid%8, rotated before it is stored.  V̂: thread -> key pair tid%32, dims
   // [8*(tid/32), +8), stored transposed as (key, key+1) words.  Every load
   // (the rotary rows too) is unconditional and its result untouched until
   // store(), so the wave waits for a tile's loads only after the current
-  // tile's products: keys past T read the tile's first key (always in range)
-  // and the mask gives them weight 0.
+  // tile's products: keys past T read a valid key of the tile (K̂ its last,
+  // V̂ its first) and the mask gives them weight 0.
   const int kk = tid >> 3, kpart = tid & 7;
   const int vkp = tid & 31, vdb = tid >> 5;
+  // rows: K̂ pair (p, p+8) and V̂ of two keys; codes: the stage words of the
+  // same dims (groups p and p + 8 for K̂, group tid/32 of both keys for V̂)
+  constexpr int NW = CS > 0 ? CS : 1;
   struct TileRegs {
-    half8 k0, k1, v0, v1, cs, sn;
+    half8 k[2][NW], v[2][NW], cs, sn;
+  };
+  // the code bytes of one tile's K̂ pair and V̂ keys (CS > 0): dword 0 holds
+  // groups p and p + 8 of key tid/8 (CS bytes each, at bytes 0 and 2), dword 1
+  // group tid/32 of keys 2(tid%32) and 2(tid%32) + 1
+  struct CodeRegs {
+    uint32_t kw, vw;
   };
   // A tile's loads are a uniform base plus per-thread 32-bit offsets fixed
   // for the whole walk (offsets within one (batch row, kv head) slice fit 32
   // bits: host-checked); a key past T, or past the rotary table, takes the
-  // offset of the tile's last valid one.
-  const uint32_t k_off = (uint32_t)(kk * a.kst + 8 * kpart);
-  const uint32_t v_off0 = (uint32_t)(2 * vkp * a.vst + 8 * vdb), v_off1 = v_off0 + (uint32_t)a.vst;
+  // offset of a valid one.
+  const int64_t rstride_k = CS > 0 ? a.cst : a.kst, rstride_v = CS > 0 ? a.cst : a.vst;
+  const uint32_t k_row = (uint32_t)(kk * rstride_k), v_row0 = (uint32_t)(2 * vkp * rstride_v),
+                 v_row1 = v_row0 + (uint32_t)rstride_v;
   const uint32_t t_off = (uint32_t)(kk * kRopeRow + 8 * kpart);
-  auto fetch = [&](int64_t tile, TileRegs& r) {
-    const int64_t first = tile * kPKT;  // < T for every tile walked
-    int64_t last = a.T - 1 - first;     // the tile's last valid key, relative
+  struct TileBase {
+    int64_t first;
+    uint32_t ko, vo0, vo1, to;  // row offsets (elements or bytes) of this thread's keys; rotary offset
+    const _Float16* tt;
+  };
+  auto tile_base = [&](int64_t tile) {
+    TileBase t;
+    t.first = tile * kPKT;               // < T for every tile walked
+    int64_t last = a.T - 1 - t.first;    // the tile's last valid key, relative
     if (last > kPKT - 1) last = kPKT - 1;
-    int64_t pos = p0 + first;           // rotary row of the tile's first key
+    int64_t pos = p0 + t.first;          // rotary row of the tile's first key
     if (pos > a.rope_len - 1) pos = a.rope_len - 1;
     if (pos < 0) pos = 0;
     int64_t tlast = a.rope_len - 1 - pos;  // keys past it use the table's last row
     if (tlast > last) tlast = last;
-    const _Float16* kt = kbase + first * a.kst;
-    const _Float16* vt = vbase + first * a.vst;
-    const _Float16* tt = a.rope + pos * kRopeRow;
     const uint32_t lk = (uint32_t)last, lt = (uint32_t)tlast;
-    const uint32_t ko = (uint32_t)kk <= lk ? k_off : (uint32_t)(last * a.kst + 8 * kpart);
-    const uint32_t to = (uint32_t)kk <= lt ? t_off : (uint32_t)(tlast * kRopeRow + 8 * kpart);
-    r.k0 = *(const half8*)(kt + ko);
-    r.k1 = *(const half8*)(kt + ko + 64);
-    r.cs = *(const half8*)(tt + to);
-    r.sn = *(const half8*)(tt + to + 64);
-    const uint32_t vo0 = (uint32_t)(2 * vkp) <= lk ? v_off0 : (uint32_t)(8 * vdb);
-    const uint32_t vo1 = (uint32_t)(2 * vkp + 1) <= lk ? v_off1 : (uint32_t)(8 * vdb);
-    r.v0 = *(const half8*)(vt + vo0);
-    r.v1 = *(const half8*)(vt + vo1);
+    t.ko = (uint32_t)kk <= lk ? k_row : (uint32_t)(last * rstride_k);
+    t.vo0 = (uint32_t)(2 * vkp) <= lk ? v_row0 : 0u;
+    t.vo1 = (uint32_t)(2 * vkp + 1) <= lk ? v_row1 : 0u;
+    t.to = (uint32_t)kk <= lt ? t_off : (uint32_t)(tlast * kRopeRow + 8 * kpart);
+    t.tt = a.rope + pos * kRopeRow;
+    return t;
+  };
+  // CS > 0: the code bytes of a tile (loaded a tile before its gathers)
+  const uint8_t* kcbase = CS > 0 ? a.kc + b * a.csb + kvh * a.csh : nullptr;
+  const uint8_t* vcbase = CS > 0 ? a.vc + b * a.csb + kvh * a.csh : nullptr;
+  auto load_codes = [&](int64_t tile, CodeRegs& c) {
+    if constexpr (CS > 0) {
+      const TileBase t = tile_base(tile);
+      const uint8_t* kr = kcbase + t.first * a.cst + t.ko;
+      const uint8_t* v0 = vcbase + t.first * a.cst + t.vo0 + vdb * CS;
+      const uint8_t* v1 = vcbase + t.first * a.cst + t.vo1 + vdb * CS;
+      if constexpr (CS == 2) {
+        c.kw = (uint32_t)*(const uint16_t*)(kr + 2 * kpart) | ((uint32_t)*(const uint16_t*)(kr + 2 * (kpart + 8)) << 16);
+        c.vw = (uint32_t)*(const uint16_t*)v0 | ((uint32_t)*(const uint16_t*)v1 << 16);
+      } else {
+        c.kw = (uint32_t)kr[kpart] | ((uint32_t)kr[kpart + 8] << 16);
+        c.vw = (uint32_t)*v0 | ((uint32_t)*v1 << 16);
+      }
+    }
+  };
+  const _Float16* ktab = CS > 0 ? a.kt16 + kvh * (int64_t)kPCodeGroups * NW * kPCodewords * 8 : nullptr;
+  const _Float16* vtab = CS > 0 ? a.vt16 + kvh * (int64_t)kPCodeGroups * NW * kPCodewords * 8 : nullptr;
+  auto word = [&](const _Float16* tab, int g, int st, uint32_t code) -> half8 {
+    return *(const half8*)(tab + ((g * NW + st) * kPCodewords + (int)code) * 8);
+  };
+  auto fetch = [&](int64_t tile, const CodeRegs& c, TileRegs& r) {
+    const TileBase t = tile_base(tile);
+    r.cs = *(const half8*)(t.tt + t.to);
+    r.sn = *(const half8*)(t.tt + t.to + 64);
+    if constexpr (CS == 0) {
+      const _Float16* kt = kbase + t.first * a.kst + 8 * kpart;
+      const _Float16* vt = vbase + t.first * a.vst + 8 * vdb;
+      r.k[0][0] = *(const half8*)(kt + t.ko);
+      r.k[1][0] = *(const half8*)(kt + t.ko + 64);
+      r.v[0][0] = *(const half8*)(vt + t.vo0);
+      r.v[1][0] = *(const half8*)(vt + t.vo1);
+    } else {
+#pragma unroll
+      for (int st = 0; st < CS; ++st) {
+        r.k[0][st] = word(ktab, kpart, st, (c.kw >> (8 * st)) & 0xffu);
+        r.k[1][st] = word(ktab, kpart + 8, st, (c.kw >> (16 + 8 * st)) & 0xffu);
+        r.v[0][st] = word(vtab, vdb, st, (c.vw >> (8 * st)) & 0xffu);
+        r.v[1][st] = word(vtab, vdb, st, (c.vw >> (16 + 8 * st)) & 0xffu);
+      }
+    }
   };
   auto store = [&](const TileRegs& r, int buf) {
+    // the codec's reconstruction: fp16 of the fp32 stage sum, which one fp16
+    // add gives for two stages
+    half8 k0 = r.k[0][0], k1 = r.k[1][0], v0 = r.v[0][0], v1 = r.v[1][0];
+    if constexpr (CS == 2) {
+      k0 = k0 + r.k[0][1];
+      k1 = k1 + r.k[1][1];
+      v0 = v0 + r.v[0][1];
+      v1 = v1 + r.v[1][1];
+    }
     half8 r0, r1;
-    rope16(r.k0, r.k1, r.cs, r.sn, &r0, &r1);
+    rope16(k0, k1, r.cs, r.sn, &r0, &r1);
     _Float16* kd = k_lds[buf] + kk * kKStride + 8 * kpart;
     *(half8*)kd = r0;
     *(half8*)(kd + 64) = r1;
     _Float16* vd = v_lds[buf] + (8 * vdb) * kVStride + 2 * vkp;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) *(uint32_t*)(vd + e * kVStride) = pair16(r.v0, r.v1, e);
+    for (int e = 0; e < 8; ++e) *(uint32_t*)(vd + e * kVStride) = pair16(v0, v1, e);
   };
 
+  // codes two tiles ahead, rows (or gathered words) one tile ahead
+  CodeRegs cn = {0u, 0u};
   if (tile0 < tile1) {
+    CodeRegs c0 = {0u, 0u};
+    load_codes(tile0, c0);
     TileRegs r;
-    fetch(tile0, r);
+    fetch(tile0, c0, r);
+    if (tile0 + 1 < tile1) load_codes(tile0 + 1, cn);
     store(r, 0);
   }
   __syncthreads();
@@ -216,7 +299,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     const int64_t key0 = tile * kPKT;
     const bool more = tile + 1 < tile1;
     TileRegs nxt;
-    if (more) fetch(tile + 1, nxt);
+    if (more) fetch(tile + 1, cn, nxt);
+    if (tile + 2 < tile1) load_codes(tile + 2, cn);
     const _Float16* kl = k_lds[buf];
     const _Float16* vl = v_lds[buf];
 
@@ -352,6 +436,37 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   }
 }
 
+// the fields and grid both entry points share; launches CS's kernel
+static int launch_prefill(PrefillArgs& a, int cs, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                          int64_t B, int64_t QH, int64_t KVH, int64_t T, const int32_t* start, int64_t window,
+                          const void* rope_table, int64_t rope_len, void* out, float* lse, hipStream_t stream) {
+  a.q = (const _Float16*)q; a.qsb = q_sb; a.qsh = q_sh; a.qst = q_st;
+  a.B = B; a.QH = QH; a.KVH = KVH; a.T = T;
+  a.start = start;
+  a.window = window;
+  a.rope = (const _Float16*)rope_table;
+  a.rope_len = rope_len;
+  a.out = (_Float16*)out;
+  a.lse = lse;
+  const int64_t NQ = QH / KVH;
+  a.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
+  a.row_sets = 8 / a.heads_per_wg;
+  a.head_groups = (int32_t)(NQ / a.heads_per_wg);
+  const int64_t nqb = ceil_div(T, 32 * (int64_t)a.row_sets);
+  const int64_t blocks = nqb * KVH * a.head_groups * B;
+  JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
+  const dim3 grid((uint32_t)blocks), block(kPThreads);
+  if (cs == 2) {
+    hipLaunchKernelGGL(prefill_attn_kernel<2>, grid, block, 0, stream, a);
+  } else if (cs == 1) {
+    hipLaunchKernelGGL(prefill_attn_kernel<1>, grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(prefill_attn_kernel<0>, grid, block, 0, stream, a);
+  }
+  JKV_CHECK_LAUNCH();
+  return JKV_OK;
+}
+
 }  // namespace jkv
 
 extern "C" {
@@ -381,25 +496,43 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   JKV_CHECK_ARG(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 == 0,
                 "prefill buffers must be 16-byte aligned");
   PrefillArgs a = {};
-  a.q = (const _Float16*)q; a.qsb = q_sb; a.qsh = q_sh; a.qst = q_st;
   a.k = (const _Float16*)k; a.ksb = k_sb; a.ksh = k_sh; a.kst = k_st;
   a.v = (const _Float16*)v; a.vsb = v_sb; a.vsh = v_sh; a.vst = v_st;
-  a.B = B; a.QH = QH; a.KVH = KVH; a.T = T;
-  a.start = start_positions;
-  a.window = window;
-  a.rope = (const _Float16*)rope_table;
-  a.rope_len = rope_len;
-  a.out = (_Float16*)out;
-  a.lse = lse;
-  a.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
-  a.row_sets = 8 / a.heads_per_wg;
-  a.head_groups = (int32_t)(NQ / a.heads_per_wg);
-  const int64_t nqb = ceil_div(T, 32 * (int64_t)a.row_sets);
-  const int64_t blocks = nqb * KVH * a.head_groups * B;
-  JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-  hipLaunchKernelGGL(prefill_attn_kernel, dim3((uint32_t)blocks), dim3(kPThreads), 0, stream, a);
-  JKV_CHECK_LAUNCH();
-  return JKV_OK;
+  return launch_prefill(a, 0, q, q_sb, q_sh, q_st, B, QH, KVH, T, start_positions, window, rope_table, rope_len,
+                        out, lse, stream);
+}
+
+int jkv_prefill_attention_codes(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const uint8_t* k_codes,
+                                const uint8_t* v_codes, int64_t code_sb, int64_t code_sh, int64_t code_st,
+                                const void* k_tables, const void* v_tables, int64_t B, int64_t QH, int64_t KVH,
+                                int64_t T, int64_t G, int64_t d, int64_t S, int64_t K,
+                                const int32_t* start_positions, int64_t window, const void* rope_table,
+                                int64_t rope_len, void* out, float* lse, jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
+  if (G != kPCodeGroups || d != 8 || (S != 1 && S != 2) || K != kPCodewords)
+    return set_error(JKV_ENOTSUP, "prefill from codes needs 16 groups of 8 dims, 1-2 stages and 256 codewords");
+  const int64_t NQ = QH / KVH;
+  JKV_CHECK_ARG((NQ & (NQ - 1)) == 0, "query heads per kv head must be a power of two");
+  JKV_CHECK_ARG(window >= 1, "window must be positive");
+  JKV_CHECK_ARG(T < ((int64_t)1 << 31), "prefill chunk too long");
+  JKV_CHECK_ARG(code_st >= G * S && T * code_st < ((int64_t)1 << 31), "code records overlap or lie too far apart");
+  if (B == 0 || T == 0) return JKV_OK;
+  JKV_CHECK_ARG(q && k_codes && v_codes && k_tables && v_tables && out && start_positions && rope_table,
+                "null buffer");
+  JKV_CHECK_ARG(rope_len >= 1, "rotary table is empty");
+  JKV_CHECK_ARG(q_sb % 8 == 0 && q_sh % 8 == 0 && q_st % 8 == 0, "prefill strides must be multiples of 8 elements");
+  JKV_CHECK_ARG(code_sb % 2 == 0 && code_sh % 2 == 0 && code_st % 2 == 0 && ((uintptr_t)k_codes % 2 == 0) &&
+                    ((uintptr_t)v_codes % 2 == 0),
+                "code records must be 2-byte aligned");
+  JKV_CHECK_ARG(((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_tables | (uintptr_t)v_tables) % 16 == 0,
+                "prefill buffers must be 16-byte aligned");
+  PrefillArgs a = {};
+  a.kc = k_codes; a.vc = v_codes; a.csb = code_sb; a.csh = code_sh; a.cst = code_st;
+  a.kt16 = (const _Float16*)k_tables; a.vt16 = (const _Float16*)v_tables;
+  return launch_prefill(a, (int)S, q, q_sb, q_sh, q_st, B, QH, KVH, T, start_positions, window, rope_table,
+                        rope_len, out, lse, stream);
 }
 
 }  // extern "C"

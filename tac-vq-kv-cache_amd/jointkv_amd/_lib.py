@@ -90,6 +90,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp],
     ),
+    "jkv_prefill_attention_codes": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp],
+    ),
     "jkv_prefill_attention_value_grad": (
         ctypes.c_int,
         [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,

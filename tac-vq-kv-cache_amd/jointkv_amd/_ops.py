@@ -543,6 +543,84 @@ def prefill_attention(
     return out
 
 
+PREFILL_CODE_GEOMETRY = (16, 8, (1, 2), 256)  # groups, group dim, stages, codewords of the fused path
+
+
+def prefill_codes_supported(key_codes: torch.Tensor, key_tables16: torch.Tensor) -> bool:
+    """Whether ``jkv_prefill_attention_codes`` takes this code geometry."""
+
+    groups, d, stages, clusters = PREFILL_CODE_GEOMETRY
+    return (key_codes.ndim == 5 and int(key_codes.shape[3]) == groups and int(key_codes.shape[4]) in stages
+            and key_tables16.ndim == 4 and int(key_tables16.shape[2]) == clusters
+            and int(key_tables16.shape[3]) == d)
+
+
+def prefill_attention_codes(
+    q: torch.Tensor,
+    key_codes: torch.Tensor,
+    value_codes: torch.Tensor,
+    key_tables16: torch.Tensor,
+    value_tables16: torch.Tensor,
+    start_positions: torch.Tensor,
+    *,
+    window: int,
+    rope_theta: float,
+    max_position: int,
+    lse: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`prefill_attention` over uint8 codes ``[B,KVH,T,16,S]`` (S 1 or
+    2) and fp16 deployed tables ``[KVH*16,S,256,8]``, K̂/V̂ rebuilt inside
+    the attention kernel.  Bit-identical to :func:`rvq_decode` at depth S
+    followed by :func:`prefill_attention`."""
+
+    device = _lib.require_device(q, key_codes, value_codes, key_tables16, value_tables16, start_positions)
+    if key_codes.shape != value_codes.shape or key_codes.dtype != torch.uint8 or value_codes.dtype != torch.uint8:
+        raise ValueError("key/value codes must be uint8 of one geometry")
+    if key_tables16.shape != value_tables16.shape or not prefill_codes_supported(key_codes, key_tables16):
+        raise ValueError("prefill from codes needs [B,KVH,T,16,S<=2] codes and [KVH*16,S,256,8] tables")
+    if q.dtype != torch.float16 or q.ndim != 4 or q.shape[-1] != 128 or q.stride(-1) != 1:
+        raise ValueError("prefill query must be fp16 [B,H,T,128] with a contiguous last axis")
+    batch, qheads, tokens, _dim = map(int, q.shape)
+    _b, kvheads, _t, groups, stages = map(int, key_codes.shape)
+    if (_b, _t) != (batch, tokens) or qheads % kvheads:
+        raise ValueError("prefill query/key/value geometry differs")
+    if tuple(key_tables16.shape[:2]) != (kvheads * groups, stages):
+        raise ValueError("code and table geometry differs")
+    if start_positions.dtype != torch.int32 or start_positions.shape != (batch,):
+        raise ValueError("start_positions must be int32 [B]")
+    start_positions = start_positions.contiguous()
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape != (batch, qheads, tokens)
+                            or not lse.is_contiguous() or lse.device != q.device):
+        raise ValueError("lse must be a contiguous fp32 [B,QH,T] tensor on the query's device")
+    if any(st % 8 for st in q.stride()[:3]) or q.data_ptr() % 16:
+        q = q.contiguous()
+    codes = []
+    for c in (key_codes, value_codes):
+        if (c.stride(-1) != 1 or c.stride(-2) != stages or c.stride() != key_codes.stride()
+                or any(st % 2 for st in c.stride()[:3]) or c.data_ptr() % 2):
+            c = c.contiguous()
+        codes.append(c)
+    if codes[0].stride() != codes[1].stride():
+        codes = [c.contiguous() for c in codes]
+    tables = []
+    for t in (key_tables16, value_tables16):
+        t = t.detach()
+        if t.dtype != torch.float16 or not t.is_contiguous() or t.data_ptr() % 16:
+            t = t.to(torch.float16).contiguous()
+        tables.append(t)
+    table = rope_table(device, rope_theta, int(max_position) + 1)
+    out = torch.empty((batch, qheads, tokens, 128), dtype=torch.float16, device=device)
+    kc, vc = codes
+    code = _lib.load().jkv_prefill_attention_codes(
+        q.data_ptr(), *q.stride()[:3], kc.data_ptr(), vc.data_ptr(), *kc.stride()[:3], tables[0].data_ptr(),
+        tables[1].data_ptr(), batch, qheads, kvheads, tokens, groups, 8, stages, 256,
+        start_positions.data_ptr(), int(window), table.data_ptr(), int(table.shape[0]),
+        out.data_ptr(), lse.data_ptr() if lse is not None else None, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return out
+
+
 def prefill_attention_backward(
     q: torch.Tensor,
     key: torch.Tensor,

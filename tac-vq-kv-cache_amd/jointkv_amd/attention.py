@@ -210,14 +210,28 @@ def prefill_attention_from_codes(
     *,
     window: int = MISTRAL_WINDOW,
     rope_theta: float = MISTRAL_ROPE_THETA,
+    fused: bool = False,
 ) -> torch.Tensor:
     """:func:`prefill_attention` for a chunk given as uint8 codes.
 
     ``key_codes``/``value_codes`` ``[B,KVH,T,G,S]`` and fp16 deployed tables
-    ``[KVH*G,S,K,d]``: K̂/V̂ are rebuilt once (fp16 of the fp32 stage sum,
-    the codec's reconstruction) and then attended.
+    ``[KVH*G,S,K,d]``; K̂/V̂ are the codec's reconstruction (fp16 of the fp32
+    stage sum).  By default K̂/V̂ are decoded once into fp16 buffers and then
+    attended.  ``fused=True`` (GSRQ geometries: 16 groups of 8 dims, 256
+    codewords, one or two stages) rebuilds each K̂/V̂ tile inside the
+    attention kernel as it loads it, so no K̂/V̂ buffer exists; every query
+    block then rebuilds the tiles it reads, which makes it the slower of the
+    two (about even at 128-token chunks, 1.45x at 2048).  Both give the same
+    bits.
     """
 
+    if fused:
+        if not _ops.prefill_codes_supported(key_codes, key_tables16):
+            raise ValueError("the fused prefill needs [B,KVH,T,16,S<=2] codes and [KVH*16,S,256,8] tables")
+        batch, _qh, tokens, _d = map(int, query.shape)
+        starts, top = _start_tensor(start_positions, batch, tokens, query.device)
+        return _ops.prefill_attention_codes(query, key_codes, value_codes, key_tables16, value_tables16, starts,
+                                            window=window, rope_theta=rope_theta, max_position=top)
     stages = int(key_codes.shape[-1])
     khat = _ops.rvq_decode(key_codes, key_tables16.float(), depth=stages, dtype=torch.float16)
     vhat = _ops.rvq_decode(value_codes, value_tables16.float(), depth=stages, dtype=torch.float16)

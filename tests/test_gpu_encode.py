@@ -207,6 +207,31 @@ def test_inputs_are_not_mutated(device):
     assert torch.equal(states, s0) and torch.equal(tables, t0)
 
 
+@pytest.mark.parametrize("heads,groups,d,stages,depth,clusters,dtype,cap", [
+    (2, 16, 8, 2, 2, 256, torch.float16, None),   # GSRQ-2: one 16-byte output per group
+    (2, 16, 8, 2, 1, 256, torch.bfloat16, 40),    # first stage only, codes as a code-cache slice
+    (1, 8, 16, 3, 3, 64, torch.float32, None),    # two 8-wide chunks per group, fp32 out
+    (2, 4, 4, 2, 2, 16, torch.float16, None),     # 4-wide chunks
+    (1, 5, 3, 2, 2, 7, torch.float32, None),      # odd width: one output at a time
+])
+def test_rvq_decode_matches_oracle(device, heads, groups, d, stages, depth, clusters, dtype, cap):
+    # the frozen-code decode, bit for bit: fp32 sum of the fp16-deployed
+    # words in stage order, one cast at the end
+    print(f"rvq_decode H={heads} G={groups} d={d} S={stages} depth={depth} K={clusters} {dtype} cap={cap}",
+          flush=True)
+    gen = _gen(4242 + d)
+    batch, tokens = 2, 33
+    tables = ref.synthetic_tables(gen, (heads * groups, stages, clusters, d), (1.0, 0.5, 0.25)[:stages],
+                                  stage_axis=1)
+    # fp32 masters off the fp16 grid, so that the deploy rounding matters
+    tables = tables + 1e-3 * torch.randn(tables.shape, generator=gen)
+    codes = torch.randint(0, clusters, (batch, heads, cap or tokens, groups, stages), generator=gen,
+                          dtype=torch.uint8)[:, :, :tokens]
+    got = jkv.closed_loop_vq._ops.rvq_decode(codes.to(device), tables.to(device), depth=depth, dtype=dtype)
+    want = ref.frozen_decode(codes.contiguous(), tables, depth, dtype)
+    assert got.dtype == dtype and torch.equal(got.cpu(), want)
+
+
 def test_full_size_layer_properties(device):
     # BASELINE config 2 at full per-layer size: [1,8,8192,128], G2 tables.
     gen = _gen(8601)

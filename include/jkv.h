@@ -4,7 +4,8 @@
  * Every entry point is `extern "C"`, takes plain device pointers, element
  * counts and strides, enqueues its work on the caller's HIP stream and never
  * synchronises the host.  The caller owns every device buffer (outputs and
- * workspaces included); the library keeps no device state between calls.
+ * workspaces included); the library keeps no device state between calls,
+ * apart from the static scratch array of jkv_decode_attention_noalloc.
  * Return value: JKV_OK (0) or a negative JKV_E* code; jkv_last_error() then
  * returns a thread-local message.
  *
@@ -469,6 +470,44 @@ int jkv_pair_block_select(const float* states, float* recon, int64_t n_recon,
                           const int64_t* second_shortlist, int64_t L,
                           int64_t* first_out, int64_t* second_out,
                           jkv_stream_t stream);
+
+/*
+ * Per-codeword sums of one k-means update of the offline gain-shape parent
+ * fitting: replaces the index_add_ calls of `fit_residual_stages`
+ * (experiments/build_frozen_gsrq_multi_exit.py:547-606).  For every head h
+ * and codeword k, over the rows n with indices[h,n] = k, in row order:
+ *   raw_sums[h,k,:]     = sum w[h,n] * x[h,n,:]
+ *   shape_sums[h,k,:]   = sum (x[h,n,:] / max(|x[h,n,:]|, 1e-8)) * w[h,n]
+ *                         (only when with_shapes)
+ *   denominators[h,k]   = sum w[h,n]
+ * with w = 1 when weights is NULL (the products are then skipped, so the
+ * raw sums are the plain row sums).
+ *   rows [H,N,D] fp32 (D in 1..128), indices [H,N] int64, weights [H,N] fp32
+ *   or NULL; outputs [H,K,D], [H,K,D], [H,K] fp32 contiguous (overwritten).
+ *   workspace  jkv_gain_shape_sums_workspace_bytes() bytes (may be NULL when
+ *            that is 0): row slices write partial sums that a second kernel
+ *            adds in slice order, so the sums do not depend on scheduling.
+ * Rows whose index lies outside [0, K) are skipped.
+ */
+int jkv_gain_shape_sums(const float* rows, int64_t H, int64_t N, int64_t D,
+                        const int64_t* indices, const float* weights, int64_t K,
+                        int32_t with_shapes, float* shape_sums, float* raw_sums,
+                        float* denominators, void* workspace,
+                        int64_t workspace_bytes, jkv_stream_t stream);
+
+/* Workspace of jkv_gain_shape_sums for this geometry (bytes). */
+int64_t jkv_gain_shape_sums_workspace_bytes(int64_t H, int64_t N, int64_t D,
+                                            int64_t K, int32_t with_shapes);
+
+/*
+ * residual[h,n,:] -= tables[h, indices[h,n], :] in place (fp32; residual
+ * [H,N,D], tables [H,K,D], indices [H,N] int64; rows with an index outside
+ * [0, K) are left unchanged): the per-stage residual update of
+ * `fit_residual_stages` (build_frozen_gsrq_multi_exit.py:617-628).
+ */
+int jkv_subtract_codewords(float* residual, int64_t H, int64_t N, int64_t D,
+                           const float* tables, int64_t K,
+                           const int64_t* indices, jkv_stream_t stream);
 
 /*
  * Rotary table for head_dim 128, fp16 [n_pos][2][64] (per position the cos of

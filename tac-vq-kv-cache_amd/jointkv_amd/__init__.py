@@ -36,6 +36,7 @@ from .closed_loop_vq import (
     hard_residual_vq_exits,
 )
 from .cq_tac import ClosedLoopGroupedCQ, hard_grouped_cq
+from .gain_shape import fit_residual_stages
 from .packed_nested import (
     PackedLayoutLedger,
     PackedNestedKVCache,
@@ -56,6 +57,7 @@ from .v_only import ClosedLoopRunContext, DecoderStack, causal_loss, run_loss, v
 __all__ = [
     "multi_exit_additive_block_refinement",
     "multi_exit_additive_coordinate_refinement",
+    "fit_residual_stages",
     "AttentionWeights",
     "artifacts",
     "causal_loss",

@@ -45,6 +45,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "jkv_nearest_f32": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "jkv_nearest_topk_f32": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "jkv_gain_shape_sums": (
+        ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "jkv_gain_shape_sums_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i32]),
+    "jkv_subtract_codewords": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "jkv_rvq_decode": (
         ctypes.c_int,
         [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i32,

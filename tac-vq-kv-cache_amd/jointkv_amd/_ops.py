@@ -184,6 +184,52 @@ def nearest_topk_f32(states: torch.Tensor, tables: torch.Tensor, candidates: int
     return out
 
 
+def gain_shape_sums(rows: torch.Tensor, indices: torch.Tensor, clusters: int, *,
+                    weights: torch.Tensor | None = None, with_shapes: bool = True):
+    """Per-codeword sums of ``rows[H,N,D]`` fp32 under ``indices[H,N]``:
+    ``(shape_sums or None, raw_sums, denominators)``, ``[H,K,D]``, ``[H,K,D]``
+    and ``[H,K]`` fp32 (see ``jkv_gain_shape_sums``)."""
+
+    device = _lib.require_device(rows, indices, weights)
+    if rows.ndim != 3 or indices.shape != rows.shape[:2]:
+        raise ValueError("gain-shape rows/indices must be [H,N,D]/[H,N]")
+    heads, tokens, dim = map(int, rows.shape)
+    rows = rows.detach().float().contiguous()
+    indices = indices.to(torch.int64).contiguous()
+    if weights is not None:
+        if weights.shape != (heads, tokens):
+            raise ValueError("gain-shape weights must be [H,N]")
+        weights = weights.detach().float().contiguous()
+    shape = torch.empty((heads, clusters, dim), dtype=torch.float32, device=device) if with_shapes else None
+    raw = torch.empty((heads, clusters, dim), dtype=torch.float32, device=device)
+    den = torch.empty((heads, clusters), dtype=torch.float32, device=device)
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_gain_shape_sums_workspace_bytes(heads, tokens, dim, clusters, int(with_shapes)))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    _lib.check(lib.jkv_gain_shape_sums(
+        rows.data_ptr(), heads, tokens, dim, indices.data_ptr(), _lib.ptr(weights), int(clusters),
+        int(with_shapes), _lib.ptr(shape), raw.data_ptr(), den.data_ptr(), _lib.ptr(workspace), ws_bytes,
+        _lib.stream_handle(device)))
+    return shape, raw, den
+
+
+def subtract_codewords(residual: torch.Tensor, tables: torch.Tensor, indices: torch.Tensor) -> None:
+    """``residual[h,n,:] -= tables[h, indices[h,n], :]`` in place (fp32
+    contiguous ``[H,N,D]``; ``tables[H,K,D]``, ``indices[H,N]``)."""
+
+    device = _lib.require_device(residual, tables, indices)
+    if (residual.dtype != torch.float32 or not residual.is_contiguous() or residual.ndim != 3
+            or tables.ndim != 3 or indices.shape != residual.shape[:2]
+            or tables.shape[0] != residual.shape[0] or tables.shape[2] != residual.shape[2]):
+        raise ValueError("residual must be contiguous fp32 [H,N,D] with tables [H,K,D] and indices [H,N]")
+    heads, tokens, dim = map(int, residual.shape)
+    tables = tables.detach().float().contiguous()
+    indices = indices.to(torch.int64).contiguous()
+    _lib.check(_lib.load().jkv_subtract_codewords(
+        residual.data_ptr(), heads, tokens, dim, tables.data_ptr(), int(tables.shape[1]), indices.data_ptr(),
+        _lib.stream_handle(device)))
+
+
 def rvq_decode(
     codes: torch.Tensor,
     tables: torch.Tensor,

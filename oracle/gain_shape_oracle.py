@@ -212,3 +212,35 @@ def fit_residual_stages(residual, seed_rows, *, stages, whitener=None, selector_
             "gradient_weighted": int(weights is not None),
         })
     return np.stack(tables, axis=1), history, smallest
+
+
+def parent_residuals(states, tables, whitener, depth):
+    """The frozen parent's residuals at exit ``depth``
+    (build_frozen_gsrq_multi_exit.py:661-738): states [B,H,T,D], tables
+    [H,S,K,D] (deployed values), whitener [H,D,D] or None.  Returns (raw
+    residual [H,B*T,D] fp32, selector residual or None, reconstruction
+    [B,H,T,D] fp32, smallest relative search margin)."""
+
+    x = np.asarray(states, dtype=np.float32)
+    batch, heads, tokens, dim = x.shape
+    raw = np.ascontiguousarray(x.transpose(1, 0, 2, 3).reshape(heads, batch * tokens, dim))
+    decoded = np.zeros_like(raw)
+    tabs = np.asarray(tables, dtype=np.float32)[:, :depth]
+    sel = sel_tabs = None
+    if whitener is not None:
+        w = np.asarray(whitener, dtype=np.float64)
+        sel = np.einsum("hde,hne->hnd", w, raw.astype(np.float64)).astype(np.float32)
+        sel_tabs = np.einsum("hske,hde->hskd", tabs.astype(np.float64), w).astype(np.float32)
+    smallest = np.inf
+    for stage in range(depth):
+        for h in range(heads):
+            search = raw[h] if sel is None else sel[h]
+            table = tabs[h, stage] if sel is None else sel_tabs[h, stage]
+            idx, gap = nearest_with_margin(search, table)
+            smallest = min(smallest, float(gap.min()))
+            decoded[h] += tabs[h, stage][idx]
+            raw[h] -= tabs[h, stage][idx]
+            if sel is not None:
+                sel[h] -= sel_tabs[h, stage][idx]
+    recon = decoded.reshape(heads, batch, tokens, dim).transpose(1, 0, 2, 3)
+    return raw, sel, recon, smallest

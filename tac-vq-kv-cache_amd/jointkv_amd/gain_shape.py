@@ -1,9 +1,10 @@
 """Offline gain-shape k-means parent fitting on gfx950 kernels.
 
-Drop-in for ``nearest_indices`` and ``fit_residual_stages`` of
-``experiments/build_frozen_gsrq_multi_exit.py`` (:364-397, :400-657): the
-residual stages that extend a frozen parent codec, fitted in the parent's
-deployed metric.
+Drop-in for ``nearest_indices``, ``fit_residual_stages`` and
+``parent_residuals_and_reconstruction`` of
+``experiments/build_frozen_gsrq_multi_exit.py`` (:364-397, :400-657,
+:661-738): the residual stages that extend a frozen parent codec, fitted in
+the parent's deployed metric, and the parent's residuals they start from.
 
 Each stage keeps, per head, K codewords as a non-negative gain times a unit
 shape (``fit_mode="gskm"``) or as plain Lloyd means (``"lloyd"``).  A Lloyd
@@ -71,6 +72,54 @@ def nearest_indices(
         states = torch.matmul(states, wt)
         centroids = torch.matmul(centroids, wt)
     return _ops.nearest_f32(states, centroids)
+
+
+@torch.no_grad()
+def parent_residuals_and_reconstruction(
+    states: torch.Tensor,
+    tables: torch.Tensor,
+    whitener: torch.Tensor | None,
+    *,
+    depth: int,
+    token_chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor]:
+    """The frozen parent's exact residuals at exit ``depth``
+    (build_frozen_gsrq_multi_exit.py:661-738).
+
+    ``states[B,H,T,D]``, parent ``tables[H,S,K,D]`` (deployed values),
+    ``whitener[H,D,D]`` or None.  Greedy stage by stage: nearest (selector)
+    codeword of the residual, whose raw word is subtracted from the raw
+    residual and added to the reconstruction (and whose selector word is
+    subtracted from the selector residual).  Returns the raw residual
+    ``[H,B*T,D]`` fp32, the selector residual (or None) and the
+    reconstruction ``[B,H,T,D]`` in the states' dtype.
+    """
+
+    batch, heads, tokens, dimension = states.shape
+    _check_chunk(token_chunk_size)
+    flat = states.permute(1, 0, 2, 3).reshape(heads, batch * tokens, dimension).float()
+    raw_residual = flat.clone()
+    negated = torch.zeros_like(raw_residual)  # minus the reconstruction: exact negation of the running sum
+    selector_residual = None
+    raw_tables = tables[:, :depth].to(device=states.device, dtype=torch.float32)
+    selector_tables = raw_tables
+    if whitener is not None:
+        w = whitener.to(device=states.device, dtype=torch.float32)
+        wt = w.transpose(-1, -2).contiguous()
+        selector_residual = torch.matmul(flat, wt).contiguous()
+        selector_tables = torch.matmul(raw_tables, wt.unsqueeze(1))
+    for stage in range(depth):
+        raw_table = raw_tables[:, stage].contiguous()
+        selector_table = selector_tables[:, stage].contiguous()
+        indices = _ops.nearest_f32(raw_residual if selector_residual is None else selector_residual,
+                                   selector_table)
+        _ops.subtract_codewords(negated, raw_table, indices)
+        _ops.subtract_codewords(raw_residual, raw_table, indices)
+        if selector_residual is not None:
+            _ops.subtract_codewords(selector_residual, selector_table, indices)
+    reconstruction = (-negated).reshape(heads, batch, tokens, dimension).permute(1, 0, 2, 3).to(
+        states.dtype).contiguous()
+    return raw_residual, selector_residual, reconstruction
 
 
 def _validate(residual, sample_weights, fit_mode, assignment_whiteners, initial_selector_residual, gain_caps):

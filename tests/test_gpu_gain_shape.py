@@ -195,6 +195,31 @@ def test_fit_matches_oracle(device, mode, whitened, weighted, capped, reserve):
     assert hist[-1]["residual_element_mse_after"] == pytest.approx(float(dev_res.square().mean()), rel=1e-6)
 
 
+@pytest.mark.parametrize("whitened", [False, True])
+def test_parent_residuals_match_oracle(device, whitened):
+    # the frozen parent's exit residuals: greedy nearest (selector) words,
+    # subtracted from the raw residual and summed into the reconstruction
+    print(f"parent residuals whitened={whitened}", flush=True)
+    gen = torch.Generator().manual_seed(408)
+    states = torch.randn(2, 2, 150, 128, generator=gen).half()
+    tables = torch.stack([torch.randn(2, 256, 128, generator=gen) * s for s in (1.0, 0.5, 0.25)], dim=1).half()
+    w = (torch.triu(torch.randn(2, 128, 128, generator=gen)) * 0.05 + torch.eye(128) * 1.5) if whitened else None
+    raw, sel, recon = gain_shape.parent_residuals_and_reconstruction(
+        states.to(device), tables.to(device), None if w is None else w.to(device), depth=2, token_chunk_size=4096)
+    want_raw, want_sel, want_recon, margin = ora.parent_residuals(
+        states.float().numpy(), tables.float().numpy(), None if w is None else w.numpy(), 2)
+    # an fp32 distance over 128 dims errs by at most 128 eps |x||c|, under
+    # 4e-6 of |x|^2 + |c|^2 for either side: a wider gap cannot flip
+    assert margin > 1e-5, margin
+    # same choices: the same fp32 subtractions and sums, bit for bit
+    assert np.array_equal(raw.cpu().numpy(), want_raw)
+    assert recon.dtype == torch.float16 and torch.equal(recon.cpu(), torch.from_numpy(want_recon).half())
+    if whitened:
+        np.testing.assert_allclose(sel.cpu().numpy(), want_sel, rtol=0, atol=2e-4 * np.abs(want_sel).max())
+    else:
+        assert sel is None
+
+
 def test_fit_config_size_properties(device):
     # a calibration-sized fit: 8 heads, 32768 rows, head dim 128, ten Lloyd
     # iterations per stage, two stages, gradient weights and gain caps

@@ -5,7 +5,9 @@ Headline line: GSRQ-2 encode of a Mistral-7B-shaped
 cache, 32 layers x {K,V} x [1,8,8192,128] fp16 with 4 outlier channels per
 head, 16 groups x 8 dims x 2 residual stages x 256 fp16 codewords per
 (head, group) (stage 1 N(0,1), stage 2 N(0,0.25)), codes + fp16
-reconstruction written.  One step = the 64 encodes of the whole cache.
+reconstruction written.  One step = the 64 encodes of the whole cache, a
+layer's K and V in one launch as the codec forward issues them (the same
+64 encodes as 64 launches are reported beside it).
 
 Extra measurements in the same JSON line:
   decode   config 4: fused packed-code GQA decode (32q/8kv, B16, 4096 window,
@@ -147,24 +149,34 @@ def encode_workload(args, device):
     gen = torch.Generator(device=device).manual_seed(8601)
     layers = []
     for _layer in range(LAYERS):
+        kv = []
         for _kind in range(2):
             states = make_states(gen, 1, HEADS, args.tokens, device)
             tables = make_tables(gen, (HEADS * GROUPS, STAGES, CLUSTERS, GROUP_DIM), (1.0, 0.5), 1, device)
-            layers.append((states, tables))
-    log(f"encode inputs ready: {len(layers)} tensors of {tuple(layers[0][0].shape)}")
+            kv.append((states, tables))
+        layers.append(kv)
+    log(f"encode inputs ready: {LAYERS} layers x {{K,V}} of {tuple(layers[0][0][0].shape)}")
 
+    # the codec forward of a layer encodes its K and V (uniform_depth_tac.py:
+    # 69-101): one launch per layer, both tensors' workgroups in one grid
     def step():
-        for states, tables in layers:
-            _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+        for (ks, kt), (vs, vt) in layers:
+            _ops.rvq_encode_kv(ks, vs, kt, vt, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+
+    def step_separate():
+        for kv in layers:
+            for states, tables in kv:
+                _ops.rvq_encode(states, tables, groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
 
     ms = timed(step, args.steps, args.warmup)
+    ms_separate = timed(step_separate, args.steps, args.warmup)
     # the timed region's HIP events over its back-to-back launches: a launch
-    # takes ~40 us while the host enqueues one in a few, so the queue never
+    # takes ~75 us while the host enqueues one in a few, so the queue never
     # drains and the average is the kernel's own duration
     avg_launch_ms = ms / len(layers)
-    vecs_per_launch = HEADS * args.tokens
+    vecs_per_launch = 2 * HEADS * args.tokens  # K and V of one layer
     flops_per_launch = vecs_per_launch * FLOP_PER_VEC_G2
-    bytes_per_launch = vecs_per_launch * (HEAD_DIM * 2 + GROUPS * STAGES + HEAD_DIM * 2) + HEADS * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 4
+    bytes_per_launch = vecs_per_launch * (HEAD_DIM * 2 + GROUPS * STAGES + HEAD_DIM * 2) + 2 * HEADS * GROUPS * STAGES * CLUSTERS * GROUP_DIM * 4
     return {
         "ms_per_step": ms,
         "tokens_per_s": args.tokens / (ms / 1e3),
@@ -173,6 +185,8 @@ def encode_workload(args, device):
         "flops_per_launch": flops_per_launch,
         "bytes_per_launch": bytes_per_launch,
         "launches_per_step": len(layers),
+        "separate_launches": {"ms_per_step": ms_separate, "tokens_per_s": args.tokens / (ms_separate / 1e3),
+                              "us_per_launch": ms_separate / (2 * len(layers)) * 1e3},
     }
 
 
@@ -600,14 +614,14 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
             "traffic": measured_traffic(ROOT / "profiles" / "rvq_encode_grouped_g2_config2.md"),
-            "kernel": "rvq_encode_grouped<8,2>",
+            "kernel": "rvq_encode_grouped<8,2,true> (a layer's K and V per launch)",
             "avg_launch_us": enc["avg_launch_ms"] * 1e3,
             "algorithmic_flop_per_launch": enc["flops_per_launch"],
             "algorithmic_bytes_per_launch": enc["bytes_per_launch"],
             "hbm_frac_at_algorithmic_bytes": enc["bytes_per_launch"] / (enc["avg_launch_ms"] / 1e3) / (HBM_PEAK_GBS * 1e9),
         },
         "cpu_baseline": cpu,
-        "extra": extras,
+        "extra": {"encode_separate_launches": enc["separate_launches"], **extras},
         "vecs_per_s": enc["vecs_per_s"],
     }
     print(json.dumps(record), flush=True)

@@ -62,24 +62,119 @@ class _HardResidualVQ(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grad_outputs):
         (codes,) = ctx.saved_tensors
-        grads = list(grad_outputs[:-1])
-        live = [(g, e) for g, e in zip(grads, ctx.exits) if g is not None]
-        grad_states = grad_tables = None
-        if live and ctx.needs_input_grad[0] and ctx.straight_through:
-            grad_states = live[0][0].clone()
-            for g, _ in live[1:]:
-                grad_states = grad_states + g
-        if live and ctx.needs_input_grad[1]:
-            grad_tables = torch.zeros(ctx.table_shape, dtype=torch.float32, device=codes.device)
-            _ops.rvq_scatter_grad(
-                [g for g, _ in live],
-                [e for _, e in live],
-                codes,
-                grad_tables,
-                group_dim=ctx.group_dim,
-                deterministic=ctx.deterministic,
-            )
+        grad_states, grad_tables = _table_and_state_grads(
+            ctx, grad_outputs[:-1], codes, ctx.table_shape, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
         return grad_states, grad_tables, None, None, None, None, None, None
+
+
+def _table_and_state_grads(ctx, grads, codes, table_shape, need_states, need_tables):
+    """The straight-through backward of one encode: the summed upstream
+    gradient for the states and the scatter-add into the table masters."""
+
+    live = [(g, e) for g, e in zip(grads, ctx.exits) if g is not None]
+    grad_states = grad_tables = None
+    if live and need_states and ctx.straight_through:
+        grad_states = live[0][0].clone()
+        for g, _ in live[1:]:
+            grad_states = grad_states + g
+    if live and need_tables:
+        grad_tables = torch.zeros(table_shape, dtype=torch.float32, device=codes.device)
+        _ops.rvq_scatter_grad(
+            [g for g, _ in live],
+            [e for _, e in live],
+            codes,
+            grad_tables,
+            group_dim=ctx.group_dim,
+            deterministic=ctx.deterministic,
+        )
+    return grad_states, grad_tables
+
+
+class _HardResidualVQPair(torch.autograd.Function):
+    """A layer's K and V through one HIP launch (same geometry, no
+    whitener); the backward is each side's own straight-through scatter."""
+
+    @staticmethod
+    def forward(ctx, key_states, value_states, key_tables, value_tables, groups, group_dim, exits,
+                straight_through, deterministic):
+        rk, ck, rv, cv = _ops.rvq_encode_kv(
+            key_states.detach(),
+            value_states.detach(),
+            key_tables.detach(),
+            value_tables.detach(),
+            groups=groups,
+            group_dim=group_dim,
+            exits=exits,
+        )
+        ctx.save_for_backward(ck, cv)
+        ctx.exits = tuple(exits)
+        ctx.group_dim = group_dim
+        ctx.table_shapes = (key_tables.shape, value_tables.shape)
+        ctx.straight_through = straight_through
+        ctx.deterministic = deterministic
+        ctx.mark_non_differentiable(ck, cv)
+        return (*rk, *rv, ck, cv)
+
+    @staticmethod
+    def backward(ctx, *grad_outputs):
+        ck, cv = ctx.saved_tensors
+        n = len(ctx.exits)
+        need = ctx.needs_input_grad
+        gsk, gtk = _table_and_state_grads(ctx, grad_outputs[:n], ck, ctx.table_shapes[0], need[0], need[2])
+        gsv, gtv = _table_and_state_grads(ctx, grad_outputs[n:2 * n], cv, ctx.table_shapes[1], need[1], need[3])
+        return gsk, gsv, gtk, gtv, None, None, None, None, None
+
+
+def hard_residual_vq_pair(
+    key_states: torch.Tensor,
+    value_states: torch.Tensor,
+    key_tables: torch.Tensor,
+    value_tables: torch.Tensor,
+    *,
+    prefixes: Sequence[int],
+    straight_through_states: bool = True,
+    deterministic_backward: bool = False,
+):
+    """A layer's K and V encode in one launch, for the codec forward
+    (uniform_depth_tac.py:69-101 encodes K, then V, with one geometry).
+
+    ``*_states[B,H,T,G*d]`` share shape and dtype; ``*_tables`` are
+    ``[H,G,S,K,d]`` (grouped) or ``[H,S,K,D]`` (one group), fp32 masters, no
+    whitener.  Returns ``(key exits, key codes, value exits, value codes)``
+    as :func:`hard_grouped_residual_vq` (grouped) or
+    :func:`hard_residual_vq_exits` would, with the same bits.
+    """
+
+    if key_states.shape != value_states.shape or key_states.dtype != value_states.dtype:
+        raise ValueError("K and V states must share their geometry")
+    if key_tables.shape != value_tables.shape or key_states.ndim != 4 or key_tables.ndim not in (4, 5):
+        raise ValueError("K and V tables must share their geometry")
+    batch, heads, tokens, dimension = map(int, key_states.shape)
+    if key_tables.ndim == 5:
+        t_heads, groups, stages, clusters, group_dim = map(int, key_tables.shape)
+    else:
+        t_heads, stages, clusters, group_dim = map(int, key_tables.shape)
+        groups = 1
+    if t_heads != heads or groups * group_dim != dimension:
+        raise ValueError("state and table geometry differs")
+    requested = tuple(sorted(set(int(depth) for depth in prefixes)))
+    if not requested or requested[0] <= 0 or requested[-1] > stages:
+        raise ValueError("requested prefixes lie outside the VQ ladder")
+
+    def flat(tables):
+        t = tables if tables.dtype == torch.float32 else tables.float()
+        return t.reshape(heads * groups, stages, clusters, group_dim).contiguous()
+
+    outputs = _HardResidualVQPair.apply(
+        key_states, value_states, flat(key_tables), flat(value_tables), groups, group_dim, requested,
+        straight_through_states, deterministic_backward,
+    )
+    n = len(requested)
+    kc, vc = outputs[2 * n], outputs[2 * n + 1]
+    if groups == 1 and key_tables.ndim == 4:
+        kc = kc.reshape(batch, heads, tokens, stages)
+        vc = vc.reshape(batch, heads, tokens, stages)
+    return dict(zip(requested, outputs[:n])), kc, dict(zip(requested, outputs[n:2 * n])), vc
 
 
 def _validate_soft_backward(topk: int, temperature: float, beta: float, cardinality: int) -> None:

@@ -14,7 +14,7 @@ from collections.abc import Sequence
 import torch
 import torch.nn as nn
 
-from .closed_loop_vq import QuantizedKV, hard_grouped_residual_vq, hard_residual_vq_exits
+from .closed_loop_vq import QuantizedKV, hard_grouped_residual_vq, hard_residual_vq_exits, hard_residual_vq_pair
 
 
 class ClosedLoopUniformResidualVQ(nn.Module):
@@ -97,8 +97,15 @@ class ClosedLoopUniformResidualVQ(nn.Module):
     ) -> QuantizedKV:
         if mode != "uniform":
             raise ValueError("uniform residual VQ exposes only uniform mode")
-        key, key_indices = self._encode(raw_key, self.key_tables[layer], self.whitener(layer))
-        value, value_indices = self._encode(raw_value, self.value_tables[layer], None)
+        whitener = self.whitener(layer)
+        if whitener is None and raw_key.shape == raw_value.shape and raw_key.dtype == raw_value.dtype:
+            # one launch for the layer's K and V (same bits as two encodes)
+            kx, key_indices, vx, value_indices = hard_residual_vq_pair(
+                raw_key, raw_value, self.key_tables[layer], self.value_tables[layer], prefixes=(self.depth,))
+            key, value = kx[self.depth], vx[self.depth]
+        else:
+            key, key_indices = self._encode(raw_key, self.key_tables[layer], whitener)
+            value, value_indices = self._encode(raw_value, self.value_tables[layer], None)
         return QuantizedKV(
             key=key,
             value=value,

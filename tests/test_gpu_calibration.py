@@ -135,6 +135,42 @@ def test_uniform_codec_equals_direct_call_and_v_only_step(device):
     torch.testing.assert_close(codec.value_tables[1].detach(), before - 0.001 * grad * scale, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("grouped,needs", [(True, "tables"), (True, "all"), (False, "all")])
+def test_pair_encode_equals_two_encodes(device, grouped, needs):
+    # a layer's K and V in one launch (the codec forward's path): the same
+    # codes, reconstructions and gradients as two encodes
+    print(f"pair encode grouped={grouped} needs={needs}", flush=True)
+    gen = torch.Generator().manual_seed(77)
+    shape = (8, 16, 2, 256, 8) if grouped else (8, 2, 256, 128)
+    stage_axis = 2 if grouped else 1
+    tabs = [ref.synthetic_tables(gen, shape, (1.0, 0.5), stage_axis=stage_axis).to(device) for _ in range(2)]
+    raw = [ref.synthetic_states(gen, 2, 8, 96).to(device) for _ in range(2)]
+    up = [(torch.randn(2, 8, 96, 128, generator=gen) * 1e-2).half().to(device) for _ in range(2)]
+
+    def leaves():
+        t = [x.clone().requires_grad_() for x in tabs]
+        s = [x.clone().requires_grad_(needs == "all") for x in raw]
+        return t, s
+
+    t1, s1 = leaves()
+    ek, ck, ev, cv = jkv.closed_loop_vq.hard_residual_vq_pair(s1[0], s1[1], t1[0], t1[1], prefixes=(1, 2))
+    (ek[2] * up[0]).float().sum().backward(retain_graph=True)
+    ((ev[2] + ev[1]) * up[1]).float().sum().backward()
+    t2, s2 = leaves()
+    one = jkv.hard_grouped_residual_vq if grouped else jkv.hard_residual_vq_exits
+    fk, dk = one(s2[0], t2[0], prefixes=(1, 2))
+    fv, dv = one(s2[1], t2[1], prefixes=(1, 2))
+    (fk[2] * up[0]).float().sum().backward(retain_graph=True)
+    ((fv[2] + fv[1]) * up[1]).float().sum().backward()
+    assert torch.equal(ck, dk) and torch.equal(cv, dv)
+    assert all(torch.equal(ek[d], fk[d]) and torch.equal(ev[d], fv[d]) for d in (1, 2))
+    assert all(torch.equal(a.grad, b.grad) for a, b in zip(t1, t2))
+    if needs == "all":
+        assert all(torch.equal(a.grad, b.grad) for a, b in zip(s1, s2))
+    with pytest.raises(ValueError, match="share their geometry"):
+        jkv.closed_loop_vq.hard_residual_vq_pair(raw[0], raw[1][:, :, :5], tabs[0], tabs[1], prefixes=(2,))
+
+
 def test_grouped_cq_codec_identity_selector(device):
     gen = torch.Generator().manual_seed(9)
     books_k = [ref.synthetic_tables(gen, (8, 16, 256, 8), (1.0,), stage_axis=0)]

@@ -113,6 +113,14 @@ class _HardResidualVQPair(torch.autograd.Function):
         ctx.straight_through = straight_through
         ctx.deterministic = deterministic
         ctx.mark_non_differentiable(ck, cv)
+        # a side whose states and tables take no gradient gives outputs that
+        # take none either (as its own encode would), so that nothing
+        # downstream forms a gradient for them
+        need = ctx.needs_input_grad
+        if not (need[0] or need[2]):
+            ctx.mark_non_differentiable(*rk)
+        if not (need[1] or need[3]):
+            ctx.mark_non_differentiable(*rv)
         return (*rk, *rv, ck, cv)
 
     @staticmethod

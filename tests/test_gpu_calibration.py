@@ -169,6 +169,12 @@ def test_pair_encode_equals_two_encodes(device, grouped, needs):
         assert all(torch.equal(a.grad, b.grad) for a, b in zip(s1, s2))
     with pytest.raises(ValueError, match="share their geometry"):
         jkv.closed_loop_vq.hard_residual_vq_pair(raw[0], raw[1][:, :, :5], tabs[0], tabs[1], prefixes=(2,))
+    # a frozen K side (the codec's K tables, states without gradient) gives
+    # outputs without gradient, as its own encode would: attention above it
+    # then forms no key gradient
+    vt = tabs[1].clone().requires_grad_()
+    ek, _ck, ev, _cv = jkv.closed_loop_vq.hard_residual_vq_pair(raw[0], raw[1], tabs[0], vt, prefixes=(2,))
+    assert not ek[2].requires_grad and ev[2].requires_grad
 
 
 def test_grouped_cq_codec_identity_selector(device):

@@ -14,7 +14,7 @@ from collections.abc import Sequence
 import torch
 import torch.nn as nn
 
-from .closed_loop_vq import QuantizedKV, _run
+from .closed_loop_vq import QuantizedKV, _run, hard_residual_vq_pair
 
 
 def hard_grouped_cq(
@@ -139,17 +139,26 @@ class ClosedLoopGroupedCQ(nn.Module):
         if mode != "uniform":
             raise ValueError("grouped CQ supports one fixed-rate uniform mode")
         whitener = None if self._identity_selector[layer] else self.key_whitener(layer)
-        key, key_indices = hard_grouped_cq(
-            raw_key,
-            self.key_tables[layer],
-            selector_whiteners=whitener,
-            token_chunk_size=self.token_chunk_size,
-        )
-        value, value_indices = hard_grouped_cq(
-            raw_value,
-            self.value_tables[layer],
-            token_chunk_size=self.token_chunk_size,
-        )
+        kt, vt = self.key_tables[layer], self.value_tables[layer]
+        heads, groups, _k, sub = map(int, kt.shape)
+        if (whitener is None and raw_key.shape == raw_value.shape and raw_key.dtype == raw_value.dtype
+                and raw_key.ndim == 4 and raw_key.shape[1] == heads and raw_key.shape[3] == groups * sub):
+            # one launch for the layer's K and V (same bits as two encodes)
+            kx, kc, vx, vc = hard_residual_vq_pair(raw_key, raw_value, kt.unsqueeze(2), vt.unsqueeze(2),
+                                                   prefixes=(1,))
+            key, key_indices, value, value_indices = kx[1], kc[..., 0], vx[1], vc[..., 0]
+        else:
+            key, key_indices = hard_grouped_cq(
+                raw_key,
+                kt,
+                selector_whiteners=whitener,
+                token_chunk_size=self.token_chunk_size,
+            )
+            value, value_indices = hard_grouped_cq(
+                raw_value,
+                vt,
+                token_chunk_size=self.token_chunk_size,
+            )
         return QuantizedKV(
             key=key,
             value=value,

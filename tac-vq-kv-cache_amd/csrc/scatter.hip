@@ -42,12 +42,21 @@ __device__ __forceinline__ float grad_sum(const ScatterArgs& a, int s, int64_t o
   return acc;
 }
 
-// fp16 value times 2^24 as an exact integer (|result| < 2^40).
-__device__ __forceinline__ long long fp16_fixed(uint32_t h) {
-  const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
-  const long long mag = e ? (long long)(m | 1024u) << (e - 1u) : (long long)m;
-  return (h & 0x8000u) ? -mag : mag;
+// fp16 value times 2^24 as an exact integer (|result| < 2^40), in four
+// instructions: f * 2^24 + 1.5 * 2^52 is an integer in [2^52, 2^53), exact in
+// fp64, whose bit pattern is that of 1.5 * 2^52 plus the integer; the low word
+// of 1.5 * 2^52 is zero, so subtracting its high word gives the int64.  The
+// high word of a finite value lies in [0x4337FF00, 0x433800FF]; inf and nan
+// give 0x7FF00000 or more, which `hmax` (the largest high word seen) reveals.
+__device__ __forceinline__ long long fp16_fixed(uint16_t bits, uint32_t& hmax) {
+  const float f = (float)__builtin_bit_cast(_Float16, bits);
+  const double y = __builtin_fma((double)f, 16777216.0, 6755399441055744.0);
+  const unsigned long long w = __builtin_bit_cast(unsigned long long, y);
+  const uint32_t hi = (uint32_t)(w >> 32);
+  hmax = max(hmax, hi);
+  return (long long)(((unsigned long long)(hi - 0x43380000u) << 32) | (uint32_t)w);
 }
+__device__ __forceinline__ bool fixed_nonfinite(uint32_t hmax) { return hmax > 0x433800FFu; }
 
 __device__ __forceinline__ float fixed_to_float(long long v) {
   return (float)v * 5.9604644775390625e-8f;  // 2^-24: exact scaling
@@ -64,11 +73,10 @@ __device__ __forceinline__ void load_slice(const void* base, int64_t off, Acc (&
   if constexpr (std::is_same<Acc, long long>::value) {
     typedef uint16_t UV __attribute__((ext_vector_type(D)));
     const UV x = *(const UV*)((const uint16_t*)base + off);
+    uint32_t hmax = 0u;
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-      v[i] = fp16_fixed(x[i]);
-      bad |= ((x[i] & 0x7C00u) == 0x7C00u);
-    }
+    for (int i = 0; i < D; ++i) v[i] = fp16_fixed(x[i], hmax);
+    bad |= fixed_nonfinite(hmax) ? 1u : 0u;
   } else {
     const TV x = *(const TV*)((const T*)base + off);
 #pragma unroll
@@ -346,14 +354,20 @@ __global__ __launch_bounds__(1024) void scatter_group8_kernel(ScatterArgs a) {
     }
     return;
   }
-  for (int i = threadIdx.x; i < S * K * D; i += blockDim.x) {
-    const int s = i / (K * D), k = (i / D) % K, c = i % D;
-    const long long v = bins[(s * K + k) * kPad + c];
-    const int64_t o = (((int64_t)p * S + s) * K + k) * d + c;
-    if (a.n_chunks == 1) {
-      a.grad_tables[o] += fixed_to_float(v);
-    } else {
-      ((long long*)a.partials)[(int64_t)chunk * a.H * a.G * S * K * d + o] = v;
+  // element i = 8k + c of stage s's bins (d = D here)
+  const int64_t pbase = (int64_t)p * S * K * D;
+  long long* part = a.n_chunks > 1 ? (long long*)a.partials + (int64_t)chunk * a.H * a.G * S * K * D + pbase
+                                   : nullptr;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    for (int i = threadIdx.x; i < K * D; i += blockDim.x) {
+      const long long v = bins[(s * K + (i >> 3)) * kPad + (i & 7)];
+      const int64_t o = (int64_t)s * K * D + i;
+      if (a.n_chunks == 1) {
+        a.grad_tables[pbase + o] += fixed_to_float(v);
+      } else {
+        part[o] = v;
+      }
     }
   }
 }

@@ -79,9 +79,12 @@ def test_workspace_queries():
     assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, F16, 1) == 0
     # bf16 deterministic: ordered partials per 256-row chunk
     assert lib.jkv_rvq_scatter_workspace_bytes(1, 8, 512, 16, 8, 2, 256, BF16, 1) == 2 * bins * 4
-    # fp16, 8-dim groups: one block per (head, group) holds every stage's bins,
-    # so config 5's 128 blocks take 2 row chunks of 4096 rows, 64-bit partials
-    assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 16, 8, 2, 256, F16, 0) == 2 * bins * 8
+    # fp16, 8-dim groups at config 5: one block per (head, group, stage)
+    # already fills the chip (256 blocks), so no row chunks and no partials
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 16, 8, 2, 256, F16, 0) == 0
+    # one stage: one block per (head, group) holds the bins, 128 blocks take
+    # 2 row chunks of 4096 rows with 64-bit partials
+    assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 16, 8, 1, 256, F16, 0) == bins * 8
     # bf16 (fp32 bins): one block per (head, group, stage, 8 dims) already fills the chip
     assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 16, 8, 2, 256, BF16, 0) == 0
     assert lib.jkv_rvq_scatter_workspace_bytes(4, 8, 2048, 1, 128, 2, 256, F16, 0) == 0

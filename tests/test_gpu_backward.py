@@ -178,18 +178,21 @@ def test_bf16_fp32_scatter_matches_oracle(device, dtype, deterministic):
         assert torch.equal(got, again)
 
 
-def test_fp16_scatter_nonfinite_gradients(device):
+@pytest.mark.parametrize("heads", [2, 8])
+def test_fp16_scatter_nonfinite_gradients(device, heads):
     # inf / nan slices: the IEEE outcome of a floating-point sum per bin
+    # (2 heads: one block per (head, group) with row chunks; 8 heads: one
+    # block per (head, group, stage))
     from jointkv_amd import _ops
 
     gen = torch.Generator().manual_seed(8641)
-    codes, grads = _random_scatter_case(gen, 1, 2, 3000, 16, 8, 2, 1, torch.float16)
+    codes, grads = _random_scatter_case(gen, 1, heads, 3000, 16, 8, 2, 1, torch.float16)
     g = grads[0]
     g[0, 0, 5, 3] = float("inf")
     g[0, 1, 2999, 17] = float("-inf")
     g[0, 1, 100, 40] = float("nan")
-    expect = ref.table_gradient([g], (2,), codes, (32, 2, 256, 8), accumulate=torch.float64).float()
-    got = torch.zeros(32, 2, 256, 8, device=device)
+    expect = ref.table_gradient([g], (2,), codes, (heads * 16, 2, 256, 8), accumulate=torch.float64).float()
+    got = torch.zeros(heads * 16, 2, 256, 8, device=device)
     _ops.rvq_scatter_grad([g.to(device)], (2,), codes.to(device), got, group_dim=8)
     got = got.cpu()
     assert torch.equal(torch.isnan(got), torch.isnan(expect))

@@ -1293,6 +1293,33 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
   const int64_t bq = blockIdx.x;  // b*QH + qh
   const int i = threadIdx.x;
   const float* ml = a.ws_ml + bq * a.n_splits * 2;
+  constexpr int kFew = 4;
+  if (a.n_splits <= kFew) {
+    // every split's (max, sum) and output element in flight together
+    float mv[kFew], lv[kFew], ov[kFew];
+#pragma unroll
+    for (int s = 0; s < kFew; ++s) {
+      if (s < a.n_splits) {
+        mv[s] = ml[2 * s];
+        lv[s] = ml[2 * s + 1];
+        ov[s] = a.ws_o[(bq * a.n_splits + s) * kHeadDim + i];
+      }
+    }
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int s = 0; s < kFew; ++s)
+      if (s < a.n_splits) M = fmaxf(M, mv[s]);
+    float Lsum = 0.f, acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < kFew; ++s) {
+      if (s >= a.n_splits || mv[s] == -__builtin_inff()) continue;
+      const float w = __expf(mv[s] - M);
+      Lsum += lv[s] * w;
+      acc += ov[s] * w;
+    }
+    a.out[bq * kHeadDim + i] = (_Float16)(Lsum > 0.f ? acc / Lsum : 0.f);
+    return;
+  }
   float M = -__builtin_inff();
   for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, ml[2 * s]);
   float Lsum = 0.f, acc = 0.f;

@@ -101,6 +101,44 @@ def test_full_backward_matches_oracle(device, batch, qh, kvh, tokens, starts, wi
         assert err <= DV_RTOL * scale + 1e-3, f"{name} max abs error {err} (scale {scale})"
 
 
+@pytest.mark.parametrize("batch,qh,kvh,tokens,starts,window", [
+    (1, 32, 8, 200, (0,), 4096),        # Mistral GQA 4
+    (2, 8, 2, 301, (0, 5000), 64),      # window binds, later positions, ragged tiles
+    (1, 8, 2, 600, (0,), 4096),         # keys split in runs (workspace + reduce)
+])
+def test_key_grad_entry_matches_backward_key_leg(device, batch, qh, kvh, tokens, starts, window):
+    # jkv_prefill_attention_key_grad given delta = rowsum(dO * O) from the
+    # host equals the full backward's key leg (which forms delta itself)
+    from jointkv_amd import _lib
+
+    print(f"key grad B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)
+    q, k, v, d = _case(2300 + tokens, batch, qh, kvh, tokens)
+    qd, kd, vd, dd = (t.to(device) for t in (q, k, v, d))
+    st = torch.tensor(starts, dtype=torch.int32, device=device)
+    max_pos = max(starts) + tokens - 1
+    lse = torch.empty(batch, qh, tokens, dtype=torch.float32, device=device)
+    out = _ops.prefill_attention(qd, kd, vd, st, window=window, rope_theta=10000.0, max_position=max_pos, lse=lse)
+    _dq, dk_full, _dv = _ops.prefill_attention_backward(
+        qd, kd, vd, out, dd, lse, st, window=window, rope_theta=10000.0, max_position=max_pos,
+        need=(False, True, False))
+    delta = (dd.float() * out.float()).sum(-1).contiguous()
+    table = _ops.rope_table(device, 10000.0, max_pos + 1)
+    lib = _lib.load()
+    ws = int(lib.jkv_prefill_value_grad_workspace_bytes(batch, kvh, tokens, window))
+    work = torch.empty(max(ws, 1), dtype=torch.uint8, device=device)
+    dk = torch.empty(batch, kvh, tokens, 128, dtype=torch.float32, device=device)
+    _lib.check(lib.jkv_prefill_attention_key_grad(
+        qd.data_ptr(), *qd.stride()[:3], kd.data_ptr(), *kd.stride()[:3], vd.data_ptr(), *vd.stride()[:3],
+        dd.data_ptr(), *dd.stride()[:3], lse.data_ptr(), delta.data_ptr(), batch, qh, kvh, tokens, 128,
+        st.data_ptr(), window, table.data_ptr(), int(table.shape[0]), dk.data_ptr(), work.data_ptr(), ws,
+        _lib.stream_handle(device)))
+    scale = float(dk_full.abs().max())
+    err = float((dk - dk_full).abs().max())
+    print(f"  dk err {err:.2e} of {scale:.2e}", flush=True)
+    # the two deltas are fp32 sums of the same fp16 products in different orders
+    assert err <= 1e-4 * scale + 1e-6
+
+
 @pytest.mark.parametrize("tokens,stages,whitened", [(96, 2, False), (150, 4, True)])
 def test_closed_loop_attention_value_step(device, tokens, stages, whitened):
     # a small decoder layer (4 query heads, 1 kv head, head_dim 128) with

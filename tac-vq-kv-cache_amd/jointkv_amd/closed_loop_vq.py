@@ -74,7 +74,9 @@ def _table_and_state_grads(ctx, grads, codes, table_shape, need_states, need_tab
     live = [(g, e) for g, e in zip(grads, ctx.exits) if g is not None]
     grad_states = grad_tables = None
     if live and need_states and ctx.straight_through:
-        grad_states = live[0][0].clone()
+        # the summed exit gradients (one exit: its gradient itself; the sums
+        # are out of place, so no caller's tensor is modified)
+        grad_states = live[0][0]
         for g, _ in live[1:]:
             grad_states = grad_states + g
     if live and need_tables:

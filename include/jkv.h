@@ -240,9 +240,12 @@ int jkv_decode_attention_append(const void* q, int64_t q_stride_b,
  * Same arguments, results and errors as jkv_decode_attention without the
  * workspace: the split partials go to a file-scope device array of the
  * library (one per GPU, jkv_decode_noalloc_max_workspace_bytes() = 16 MiB,
- * held until the process ends).  Calls that need more partial space than
- * that (jkv_decode_workspace_bytes(B, QH, 128, window) above the maximum)
- * return JKV_EINVAL.  The array is looked up on the first call on each
+ * held until the process ends).  Calls whose kernel needs more partial
+ * space than that return JKV_EINVAL: B*QH*n_splits*(128+2)*4 bytes, with
+ * n_splits = ceil(window/2048) for group dims 4 and 8 on 16-byte aligned
+ * codes and tables (e.g. config 4 up to B*QH = 16,131 at a 4096-token
+ * window) and ceil(window/256) otherwise (the bound that
+ * jkv_decode_workspace_bytes reports).  The array is looked up on the first call on each
  * device (the current HIP device); no call allocates or frees memory.  Every
  * call on a device shares that device's array: calls that overlap on one
  * GPU (two streams, two threads) race and must be serialised by the caller.

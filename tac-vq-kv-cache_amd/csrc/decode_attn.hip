@@ -1381,6 +1381,36 @@ static int64_t g8_split_tokens(int64_t G, int64_t S, int64_t K, int64_t nq, int6
   return w < kG8MaxSplit ? w : kG8MaxSplit;
 }
 
+// Tokens per split of the kernel launch_decode picks for a packed-code
+// geometry (the LDS-table kernels take up to 2048-token splits, the L2
+// split kernel kSplitTokens), so callers can size the partials exactly.
+static int64_t packed_split_tokens(int64_t G, int64_t d, int64_t S, int64_t K, int64_t nq, int64_t window,
+                                   bool lds_ok) {
+  if (lds_ok && d == 8) {
+    const int64_t g8 = g8_split_tokens(G, S, K, nq, window);
+    if (g8 > 0) return g8;
+  }
+  if (lds_ok && (d == 8 || d == 4)) {
+    const int64_t lds = lds_split_tokens(G, S, K, nq, window);
+    if (lds > 0) return lds;
+  }
+  return kSplitTokens;
+}
+
+// Bytes of split partials ([B,QH,n_splits] x (128 + 2) fp32) that launch.
+static int64_t packed_partial_bytes(int64_t B, int64_t QH, int64_t G, int64_t d, int64_t S, int64_t K, int64_t nq,
+                                    int64_t window, bool lds_ok) {
+  const int64_t ns = ceil_div(window, packed_split_tokens(G, d, S, K, nq, window, lds_ok));
+  return B * QH * ns * (kHeadDim + 2) * (int64_t)sizeof(float);
+}
+
+// The LDS-table kernels copy code records and tables in 16-byte pieces.
+static bool packed_lds_ok(const void* k_codes, const void* v_codes, int64_t code_stride_b, int64_t code_stride_h,
+                          const void* k_tables, const void* v_tables) {
+  return ((uintptr_t)k_codes % 16 == 0) && ((uintptr_t)v_codes % 16 == 0) && code_stride_b % 16 == 0 &&
+         code_stride_h % 16 == 0 && ((uintptr_t)k_tables % 16 == 0) && ((uintptr_t)v_tables % 16 == 0);
+}
+
 template <int D, int NQ>
 static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream, bool append = false) {
   const int64_t split = lds_ok && D != 128 && D != 0 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
@@ -1484,7 +1514,10 @@ static int decode_packed(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   if (B == 0) return JKV_OK;
   JKV_CHECK_ARG(q && k_codes && v_codes && k_tables && v_tables && lengths && out && rope_table,
                 "null buffer");
-  const int64_t need = jkv_decode_workspace_bytes(B, QH, kHeadDim, window);
+  const bool lds_ok = packed_lds_ok(k_codes, v_codes, code_stride_b, code_stride_h, k_tables, v_tables);
+  // what the chosen kernel writes; jkv_decode_workspace_bytes() is an upper
+  // bound of it for every packed geometry
+  const int64_t need = packed_partial_bytes(B, QH, G, d, S, K, nq, window, lds_ok);
   JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                 "decode attention needs %lld bytes of workspace", (long long)need);
   DecodeArgs a = {};
@@ -1514,10 +1547,6 @@ static int decode_packed(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.kc_out = const_cast<uint8_t*>(k_codes);
     a.vc_out = const_cast<uint8_t*>(v_codes);
   }
-  // LDS-table kernel: code records and tables copied in 16-byte pieces
-  const bool lds_ok = ((uintptr_t)k_codes % 16 == 0) && ((uintptr_t)v_codes % 16 == 0) &&
-                      code_stride_b % 16 == 0 && code_stride_h % 16 == 0 &&
-                      ((uintptr_t)k_tables % 16 == 0) && ((uintptr_t)v_tables % 16 == 0);
 #define JKV_DEC(DD, NN) \
   if (d == DD && nq == NN) return launch_decode<DD, NN>(a, lds_ok, stream, append);
   JKV_DEC(8, 1) JKV_DEC(8, 2) JKV_DEC(8, 4) JKV_DEC(8, 8)
@@ -1596,8 +1625,11 @@ int jkv_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_st
                                  const void* rope_table, int64_t rope_len, void* out,
                                  jkv_stream_t stream) {
   using namespace jkv;
-  JKV_CHECK_ARG(B >= 0 && QH > 0 && window > 0, "invalid head geometry");
-  const int64_t need = jkv_decode_workspace_bytes(B, QH, kHeadDim, window);
+  JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && QH % KVH == 0 && window > 0, "invalid head geometry");
+  // the partials of the kernel this call will run: 2048-token splits on the
+  // LDS-table kernels (group dims 4 and 8), 256-token splits otherwise
+  const bool lds_ok = packed_lds_ok(k_codes, v_codes, code_stride_b, code_stride_h, k_tables, v_tables);
+  const int64_t need = packed_partial_bytes(B, QH, G, d, S, K, QH / KVH, window, lds_ok);
   JKV_CHECK_ARG(need <= kNoAllocScratchBytes,
                 "allocation-free decode attention holds at most %lld bytes of split partials; "
                 "B=%lld, QH=%lld, window=%lld need %lld (use jkv_decode_attention with a workspace)",

@@ -322,11 +322,21 @@ class PackedCodeCache:
 
         if (key.ndim == 4 and key.shape[2] != 1) or (value.ndim == 4 and value.shape[2] != 1):
             raise ValueError("attend_append takes one token per sequence")
-        self._host_length += 1
-        self.lengths.fill_(self._host_length)
-        return decode_attention(query, self.key, self.value, key_tables16, value_tables16, self.lengths,
-                                window=window, rope_theta=rope_theta, max_length=self._host_length,
-                                key_new=key, value_new=value)
+        # the cache counts the new token only once the launch that writes its
+        # codes has been accepted: a refused geometry (the fused append serves
+        # 16 groups of 8 dims, S <= 2) leaves length and lengths unchanged, so
+        # a caller can fall back to encode_append + decode_attention
+        new_length = self._host_length + 1
+        self.lengths.fill_(new_length)
+        try:
+            out = decode_attention(query, self.key, self.value, key_tables16, value_tables16, self.lengths,
+                                   window=window, rope_theta=rope_theta, max_length=new_length,
+                                   key_new=key, value_new=value)
+        except BaseException:
+            self.lengths.fill_(self._host_length)
+            raise
+        self._host_length = new_length
+        return out
 
     def payload_bytes(self) -> int:
         visible = min(self._host_length, self.capacity)

@@ -11,6 +11,7 @@ import torch
 
 from jointkv_amd import gain_shape
 from oracle import gain_shape_oracle as ora
+from oracle import jointkv_oracle as ref
 
 
 def test_codeword_sums_and_update_hand_worked():
@@ -117,6 +118,53 @@ def test_fit_invariants_on_clustered_data():
         assert rec["gain_cap_min"] == 9.0 and rec["gain_cap_max"] == 12.0
     # the second stage works on the first stage's residual
     assert history[1]["residual_element_mse_before"] == pytest.approx(history[0]["residual_element_mse_after"])
+
+
+def test_lloyd_update_is_the_plain_mean_of_each_codewords_rows():
+    # build_frozen_gsrq_multi_exit.py:592-603: 255 clusters on a grid 4 apart,
+    # each with rows c, c + 2u, c + 4u (u = 0.25 e0) and seeded at c; one
+    # update moves every codeword to the rows' mean c + 2u (exact in fp16),
+    # which is a fixed point, and codeword 0 stays the reserved zero
+    grid = np.stack(np.meshgrid(*[np.arange(1, 5)] * 4, indexing="ij"), -1).reshape(-1, 4)[:255]
+    centers = 4.0 * grid.astype(np.float64)
+    u = np.array([0.25, 0.0, 0.0, 0.0])
+    rows = np.stack([centers, centers + 2 * u, centers + 4 * u], axis=1).reshape(1, 765, 4)
+    seeds = [[np.arange(255) * 3]]
+    for iterations in (1, 2):
+        tables, history, _gap = ora.fit_residual_stages(rows.astype(np.float32), seeds, stages=1,
+                                                        iterations=iterations, fit_mode="lloyd")
+        assert np.all(tables[0, 0, 0] == 0)
+        np.testing.assert_array_equal(tables[0, 0, 1:].astype(np.float64), centers + 2 * u)
+        # residuals -2u, 0, +2u along e0: element MSE (0.25 + 0 + 0.25) / 3 / 4
+        assert history[0]["residual_element_mse_after"] == pytest.approx(0.5 / 12, rel=1e-12)
+        assert history[0]["fit_mode"] == "lloyd" and history[0]["occupied_clusters_min"] == 255
+
+
+def test_parent_residuals_equal_the_greedy_operator():
+    # build_frozen_gsrq_multi_exit.py:661-738 walks the parent's stages with
+    # the same greedy search as closed_loop_vq.py:235-410: its reconstruction
+    # is the operator's exit (fp16 of the fp32 stage sum) and its residual is
+    # what the rows keep after subtracting it, with and without a whitener
+    gen = torch.Generator().manual_seed(31)
+    states = torch.randn(2, 3, 40, 16, generator=gen).half()
+    tables = (torch.randn(3, 3, 256, 16, generator=gen) * torch.tensor([1.0, 0.5, 0.25])[None, :, None, None]).half()
+    w = (torch.triu(torch.randn(3, 16, 16, generator=gen)) * 0.2 + torch.eye(16) * 1.5)
+    for whitener in (None, w):
+        for depth in (1, 3):
+            raw, sel, recon, gap = ora.parent_residuals(states.float().numpy(), tables.float().numpy(),
+                                                        None if whitener is None else whitener.numpy(), depth)
+            exits, codes, d1, d2 = ref.hard_residual_vq_exits(
+                states, tables.float(), prefixes=(depth,), assignment_whiteners=whitener, return_margins=True)
+            # the inputs keep every search margin clear of fp32 rounding
+            assert gap > 1e-5 and float(((d2 - d1) / d1.abs().clamp_min(1e-6)).min()) > 1e-4
+            assert torch.equal(torch.from_numpy(recon).half(), exits[depth].detach())
+            flat = states.float().permute(1, 0, 2, 3).reshape(3, 80, 16).numpy()
+            np.testing.assert_allclose(raw, flat - recon.transpose(1, 0, 2, 3).reshape(3, 80, 16), atol=2e-6)
+            if whitener is None:
+                assert sel is None
+            else:
+                want = np.einsum("hde,hne->hnd", whitener.double().numpy(), raw.astype(np.float64))
+                np.testing.assert_allclose(sel, want, atol=2e-4)
 
 
 def test_argument_checks_keep_the_reference_texts():

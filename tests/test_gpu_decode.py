@@ -65,6 +65,7 @@ def test_decode_matches_oracle(device, batch, qh, kvh, groups, stages, d, length
     (3, 8, 2, 2, (1, 257, 5000), 4096, 4096),   # first token; chunk 1's first key; ring wrap
     (2, 16, 2, 1, (600, 2049), 4096, 4096),     # one stage, GQA 8; the new token opens split 2
     (2, 4, 2, 2, (513, 700), 512, 1024),        # window of two chunks, partial last chunk
+    (16, 32, 8, 2, (4096,) * 16, 4096, 4096),   # config 4 exactly: batch 16, the benchmarked grid
 ])
 def test_decode_append_matches_encode_then_decode(device, batch, qh, kvh, stages, lengths, window, cap):
     # the fused step encodes the new token into its slot and attends with it
@@ -117,6 +118,60 @@ def test_decode_append_entry_point_limits(device):
         jkv.decode_attention(q.to(device), kc.to(device), vc.to(device), kt.half().to(device), vt.half().to(device),
                              torch.tensor([5], dtype=torch.int32, device=device), window=512,
                              key_new=knew.to(device))
+
+
+def test_attend_append_serving_loop(device):
+    # PackedCodeCache.attend_append: each step's codes land in the ring slot
+    # (the codec's greedy search, checked against the oracle), the output is
+    # the plain decode over the updated cache bit for bit, and the cache
+    # counts the token; the 4-slot ring wraps
+    gen = torch.Generator().manual_seed(8621)
+    batch, kvh, qh, cap = 3, 2, 8, 4
+    kt = ref.synthetic_tables(gen, (kvh * 16, 2, 256, 8), (1.0, 0.5), stage_axis=1)
+    vt = ref.synthetic_tables(gen, (kvh * 16, 2, 256, 8), (1.0, 0.5), stage_axis=1)
+    kt16, vt16 = kt.half().to(device), vt.half().to(device)
+    cache = jkv.PackedCodeCache(batch, kvh, 16, 2, capacity=cap, device=device)
+    for step in range(6):
+        k = ref.synthetic_states(gen, batch, kvh, 1)
+        v = ref.synthetic_states(gen, batch, kvh, 1)
+        q = torch.randn(batch, qh, 1, 128, generator=gen).half().to(device)
+        out = cache.attend_append(q, k.to(device), v.to(device), kt16, vt16, window=cap)
+        assert cache.length == step + 1 and torch.equal(cache.lengths.cpu(), torch.full((batch,), step + 1,
+                                                                                          dtype=torch.int32))
+        slot = step % cap
+        for raw, tabs, got in ((k, kt, cache.key), (v, vt, cache.value)):
+            _o, want, d1, d2 = ref.grouped_residual_vq(raw, tabs.reshape(kvh, 16, 2, 256, 8), prefixes=(2,),
+                                                       return_margins=True)
+            verdict = compare_codes(got[:, :, slot : slot + 1].cpu(), want, d1, d2)
+            assert verdict["clear_mismatches"] == 0, f"step {step}"
+        again = jkv.decode_attention(q, cache.key, cache.value, kt16, vt16, cache.lengths, window=cap,
+                                     max_length=cache.length)
+        assert torch.equal(out, again), f"step {step}"
+        e = _expect(q.cpu(), cache.key.cpu(), cache.value.cpu(), kt, vt, step + 1, cap, cap)
+        err = float((out.cpu().float() - e.float()).abs().max())
+        assert err <= ATOL, f"step {step}: {err}"
+
+
+def test_attend_append_refused_geometry_keeps_length(device):
+    # a geometry the fused append does not serve (cq2: 32 groups of 4 dims)
+    # raises before anything is written, and the cache still counts only the
+    # tokens whose codes it holds
+    gen = torch.Generator().manual_seed(8623)
+    cache = jkv.PackedCodeCache(1, 2, 32, 1, capacity=16, device=device)
+    codes = torch.randint(0, 256, (1, 2, 3, 32, 1), generator=gen, dtype=torch.uint8).to(device)
+    cache.append(codes, codes)
+    before_k, before_v = cache.key.clone(), cache.value.clone()
+    t16 = ref.synthetic_tables(gen, (2 * 32, 1, 256, 4), (1.0,), stage_axis=1).half().to(device)
+    q = torch.randn(1, 8, 1, 128, generator=gen).half().to(device)
+    raw = ref.synthetic_states(gen, 1, 2, 1).to(device)
+    with pytest.raises(ValueError):
+        cache.attend_append(q, raw, raw, t16, t16, window=16)
+    assert cache.length == 3 and torch.equal(cache.lengths.cpu(), torch.tensor([3], dtype=torch.int32))
+    assert torch.equal(cache.key, before_k) and torch.equal(cache.value, before_v)
+    # the fallback path then serves the step
+    out = jkv.decode_attention(q, cache.key, cache.value, t16, t16, cache.lengths, window=16,
+                               max_length=cache.length)
+    assert out.shape == (1, 8, 1, 128)
 
 
 def test_ragged_lengths_and_cache_append(device):

@@ -155,6 +155,25 @@ def test_prefill_config4_chunk_one_row(device):
     assert err <= ATOL, f"max abs error {err}"
 
 
+def test_prefill_batch16_block_mapping(device):
+    # the benchmarked batch of 16 (32/8 heads): every batch row at a 256-token
+    # chunk against the oracle, then rows 0, 9 and 15 of the full 2048-token
+    # config-4 chunk, so the block -> (batch, kv head, head group, rows)
+    # mapping of the launch the bench times is checked at its own grid
+    q, k, v = _case(8602, 16, 32, 8, 256)
+    out = jkv.prefill_attention(q.to(device), k.to(device), v.to(device), 0)
+    expect = ref.prefill_attention(q, k, v, (0,) * 16)
+    err = float((out.cpu().float() - expect.float()).abs().max())
+    assert err <= ATOL, f"T=256 max abs error {err}"
+    q, k, v = _case(8603, 16, 32, 8, 2048)
+    out = jkv.prefill_attention(q.to(device), k.to(device), v.to(device), 0).cpu()
+    for b in (0, 9, 15):
+        print(f"prefill B=16 T=2048 row {b}", flush=True)
+        expect = ref.prefill_attention(q[b : b + 1], k[b : b + 1], v[b : b + 1], (0,))
+        err = float((out[b : b + 1].float() - expect.float()).abs().max())
+        assert err <= ATOL, f"T=2048 row {b}: max abs error {err}"
+
+
 def test_prefill_rejects_bad_geometry(device):
     q, k, v = _case(1, 1, 4, 2, 8)
     with pytest.raises(ValueError):

@@ -97,6 +97,21 @@ def test_exits_equal_decode_of_codes_and_fp16_codewords():
         assert torch.equal(out[depth].detach(), decoded)
 
 
+def test_frozen_decode_of_grouped_codes_equals_the_grouped_exits():
+    # the deployment layout [B,H,T,G,S] codes with [H*G,S,K,d] tables at G = 16
+    # groups of 8 dims: decoding the grouped operator's codes rebuilds its exits
+    # bit for bit at every depth (a group or stage axis taken in the wrong order
+    # lands codewords in the wrong 8-dim slice)
+    gen = torch.Generator().manual_seed(16)
+    states = ref.synthetic_states(gen, 2, 2, 24)
+    tables = ref.synthetic_tables(gen, (2, 16, 2, 256, 8), (1.0, 0.5), stage_axis=2)
+    exits, codes = ref.grouped_residual_vq(states, tables, prefixes=(1, 2))
+    assert codes.shape == (2, 2, 24, 16, 2)
+    for depth in (1, 2):
+        got = ref.frozen_decode(codes, tables.reshape(32, 2, 256, 8), depth, torch.float16)
+        assert torch.equal(got, exits[depth].detach())
+
+
 def test_chunk_size_does_not_change_codes():
     gen = torch.Generator().manual_seed(7)
     states = torch.randn(1, 2, 12, 4, generator=gen)

@@ -72,13 +72,26 @@ def test_noalloc_decode_matches_workspace_decode_on_two_calls(device):
         assert err <= 2e-3, f"batch {b}: {err}"
 
 
+def test_noalloc_decode_sizes_partials_by_the_kernel_it_runs(device):
+    # 64 sequences x 32 heads x a 4096-token window: the conservative query
+    # (256-token splits) says 17 MB, beyond the 16 MiB scratch, but the
+    # group-dim-8 kernel takes 2048-token splits and writes 2.1 MB, so the
+    # call is served, with the workspace entry point's bits
+    lib = _lib.load()
+    cap_bytes = int(lib.jkv_decode_noalloc_max_workspace_bytes())
+    assert int(lib.jkv_decode_workspace_bytes(64, 32, 128, 4096)) > cap_bytes
+    print("noalloc decode between the old and new limits: B=64 QH=32 KVH=8 window=4096", flush=True)
+    ref_out, out = _both(device, *_inputs(6, 64, 32, 8, 4096, 4096, device), 4096)
+    assert torch.equal(out, ref_out)
+
+
 def test_noalloc_decode_rejects_calls_beyond_its_scratch(device):
     lib = _lib.load()
     cap_bytes = int(lib.jkv_decode_noalloc_max_workspace_bytes())
     assert cap_bytes == 16 << 20
-    # 64 sequences x 32 heads x 4096-token window need 16 splits x 130 floats each: 17 MB
-    q, kc, vc, kt, vt, lengths = _inputs(5, 64, 32, 8, 8, 4096, device)
-    assert int(lib.jkv_decode_workspace_bytes(64, 32, 128, 4096)) > cap_bytes
+    # 256 sequences x 64 heads x a 4096-token window need 2 splits x 130
+    # floats each on the group-dim-8 kernel: 17 MB
+    q, kc, vc, kt, vt, lengths = _inputs(5, 256, 64, 8, 8, 4096, device)
     table = _ops.rope_table(device, 10000.0, 16)
     out = torch.empty_like(q)
     rc = lib.jkv_decode_attention_noalloc(*_args(q, kc, vc, kt, vt, lengths, 4096, table, out),

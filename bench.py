@@ -15,6 +15,10 @@ Extra measurements in the same JSON line:
            attention per layer), us/step
   prefill  config 4: 2048-token causal prefill chunk (B16, 32q/8kv), us per
            layer and MFMA fraction
+  vstack   config 5 as the reference runs it: the V-only step over a
+           synthetic 32-layer Mistral-7B-shaped decoder (batch 4, 2048
+           tokens), forward + backward through the stack, per_layer_kv clip,
+           SGD; steps/s
   vstep    config 5: V-only STE calibration step over 32 layers at
            [4,8,2048,128] (encode fwd, scatter bwd, global clip, SGD), steps/s
   cq2      config 3: reference cq2 grouped-CQ encode ([8,32,256,4]) of
@@ -431,6 +435,45 @@ def adapter_workload(args, device):
     }
 
 
+def vstack_workload(args, device):
+    """The V-only calibration step over a synthetic 32-layer Mistral-7B-shaped
+    decoder at config 5's shape (batch 4, 2048 tokens; hidden 4096, 32 query /
+    8 kv heads, MLP 14336, vocabulary 32000; random frozen fp16 weights,
+    random token ids), every layer's K/V through a GSRQ-2 codec, in the
+    order of train_mistral_v_only.py:143-153: forward, causal loss, checks,
+    backward (value leg in the first layer, full attention backward above
+    it), per_layer_kv clip at 1.0, SGD at lr 0.001."""
+
+    import torch
+    import jointkv_amd as jkv
+    from jointkv_amd.v_only import ClosedLoopRunContext, DecoderStack, run_loss, v_only_step
+
+    batch, tokens, vocab, inter = 4, 2048, 32000, 14336
+    gen = torch.Generator(device=device).manual_seed(8601)
+    stack = DecoderStack.synthetic(gen, layers=LAYERS, hidden=HEADS * 4 * HEAD_DIM, kv_heads=HEADS,
+                                   intermediate=inter, vocab=vocab)
+    shape = (HEADS, GROUPS, STAGES, CLUSTERS, GROUP_DIM)
+    ktabs = [make_tables(gen, shape, (1.0, 0.5), 2, device) for _ in range(LAYERS)]
+    vtabs = [make_tables(gen, shape, (1.0, 0.5), 2, device) for _ in range(LAYERS)]
+    codec = jkv.ClosedLoopUniformResidualVQ(ktabs, vtabs, [None] * LAYERS, depth=STAGES, dynamic_bpa=2.0).to(device)
+    context = ClosedLoopRunContext(codec, "uniform")
+    ids = torch.randint(0, vocab, (batch, tokens), generator=gen, device=device)
+    log(f"stacked V-only step: {LAYERS} layers, hidden {HEADS * 4 * HEAD_DIM}, MLP {inter}, batch {batch} x {tokens}")
+    count = [0]
+
+    def step():
+        v_only_step(context, lambda: run_loss(stack, context, ids, mode="uniform"), step=count[0])
+        count[0] += 1
+
+    ms = timed(step, 2, 1)
+    peak = torch.cuda.max_memory_allocated(device)
+    del stack, codec, context
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "layers": LAYERS, "batch": batch, "tokens": tokens,
+            "hidden": HEADS * 4 * HEAD_DIM, "intermediate": inter, "vocab": vocab, "clip": "per_layer_kv 1.0",
+            "peak_hbm_gib": peak / 2 ** 30}
+
+
 def _cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -544,7 +587,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
-    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,adapter,cq1,cq2,full,cpu")
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,vstack,adapter,cq1,cq2,full,cpu")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
@@ -581,6 +624,9 @@ def main() -> int:
     if "vstep" not in skip:
         log("V-only step workload (config 5)")
         extras["v_only_step"] = vstep_workload(args, device)
+    if "vstack" not in skip:
+        log("stacked V-only step (config 5 shape, 32 Mistral-7B-shaped layers) ...")
+        extras["v_only_stack_step"] = vstack_workload(args, device)
     if "adapter" not in skip:
         log("closed-loop attention layer step (config 5 shape)")
         extras["closed_loop_attention"] = adapter_workload(args, device)

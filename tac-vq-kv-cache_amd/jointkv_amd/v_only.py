@@ -86,17 +86,20 @@ class DecoderStack:
     def synthetic(cls, generator: torch.Generator, *, layers: int, hidden: int, kv_heads: int,
                   intermediate: int, vocab: int, head_dim: int = 128, window: int = MISTRAL_WINDOW,
                   rope_theta: float = MISTRAL_ROPE_THETA) -> "DecoderStack":
-        """Random fp16 weights of the given shape on the CPU (N(0, 1/fan_in)
-        matrices, norm weights near 1); move with :meth:`to`."""
+        """Random fp16 weights of the given shape (N(0, 1/fan_in) matrices,
+        norm weights near 1), drawn on the generator's device; move with
+        :meth:`to`."""
 
         if hidden % head_dim or layers <= 0 or kv_heads <= 0 or (hidden // head_dim) % kv_heads:
             raise ValueError("invalid synthetic decoder geometry")
 
+        dev = generator.device
+
         def mat(rows, cols):
-            return (torch.randn(rows, cols, generator=generator) / cols ** 0.5).half()
+            return (torch.randn(rows, cols, generator=generator, device=dev) / cols ** 0.5).half()
 
         def norm():
-            return (1.0 + 0.1 * torch.randn(hidden, generator=generator)).half()
+            return (1.0 + 0.1 * torch.randn(hidden, generator=generator, device=dev)).half()
 
         stack = []
         for _ in range(layers):
@@ -104,7 +107,7 @@ class DecoderStack:
                                          mat(head_dim * kv_heads, hidden), mat(hidden, hidden), head_dim)
             stack.append(DecoderLayerWeights(norm(), attention, norm(), mat(intermediate, hidden),
                                              mat(intermediate, hidden), mat(hidden, intermediate)))
-        return cls(torch.randn(vocab, hidden, generator=generator).half(), tuple(stack), norm(),
+        return cls(torch.randn(vocab, hidden, generator=generator, device=dev).half(), tuple(stack), norm(),
                    mat(vocab, hidden), window=window, rope_theta=rope_theta)
 
     def to(self, device) -> "DecoderStack":

@@ -53,11 +53,14 @@ class _Recording:
         return out
 
 
-@pytest.mark.parametrize("layers,tokens,steps", [(4, 160, 3)])
-def test_stacked_v_only_trajectory_matches_oracle(device, layers, tokens, steps):
-    print(f"stacked V-only layers={layers} T={tokens} steps={steps}", flush=True)
+@pytest.mark.parametrize("layers,tokens,steps,hidden,kvh,cap", [
+    (4, 160, 3, 512, 1, CAP),      # four layers, one kv head: lower layers clip, upper ones not
+    (2, 256, 2, 4096, 8, CAP),     # Mistral's attention width: hidden 4096, 32 query / 8 kv heads
+])
+def test_stacked_v_only_trajectory_matches_oracle(device, layers, tokens, steps, hidden, kvh, cap):
+    print(f"stacked V-only layers={layers} T={tokens} steps={steps} hidden={hidden} kv_heads={kvh}", flush=True)
     gen = torch.Generator().manual_seed(8601)
-    vocab, hidden, inter, kvh = 1000, 512, 1024, 1
+    vocab, inter = 1000, 1024  # the MLP and vocabulary stay small so the fp32 CPU oracle is quick
     stack = DecoderStack.synthetic(gen, layers=layers, hidden=hidden, kv_heads=kvh, intermediate=inter,
                                    vocab=vocab)
     shape = (kvh, 16, 2, 256, 8)  # GSRQ-2: 16 groups of 8 dims, two stages
@@ -75,7 +78,7 @@ def test_stacked_v_only_trajectory_matches_oracle(device, layers, tokens, steps)
         ids_d = ids.to(device)
         tables_before = [t.detach().cpu().clone() for t in codec.value_tables]
         res = v_only_step(context, lambda: run_loss(dstack, context, ids_d, mode="uniform"), step=step,
-                          maximum_norm=CAP)
+                          maximum_norm=cap)
         # the device's codes against the oracle's search of the device's raw K/V
         judged = equal = 0
         for layer in range(layers):
@@ -88,7 +91,7 @@ def test_stacked_v_only_trajectory_matches_oracle(device, layers, tokens, steps)
                 equal += int((ours.long() == own.long()).sum())
         assert equal / judged >= CODE_AGREEMENT, f"code agreement {equal / judged:.6f}"
         forced = [recording.codes[layer] for layer in range(layers)]
-        want = ref.v_only_stack_step(ids, weights, ktabs, oracle_tables, depth=2, maximum_norm=CAP,
+        want = ref.v_only_stack_step(ids, weights, ktabs, oracle_tables, depth=2, maximum_norm=cap,
                                      forced_codes=forced)
         oracle_tables = want["value_tables"]
         # how far the oracle's own hidden states would have moved the codes
@@ -120,6 +123,8 @@ def test_stacked_v_only_trajectory_matches_oracle(device, layers, tokens, steps)
             assert rel <= GRAD_RTOL, f"layer {layer} clipped gradient relative error {rel}"
             assert t_err <= 1e-6
         clipped_layers = sum(bool(r["clip_activated"]) for r in want["clip"]["per_group"] if r["kind"] == "value")
-        assert res["clipped_value_layers"] == clipped_layers and 0 < clipped_layers < layers
+        assert res["clipped_value_layers"] == clipped_layers
+        if layers == 4:
+            assert 0 < clipped_layers < layers
         # the key tables are frozen: no gradient
         assert all(t.grad is None for t in codec.key_tables)

@@ -112,7 +112,44 @@ __device__ __forceinline__ half8 rebuild8(const uint8_t* codes_tok, const _Float
   }
 }
 
-template <int D, int NQ>
+// Full-vector codebooks (one 128-dim group) with SS stages known at compile
+// time: dims [8 c8, 8 c8 + 8) of one token, the fp32 sum of its SS codewords'
+// 16-byte slices in stage order, cast once.  The token's code bytes come in
+// as dwords; the slice loads go out eight stages at a time, each group's
+// eight together.
+template <int SS>
+__device__ __forceinline__ half8 rebuild8_full(const uint8_t* codes_tok, const _Float16* tab_head, int c8) {
+  static_assert(SS % 8 == 0, "stages in groups of eight");
+  uint32_t cw[SS / 4];
+#pragma unroll
+  for (int i = 0; i < SS / 4; ++i) cw[i] = ((const uint32_t*)codes_tok)[i];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s0 = 0; s0 < SS; s0 += 8) {
+    half8 w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u;
+      const uint32_t code = __builtin_amdgcn_ubfe(cw[s >> 2], 8u * (uint32_t)(s & 3), 8u);
+      w[u] = *(const half8*)(tab_head + ((uint32_t)s * 256u + code) * 128u + 8u * (uint32_t)c8);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += (float)w[u][e];
+    // eight slices in flight per lane at a time: the register budget of
+    // four waves per SIMD
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  half8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (_Float16)acc[e];
+  return r;
+}
+
+// SS: the stage count of full-vector codebooks (D = 128) when it is 16 or
+// 32, else 0 (a.S at run time).
+template <int D, int NQ, int SS>
 __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   __shared__ _Float16 q_lds[NQ][kHeadDim];
   constexpr int kTok = D == 0 ? kWinSplitTokens : kSplitTokens;
@@ -128,10 +165,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int lg = lane >> 4, ln = lane & 15;
-  const int64_t split = blockIdx.x % a.n_splits;
-  const int64_t bk = blockIdx.x / a.n_splits;
-  const int64_t kvh = bk % a.KVH;
-  const int64_t b = bk / a.KVH;
+  // logical block: split fastest, then batch row, then kv head, so that the
+  // blocks of one kv head (its codebooks) sit on one XCD and share its L2
+  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t split = bid % (uint32_t)a.n_splits;
+  const int64_t b = (bid / (uint32_t)a.n_splits) % (uint32_t)a.B;
+  const int64_t kvh = bid / ((uint32_t)a.n_splits * (uint32_t)a.B);
   const int64_t L = a.lengths[b];
   const int64_t n_vis = L < a.window ? L : a.window;
   const int64_t start = L - n_vis;
@@ -215,9 +254,47 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       load_trig8(trow, 8 * lg, &kt.c0, &kt.s0);
       load_trig8(trow, 8 * (lg + 4), &kt.c1, &kt.s1);
     };
+    if constexpr (SS != 0) {
+      // full-vector codebooks with 16 or 32 stages: no tile runs ahead (a
+      // tile's slice loads alone fill the register budget); the four chunks
+      // are rebuilt eight stages at a time, then rotated and multiplied in
+      // the same order as below
+      const _Float16* ktab = a.kt + kvh * SS * 256 * 128;
+      for (int tile = wave; tile < ntiles; tile += 4) {
+        const int tt = tile * 16 + ln;
+        const bool valid = tt < ntok;
+        const int64_t pos = valid ? t0 + tt : t0;
+        const uint8_t* ct = key_codes(valid ? tt : 0);
+        const _Float16* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
+        half8 c0, s0, c1, s1;
+        load_trig8(trow, 8 * lg, &c0, &s0);
+        load_trig8(trow, 8 * (lg + 4), &c1, &s1);
+        half8 k[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) k[q] = rebuild8_full<SS>(ct, ktab, lg + 4 * q);
+        half8 r0, r1, r2, r3;
+        rope16(k[0], k[2], c0, s0, &r0, &r2);
+        rope16(k[1], k[3], c1, s1, &r1, &r3);
+        if (!valid) {
+          r0 = half8{}; r1 = half8{}; r2 = half8{}; r3 = half8{};
+        }
+        float4v acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r0, qb[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r1, qb[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2, qb[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r3, qb[3], acc, 0, 0, 0);
+        if (ln < NQ) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = tile * 16 + 4 * lg + r;
+            if (tok < ntok) s_lds[ln][tok] = acc[r] * scale;
+          }
+        }
+      }
+    }
     KTile nxt;
-    if (wave < ntiles) load_ktile(wave, nxt);
-    for (int tile = wave; tile < ntiles; tile += 4) {
+    if (SS == 0 && wave < ntiles) load_ktile(wave, nxt);
+    for (int tile = wave; SS == 0 && tile < ntiles; tile += 4) {
       const KTile cur = nxt;
       if (tile + 4 < ntiles) load_ktile(tile + 4, nxt);
       const bool valid = tile * 16 + ln < ntok;
@@ -292,8 +369,23 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
         v[u] = rebuild8<D>(value_codes(j < ntok ? j : j0), a.vt, kvh, a.G, S, ch);
       }
     };
-    if (tl < ntok) load_v(tl, vn);
-    for (int j0 = tl; j0 < ntok; j0 += 64) {
+    if constexpr (SS != 0) {
+      // full-vector codebooks with 16 or 32 stages: one token at a time (its
+      // slice loads alone fill the register budget), the products in the
+      // same order as below
+      const _Float16* vtab = a.vt + kvh * SS * 256 * 128;
+      for (int j = tl; j < ntok; j += 16) {
+        const half8 v = rebuild8_full<SS>(value_codes(j), vtab, ch);
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) {
+          const float p = s_lds[h][j];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[h][e] = fmaf(p, (float)v[e], o[h][e]);
+        }
+      }
+    }
+    if (SS == 0 && tl < ntok) load_v(tl, vn);
+    for (int j0 = tl; SS == 0 && j0 < ntok; j0 += 64) {
       half8 v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) v[u] = vn[u];
@@ -1411,13 +1503,26 @@ static bool packed_lds_ok(const void* k_codes, const void* v_codes, int64_t code
          code_stride_h % 16 == 0 && ((uintptr_t)k_tables % 16 == 0) && ((uintptr_t)v_tables % 16 == 0);
 }
 
+// The L2 split kernel, with the full-vector stage count as a template
+// argument where it is 16 or 32 (R16 / R32 codecs).
+template <int D, int NQ>
+static void launch_split(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 grid((uint32_t)(a.B * a.KVH * a.n_splits));
+  if (D == 128 && a.S == 16) {
+    hipLaunchKernelGGL((decode_split_kernel<D, NQ, 16>), grid, dim3(256), 0, stream, a);
+  } else if (D == 128 && a.S == 32) {
+    hipLaunchKernelGGL((decode_split_kernel<D, NQ, 32>), grid, dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_split_kernel<D, NQ, 0>), grid, dim3(256), 0, stream, a);
+  }
+}
+
 template <int D, int NQ>
 static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream, bool append = false) {
   const int64_t split = lds_ok && D != 128 && D != 0 ? lds_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
   const int64_t g8_split = lds_ok && D == 8 ? g8_split_tokens(a.G, a.S, a.K, NQ, a.window) : 0;
   if constexpr (D == 128 || D == 0) {
-    hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
-                       dim3(256), 0, stream, a);
+    launch_split<D, NQ>(a, stream);
   } else if (D == 8 && g8_split > 0) {
     a.split_tokens = (int32_t)g8_split;
     a.n_splits = (int32_t)ceil_div(a.window, g8_split);
@@ -1452,8 +1557,7 @@ static int launch_decode(DecodeArgs a, bool lds_ok, hipStream_t stream, bool app
       hipLaunchKernelGGL((decode_lds_kernel<D, NQ, 1>), grid, dim3(kLdsThreads), lds, stream, a);
     }
   } else {
-    hipLaunchKernelGGL((decode_split_kernel<D, NQ>), dim3((uint32_t)(a.B * a.KVH * a.n_splits)),
-                       dim3(256), 0, stream, a);
+    launch_split<D, NQ>(a, stream);
   }
   JKV_CHECK_LAUNCH();
   hipLaunchKernelGGL(decode_combine_kernel, dim3((uint32_t)(a.B * a.QH)), dim3(kHeadDim), 0,

@@ -309,6 +309,40 @@ def decode_workload(args, device):
     }
 
 
+def full_decode_workload(args, device):
+    """Packed-code decode for the reference's full-vector codecs (one 128-dim
+    group, R16 / R32: 16 or 32 stages of 256 fp16 codewords per kv head,
+    train_mistral_v_only.py:58-62) at config 4's shape (B16, 32/8 heads,
+    4096-token window): us per layer, and the decoded-window path
+    (evaluate_mistral_longbench.py:44-70) over the same shape."""
+
+    import torch
+    from jointkv_amd import _ops
+
+    batch, qh, kvh, window = 16, 32, 8, 4096
+    gen = torch.Generator(device=device).manual_seed(8611)
+    q = torch.randn(batch, qh, HEAD_DIM, generator=gen, device=device).half()
+    lengths = torch.full((batch,), window, dtype=torch.int32, device=device)
+    out = {}
+    for stages in (16, 32):
+        sig = torch.tensor([0.8 ** s for s in range(stages)], device=device)
+        kt = (torch.randn(kvh, stages, CLUSTERS, HEAD_DIM, generator=gen, device=device) * sig[None, :, None, None]).half()
+        vt = (torch.randn(kvh, stages, CLUSTERS, HEAD_DIM, generator=gen, device=device) * sig[None, :, None, None]).half()
+        kc = torch.randint(0, 256, (batch, kvh, window, 1, stages), generator=gen, device=device, dtype=torch.uint8)
+        vc = torch.randint(0, 256, (batch, kvh, window, 1, stages), generator=gen, device=device, dtype=torch.uint8)
+        f = lambda: _ops.decode_attention(q, kc, vc, kt, vt, lengths, window=window, rope_theta=10000.0,
+                                          max_length=window)
+        out[f"r{stages}_packed_us_per_layer"] = per_launch_ms([f] * 20) * 1e3
+        # codeword bytes gathered per layer (K and V), the path's L2 traffic
+        out[f"r{stages}_gathered_bytes_per_layer"] = 2 * batch * kvh * window * stages * CLUSTERS
+    kw = torch.randn(batch, kvh, window, HEAD_DIM, generator=gen, device=device).half()
+    vw = torch.randn(batch, kvh, window, HEAD_DIM, generator=gen, device=device).half()
+    f = lambda: _ops.decode_attention_window(q, kw, vw, lengths, window=window, rope_theta=10000.0,
+                                             max_length=window)
+    out["decoded_window_us_per_layer"] = per_launch_ms([f] * 20) * 1e3
+    return out
+
+
 def prefill_workload(args, device):
     """Config 4 prefill chunk: 2048 tokens, B16, 32/8 heads, causal with the
     4096 sliding window, fp16 K/V as the codec reconstructs them; 32 layers
@@ -587,7 +621,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--cpu-tokens", type=int, default=2048)
-    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,prefill,vstep,vstack,adapter,cq1,cq2,full,cpu")
+    parser.add_argument("--skip", default="", help="comma list of extras to skip: decode,rdecode,prefill,vstep,vstack,adapter,cq1,cq2,full,cpu")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the 256 MiB copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = parser.parse_args()
@@ -618,6 +652,9 @@ def main() -> int:
     if "decode" not in skip:
         log("decode workload (config 4)")
         extras["decode"] = decode_workload(args, device)
+    if "rdecode" not in skip:
+        log("full-vector (R16/R32) packed decode ...")
+        extras["full_vector_decode"] = full_decode_workload(args, device)
     if "prefill" not in skip:
         log("prefill workload (config 4 prefill chunk)")
         extras["prefill"] = prefill_workload(args, device)

@@ -113,38 +113,58 @@ __device__ __forceinline__ half8 rebuild8(const uint8_t* codes_tok, const _Float
 }
 
 // Full-vector codebooks (one 128-dim group) with SS stages known at compile
-// time: dims [8 c8, 8 c8 + 8) of one token, the fp32 sum of its SS codewords'
-// 16-byte slices in stage order, cast once.  The token's code bytes come in
-// as dwords; the slice loads go out eight stages at a time, each group's
-// eight together.
-template <int SS>
-__device__ __forceinline__ half8 rebuild8_full(const uint8_t* codes_tok, const _Float16* tab_head, int c8) {
-  static_assert(SS % 8 == 0, "stages in groups of eight");
-  uint32_t cw[SS / 4];
+// time.  gather_sum adds up N items of SS 16-byte codeword slices each (8
+// dims of one token) and hands item i to done(i, acc) with acc = the fp32
+// sum over stages s of slice(i, s), in stage order.  The slices stream in
+// groups of kGatherStages, one group ahead of the group being summed, so two
+// groups are in flight per lane.  Each add is one v_fma_mix_f32 taking the
+// fp16 word as it is: x * 1 + acc rounds once, exactly as the fp32 add of the
+// converted word.
+constexpr int kGatherStages = 4;
+
+template <int N, int SS, typename Slice, typename Done>
+__device__ __forceinline__ void gather_sum(Slice slice, Done done) {
+  constexpr int GS = kGatherStages;
+  static_assert(SS % GS == 0, "whole groups of stages");
+  constexpr int G = SS / GS, T = N * G;
+  _Float16 one = (_Float16)1.f;
+  asm volatile("" : "+v"(one));  // an opaque 1, so the fma is not folded back into cvt + add
+  float acc[8];
+  half8 buf[2][GS];
+  auto issue = [&](int t, half8 (&b)[GS]) {
 #pragma unroll
-  for (int i = 0; i < SS / 4; ++i) cw[i] = ((const uint32_t*)codes_tok)[i];
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < GS; ++u) b[u] = slice(t / G, GS * (t % G) + u);
+  };
+  issue(0, buf[0]);
 #pragma unroll
-  for (int s0 = 0; s0 < SS; s0 += 8) {
-    half8 w[8];
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 < T) issue(t + 1, buf[(t + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t % G == 0)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u;
-      const uint32_t code = __builtin_amdgcn_ubfe(cw[s >> 2], 8u * (uint32_t)(s & 3), 8u);
-      w[u] = *(const half8*)(tab_head + ((uint32_t)s * 256u + code) * 128u + 8u * (uint32_t)c8);
-    }
+      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < GS; ++u)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += (float)w[u][e];
-    // eight slices in flight per lane at a time: the register budget of
-    // four waves per SIMD
+      for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf((float)buf[t & 1][u][e], (float)one, acc[e]);
+    if (t % G == G - 1) done(t / G, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
-  half8 r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (_Float16)acc[e];
-  return r;
+}
+
+// one 16-byte codeword slice of a stage table (SS x 256 x 128 fp16, 64 KiB a
+// stage) held in a buffer resource: the stage offset is uniform (scalar), the
+// code and chunk a 32-bit lane offset, and a read past the resource's size
+// returns zeros
+__device__ __forceinline__ half8 table_slice(__amdgpu_buffer_rsrc_t tab, int stage, uint32_t code, int c8) {
+  const auto w = __builtin_amdgcn_raw_buffer_load_b128(tab, (int)(code * 256u + 16u * (uint32_t)c8), stage * 65536, 0);
+  return __builtin_bit_cast(half8, w);
+}
+
+// the stage-s code of a token whose SS code bytes are held as dwords
+template <int SS>
+__device__ __forceinline__ uint32_t stage_code(const uint32_t (&cw)[SS / 4], int s) {
+  return __builtin_amdgcn_ubfe(cw[s >> 2], 8u * (uint32_t)(s & 3), 8u);
 }
 
 // SS: the stage count of full-vector codebooks (D = 128) when it is 16 or
@@ -255,11 +275,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       load_trig8(trow, 8 * (lg + 4), &kt.c1, &kt.s1);
     };
     if constexpr (SS != 0) {
-      // full-vector codebooks with 16 or 32 stages: no tile runs ahead (a
-      // tile's slice loads alone fill the register budget); the four chunks
-      // are rebuilt eight stages at a time, then rotated and multiplied in
-      // the same order as below
-      const _Float16* ktab = a.kt + kvh * SS * 256 * 128;
+      // full-vector codebooks with 16 or 32 stages: no tile runs ahead (the
+      // slice loads in flight fill the register budget); the four chunks are
+      // gathered one after another through gather_sum, then rotated and
+      // multiplied in the same order as below
+      const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(a.kt + kvh * SS * 256 * 128), (short)0, SS * 65536, 0x00020000);
       for (int tile = wave; tile < ntiles; tile += 4) {
         const int tt = tile * 16 + ln;
         const bool valid = tt < ntok;
@@ -269,9 +290,16 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
         half8 c0, s0, c1, s1;
         load_trig8(trow, 8 * lg, &c0, &s0);
         load_trig8(trow, 8 * (lg + 4), &c1, &s1);
-        half8 k[4];
+        uint32_t cw[SS / 4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) k[q] = rebuild8_full<SS>(ct, ktab, lg + 4 * q);
+        for (int i = 0; i < SS / 4; ++i) cw[i] = ((const uint32_t*)ct)[i];
+        half8 k[4];
+        gather_sum<4, SS>([&](int q, int st) {
+          return table_slice(krsrc, st, stage_code<SS>(cw, st), lg + 4 * q);
+        }, [&](int q, const float (&acc)[8]) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) k[q][e] = (_Float16)acc[e];
+        });
         half8 r0, r1, r2, r3;
         rope16(k[0], k[2], c0, s0, &r0, &r2);
         rope16(k[1], k[3], c1, s1, &r1, &r3);
@@ -370,18 +398,36 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       }
     };
     if constexpr (SS != 0) {
-      // full-vector codebooks with 16 or 32 stages: one token at a time (its
-      // slice loads alone fill the register budget), the products in the
-      // same order as below
-      const _Float16* vtab = a.vt + kvh * SS * 256 * 128;
-      for (int j = tl; j < ntok; j += 16) {
-        const half8 v = rebuild8_full<SS>(value_codes(j), vtab, ch);
+      // full-vector codebooks with 16 or 32 stages: two tokens per gather_sum
+      // (the slice loads in flight fill the register budget), the products in
+      // token order as below
+      const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(a.vt + kvh * SS * 256 * 128), (short)0, SS * 65536, 0x00020000);
+      for (int j = tl; j < ntok; j += 32) {
+        // tokens j and j + 16 (the second past the split reads the first's
+        // codes and is not used)
+        const int j2 = j + 16 < ntok ? j + 16 : j;
+        uint32_t cw[2][SS / 4];
 #pragma unroll
-        for (int h = 0; h < NQ; ++h) {
-          const float p = s_lds[h][j];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[h][e] = fmaf(p, (float)v[e], o[h][e]);
+        for (int i = 0; i < SS / 4; ++i) {
+          cw[0][i] = ((const uint32_t*)value_codes(j))[i];
+          cw[1][i] = ((const uint32_t*)value_codes(j2))[i];
         }
+        gather_sum<2, SS>([&](int u, int st) {
+          return table_slice(vrsrc, st, stage_code<SS>(cw[u], st), ch);
+        }, [&](int u, const float (&acc)[8]) {
+          if (u == 1 && j + 16 >= ntok) return;
+          const int jj = j + 16 * u;
+          half8 v;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (_Float16)acc[e];
+#pragma unroll
+          for (int h = 0; h < NQ; ++h) {
+            const float p = s_lds[h][jj];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[h][e] = fmaf(p, (float)v[e], o[h][e]);
+          }
+        });
       }
     }
     if (SS == 0 && tl < ntok) load_v(tl, vn);
@@ -1508,13 +1554,17 @@ static bool packed_lds_ok(const void* k_codes, const void* v_codes, int64_t code
 template <int D, int NQ>
 static void launch_split(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid((uint32_t)(a.B * a.KVH * a.n_splits));
-  if (D == 128 && a.S == 16) {
-    hipLaunchKernelGGL((decode_split_kernel<D, NQ, 16>), grid, dim3(256), 0, stream, a);
-  } else if (D == 128 && a.S == 32) {
-    hipLaunchKernelGGL((decode_split_kernel<D, NQ, 32>), grid, dim3(256), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((decode_split_kernel<D, NQ, 0>), grid, dim3(256), 0, stream, a);
+  if constexpr (D == 128) {
+    if (a.S == 16) {
+      hipLaunchKernelGGL((decode_split_kernel<D, NQ, 16>), grid, dim3(256), 0, stream, a);
+      return;
+    }
+    if (a.S == 32) {
+      hipLaunchKernelGGL((decode_split_kernel<D, NQ, 32>), grid, dim3(256), 0, stream, a);
+      return;
+    }
   }
+  hipLaunchKernelGGL((decode_split_kernel<D, NQ, 0>), grid, dim3(256), 0, stream, a);
 }
 
 template <int D, int NQ>

@@ -120,6 +120,7 @@ EXACT_CASES = [
     # (B, H, T, G, d, S, exits): one chunk, row chunks (one head), several
     # exits, full-vector RVQ (d = 128 in 8-dim slices), grouped CQ (d = 4)
     (4, 8, 200, 16, 8, 2, (2,)),
+    (4, 8, 2048, 16, 8, 2, (2,)),  # config-5 layer: 8192 rows per (head, group, stage) block
     (2, 8, 100, 16, 8, 2, (1, 2)),  # one block per (head, group, stage), two exits
     (4, 1, 2048, 16, 8, 2, (2,)),
     (4, 1, 2048, 16, 8, 2, (1, 2)),

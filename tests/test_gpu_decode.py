@@ -47,6 +47,9 @@ def _expect(q, kc, vc, kt, vt, length, window, cap):
     (1, 8, 2, 16, 3, 8, 600, 4096, 4096),     # three stages: the generic split kernel
     (1, 8, 2, 1, 4, 128, 600, 4096, 4096),    # full-vector codebooks, 4 stages (codewords from L2)
     (2, 32, 8, 1, 16, 128, 700, 256, 512),    # full-vector R16 geometry, sliding window, ring wraps
+    (1, 16, 2, 1, 16, 128, 300, 4096, 512),   # R16 codes, GQA 8
+    (1, 8, 2, 1, 32, 128, 333, 4096, 512),    # R32 codes, ragged last tile
+    (1, 2, 2, 1, 32, 128, 170, 4096, 256),    # R32 codes, one query head per kv head
 ])
 def test_decode_matches_oracle(device, batch, qh, kvh, groups, stages, d, length, window, cap):
     q, kc, vc, kt, vt = _case(length + qh, batch, qh, kvh, groups, stages, d, length, cap)

@@ -178,9 +178,13 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   __shared__ float o_red[4][NQ][kHeadDim];
   // the split's K and V code records (up to 64 bytes per token), fetched once
   // (a decoded window, D = 0, reads its rows from global memory instead)
-  constexpr int kRecLds = D == 0 ? 16 : kTok * kMaxCodeBytes;
+  constexpr int kRecLds = D == 0 ? 16 : kTok * (SS != 0 ? SS : kMaxCodeBytes);
   __shared__ __align__(16) uint8_t kc_lds[kRecLds];
   __shared__ __align__(16) uint8_t vc_lds[kRecLds];
+  // SS != 0: each wave's rotated 16-key K tile, rebuilt in the gather layout
+  // and read back in the MFMA layout (rows padded to 272 bytes)
+  constexpr int kKRow = kHeadDim + 8;
+  __shared__ __align__(16) _Float16 kt_lds[SS != 0 ? 4 : 1][SS != 0 ? 16 * kKRow : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -224,7 +228,8 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     }
   }
   // ---- the split's code records into LDS, 16-byte chunks, one pass ----
-  const bool codes_in_lds = D != 0 && code_bytes <= kMaxCodeBytes && (code_bytes % 16) == 0;
+  const bool codes_in_lds = D != 0 && code_bytes <= kMaxCodeBytes && (code_bytes % 16) == 0 &&
+                            code_bytes * kTok <= kRecLds;
   if (codes_in_lds) {
     const int per_tok = (int)(code_bytes / 16);
     const int64_t kbase = b * a.csb + kvh * a.csh;
@@ -276,46 +281,65 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     };
     if constexpr (SS != 0) {
       // full-vector codebooks with 16 or 32 stages: no tile runs ahead (the
-      // slice loads in flight fill the register budget); the four chunks are
-      // gathered one after another through gather_sum, then rotated and
-      // multiplied in the same order as below
+      // slice loads in flight fill the register budget).  The gather runs in
+      // its own layout: lane (t8, c8) = (lane / 8, lane % 8) rebuilds dims
+      // [8c8, 8c8 + 8) and their rotary partners [64 + 8c8, ..) of keys t8 and
+      // 8 + t8 of the tile, so each slice load covers whole 128-byte lines
+      // of eight codeword rows (half the lines per load of the MFMA layout).
+      // Each chunk is the fp32 stage sum in stage order rounded to fp16,
+      // rotated as below; the rotated rows pass through LDS into the MFMA
+      // layout, so the products are those of the path below.
       const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(a.kt + kvh * SS * 256 * 128), (short)0, SS * 65536, 0x00020000);
+      const int t8 = lane >> 3, c8 = lane & 7;
+      _Float16* const ktile = kt_lds[SS != 0 ? wave : 0];
       for (int tile = wave; tile < ntiles; tile += 4) {
-        const int tt = tile * 16 + ln;
-        const bool valid = tt < ntok;
-        const int64_t pos = valid ? t0 + tt : t0;
-        const uint8_t* ct = key_codes(valid ? tt : 0);
-        const _Float16* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
-        half8 c0, s0, c1, s1;
-        load_trig8(trow, 8 * lg, &c0, &s0);
-        load_trig8(trow, 8 * (lg + 4), &c1, &s1);
-        uint32_t cw[SS / 4];
+        uint32_t cw[2][SS / 4];
+        half8 cs[2], sn[2];
+        bool valid[2];
 #pragma unroll
-        for (int i = 0; i < SS / 4; ++i) cw[i] = ((const uint32_t*)ct)[i];
-        half8 k[4];
-        gather_sum<4, SS>([&](int q, int st) {
-          return table_slice(krsrc, st, stage_code<SS>(cw, st), lg + 4 * q);
-        }, [&](int q, const float (&acc)[8]) {
+        for (int h = 0; h < 2; ++h) {
+          const int tt = tile * 16 + 8 * h + t8;
+          valid[h] = tt < ntok;
+          const int64_t pos = valid[h] ? t0 + tt : t0;
+          const uint8_t* ct = key_codes(valid[h] ? tt : 0);
+          const _Float16* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
+          load_trig8(trow, 8 * c8, &cs[h], &sn[h]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) k[q][e] = (_Float16)acc[e];
-        });
-        half8 r0, r1, r2, r3;
-        rope16(k[0], k[2], c0, s0, &r0, &r2);
-        rope16(k[1], k[3], c1, s1, &r1, &r3);
-        if (!valid) {
-          r0 = half8{}; r1 = half8{}; r2 = half8{}; r3 = half8{};
+          for (int i = 0; i < SS / 4; ++i) cw[h][i] = ((const uint32_t*)ct)[i];
         }
+        half8 kh[2][2];  // [key half][dims 8c8.. | 64 + 8c8..]
+        gather_sum<4, SS>([&](int i, int st) {
+          return table_slice(krsrc, st, stage_code<SS>(cw[i >> 1], st), c8 + 8 * (i & 1));
+        }, [&](int i, const float (&acc)[8]) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kh[i >> 1][i & 1][e] = (_Float16)acc[e];
+        });
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          half8 r0, r1;
+          rope16(kh[h][0], kh[h][1], cs[h], sn[h], &r0, &r1);
+          if (!valid[h]) {
+            r0 = half8{}; r1 = half8{};
+          }
+          _Float16* row = ktile + (8 * h + t8) * kKRow;
+          *(half8*)(row + 8 * c8) = r0;
+          *(half8*)(row + 64 + 8 * c8) = r1;
+        }
+        // MFMA layout: lane (ln, lg) holds chunk lg + 4m of key ln for MFMA m
+        half8 r[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) r[m] = *(const half8*)(ktile + ln * kKRow + 8 * (lg + 4 * m));
         float4v acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r0, qb[0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r1, qb[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2, qb[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r3, qb[3], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[0], qb[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[1], qb[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[2], qb[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[3], qb[3], acc, 0, 0, 0);
         if (ln < NQ) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = tile * 16 + 4 * lg + r;
-            if (tok < ntok) s_lds[ln][tok] = acc[r] * scale;
+          for (int rr = 0; rr < 4; ++rr) {
+            const int tok = tile * 16 + 4 * lg + rr;
+            if (tok < ntok) s_lds[ln][tok] = acc[rr] * scale;
           }
         }
       }

@@ -28,11 +28,14 @@ one rounding order among many); the deploy keeps the fp16 rounding and the
 search keeps fp32, which decide what the fitted codec is.
 
 Pins (tests/test_gain_shape_oracle.py): the per-codeword sums and update
-against a hand-worked example; a fit of exact gain-shape data whose
+against a hand-worked example; the lloyd update as the plain mean of each
+codeword's rows, worked by hand; a fit of exact gain-shape data whose
 codewords must come out as fp16(gain * shape) of the data; the whitened
 deploy against the goal it solves for; invariants (unit shapes, gains in
 [0, cap], the reserved zero codeword, non-increasing residual energy on
-clustered data).  The search is the additive oracle's ``nearest``, pinned
+clustered data); ``parent_residuals`` against the greedy operator
+``jointkv_oracle.hard_residual_vq_exits`` (itself pinned by an exhaustive
+float64 search).  The search is the additive oracle's ``nearest``, pinned
 against an exhaustive float64 search there.
 """
 

@@ -181,10 +181,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
   constexpr int kRecLds = D == 0 ? 16 : kTok * (SS != 0 ? SS : kMaxCodeBytes);
   __shared__ __align__(16) uint8_t kc_lds[kRecLds];
   __shared__ __align__(16) uint8_t vc_lds[kRecLds];
-  // SS != 0: each wave's rotated 16-key K tile, rebuilt in the gather layout
-  // and read back in the MFMA layout (rows padded to 272 bytes)
+  // SS != 0 and the decoded window (D = 0): each wave's rotated 16-key K
+  // tile, built in the line layout and read back in the MFMA layout (rows
+  // padded to 272 bytes)
+  constexpr bool kLineK = SS != 0 || D == 0;
   constexpr int kKRow = kHeadDim + 8;
-  __shared__ __align__(16) _Float16 kt_lds[SS != 0 ? 4 : 1][SS != 0 ? 16 * kKRow : 8];
+  __shared__ __align__(16) _Float16 kt_lds[kLineK ? 4 : 1][kLineK ? 16 * kKRow : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -279,47 +281,39 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       load_trig8(trow, 8 * lg, &kt.c0, &kt.s0);
       load_trig8(trow, 8 * (lg + 4), &kt.c1, &kt.s1);
     };
-    if constexpr (SS != 0) {
-      // full-vector codebooks with 16 or 32 stages: no tile runs ahead (the
-      // slice loads in flight fill the register budget).  The gather runs in
-      // its own layout: lane (t8, c8) = (lane / 8, lane % 8) rebuilds dims
-      // [8c8, 8c8 + 8) and their rotary partners [64 + 8c8, ..) of keys t8 and
-      // 8 + t8 of the tile, so each slice load covers whole 128-byte lines
-      // of eight codeword rows (half the lines per load of the MFMA layout).
-      // Each chunk is the fp32 stage sum in stage order rounded to fp16,
-      // rotated as below; the rotated rows pass through LDS into the MFMA
-      // layout, so the products are those of the path below.
-      const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(a.kt + kvh * SS * 256 * 128), (short)0, SS * 65536, 0x00020000);
+    if constexpr (kLineK) {
+      // The line layout: lane (t8, c8) = (lane / 8, lane % 8) holds dims
+      // [8c8, 8c8 + 8) and their rotary partners [64 + 8c8, ..) of keys t8
+      // and 8 + t8 of a 16-key tile, so each 16-byte load covers whole
+      // 128-byte lines of eight rows (codeword rows, or the decoded window's
+      // K rows): half the lines per load of the MFMA layout, and the vector
+      // memory path pays per line.  The rotated rows pass through a per-wave
+      // LDS tile into the MFMA layout, so the products are those of the
+      // path below.
       const int t8 = lane >> 3, c8 = lane & 7;
-      _Float16* const ktile = kt_lds[SS != 0 ? wave : 0];
-      for (int tile = wave; tile < ntiles; tile += 4) {
-        uint32_t cw[2][SS / 4];
-        half8 cs[2], sn[2];
+      _Float16* const ktile = kt_lds[kLineK ? wave : 0];
+      struct LineTile {
+        half8 k[2][2], cs[2], sn[2];  // [key half][dims 8c8.. | 64 + 8c8..]
         bool valid[2];
+      };
+      // the tile's rotary rows and validity; key records for the gather
+      auto tile_keys = [&](int tile, LineTile& w, const uint8_t* (&ct)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int tt = tile * 16 + 8 * h + t8;
-          valid[h] = tt < ntok;
-          const int64_t pos = valid[h] ? t0 + tt : t0;
-          const uint8_t* ct = key_codes(valid[h] ? tt : 0);
+          w.valid[h] = tt < ntok;
+          const int64_t pos = w.valid[h] ? t0 + tt : t0;
+          ct[h] = key_codes(w.valid[h] ? tt : 0);
           const _Float16* trow = a.rope + (pos < a.rope_len ? pos : a.rope_len - 1) * kRopeRow;
-          load_trig8(trow, 8 * c8, &cs[h], &sn[h]);
-#pragma unroll
-          for (int i = 0; i < SS / 4; ++i) cw[h][i] = ((const uint32_t*)ct)[i];
+          load_trig8(trow, 8 * c8, &w.cs[h], &w.sn[h]);
         }
-        half8 kh[2][2];  // [key half][dims 8c8.. | 64 + 8c8..]
-        gather_sum<4, SS>([&](int i, int st) {
-          return table_slice(krsrc, st, stage_code<SS>(cw[i >> 1], st), c8 + 8 * (i & 1));
-        }, [&](int i, const float (&acc)[8]) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kh[i >> 1][i & 1][e] = (_Float16)acc[e];
-        });
+      };
+      auto tile_scores = [&](int tile, const LineTile& w) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           half8 r0, r1;
-          rope16(kh[h][0], kh[h][1], cs[h], sn[h], &r0, &r1);
-          if (!valid[h]) {
+          rope16(w.k[h][0], w.k[h][1], w.cs[h], w.sn[h], &r0, &r1);
+          if (!w.valid[h]) {
             r0 = half8{}; r1 = half8{};
           }
           _Float16* row = ktile + (8 * h + t8) * kKRow;
@@ -342,11 +336,53 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
             if (tok < ntok) s_lds[ln][tok] = acc[rr] * scale;
           }
         }
+      };
+      if constexpr (D == 0) {
+        // decoded window: the rows stream from HBM, one tile ahead
+        auto load_rows = [&](int tile, LineTile& w) {
+          const uint8_t* ct[2];
+          tile_keys(tile, w, ct);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            w.k[h][0] = *(const half8*)(ct[h] + 16 * c8);
+            w.k[h][1] = *(const half8*)(ct[h] + 16 * (c8 + 8));
+          }
+        };
+        LineTile nxt;
+        if (wave < ntiles) load_rows(wave, nxt);
+        for (int tile = wave; tile < ntiles; tile += 4) {
+          const LineTile cur = nxt;
+          if (tile + 4 < ntiles) load_rows(tile + 4, nxt);
+          tile_scores(tile, cur);
+        }
+      } else {
+        // full-vector codebooks with 16 or 32 stages: each chunk is the fp32
+        // stage sum in stage order rounded to fp16; no tile runs ahead (the
+        // slice loads in flight fill the register budget)
+        const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.kt + kvh * SS * 256 * 128), (short)0, SS * 65536, 0x00020000);
+        for (int tile = wave; tile < ntiles; tile += 4) {
+          LineTile w;
+          const uint8_t* ct[2];
+          tile_keys(tile, w, ct);
+          uint32_t cw[2][SS != 0 ? SS / 4 : 1];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < SS / 4; ++i) cw[h][i] = ((const uint32_t*)ct[h])[i];
+          gather_sum<4, SS>([&](int i, int st) {
+            return table_slice(krsrc, st, stage_code<SS>(cw[i >> 1], st), c8 + 8 * (i & 1));
+          }, [&](int i, const float (&acc)[8]) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w.k[i >> 1][i & 1][e] = (_Float16)acc[e];
+          });
+          tile_scores(tile, w);
+        }
       }
     }
     KTile nxt;
-    if (SS == 0 && wave < ntiles) load_ktile(wave, nxt);
-    for (int tile = wave; SS == 0 && tile < ntiles; tile += 4) {
+    if (!kLineK && wave < ntiles) load_ktile(wave, nxt);
+    for (int tile = wave; !kLineK && tile < ntiles; tile += 4) {
       const KTile cur = nxt;
       if (tile + 4 < ntiles) load_ktile(tile + 4, nxt);
       const bool valid = tile * 16 + ln < ntok;

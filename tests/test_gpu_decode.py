@@ -300,3 +300,43 @@ def test_decoded_window_cache_equals_packed_decode(device):
         assert torch.equal(a, b), f"step {step}: window and packed decode differ"
     assert torch.equal(win.codes.key, packed.key) and win.length == packed.length == 11
     assert win.payload_bytes() == packed.payload_bytes()
+
+
+@pytest.mark.parametrize("stages", [16, 32])
+def test_decoded_window_equals_packed_decode_over_many_splits(device, stages):
+    # 700 tokens through 512-slot rings (the second append wraps), then
+    # windows of 256, 512 and 300 tokens: every key tile and wave of both
+    # kernels, ragged last tiles, GQA 4.  Within one split the two kernels
+    # form the same products in the same order, so a window that each covers
+    # with one split (256 tokens) gives the same bits; longer windows are
+    # split at 512 tokens by the window kernel and at 256 by the packed one,
+    # so their split combines add in different orders and the outputs agree
+    # to fp32 rounding of the fp16 result
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(8619 + stages)
+    kvh, batch, cap = 2, 2, 512
+    sig = tuple(0.8 ** s for s in range(stages))
+    tk = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1).to(device)
+    tv = ref.synthetic_tables(gen, (kvh, stages, 256, 128), sig, stage_axis=1).to(device)
+    win = jkv.DecodedWindowCache(batch, kvh, 1, stages, capacity=cap, device=device)
+    packed = jkv.PackedCodeCache(batch, kvh, 1, stages, capacity=cap, device=device)
+    for tokens in (400, 300):
+        k = ref.synthetic_states(gen, batch, kvh, tokens).to(device)
+        v = ref.synthetic_states(gen, batch, kvh, tokens).to(device)
+        (rk,), ck = _ops.rvq_encode(k, tk, groups=1, group_dim=128, exits=(stages,))
+        (rv,), cv = _ops.rvq_encode(v, tv, groups=1, group_dim=128, exits=(stages,))
+        win.append(ck, cv, rk, rv)
+        packed.append(ck, cv)
+    assert packed.length == 700
+    q = torch.randn(batch, 8, 1, 128, generator=gen).half().to(device)
+    for window in (256, cap, 300):
+        print(f"window and packed decode S={stages} len=700 window={window}", flush=True)
+        a = win.attention(q, window=window)
+        b = jkv.decode_attention(q, packed.key, packed.value, tk.half(), tv.half(), packed.lengths,
+                                 window=window, max_length=packed.length)
+        if window <= 256:
+            assert torch.equal(a, b), f"window {window}: window and packed decode differ"
+        else:
+            err = float((a.float() - b.float()).abs().max())
+            assert err <= 2e-3 * max(1.0, float(a.float().abs().max())), f"window {window}: max abs difference {err}"

@@ -14,13 +14,16 @@ from oracle import jointkv_oracle as ref
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(seed, batch, qh, kvh, length, cap, device):
+def _inputs(seed, batch, qh, kvh, length, cap, device, groups=16, stages=2):
+    # G2 codes by default; groups=1, stages=16/32 gives full-vector R16/R32
     gen = torch.Generator().manual_seed(seed)
+    d = 128 // groups
+    sig = (1.0, 0.5) if stages == 2 else tuple(0.8 ** s for s in range(stages))
     q = torch.randn(batch, qh, 128, generator=gen).half().to(device)
-    kc = torch.randint(0, 256, (batch, kvh, cap, 16, 2), generator=gen, dtype=torch.uint8).to(device)
-    vc = torch.randint(0, 256, (batch, kvh, cap, 16, 2), generator=gen, dtype=torch.uint8).to(device)
-    kt = ref.synthetic_tables(gen, (kvh * 16, 2, 256, 8), (1.0, 0.5), stage_axis=1).half().to(device)
-    vt = ref.synthetic_tables(gen, (kvh * 16, 2, 256, 8), (1.0, 0.5), stage_axis=1).half().to(device)
+    kc = torch.randint(0, 256, (batch, kvh, cap, groups, stages), generator=gen, dtype=torch.uint8).to(device)
+    vc = torch.randint(0, 256, (batch, kvh, cap, groups, stages), generator=gen, dtype=torch.uint8).to(device)
+    kt = ref.synthetic_tables(gen, (kvh * groups, stages, 256, d), sig, stage_axis=1).half().to(device)
+    vt = ref.synthetic_tables(gen, (kvh * groups, stages, 256, d), sig, stage_axis=1).half().to(device)
     lengths = torch.randint(max(1, length // 2), length + 1, (batch,), generator=gen, dtype=torch.int32)
     lengths[0] = length
     return q, kc, vc, kt, vt, lengths.to(device)
@@ -30,8 +33,8 @@ def _args(q, kc, vc, kt, vt, lengths, window, table, out):
     batch, qh, _d = q.shape
     _b, kvh, cap, groups, stages = kc.shape
     return [q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), cap,
-            kt.data_ptr(), vt.data_ptr(), batch, qh, kvh, groups, 8, stages, 256, lengths.data_ptr(), window,
-            table.data_ptr(), int(table.shape[0]), out.data_ptr()]
+            kt.data_ptr(), vt.data_ptr(), batch, qh, kvh, groups, 128 // groups, stages, 256, lengths.data_ptr(),
+            window, table.data_ptr(), int(table.shape[0]), out.data_ptr()]
 
 
 def _both(device, q, kc, vc, kt, vt, lengths, window):
@@ -70,6 +73,19 @@ def test_noalloc_decode_matches_workspace_decode_on_two_calls(device):
         expect = ref.decode_attention(q[b : b + 1, :, None], khat, vhat, L - 1, pos)
         err = float((out[b : b + 1].cpu().float() - expect[:, :, 0].float()).abs().max())
         assert err <= 2e-3, f"batch {b}: {err}"
+
+
+def test_noalloc_decode_full_vector_codes(device):
+    # the full-vector (R16 / R32) kernels through the same scratch: 256-token
+    # splits, a larger call, then a smaller one with fewer splits
+    print("noalloc decode R16: B=4 QH=32 KVH=8 window=1024", flush=True)
+    first = _inputs(7, 4, 32, 8, 1024, 1024, device, groups=1, stages=16)
+    ref_out, out = _both(device, *first, 1024)
+    assert torch.equal(out, ref_out)
+    print("noalloc decode R32: B=1 QH=8 KVH=2 window=300", flush=True)
+    second = _inputs(8, 1, 8, 2, 290, 512, device, groups=1, stages=32)
+    ref_out, out = _both(device, *second, 300)
+    assert torch.equal(out, ref_out)
 
 
 def test_noalloc_decode_sizes_partials_by_the_kernel_it_runs(device):

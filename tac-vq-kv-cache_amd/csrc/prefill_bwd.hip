@@ -154,45 +154,69 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
   const TileRun run = tile_run(key0, a.T, a.window, a.chunk_tiles, a.slots, chunk);
   if (run.n == 0) return;
   const int64_t t_top = run.top;
-  const int64_t nsteps = run.n * NQ;
+  const int32_t nsteps = (int32_t)run.n * NQ;
 
   // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
   // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
-  // dims [8*(tid/16), +8), stored transposed as (row, row+1) words.  A step
-  // (tile ft, head fh) is addressed as a uniform base plus per-thread offsets
-  // fixed for the whole loop ----
+  // dims [8*(tid/16), +8), stored transposed as (row, row+1) words.
+  //   A step (tile, head) is addressed as the tile's uniform 64-bit byte
+  // address (head 0, set once per tile) plus a per-thread 32-bit byte offset
+  // that also carries the head (one add per step), so the loads take the
+  // scalar-base form and a step does no 64-bit arithmetic.  The offsets over
+  // a tile's rows and the group's heads, and the rotary rows, fit 32 bits
+  // (host-checked) ----
   const int qr = tid >> 3, qp = tid & 7;
   const int drp = tid & 15, ddb = tid >> 4;
-  const int64_t q_thr = (int64_t)qr * a.qst + 8 * qp;
-  const int64_t d_thr0 = (int64_t)(2 * drp) * a.dst + 8 * ddb;
-  const int64_t d_thr1 = d_thr0 + a.dst;
-  const _Float16* q_b = a.q + b * a.qsb + kvh * NQ * a.qsh;
-  const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
-  const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
+  const uint32_t q_thr = (uint32_t)(qr * a.qst + 8 * qp) * 2u;
+  const uint32_t d_thr0 = (uint32_t)((2 * drp) * a.dst + 8 * ddb) * 2u;
+  const uint32_t d_thr1 = d_thr0 + (uint32_t)a.dst * 2u;
+  const uint32_t q_head = (uint32_t)a.qsh * 2u, d_head = (uint32_t)a.dsh * 2u, l_head = (uint32_t)a.T * 4u;
+  const int32_t T32 = (int32_t)a.T;
+  const int32_t p32 = (int32_t)p0, rlast32 = (int32_t)rope_last;
+  const char* q_b = (const char*)(a.q + b * a.qsb + kvh * NQ * a.qsh);
+  const char* d_b = (const char*)(a.dout + b * a.dsb + kvh * NQ * a.dsh);
+  const char* l_b = (const char*)(a.lse + (b * a.QH + kvh * NQ) * a.T);
+  const char* trig = (const char*)a.rope;
   // Every load of a step is unconditional: rows past the end read the step's
-  // first row (a step's first row is always in range).  A select right after
-  // a load, or a load inside a branch, would make the wave wait for this
-  // step's whole prefetch where it is issued; the P mask gives those rows
-  // weight 0, so their values are never used.
+  // first row (a step's first row is always in range; only the top tile can
+  // have rows past T).  A select right after a load, or a load inside a
+  // branch, would make the wave wait for this step's whole prefetch where it
+  // is issued; the P mask gives those rows weight 0, so their values are
+  // never used.  The offsets are re-aimed when the fetch moves to a new tile.
+  int32_t fr0 = (int32_t)(t_top * kBRows);  // first row of the tile being fetched
+  const char *qf, *df, *lf;
+  uint32_t q_off, t_off, d_off0, d_off1, l_off;
+  auto aim = [&]() {
+    qf = q_b + (int64_t)fr0 * (2 * a.qst);
+    df = d_b + (int64_t)fr0 * (2 * a.dst);
+    lf = l_b + (int64_t)fr0 * 4;
+    const int32_t row = fr0 + qr;
+    const bool ok = row < T32;
+    q_off = ok ? q_thr : 16u * qp;
+    int32_t pos = p32 >= rlast32 ? rlast32 : p32 + (ok ? row : fr0);  // (no int32 overflow)
+    pos = pos < 0 ? 0 : (pos < rlast32 ? pos : rlast32);
+    t_off = (uint32_t)pos * (2u * kRopeRow) + 16u * qp;
+    d_off0 = fr0 + 2 * drp < T32 ? d_thr0 : 16u * ddb;
+    d_off1 = fr0 + 2 * drp + 1 < T32 ? d_thr1 : 16u * ddb;
+    l_off = tid < kBRows && fr0 + tid < T32 ? 4u * tid : 0u;
+  };
+  aim();
   struct StepRegs {
     half8 q0, q1, cs, sn, d0, d1;
     float l;
   };
-  const int lrow = tid < kBRows ? tid : 0;
-  auto fetch = [&](int ft, int fh, StepRegs& r) {
-    const int64_t r0 = (t_top - ft) * kBRows;
-    const int64_t row = r0 + qr;
-    const bool ok = row < a.T;
-    const _Float16* qrow = q_b + fh * a.qsh + r0 * a.qst + (ok ? q_thr : 8 * qp);
-    r.q0 = *(const half8*)qrow;
-    r.q1 = *(const half8*)(qrow + 64);
-    load_trig8(rope_row(p0 + (ok ? row : r0)), 8 * qp, &r.cs, &r.sn);
-    const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
-    r.d0 = *(const half8*)(dstep + (r0 + 2 * drp < a.T ? d_thr0 : 8 * ddb));
-    r.d1 = *(const half8*)(dstep + (r0 + 2 * drp + 1 < a.T ? d_thr1 : 8 * ddb));
-    r.l = l_b[fh * a.T + r0 + (tid < kBRows && r0 + tid < a.T ? lrow : 0)];
+  auto fetch = [&](StepRegs& r) {
+    r.q0 = *(const half8*)(qf + q_off);
+    r.q1 = *(const half8*)(qf + q_off + 128);
+    r.cs = *(const half8*)(trig + t_off);
+    r.sn = *(const half8*)(trig + t_off + 128);
+    r.d0 = *(const half8*)(df + d_off0);
+    r.d1 = *(const half8*)(df + d_off1);
+    r.l = *(const float*)(lf + l_off);
   };
-  auto store = [&](const StepRegs& r, int buf) {
+  // stage a step whose first row is srow0; rows past T get lse = +inf, which
+  // gives them weight exactly 0 (their scores are finite)
+  auto store = [&](const StepRegs& r, int buf, int32_t srow0) {
     half8 r0, r1;
     rope16(r.q0, r.q1, r.cs, r.sn, &r0, &r1);
     _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
@@ -201,46 +225,54 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
     _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
 #pragma unroll
     for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(r.d0, r.d1, e);
-    if (tid < kBRows) l_lds[buf][tid] = r.l * 1.4426950408889634f;
+    if (tid < kBRows) l_lds[buf][tid] = srow0 + tid < T32 ? r.l * 1.4426950408889634f : __builtin_inff();
   };
 
   // step s+1 waits in registers while s is computed and s+2 is in flight;
   // steps run tile by tile, the group's heads within a tile.  The two steps
   // ahead alternate between two register sets, so that no load result is
   // copied (a copy would wait for its load where it stands)
-  int ft = 0, fh = 0;  // the next step to fetch
+  int fh = 0;  // head of the next step to fetch
   auto advance = [&]() {
     if (++fh == NQ) {
       fh = 0;
-      ++ft;
+      fr0 -= kBRows;
+      aim();
+    } else {
+      q_off += q_head;
+      d_off0 += d_head;
+      d_off1 += d_head;
+      l_off += l_head;
     }
   };
   StepRegs ra, rb;
   if (nsteps > 0) {
     StepRegs r;
-    fetch(ft, fh, r);
+    fetch(r);
     advance();
     if (nsteps > 1) {
-      fetch(ft, fh, ra);
+      fetch(ra);
       advance();
     }
-    store(r, 0);
+    store(r, 0, (int32_t)(t_top * kBRows));
   }
   __syncthreads();
 
-  int ct = 0, ch = 0;  // the step being computed
+  int ch = 0;                               // head of the step being computed
+  int32_t r0 = (int32_t)(t_top * kBRows);   // and its first row
+  const int32_t kw32 = (int32_t)kw0;
+  const int32_t win = a.window < 0x40000000 ? (int32_t)a.window : 0x40000000;
   // stage step + 1 from `nxt` (its buffer was freed by the last barrier);
   // load step + 2 into `ahead`; compute step `step`
-  auto run_step = [&](int64_t step, StepRegs& ahead, const StepRegs& nxt) {
-    const int buf = (int)(step & 1);
-    if (step + 1 < nsteps) store(nxt, buf ^ 1);
+  auto run_step = [&](int32_t step, StepRegs& ahead, const StepRegs& nxt) {
+    const int buf = step & 1;
+    if (step + 1 < nsteps) store(nxt, buf ^ 1, ch + 1 == NQ ? r0 - kBRows : r0);
     if (step + 2 < nsteps) {
-      fetch(ft, fh, ahead);
+      fetch(ahead);
       advance();
     }
-    const int64_t r0 = (t_top - ct) * kBRows;
     // does any row of the step see any of this wave's keys?
-    const bool any = r0 + kBRows - 1 >= kw0 && r0 - (kw0 + 31) < a.window && kw0 < a.T;
+    const bool any = r0 + kBRows - 1 >= kw32 && r0 - (kw32 + 31) < win && kw32 < T32;
     if (any) {
       const _Float16* ql = q_lds[buf];
       const _Float16* dl = d_lds[buf];
@@ -262,11 +294,8 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
       // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
       // kw0 + 16kt + ln; pa[kt] contraction slot 4rg + e (of lane group lg)
       // <-> row 16rg + 4lg + e ----
-      const bool full = r0 >= kw0 + 31 && r0 + kBRows - 1 - kw0 < a.window && r0 + kBRows <= a.T;
-      const int base = (int)(r0 - kw0) + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
-      const int rows_left = (int)(a.T - r0 < kBRows ? a.T - r0 : kBRows);
-      const int keys_left = (int)(a.T - kw0 < 32 ? a.T - kw0 : 32);
-      const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
+      const bool full = r0 >= kw32 + 31 && r0 + kBRows - 1 - kw32 < win && r0 + kBRows <= T32;
+      const int base = r0 - kw32 + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
       // the dOᵀ operands of the second product go out now, under the
       // exponentials (left alone, the reads sink next to their products)
       half8 db[8];
@@ -278,8 +307,9 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
         db[dt] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
       __builtin_amdgcn_sched_barrier(0);
-      // (rows past T hold the step's first row and keys past T zeros: the
-      // mask zeroes their weights by selection, so no product reads them)
+      // (rows past T hold the step's first row and lse +inf, keys past T
+      // zeros: their scores are finite and their weights 0, rows by the
+      // lse and keys by the mask, since a visible key is at most the row)
       half8 pa[2];
       auto make_p = [&](auto masked_tag) {
         constexpr bool masked = decltype(masked_tag)::value;
@@ -291,14 +321,16 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
           for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
+              // hidden elements take exponent -inf (weight exactly 0); the
+              // selection goes before the exponential, which every lane
+              // then runs (a selection after it becomes a branch round it).
+              // Visible: 0 <= row - key < window, one unsigned compare
+              float x = fmaf(sacc[rg][kt][e], scale2, -l2[e]);
               if constexpr (masked) {
-                const int diff = base + 16 * rg + e - 16 * kt;
-                const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
-                                 16 * kt + ln < keys_left;
-                p = vis ? p : 0.f;
+                const uint32_t diff = (uint32_t)(base + 16 * rg + e - 16 * kt);
+                x = diff < (uint32_t)win ? x : -__builtin_inff();
               }
-              pa[kt][4 * rg + e] = (_Float16)p;
+              pa[kt][4 * rg + e] = (_Float16)__builtin_amdgcn_exp2f(x);
             }
         }
       };
@@ -320,10 +352,10 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
     __syncthreads();
     if (++ch == NQ) {
       ch = 0;
-      ++ct;
+      r0 -= kBRows;
     }
   };
-  for (int64_t step = 0; step < nsteps; step += 2) {
+  for (int32_t step = 0; step < nsteps; step += 2) {
     run_step(step, rb, ra);
     if (step + 1 < nsteps) run_step(step + 1, ra, rb);
   }
@@ -1018,6 +1050,17 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   JKV_CHECK_ARG(a.q && a.k && a.dout && a.lse && d_out_buf && a.start && rope_table, "null buffer");
   JKV_CHECK_ARG(!DK || (a.v && a.delta), "null buffer");
   JKV_CHECK_ARG(a.rope_len >= 1, "rotary table is empty");
+  // the value kernel's 32-bit row offsets: positions, rotary rows and the
+  // rows of one 32-row tile
+  JKV_CHECK_ARG(T < ((int64_t)1 << 30) && a.rope_len < ((int64_t)1 << 23),
+                "prefill gradients support at most 2^30 tokens and 2^23 rotary positions");
+  {
+    const int64_t lim = (int64_t)1 << 30, nq1 = QH / KVH - 1;
+    JKV_CHECK_ARG(a.qst >= 0 && a.dst >= 0 && a.qsh >= 0 && a.dsh >= 0 && nq1 * a.qsh + kBRows * a.qst < lim &&
+                      nq1 * a.dsh + kBRows * a.dst < lim && nq1 * T + kBRows < (lim >> 1),
+                  "prefill gradients: the query heads of one kv head and a 32-row tile must span "
+                  "under 2^30 elements");
+  }
   for (int i = 0; i < nstrides; ++i)
     JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");
   JKV_CHECK_ARG(((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.dout | (uintptr_t)d_out_buf |

@@ -359,7 +359,10 @@ int jkv_prefill_attention_codes(const void* q, int64_t q_stride_b, int64_t q_str
  *            are split into runs that fill the device evenly, each writing
  *            a partial slot that a second kernel adds up
  * Deterministic: each key's sum runs over the heads, rows and runs in one
- * fixed order.
+ * fixed order.  Limits (JKV_EINVAL past them): T < 2^30,
+ * rope_len < 2^23, and the query heads of one kv head plus 32 rows span
+ * under 2^30 elements in q and d_out ((QH/KVH - 1) * stride_h +
+ * 32 * stride_t), with (QH/KVH - 1) * T + 32 < 2^29 for lse.
  */
 int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                      int64_t q_stride_t, const void* k, int64_t k_stride_b,

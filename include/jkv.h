@@ -390,7 +390,8 @@ int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T
  * sqrt(128), dV = Pᵀ dO, with P recomputed from the forward's lse.
  *   out      the forward output [B,QH,T,128] fp16 (for rowsum(dO * O))
  *   workspace  jkv_prefill_backward_workspace_bytes() bytes, 16-byte aligned
- * Query heads per kv head: 1, 2 or a multiple of 4.  Deterministic.
+ * Query heads per kv head: 1, 2 or a multiple of 4.  Deterministic.  The
+ * key and value legs have the limits of jkv_prefill_attention_value_grad.
  */
 int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                                    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
@@ -409,7 +410,8 @@ int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH,
 /*
  * The key-gradient leg of jkv_prefill_attention_backward alone, given
  * delta = rowsum(dO * O) [B,QH,T] fp32 (the backward computes it in its query
- * leg).  Same buffers and workspace rule as jkv_prefill_attention_value_grad.
+ * leg).  Same buffers, workspace rule and limits as
+ * jkv_prefill_attention_value_grad.
  */
 int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                                    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,

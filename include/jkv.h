@@ -355,14 +355,14 @@ int jkv_prefill_attention_codes(const void* q, int64_t q_stride_b, int64_t q_str
  *   lse      [B,QH,T] fp32 from jkv_prefill_attention
  *   d_value  [B,KVH,T,128] fp32 contiguous (written, not accumulated)
  *   workspace  jkv_prefill_value_grad_workspace_bytes() bytes, 16-byte
- *            aligned (may be NULL when that is 0): a key block's query rows
- *            are split into runs that fill the device evenly, each writing
- *            a partial slot that a second kernel adds up
+ *            aligned: the rotated queries [B,QH,T,128] fp16, and when a key
+ *            block's query rows are split into runs that fill the device
+ *            evenly, the runs' partial slots that a second kernel adds up
  * Deterministic: each key's sum runs over the heads, rows and runs in one
- * fixed order.  Limits (JKV_EINVAL past them): T < 2^30,
- * rope_len < 2^23, and the query heads of one kv head plus 32 rows span
- * under 2^30 elements in q and d_out ((QH/KVH - 1) * stride_h +
- * 32 * stride_t), with (QH/KVH - 1) * T + 32 < 2^29 for lse.
+ * fixed order.  Limits (JKV_EINVAL past them): B and QH < 65536, T < 2^30,
+ * rope_len < 2^23, and for the query heads of one kv head under 2^31 bytes
+ * of rotated queries (QH/KVH * T * 256), of d_out ((QH/KVH - 1) * stride_h
+ * + (T - 1) * stride_t + 128 elements) and of lse.
  */
 int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                      int64_t q_stride_t, const void* k, int64_t k_stride_b,
@@ -373,9 +373,9 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
                                      const void* rope_table, int64_t rope_len, float* d_value,
                                      void* workspace, int64_t workspace_bytes, jkv_stream_t stream);
 
-/* Workspace of jkv_prefill_attention_value_grad for this geometry (bytes;
- * 0 when one run covers every key block's rows). */
-int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T, int64_t window);
+/* Workspace of jkv_prefill_attention_value_grad for this geometry (bytes):
+ * the runs' partial slots when there are several, then the rotated queries. */
+int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window);
 
 /*
  * The full backward of jkv_prefill_attention (the SDPA backward under the
@@ -391,7 +391,7 @@ int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T
  *   out      the forward output [B,QH,T,128] fp16 (for rowsum(dO * O))
  *   workspace  jkv_prefill_backward_workspace_bytes() bytes, 16-byte aligned
  * Query heads per kv head: 1, 2 or a multiple of 4.  Deterministic.  The
- * key and value legs have the limits of jkv_prefill_attention_value_grad.
+ * value leg has the limits of jkv_prefill_attention_value_grad.
  */
 int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                                    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
@@ -410,8 +410,9 @@ int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH,
 /*
  * The key-gradient leg of jkv_prefill_attention_backward alone, given
  * delta = rowsum(dO * O) [B,QH,T] fp32 (the backward computes it in its query
- * leg).  Same buffers, workspace rule and limits as
- * jkv_prefill_attention_value_grad.
+ * leg).  Same buffers and workspace rule as jkv_prefill_attention_value_grad
+ * (which sizes it for the rotated queries too; this leg needs only the
+ * slots).
  */
 int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                                    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,

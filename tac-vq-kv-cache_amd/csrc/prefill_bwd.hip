@@ -9,20 +9,26 @@
 // 142-150 step): the K tables and the backbone are frozen there, so the query
 // and key gradients are not needed for the value tables.
 //
-// One workgroup of 4 waves per (batch row, kv head, block of 128 keys); wave
-// w owns keys 32w..32w+31 of the block and keeps their rotated K̂ in registers
-// as MFMA B operands and their dV̂ in accumulators.  The workgroup walks
-// (32-row query tile, query head of the group) steps; each step's rotated q
-// rows ([row][dim]), dO transposed ([dim][row]) and lse land in LDS once,
-// double-buffered, and serve all four waves.  Per step and wave, on
+// The entry point first writes the rotated queries q_rot (the reference's
+// fp16 rotary at each row's position) into its workspace, once for all key
+// blocks.  Then one workgroup of 4 waves per (batch row, kv head, block of
+// 128 keys) and run of query tiles; wave w owns keys 32w..32w+31 of the block
+// and keeps their rotated K̂ in registers as MFMA B operands and their dV̂ in
+// accumulators.  The workgroup walks (32-row query tile, query head of the
+// group) steps; each step's q_rot and dO rows go straight from global memory
+// into LDS (buffer loads with the LDS destination, two steps ahead into
+// three buffers, 16-byte chunks XOR-swizzled per row) and serve all four
+// waves; its lse goes through a register.  Per step and wave, on
 // v_mfma_f32_16x16x32_f16:
-//   S[row][key]    = Q K̂ᵀ      A = q rows from LDS, B = the wave's K̂
+//   S[row][key]    = Q K̂ᵀ      A = q_rot rows from LDS, B = the wave's K̂
 //   P              = exp2(S log2e/sqrt(D) - lse log2e), masked, fp16
 //   dV̂[key][dim] += Pᵀ dO      A = P read straight off the S accumulators
 //                              (two 16-row tiles interleaved into the 32
-//                              contraction slots), B = dOᵀ rows from LDS in
+//                              contraction slots), B = dOᵀ read from the
+//                              row-major dO tile with ds_read_b64_tr_b16, in
 //                              the same slot order
-// Steps where none of a wave's keys is visible skip its arithmetic.
+// Steps where none of a wave's keys is visible skip its arithmetic.  168
+// registers: three workgroups per CU.
 #include <math.h>
 
 #include <type_traits>
@@ -42,7 +48,7 @@ static const int kQTile = kBRows * kQStride;
 static const int kDTile = kBD * kDStride;
 
 struct ValueGradArgs {
-  const _Float16* q;
+  const _Float16* q;  // pre-RoPE q; for the value kernel the rotated q_rot, contiguous [B,QH,T,128]
   int64_t qsb, qsh, qst;
   const _Float16* k;
   int64_t ksb, ksh, kst;
@@ -97,9 +103,54 @@ __device__ __forceinline__ uint32_t pair_words(half8 a, half8 b, int e) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-__global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGradArgs a) {
-  __shared__ __align__(16) _Float16 q_lds[2][kQTile];
-  __shared__ __align__(16) _Float16 d_lds[2][kDTile];
+// Rotated queries for the value kernel: q_rot[b,h,t,:] = the reference's fp16
+// rotary of q[b,h,t,:] at position start[b] + t (clamped to the table),
+// contiguous [B,QH,T,128].  One thread per (row, rotary chunk pair p): dims
+// [8p, +8) and their partners [64 + 8p, +8).  Grid (ceil(8T/256), QH, B).
+__global__ __launch_bounds__(256) void rotate_query_rows_kernel(const _Float16* __restrict__ q, int64_t qsb,
+                                                                int64_t qsh, int64_t qst, int64_t T,
+                                                                const int32_t* __restrict__ start,
+                                                                const _Float16* __restrict__ rope,
+                                                                int64_t rope_len, _Float16* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t t = i >> 3;
+  if (t >= T) return;
+  const int p = (int)(i & 7);
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  int64_t pos = (int64_t)start[b] + t;
+  pos = pos < 0 ? 0 : (pos < rope_len - 1 ? pos : rope_len - 1);
+  const _Float16* src = q + b * qsb + h * qsh + t * qst + 8 * p;
+  half8 cs, sn, r0, r1;
+  load_trig8(rope + pos * kRopeRow, 8 * p, &cs, &sn);
+  rope16(*(const half8*)src, *(const half8*)(src + 64), cs, sn, &r0, &r1);
+  _Float16* dst = out + ((b * gridDim.y + h) * T + t) * kBD + 8 * p;
+  *(half8*)dst = r0;
+  *(half8*)(dst + 64) = r1;
+}
+
+// transposing LDS read of the 8-byte piece at LDS byte address addr: in each
+// 16-lane block, lane 4j + e receives element e of the pieces that the
+// block's lanes j, j+4, j+8, j+12 address (ds_read_b64_tr_b16)
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+__device__ __forceinline__ half4 lds_read_tr16(uint32_t addr) {
+  return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(size_t)addr));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const void __attribute__((address_space(3)))*)p;
+}
+
+// Staged rows (q_rot and dO tiles, 32 rows x 256 bytes) hold their 16-byte
+// chunks XOR-swizzled: chunk j of row r sits in slot j ^ swz(r).  q rows use
+// swz = r & 15 (the A-operand reads take 16 consecutive rows at one chunk),
+// dO rows swz = 2 (r & 7) (the transposing reads take 32 bytes of eight
+// consecutive rows).  Both keep a read's lanes on distinct banks.
+__device__ __forceinline__ uint32_t q_slot(int r, int j) { return (uint32_t)(j ^ (r & 15)); }
+__device__ __forceinline__ uint32_t d_slot(int r, int j) { return (uint32_t)(j ^ (2 * (r & 7))); }
+
+__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) void prefill_value_grad_kernel(ValueGradArgs a) {
+  __shared__ __align__(1024) _Float16 q_lds[3][kBRows * kBD];
+  __shared__ __align__(1024) _Float16 d_lds[3][kBRows * kBD];
   __shared__ __align__(16) float l_lds[2][kBRows];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -156,133 +207,137 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
   const int64_t t_top = run.top;
   const int32_t nsteps = (int32_t)run.n * NQ;
 
-  // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
-  // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
-  // dims [8*(tid/16), +8), stored transposed as (row, row+1) words.
-  //   A step (tile, head) is addressed as the tile's uniform 64-bit byte
-  // address (head 0, set once per tile) plus a per-thread 32-bit byte offset
-  // that also carries the head (one add per step), so the loads take the
-  // scalar-base form and a step does no 64-bit arithmetic.  The offsets over
-  // a tile's rows and the group's heads, and the rotary rows, fit 32 bits
-  // (host-checked) ----
-  const int qr = tid >> 3, qp = tid & 7;
-  const int drp = tid & 15, ddb = tid >> 4;
-  const uint32_t q_thr = (uint32_t)(qr * a.qst + 8 * qp) * 2u;
-  const uint32_t d_thr0 = (uint32_t)((2 * drp) * a.dst + 8 * ddb) * 2u;
-  const uint32_t d_thr1 = d_thr0 + (uint32_t)a.dst * 2u;
-  const uint32_t q_head = (uint32_t)a.qsh * 2u, d_head = (uint32_t)a.dsh * 2u, l_head = (uint32_t)a.T * 4u;
+  // ---- staging.  A step's q_rot and dO rows go global -> LDS directly
+  // (buffer_load_dwordx4 ... lds: lane i of an instruction lands at its LDS
+  // base + 16 i, so an instruction fills 4 rows), two steps ahead into three
+  // buffers: wave w fills rows 8w..8w+7 with two instructions per tensor,
+  // lane -> row 8w + 4i + lane/16, slot lane%16, loading the chunk that
+  // belongs in that slot.  (The MUBUF form: the compiler's wait counting
+  // takes global_load_lds for an access to both memories and drains every
+  // LDS read behind it.)  The step's lse goes through a register one step
+  // ahead, loaded before the step-ahead copies so that one wait (vmcnt 4)
+  // covers the next step's copies and lse.  A load's address is the (batch
+  // row, kv head)'s buffer, a uniform tile offset and a per-thread offset
+  // that also carries the head (one add per step); they fit 31 bits
+  // (host-checked).  Rows past T read the step's first row (every step's
+  // first row is in range; only the top tile has rows past T) and are staged
+  // with lse = +inf, which gives them weight exactly 0 ----
+  const int srow = 8 * wave + (lane >> 4), slot = lane & 15;
   const int32_t T32 = (int32_t)a.T;
-  const int32_t p32 = (int32_t)p0, rlast32 = (int32_t)rope_last;
-  const char* q_b = (const char*)(a.q + b * a.qsb + kvh * NQ * a.qsh);
-  const char* d_b = (const char*)(a.dout + b * a.dsb + kvh * NQ * a.dsh);
+  // q_rot is contiguous [B,QH,T,128]
+  const uint32_t q_head = (uint32_t)a.T * (2u * kBD), d_head = (uint32_t)a.dsh * 2u, l_head = (uint32_t)a.T * 4u;
+  const __amdgpu_buffer_rsrc_t q_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.q + ((b * a.QH + kvh * NQ) * a.T) * kBD), (short)0, (int)(NQ * a.T * 2 * kBD), 0x00020000);
+  const __amdgpu_buffer_rsrc_t d_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.dout + b * a.dsb + kvh * NQ * a.dsh), (short)0,
+      (int)(((NQ - 1) * a.dsh + (a.T - 1) * a.dst + kBD) * 2), 0x00020000);
   const char* l_b = (const char*)(a.lse + (b * a.QH + kvh * NQ) * a.T);
-  const char* trig = (const char*)a.rope;
-  // Every load of a step is unconditional: rows past the end read the step's
-  // first row (a step's first row is always in range; only the top tile can
-  // have rows past T).  A select right after a load, or a load inside a
-  // branch, would make the wave wait for this step's whole prefetch where it
-  // is issued; the P mask gives those rows weight 0, so their values are
-  // never used.  The offsets are re-aimed when the fetch moves to a new tile.
-  int32_t fr0 = (int32_t)(t_top * kBRows);  // first row of the tile being fetched
-  const char *qf, *df, *lf;
-  uint32_t q_off, t_off, d_off0, d_off1, l_off;
+  // copies: the next step to copy
+  int fh = 0;
+  int32_t fr0 = (int32_t)(t_top * kBRows);  // first row of its tile
+  uint32_t q_tile, d_tile;                  // the tile's byte offsets (uniform)
+  uint32_t qo[2], dof[2];
   auto aim = [&]() {
-    qf = q_b + (int64_t)fr0 * (2 * a.qst);
-    df = d_b + (int64_t)fr0 * (2 * a.dst);
-    lf = l_b + (int64_t)fr0 * 4;
-    const int32_t row = fr0 + qr;
-    const bool ok = row < T32;
-    q_off = ok ? q_thr : 16u * qp;
-    int32_t pos = p32 >= rlast32 ? rlast32 : p32 + (ok ? row : fr0);  // (no int32 overflow)
-    pos = pos < 0 ? 0 : (pos < rlast32 ? pos : rlast32);
-    t_off = (uint32_t)pos * (2u * kRopeRow) + 16u * qp;
-    d_off0 = fr0 + 2 * drp < T32 ? d_thr0 : 16u * ddb;
-    d_off1 = fr0 + 2 * drp + 1 < T32 ? d_thr1 : 16u * ddb;
-    l_off = tid < kBRows && fr0 + tid < T32 ? 4u * tid : 0u;
+    q_tile = (uint32_t)fr0 * (2u * kBD);
+    d_tile = (uint32_t)fr0 * (uint32_t)a.dst * 2u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = srow + 4 * i;
+      const uint32_t rr = fr0 + r < T32 ? (uint32_t)r : 0u;
+      qo[i] = rr * (2u * kBD) + 16u * q_slot(r, slot);
+      dof[i] = rr * (uint32_t)a.dst * 2u + 16u * d_slot(r, slot);
+    }
   };
   aim();
-  struct StepRegs {
-    half8 q0, q1, cs, sn, d0, d1;
-    float l;
-  };
-  auto fetch = [&](StepRegs& r) {
-    r.q0 = *(const half8*)(qf + q_off);
-    r.q1 = *(const half8*)(qf + q_off + 128);
-    r.cs = *(const half8*)(trig + t_off);
-    r.sn = *(const half8*)(trig + t_off + 128);
-    r.d0 = *(const half8*)(df + d_off0);
-    r.d1 = *(const half8*)(df + d_off1);
-    r.l = *(const float*)(lf + l_off);
-  };
-  // stage a step whose first row is srow0; rows past T get lse = +inf, which
-  // gives them weight exactly 0 (their scores are finite)
-  auto store = [&](const StepRegs& r, int buf, int32_t srow0) {
-    half8 r0, r1;
-    rope16(r.q0, r.q1, r.cs, r.sn, &r0, &r1);
-    _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
-    *(half8*)qd = r0;
-    *(half8*)(qd + 64) = r1;
-    _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
+  auto copy = [&](int buf) {
+    char* qd = (char*)q_lds[buf] + 2048 * wave;
+    char* dd = (char*)d_lds[buf] + 2048 * wave;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(r.d0, r.d1, e);
-    if (tid < kBRows) l_lds[buf][tid] = srow0 + tid < T32 ? r.l * 1.4426950408889634f : __builtin_inff();
-  };
-
-  // step s+1 waits in registers while s is computed and s+2 is in flight;
-  // steps run tile by tile, the group's heads within a tile.  The two steps
-  // ahead alternate between two register sets, so that no load result is
-  // copied (a copy would wait for its load where it stands)
-  int fh = 0;  // head of the next step to fetch
-  auto advance = [&]() {
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rsrc, (void __attribute__((address_space(3)))*)(qd + 1024 * i), 16,
+                                               qo[i], q_tile, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(d_rsrc, (void __attribute__((address_space(3)))*)(dd + 1024 * i), 16,
+                                               dof[i], d_tile, 0, 0);
+    }
     if (++fh == NQ) {
       fh = 0;
       fr0 -= kBRows;
       aim();
     } else {
-      q_off += q_head;
-      d_off0 += d_head;
-      d_off1 += d_head;
+      qo[0] += q_head;
+      qo[1] += q_head;
+      dof[0] += d_head;
+      dof[1] += d_head;
+    }
+  };
+  // lse: the next step to load, in every wave (uniform wait counts); the
+  // first kBRows threads keep theirs
+  int lh = 0;
+  int32_t lr0 = (int32_t)(t_top * kBRows);
+  const char* lf;
+  uint32_t l_off;
+  auto aim_l = [&]() {
+    lf = l_b + (int64_t)lr0 * 4;
+    l_off = tid < kBRows && lr0 + tid < T32 ? 4u * tid : 0u;
+  };
+  aim_l();
+  float lreg = 0.f;
+  auto load_lse = [&]() {
+    lreg = *(const float*)(lf + l_off);
+    if (++lh == NQ) {
+      lh = 0;
+      lr0 -= kBRows;
+      aim_l();
+    } else {
       l_off += l_head;
     }
   };
-  StepRegs ra, rb;
-  if (nsteps > 0) {
-    StepRegs r;
-    fetch(r);
-    advance();
-    if (nsteps > 1) {
-      fetch(ra);
-      advance();
-    }
-    store(r, 0, (int32_t)(t_top * kBRows));
+  // after the wait: the staged step's lse (log2 units), +inf past T
+  auto put_lse = [&](int buf, int32_t srow0) {
+    if (tid < kBRows) l_lds[buf][tid] = srow0 + tid < T32 ? lreg * 1.4426950408889634f : __builtin_inff();
+  };
+  // s_waitcnt vmcnt(4), leaving the other counters alone (gfx9 encoding:
+  // vmcnt [3:0], expcnt [6:4] = 7, lgkmcnt [11:8] = 15)
+  constexpr int kWaitVm4 = 4 | (7 << 4) | (15 << 8);
+
+  load_lse();
+  copy(0);
+  if (nsteps > 1) {
+    copy(1);
+    __builtin_amdgcn_s_waitcnt(kWaitVm4);  // step 0's copies and lse have landed
+  } else {
+    __builtin_amdgcn_s_waitcnt(0);
   }
+  put_lse(0, (int32_t)(t_top * kBRows));
   __syncthreads();
 
   int ch = 0;                               // head of the step being computed
   int32_t r0 = (int32_t)(t_top * kBRows);   // and its first row
   const int32_t kw32 = (int32_t)kw0;
   const int32_t win = a.window < 0x40000000 ? (int32_t)a.window : 0x40000000;
-  // stage step + 1 from `nxt` (its buffer was freed by the last barrier);
-  // load step + 2 into `ahead`; compute step `step`
-  auto run_step = [&](int32_t step, StepRegs& ahead, const StepRegs& nxt) {
-    const int buf = step & 1;
-    if (step + 1 < nsteps) store(nxt, buf ^ 1, ch + 1 == NQ ? r0 - kBRows : r0);
-    if (step + 2 < nsteps) {
-      fetch(ahead);
-      advance();
-    }
+  // per-lane LDS byte offsets of the operand reads: q row 16rg + ln, chunk
+  // 4c + lg; dO rows 4lg + ln/4 (+16), dims 16dt + 4(ln%4), 8 bytes
+  const int dr = 4 * lg + (ln >> 2);
+  const uint32_t d_rd = (uint32_t)dr * 256u + 8u * (ln & 1);
+  int buf = 0, buf2 = 2;  // buffers of this step and of step + 2
+  for (int32_t step = 0; step < nsteps; ++step) {
+    const bool more = step + 1 < nsteps, more2 = step + 2 < nsteps;
+    // the lse of step + 1, then step + 2's copies into the buffer that step
+    // - 1 used (freed by the last barrier)
+    if (more) load_lse();
+    if (more2) copy(buf2);
     // does any row of the step see any of this wave's keys?
     const bool any = r0 + kBRows - 1 >= kw32 && r0 - (kw32 + 31) < win && kw32 < T32;
     if (any) {
-      const _Float16* ql = q_lds[buf];
-      const _Float16* dl = d_lds[buf];
+      const char* ql = (const char*)q_lds[buf];
+      const uint32_t dl = lds_addr(d_lds[buf]);
       // ---- S[row][key]: 2 row tiles x 2 key tiles ----
       float4v sacc[2][2];
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg) {
         half8 qa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qa[c] = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
+        for (int c = 0; c < 4; ++c) qa[c] = *(const half8*)(ql + (16 * rg + ln) * 256 + 16 * q_slot(ln, 4 * c + lg));
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -296,17 +351,6 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
       // <-> row 16rg + 4lg + e ----
       const bool full = r0 >= kw32 + 31 && r0 + kBRows - 1 - kw32 < win && r0 + kBRows <= T32;
       const int base = r0 - kw32 + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
-      // the dOᵀ operands of the second product go out now, under the
-      // exponentials (left alone, the reads sink next to their products)
-      half8 db[8];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const _Float16* dr = dl + (16 * dt + ln) * kDStride + 4 * lg;
-        const half4 lo = *(const half4*)dr;
-        const half4 hi = *(const half4*)(dr + 16);
-        db[dt] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-      __builtin_amdgcn_sched_barrier(0);
       // (rows past T hold the step's first row and lse +inf, keys past T
       // zeros: their scores are finite and their weights 0, rows by the
       // lse and keys by the mask, since a visible key is at most the row)
@@ -315,7 +359,7 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
         constexpr bool masked = decltype(masked_tag)::value;
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg) {
-          const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
+          const float4 l4 = *(const float4*)(&l_lds[step & 1][16 * rg + 4 * lg]);
           const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt)
@@ -341,23 +385,34 @@ __global__ __launch_bounds__(kBThreads) void prefill_value_grad_kernel(ValueGrad
       } else {
         make_p(std::true_type{});
       }
-      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
-      // {16+4lg..16+4lg+3} ----
+      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln): slots {4lg..4lg+3} =
+      // rows 4lg..4lg+3 and {16+4lg..} = rows 16+4lg.., two transposing reads ----
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint32_t at = dl + d_rd + 16u * d_slot(dr, 2 * dt + ((ln & 3) >> 1));
+        const half4 lo = lds_read_tr16(at);
+        const half4 hi = lds_read_tr16(at + 16u * 256u);
+        const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
-          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db[dt], acc[kt][dt], 0, 0, 0);
+          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
+      }
     }
-    __syncthreads();
     if (++ch == NQ) {
       ch = 0;
       r0 -= kBRows;
     }
-  };
-  for (int32_t step = 0; step < nsteps; step += 2) {
-    run_step(step, rb, ra);
-    if (step + 1 < nsteps) run_step(step + 1, ra, rb);
+    // step + 1's copies and lse have landed (this wave's part; the barrier
+    // covers the rest)
+    if (more2) {
+      __builtin_amdgcn_s_waitcnt(kWaitVm4);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    if (more) put_lse((step + 1) & 1, r0);
+    __syncthreads();
+    buf = buf == 2 ? 0 : buf + 1;
+    buf2 = buf2 == 2 ? 0 : buf2 + 1;
   }
 
   // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
@@ -1006,6 +1061,18 @@ __global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __r
 // Tiles per chunk and partial slots of the key-block kernels: chunks of 16
 // tiles, or of an eighth of the longest block's rows when that is more; the
 // slots are the most chunks one block meets.
+static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* slots);
+
+// bytes of the value gradient's workspace: the chunks' partial slots (when
+// there are several), then the rotated queries [B,QH,T,128] fp16 at a
+// 256-byte boundary
+static int64_t value_grad_workspace(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window) {
+  int chunk_tiles, chunks;
+  value_grad_chunks(T, window, &chunk_tiles, &chunks);
+  const int64_t slots = chunks > 1 ? (int64_t)chunks * B * KVH * T * kBD * (int64_t)sizeof(float) : 0;
+  return ceil_div(slots, 256) * 256 + B * QH * T * kBD * 2;
+}
+
 static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* slots) {
   int64_t rows = (int64_t)kBKeys - 1 + window;
   if (rows > T || rows < 0) rows = T;
@@ -1022,12 +1089,9 @@ static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* 
 
 extern "C" {
 
-int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t KVH, int64_t T, int64_t window) {
-  using namespace jkv;
-  if (B <= 0 || KVH <= 0 || T <= 0 || window < 1) return 0;
-  int chunk_tiles, chunks;
-  value_grad_chunks(T, window, &chunk_tiles, &chunks);
-  return chunks > 1 ? (int64_t)chunks * B * KVH * T * kBD * (int64_t)sizeof(float) : 0;
+int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window) {
+  if (B <= 0 || QH <= 0 || KVH <= 0 || T <= 0 || window < 1) return 0;
+  return jkv::value_grad_workspace(B, QH, KVH, T, window);
 }
 
 }  // extern "C"
@@ -1050,16 +1114,18 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   JKV_CHECK_ARG(a.q && a.k && a.dout && a.lse && d_out_buf && a.start && rope_table, "null buffer");
   JKV_CHECK_ARG(!DK || (a.v && a.delta), "null buffer");
   JKV_CHECK_ARG(a.rope_len >= 1, "rotary table is empty");
-  // the value kernel's 32-bit row offsets: positions, rotary rows and the
-  // rows of one 32-row tile
-  JKV_CHECK_ARG(T < ((int64_t)1 << 30) && a.rope_len < ((int64_t)1 << 23),
-                "prefill gradients support at most 2^30 tokens and 2^23 rotary positions");
-  {
-    const int64_t lim = (int64_t)1 << 30, nq1 = QH / KVH - 1;
-    JKV_CHECK_ARG(a.qst >= 0 && a.dst >= 0 && a.qsh >= 0 && a.dsh >= 0 && nq1 * a.qsh + kBRows * a.qst < lim &&
-                      nq1 * a.dsh + kBRows * a.dst < lim && nq1 * T + kBRows < (lim >> 1),
-                  "prefill gradients: the query heads of one kv head and a 32-row tile must span "
-                  "under 2^30 elements");
+  JKV_CHECK_ARG(B < 65536 && QH < 65536, "prefill gradients: batch and query heads must be below 65536");
+  if constexpr (!DK) {
+    // the value kernel's 32-bit offsets: positions, rotary rows, and the
+    // bytes of one (batch row, kv head)'s rotated queries, output gradient
+    // and lse
+    const int64_t nq1 = NQ - 1, lim = (int64_t)1 << 31;
+    JKV_CHECK_ARG(T < ((int64_t)1 << 30) && a.rope_len < ((int64_t)1 << 23),
+                  "prefill gradients support at most 2^30 tokens and 2^23 rotary positions");
+    JKV_CHECK_ARG(a.dst >= 0 && a.dsh >= 0 && NQ * T * kBD * 2 < lim &&
+                      (nq1 * a.dsh + (T - 1) * a.dst + kBD) * 2 < lim && (nq1 * T + kBRows) * 4 < lim,
+                  "prefill value gradient: the query heads of one kv head must span under 2^31 bytes "
+                  "of q, d_out and lse");
   }
   for (int i = 0; i < nstrides; ++i)
     JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");
@@ -1073,12 +1139,17 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   a.chunk_tiles = chunk_tiles;
   a.slots = chunks;
   const int64_t n = B * KVH * T * kBD;
-  if (chunks > 1) {
-    const int64_t need = (int64_t)chunks * n * (int64_t)sizeof(float);
+  // workspace: the chunks' partial slots, then (value gradient) the rotated
+  // queries
+  const int64_t slot_bytes = chunks > 1 ? (int64_t)chunks * n * (int64_t)sizeof(float) : 0;
+  const int64_t need = DK ? slot_bytes : value_grad_workspace(B, QH, KVH, T, a.window);
+  if (need > 0) {
     JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                   "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
                   (long long)need);
     JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  }
+  if (chunks > 1) {
     a.dv = (float*)workspace;
     a.slot_stride = n;
   } else {
@@ -1091,6 +1162,11 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
     hipLaunchKernelGGL(prefill_kv_grad_kernel<true>, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
                        stream, a);
   } else {
+    _Float16* q_rot = (_Float16*)((unsigned char*)workspace + ceil_div(slot_bytes, 256) * 256);
+    hipLaunchKernelGGL(rotate_query_rows_kernel, dim3((uint32_t)ceil_div(8 * T, 256), (uint32_t)QH, (uint32_t)B),
+                       dim3(256), 0, stream, a.q, a.qsb, a.qsh, a.qst, T, a.start, a.rope, a.rope_len, q_rot);
+    JKV_CHECK_LAUNCH();
+    a.q = q_rot;  // contiguous [B,QH,T,128]
     hipLaunchKernelGGL(prefill_value_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
                        stream, a);
   }
@@ -1165,7 +1241,11 @@ int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH,
   int chunk_tiles, chunks;
   value_grad_chunks(T, window, &chunk_tiles, &chunks);
   const int64_t delta = ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
-  return delta + (int64_t)chunks * B * QH * T * kBD * (int64_t)sizeof(float);
+  // the slot area serves the query leg (delta only), the key leg's slots and
+  // the value leg's slots and rotated queries in turn
+  const int64_t qk = (int64_t)chunks * B * QH * T * kBD * (int64_t)sizeof(float);
+  const int64_t v = value_grad_workspace(B, QH, KVH, T, window);
+  return delta + (qk > v ? qk : v);
 }
 
 int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,

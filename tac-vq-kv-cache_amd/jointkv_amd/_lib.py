@@ -104,7 +104,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
          _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
     ),
-    "jkv_prefill_value_grad_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "jkv_prefill_value_grad_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "jkv_prefill_attention_backward": (
         ctypes.c_int,
         [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,

@@ -736,7 +736,7 @@ def prefill_attention_value_grad(
     table = rope_table(device, rope_theta, int(max_position) + 1)
     d_value = torch.empty((batch, kvheads, tokens, 128), dtype=torch.float32, device=device)
     lib = _lib.load()
-    ws_bytes = int(lib.jkv_prefill_value_grad_workspace_bytes(batch, kvheads, tokens, int(window)))
+    ws_bytes = int(lib.jkv_prefill_value_grad_workspace_bytes(batch, qheads, kvheads, tokens, int(window)))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     code = lib.jkv_prefill_attention_value_grad(
         q.data_ptr(), *q.stride()[:3], key.data_ptr(), *key.stride()[:3], d_out.data_ptr(),

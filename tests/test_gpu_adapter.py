@@ -40,7 +40,7 @@ def _case(seed, batch, qh, kvh, tokens):
     (1, 8, 2, 1500, (0,), 256),         # window binds over many tiles: blocks meet chunks that wrap the slots
 ])
 def test_lse_and_value_grad_match_oracle(device, batch, qh, kvh, tokens, starts, window):
-    ws = int(_ops._lib.load().jkv_prefill_value_grad_workspace_bytes(batch, kvh, tokens, window))
+    ws = int(_ops._lib.load().jkv_prefill_value_grad_workspace_bytes(batch, qh, kvh, tokens, window))
     print(f"value grad B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window} ws={ws}", flush=True)
     q, k, v, d = _case(900 + tokens, batch, qh, kvh, tokens)
     qd, kd, vd, dd = (t.to(device) for t in (q, k, v, d))
@@ -124,7 +124,7 @@ def test_key_grad_entry_matches_backward_key_leg(device, batch, qh, kvh, tokens,
     delta = (dd.float() * out.float()).sum(-1).contiguous()
     table = _ops.rope_table(device, 10000.0, max_pos + 1)
     lib = _lib.load()
-    ws = int(lib.jkv_prefill_value_grad_workspace_bytes(batch, kvh, tokens, window))
+    ws = int(lib.jkv_prefill_value_grad_workspace_bytes(batch, qh, kvh, tokens, window))
     work = torch.empty(max(ws, 1), dtype=torch.uint8, device=device)
     dk = torch.empty(batch, kvh, tokens, 128, dtype=torch.float32, device=device)
     _lib.check(lib.jkv_prefill_attention_key_grad(

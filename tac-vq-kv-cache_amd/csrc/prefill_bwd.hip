@@ -141,17 +141,30 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 
 // Staged rows (q_rot and dO tiles, 32 rows x 256 bytes) hold their 16-byte
-// chunks XOR-swizzled: chunk j of row r sits in slot j ^ swz(r).  q rows use
-// swz = r & 15 (the A-operand reads take 16 consecutive rows at one chunk),
-// dO rows swz = 2 (r & 7) (the transposing reads take 32 bytes of eight
-// consecutive rows).  Both keep a read's lanes on distinct banks.
-__device__ __forceinline__ uint32_t q_slot(int r, int j) { return (uint32_t)(j ^ (r & 15)); }
-__device__ __forceinline__ uint32_t d_slot(int r, int j) { return (uint32_t)(j ^ (2 * (r & 7))); }
+// chunks XOR-swizzled: chunk j of row r sits in slot j ^ f(r), f(r) =
+// 2 (r & 7) + ((r >> 3) & 1).  An A-operand read takes 16 consecutive rows
+// at one chunk (f is one-to-one on r mod 16); a transposing read takes
+// chunks 2t, 2t + 1 of 8 aligned consecutive rows (f / 2 is one-to-one on r
+// mod 8).  Either way a read's lanes sit on distinct banks.
+__device__ __forceinline__ uint32_t row_slot(int r, int j) {
+  return (uint32_t)(j ^ (((r & 7) << 1) | ((r >> 3) & 1)));
+}
 
-__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) void prefill_value_grad_kernel(ValueGradArgs a) {
+// The key-block walk of the value gradient (DK = false) and of the key
+// gradient (DK = true):
+//   DK = false  dV̂ += Pᵀ dO
+//   DK = true   dP = dO V̂ᵀ, dS = P (dP - delta_row), dK̂_rot += dSᵀ Q_rot /
+//               sqrt(D), then the rotary's transpose at the key's position
+// (delta = rowsum(dO * O) from the query kernel).  For the key gradient the
+// wave's V̂ rows join its K̂ as B operands, the staged dO rows are the A
+// operand of dP, and Q_rotᵀ for the last product comes off the staged q
+// rows with the same transposing reads that give dOᵀ to the value gradient.
+template <bool DK>
+__device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
   __shared__ __align__(1024) _Float16 q_lds[3][kBRows * kBD];
   __shared__ __align__(1024) _Float16 d_lds[3][kBRows * kBD];
   __shared__ __align__(16) float l_lds[2][kBRows];
+  __shared__ __align__(16) float x_lds[DK ? 2 : 1][kBRows];  // delta (DK)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the step tests below branch on it
@@ -177,8 +190,8 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
 
   // ---- the wave's rotated keys as B operands: kop[kt][c] = dims
   // [32c + 8lg, +8) of key kw0 + 16kt + ln (chunks c and c+2 are rotary
-  // partners) ----
-  half8 kop[2][4];
+  // partners); DK: its V̂ rows the same way (no rotary) ----
+  half8 kop[2][4], vop[2][4];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
     const int64_t key = kw0 + 16 * kt + ln;
@@ -194,8 +207,13 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       kop[kt][c] = ok ? r0 : zero8;
       kop[kt][c + 2] = ok ? r1 : zero8;
     }
+    if constexpr (DK) {
+      const _Float16* vp = a.v + b * a.vsb + kvh * a.vsh + (ok ? key : 0) * a.vst;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) vop[kt][c] = ok ? *(const half8*)(vp + 32 * c + 8 * lg) : zero8;
+    }
   }
-  float4v acc[2][8];  // dV̂[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
+  float4v acc[2][8];  // d[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -214,14 +232,14 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   // lane -> row 8w + 4i + lane/16, slot lane%16, loading the chunk that
   // belongs in that slot.  (The MUBUF form: the compiler's wait counting
   // takes global_load_lds for an access to both memories and drains every
-  // LDS read behind it.)  The step's lse goes through a register one step
-  // ahead, loaded before the step-ahead copies so that one wait (vmcnt 4)
-  // covers the next step's copies and lse.  A load's address is the (batch
-  // row, kv head)'s buffer, a uniform tile offset and a per-thread offset
-  // that also carries the head (one add per step); they fit 31 bits
-  // (host-checked).  Rows past T read the step's first row (every step's
-  // first row is in range; only the top tile has rows past T) and are staged
-  // with lse = +inf, which gives them weight exactly 0 ----
+  // LDS read behind it.)  The step's lse (and delta) go through registers
+  // one step ahead, loaded before the step-ahead copies so that one wait
+  // (vmcnt 4) covers the next step's copies, lse and delta.  A load's
+  // address is the (batch row, kv head)'s buffer, a uniform tile offset and
+  // a per-thread offset that also carries the head (one add per step); they
+  // fit 31 bits (host-checked).  Rows past T read the step's first row
+  // (every step's first row is in range; only the top tile has rows past T)
+  // and are staged with lse = +inf, which gives them weight exactly 0 ----
   const int srow = 8 * wave + (lane >> 4), slot = lane & 15;
   const int32_t T32 = (int32_t)a.T;
   // q_rot is contiguous [B,QH,T,128]
@@ -231,7 +249,9 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   const __amdgpu_buffer_rsrc_t d_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.dout + b * a.dsb + kvh * NQ * a.dsh), (short)0,
       (int)(((NQ - 1) * a.dsh + (a.T - 1) * a.dst + kBD) * 2), 0x00020000);
-  const char* l_b = (const char*)(a.lse + (b * a.QH + kvh * NQ) * a.T);
+  const int64_t lrow0 = (b * a.QH + kvh * NQ) * a.T;
+  const char* l_b = (const char*)(a.lse + lrow0);
+  const char* x_b = DK ? (const char*)(a.delta + lrow0) : nullptr;
   // copies: the next step to copy
   int fh = 0;
   int32_t fr0 = (int32_t)(t_top * kBRows);  // first row of its tile
@@ -244,8 +264,8 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     for (int i = 0; i < 2; ++i) {
       const int r = srow + 4 * i;
       const uint32_t rr = fr0 + r < T32 ? (uint32_t)r : 0u;
-      qo[i] = rr * (2u * kBD) + 16u * q_slot(r, slot);
-      dof[i] = rr * (uint32_t)a.dst * 2u + 16u * d_slot(r, slot);
+      qo[i] = rr * (2u * kBD) + 16u * row_slot(r, slot);
+      dof[i] = rr * (uint32_t)a.dst * 2u + 16u * row_slot(r, slot);
     }
   };
   aim();
@@ -270,20 +290,20 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       dof[1] += d_head;
     }
   };
-  // lse: the next step to load, in every wave (uniform wait counts); the
-  // first kBRows threads keep theirs
+  // lse (and delta): the next step to load, in every wave (uniform wait
+  // counts); the first kBRows threads keep theirs
   int lh = 0;
   int32_t lr0 = (int32_t)(t_top * kBRows);
-  const char* lf;
-  uint32_t l_off;
+  uint32_t l_tile, l_off;
   auto aim_l = [&]() {
-    lf = l_b + (int64_t)lr0 * 4;
+    l_tile = (uint32_t)lr0 * 4u;
     l_off = tid < kBRows && lr0 + tid < T32 ? 4u * tid : 0u;
   };
   aim_l();
-  float lreg = 0.f;
+  float lreg = 0.f, xreg = 0.f;
   auto load_lse = [&]() {
-    lreg = *(const float*)(lf + l_off);
+    lreg = *(const float*)(l_b + l_tile + l_off);
+    if constexpr (DK) xreg = *(const float*)(x_b + l_tile + l_off);
     if (++lh == NQ) {
       lh = 0;
       lr0 -= kBRows;
@@ -292,9 +312,12 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       l_off += l_head;
     }
   };
-  // after the wait: the staged step's lse (log2 units), +inf past T
+  // after the wait: the staged step's lse (log2 units; +inf past T) and delta
   auto put_lse = [&](int buf, int32_t srow0) {
-    if (tid < kBRows) l_lds[buf][tid] = srow0 + tid < T32 ? lreg * 1.4426950408889634f : __builtin_inff();
+    if (tid < kBRows) {
+      l_lds[buf][tid] = srow0 + tid < T32 ? lreg * 1.4426950408889634f : __builtin_inff();
+      if constexpr (DK) x_lds[buf][tid] = xreg;
+    }
   };
   // s_waitcnt vmcnt(4), leaving the other counters alone (gfx9 encoding:
   // vmcnt [3:0], expcnt [6:4] = 7, lgkmcnt [11:8] = 15)
@@ -315,10 +338,10 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   int32_t r0 = (int32_t)(t_top * kBRows);   // and its first row
   const int32_t kw32 = (int32_t)kw0;
   const int32_t win = a.window < 0x40000000 ? (int32_t)a.window : 0x40000000;
-  // per-lane LDS byte offsets of the operand reads: q row 16rg + ln, chunk
-  // 4c + lg; dO rows 4lg + ln/4 (+16), dims 16dt + 4(ln%4), 8 bytes
-  const int dr = 4 * lg + (ln >> 2);
-  const uint32_t d_rd = (uint32_t)dr * 256u + 8u * (ln & 1);
+  // per-lane LDS byte offsets of the transposing reads: rows 4lg + ln/4
+  // (+16), dims 16dt + 4(ln%4), 8 bytes
+  const int tr_row = 4 * lg + (ln >> 2);
+  const uint32_t tr_off = (uint32_t)tr_row * 256u + 8u * (ln & 1);
   int buf = 0, buf2 = 2;  // buffers of this step and of step + 2
   for (int32_t step = 0; step < nsteps; ++step) {
     const bool more = step + 1 < nsteps, more2 = step + 2 < nsteps;
@@ -330,20 +353,37 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     const bool any = r0 + kBRows - 1 >= kw32 && r0 - (kw32 + 31) < win && kw32 < T32;
     if (any) {
       const char* ql = (const char*)q_lds[buf];
-      const uint32_t dl = lds_addr(d_lds[buf]);
-      // ---- S[row][key]: 2 row tiles x 2 key tiles ----
-      float4v sacc[2][2];
+      const char* dl = (const char*)d_lds[buf];
+      // ---- S[row][key] (and DK: dP[row][key] = dO V̂ᵀ): 2 row tiles x 2
+      // key tiles; A = the staged rows (row 16rg + ln, chunk 4c + lg) ----
+      float4v sacc[2][2], dpacc[2][2];
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg) {
         half8 qa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qa[c] = *(const half8*)(ql + (16 * rg + ln) * 256 + 16 * q_slot(ln, 4 * c + lg));
+        for (int c = 0; c < 4; ++c) qa[c] = *(const half8*)(ql + (16 * rg + ln) * 256 + 16 * row_slot(ln, 4 * c + lg));
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < 4; ++c)
             sacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kop[kt][c], sacc[rg][kt], 0, 0, 0);
+        }
+      }
+      if constexpr (DK) {
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          half8 da[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            da[c] = *(const half8*)(dl + (16 * rg + ln) * 256 + 16 * row_slot(ln, 4 * c + lg));
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            dpacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              dpacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[c], vop[kt][c], dpacc[rg][kt], 0, 0, 0);
+          }
         }
       }
       // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
@@ -361,6 +401,14 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
         for (int rg = 0; rg < 2; ++rg) {
           const float4 l4 = *(const float4*)(&l_lds[step & 1][16 * rg + 4 * lg]);
           const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
+          float x4[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (DK) {
+            const float4 d4 = *(const float4*)(&x_lds[step & 1][16 * rg + 4 * lg]);
+            x4[0] = d4.x;
+            x4[1] = d4.y;
+            x4[2] = d4.z;
+            x4[3] = d4.w;
+          }
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -374,7 +422,16 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
                 const uint32_t diff = (uint32_t)(base + 16 * rg + e - 16 * kt);
                 x = diff < (uint32_t)win ? x : -__builtin_inff();
               }
-              pa[kt][4 * rg + e] = (_Float16)__builtin_amdgcn_exp2f(x);
+              float p = __builtin_amdgcn_exp2f(x);
+              // DK: dS = P (dP - delta_row) in place of P, rounded to fp32
+              // and then to fp16 in every element (the empty asm keeps the
+              // compiler from fusing the product into the conversion,
+              // v_fma_mixlo_f16, in some elements and not in others)
+              if constexpr (DK) {
+                p *= dpacc[rg][kt][e] - x4[e];
+                asm volatile("" : "+v"(p));
+              }
+              pa[kt][4 * rg + e] = (_Float16)p;
             }
         }
       };
@@ -385,11 +442,13 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       } else {
         make_p(std::true_type{});
       }
-      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln): slots {4lg..4lg+3} =
-      // rows 4lg..4lg+3 and {16+4lg..} = rows 16+4lg.., two transposing reads ----
+      // ---- d += Pᵀ dO (DK: dSᵀ Q_rot): B = the staged rows' dim 16dt + ln
+      // at slots {4lg..4lg+3} = rows 4lg..4lg+3 and {16+4lg..} = rows
+      // 16+4lg.., two transposing reads of dO (DK: q_rot) ----
+      const uint32_t tl = lds_addr(DK ? (const void*)ql : (const void*)dl) + tr_off;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint32_t at = dl + d_rd + 16u * d_slot(dr, 2 * dt + ((ln & 3) >> 1));
+        const uint32_t at = tl + 16u * row_slot(tr_row, 2 * dt + ((ln & 3) >> 1));
         const half4 lo = lds_read_tr16(at);
         const half4 hi = lds_read_tr16(at + 16u * 256u);
         const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -423,334 +482,6 @@ __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     for (int e = 0; e < 4; ++e) {
       const int64_t key = kw0 + 16 * kt + 4 * lg + e;
       if (key >= a.T) continue;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) out[key * kBD + 16 * dt + ln] = acc[kt][dt][e];
-    }
-}
-
-// The same walk for dK̂ (DK = true) of the same attention; DK = false is the
-// value gradient again, kept as the template's reference instance (the value
-// gradient launches prefill_value_grad_kernel above, which the compiler
-// schedules with fewer waits: 522 against 626 us at the config-5 shape):
-//   dP = dO V̂ᵀ, dS = P (dP - delta_row), dK̂_rot += dSᵀ Q_rot / sqrt(D),
-// then the inverse rotary at the key's position.  There the staged dO rows
-// stay row-major (A operand of dP), the wave's V̂ rows join its K̂ as B
-// operands, and Q_rotᵀ for the last product comes from the q operands already
-// in registers by MFMAs against identity columns (exact).
-template <bool DK>
-__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void prefill_kv_grad_kernel(ValueGradArgs a) {
-  __shared__ __align__(16) _Float16 q_lds[2][kQTile];
-  __shared__ __align__(16) _Float16 d_lds[2][kDTile];  // dOᵀ [dim][row], or dO rows when DK
-  __shared__ __align__(16) float l_lds[2][kBRows];
-  __shared__ __align__(16) float x_lds[2][kBRows];     // delta (DK)
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the step tests below branch on it
-  const int ln = lane & 15, lg = lane >> 4;
-  const int NQ = a.nq;
-  const int64_t nkb = ceil_div(a.T, kBKeys);
-  // key blocks fastest: the blocks of one (batch row, kv head) share its q and
-  // dO rows in one XCD's L2
-  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int chunk = blockIdx.y;  // grid row: the chunk of query tiles (chunk index mod slots)
-  const int64_t kb = bid % (uint32_t)nkb;
-  const int64_t kvh = (bid / (uint32_t)nkb) % (uint32_t)a.KVH;
-  const int64_t b = bid / ((uint32_t)nkb * (uint32_t)a.KVH);
-  const int64_t key0 = kb * kBKeys;
-  const int64_t kw0 = key0 + 32 * wave;  // this wave's first key
-  const int64_t p0 = a.start[b];
-  const float scale2 = 1.4426950408889634f / sqrtf((float)kBD);
-  const int64_t rope_last = a.rope_len - 1;
-  auto rope_row = [&](int64_t pos) -> const _Float16* {
-    return a.rope + (pos < 0 ? 0 : (pos < rope_last ? pos : rope_last)) * kRopeRow;
-  };
-  const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-
-  // ---- the wave's rotated keys as B operands: kop[kt][c] = dims
-  // [32c + 8lg, +8) of key kw0 + 16kt + ln (chunks c and c+2 are rotary
-  // partners) ----
-  half8 kop[2][4];
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    const int64_t key = kw0 + 16 * kt + ln;
-    const bool ok = key < a.T;
-    const _Float16* kp = a.k + b * a.ksb + kvh * a.ksh + (ok ? key : 0) * a.kst;
-    const _Float16* tr = rope_row(p0 + (ok ? key : 0));
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int d0 = 32 * c + 8 * lg;
-      half8 cs, sn, r0, r1;
-      load_trig8(tr, d0, &cs, &sn);
-      rope16(*(const half8*)(kp + d0), *(const half8*)(kp + d0 + 64), cs, sn, &r0, &r1);
-      kop[kt][c] = ok ? r0 : zero8;
-      kop[kt][c + 2] = ok ? r1 : zero8;
-    }
-  }
-  // DK: the wave's V̂ rows as B operands, same layout (no rotary), and the
-  // identity columns of the transposing MFMAs
-  half8 vop[2][4], ident[2];
-  if constexpr (DK) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int64_t key = kw0 + 16 * kt + ln;
-      const bool ok = key < a.T;
-      const _Float16* vp = a.v + b * a.vsb + kvh * a.vsh + (ok ? key : 0) * a.vst;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) vop[kt][c] = ok ? *(const half8*)(vp + 32 * c + 8 * lg) : zero8;
-    }
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ident[hf][e] = (_Float16)(8 * lg + e == 16 * hf + ln ? 1.f : 0.f);
-  }
-  float4v acc[2][8];  // d[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
-
-  // this workgroup's query tiles, top first (none: no slot to write)
-  const TileRun run = tile_run(key0, a.T, a.window, a.chunk_tiles, a.slots, chunk);
-  if (run.n == 0) return;
-  const int64_t t_top = run.top;
-  const int64_t nsteps = run.n * NQ;
-
-  // ---- step loaders.  q: thread -> row tid/8, rotary chunk pair (p, p+8),
-  // p = tid%8, rotated before it is stored.  dO: thread -> row pair tid%16,
-  // dims [8*(tid/16), +8), stored transposed as (row, row+1) words.  A step
-  // (tile ft, head fh) is addressed as a uniform base plus per-thread offsets
-  // fixed for the whole loop ----
-  const int qr = tid >> 3, qp = tid & 7;
-  const int drp = tid & 15, ddb = tid >> 4;
-  const int64_t q_thr = (int64_t)qr * a.qst + 8 * qp;
-  const int64_t d_thr0 = (int64_t)(2 * drp) * a.dst + 8 * ddb;
-  const int64_t d_thr1 = d_thr0 + a.dst;
-  const _Float16* q_b = a.q + b * a.qsb + kvh * NQ * a.qsh;
-  const _Float16* d_b = a.dout + b * a.dsb + kvh * NQ * a.dsh;
-  const float* l_b = a.lse + (b * a.QH + kvh * NQ) * a.T;
-  // Every load of a step is unconditional (rows past the end read the step's
-  // first row, which is always in range) and the zero fill happens in
-  // store(): a select right after a load, or a load inside a branch, would
-  // make the wave wait for the whole prefetch where it is issued.
-  struct StepRegs {
-    half8 q0, q1, d0, d1;
-    float l, x;
-    int64_t pos;  // the q row's position (its trig row is read at store time)
-    bool ok, ok0, ok1, lok;
-  };
-  const int lrow = tid < kBRows ? tid : 0;
-  auto fetch = [&](int ft, int fh, StepRegs& r) {
-    const int64_t r0 = (t_top - ft) * kBRows;
-    const int64_t row = r0 + qr;
-    r.ok = row < a.T;
-    const _Float16* qrow = q_b + fh * a.qsh + r0 * a.qst + (r.ok ? q_thr : 8 * qp);
-    r.q0 = *(const half8*)qrow;
-    r.q1 = *(const half8*)(qrow + 64);
-    r.pos = p0 + (r.ok ? row : r0);
-    const _Float16* dstep = d_b + fh * a.dsh + r0 * a.dst;
-    r.lok = tid < kBRows && r0 + tid < a.T;
-    const int64_t lr = r0 + (r.lok ? lrow : 0);
-    if constexpr (DK) {
-      // dO row qr, dims [8qp, +8) and [8qp + 64, +8), as the q rows
-      const _Float16* drow = dstep + (r.ok ? (int64_t)qr * a.dst : 0) + 8 * qp;
-      r.d0 = *(const half8*)drow;
-      r.d1 = *(const half8*)(drow + 64);
-      r.x = a.delta[(b * a.QH + kvh * NQ + fh) * a.T + lr];
-    } else {
-      r.ok0 = r0 + 2 * drp < a.T;
-      r.ok1 = r0 + 2 * drp + 1 < a.T;
-      r.d0 = *(const half8*)(dstep + (r.ok0 ? d_thr0 : 8 * ddb));
-      r.d1 = *(const half8*)(dstep + (r.ok1 ? d_thr1 : 8 * ddb));
-    }
-    r.l = l_b[fh * a.T + lr];
-  };
-  auto store = [&](const StepRegs& r, int buf) {
-    half8 cs, sn, r0, r1;
-    load_trig8(rope_row(r.pos), 8 * qp, &cs, &sn);
-    rope16(r.ok ? r.q0 : zero8, r.ok ? r.q1 : zero8, cs, sn, &r0, &r1);
-    _Float16* qd = q_lds[buf] + qr * kQStride + 8 * qp;
-    *(half8*)qd = r0;
-    *(half8*)(qd + 64) = r1;
-    if constexpr (DK) {
-      _Float16* dd = d_lds[buf] + qr * kQStride + 8 * qp;
-      *(half8*)dd = r.ok ? r.d0 : zero8;
-      *(half8*)(dd + 64) = r.ok ? r.d1 : zero8;
-      if (tid < kBRows) x_lds[buf][tid] = r.lok ? r.x : 0.f;
-    } else {
-      const half8 d0 = r.ok0 ? r.d0 : zero8, d1 = r.ok1 ? r.d1 : zero8;
-      _Float16* dd = d_lds[buf] + (8 * ddb) * kDStride + 2 * drp;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) *(uint32_t*)(dd + e * kDStride) = pair_words(d0, d1, e);
-    }
-    if (tid < kBRows) l_lds[buf][tid] = r.lok ? r.l * 1.4426950408889634f : 0.f;
-  };
-
-  // step s+1 waits in registers while s is computed and s+2 is in flight;
-  // steps run tile by tile, the group's heads within a tile
-  int ft = 0, fh = 0;  // the next step to fetch
-  auto advance = [&]() {
-    if (++fh == NQ) {
-      fh = 0;
-      ++ft;
-    }
-  };
-  // (DK: one step ahead only; its registers are needed elsewhere)
-  StepRegs nxt;
-  if (nsteps > 0) {
-    StepRegs r;
-    fetch(ft, fh, r);
-    advance();
-    if (!DK && nsteps > 1) {
-      fetch(ft, fh, nxt);
-      advance();
-    }
-    store(r, 0);
-  }
-  __syncthreads();
-
-  int ct = 0, ch = 0;  // the step being computed
-  for (int64_t step = 0; step < nsteps; ++step) {
-    const int buf = (int)(step & 1);
-    const bool more = step + 1 < nsteps;
-    StepRegs ahead;
-    if constexpr (DK) {
-      if (more) {
-        fetch(ft, fh, nxt);
-        advance();
-      }
-    } else if (step + 2 < nsteps) {
-      fetch(ft, fh, ahead);
-      advance();
-    }
-    const int64_t r0 = (t_top - ct) * kBRows;
-    // does any row of the step see any of this wave's keys?
-    const bool any = r0 + kBRows - 1 >= kw0 && r0 - (kw0 + 31) < a.window && kw0 < a.T;
-    if (any) {
-      const _Float16* ql = q_lds[buf];
-      const _Float16* dl = d_lds[buf];
-      // ---- S[row][key]: 2 row tiles x 2 key tiles ----
-      float4v sacc[2][2];
-      half8 qa[4];  // one row tile's q operands at a time
-#pragma unroll
-      for (int rg = 0; rg < 2; ++rg) {
-        half8 (&qr)[4] = qa;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qr[c] = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            sacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qr[c], kop[kt][c], sacc[rg][kt], 0, 0, 0);
-        }
-      }
-      // DK: dP[row][key] = dO V̂ᵀ (A = the staged dO rows)
-      float4v dpacc[2][2];
-      if constexpr (DK) {
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-          half8 da[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) da[c] = *(const half8*)(dl + (16 * rg + ln) * kQStride + 32 * c + 8 * lg);
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
-            dpacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              dpacc[rg][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[c], vop[kt][c], dpacc[rg][kt], 0, 0, 0);
-          }
-        }
-      }
-      // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
-      // kw0 + 16kt + ln; pa[kt] contraction slot 4rg + e (of lane group lg)
-      // <-> row 16rg + 4lg + e ----
-      const bool full = r0 >= kw0 + 31 && r0 + kBRows - 1 - kw0 < a.window && r0 + kBRows <= a.T;
-      const int base = (int)(r0 - kw0) + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
-      const int rows_left = (int)(a.T - r0 < kBRows ? a.T - r0 : kBRows);
-      const int keys_left = (int)(a.T - kw0 < 32 ? a.T - kw0 : 32);
-      const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
-      half8 pa[2];
-      auto make_p = [&](auto masked_tag) {
-        constexpr bool masked = decltype(masked_tag)::value;
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-          const float4 l4 = *(const float4*)(&l_lds[buf][16 * rg + 4 * lg]);
-          const float l2[4] = {l4.x, l4.y, l4.z, l4.w};
-          float x4[4] = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (DK) {
-            const float4 d4 = *(const float4*)(&x_lds[buf][16 * rg + 4 * lg]);
-            x4[0] = d4.x; x4[1] = d4.y; x4[2] = d4.z; x4[3] = d4.w;
-          }
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float p = __builtin_amdgcn_exp2f(fmaf(sacc[rg][kt][e], scale2, -l2[e]));
-              if constexpr (masked) {
-                const int diff = base + 16 * rg + e - 16 * kt;
-                const bool vis = diff >= 0 && diff < win && 16 * rg + 4 * lg + e < rows_left &&
-                                 16 * kt + ln < keys_left;
-                p = vis ? p : 0.f;
-              }
-              // DK: dS = P (dP - delta_row) in place of P
-              if constexpr (DK) p *= dpacc[rg][kt][e] - x4[e];
-              pa[kt][4 * rg + e] = (_Float16)p;
-            }
-        }
-      };
-      // a uniform branch: the steps away from the diagonal and the ends pay
-      // for no mask
-      if (full) {
-        make_p(std::false_type{});
-      } else {
-        make_p(std::true_type{});
-      }
-      // ---- dV̂ += Pᵀ dO: B = dOᵀ row (dim 16dt + ln), rows {4lg..4lg+3} and
-      // {16+4lg..16+4lg+3}.  DK: dK̂_rot += dSᵀ Q_rot, B = Q_rotᵀ from the
-      // transposing MFMAs in the same slot order ----
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        half8 db;
-        if constexpr (DK) {
-#pragma unroll
-          for (int rg = 0; rg < 2; ++rg) {
-            // the q operand again from LDS (cheaper than keeping both row tiles live)
-            const half8 qav = *(const half8*)(ql + (16 * rg + ln) * kQStride + 32 * (dt >> 1) + 8 * lg);
-            const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(qav, ident[dt & 1],
-                                                                   float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) db[4 * rg + e] = (_Float16)t[e];
-          }
-        } else {
-          const _Float16* dr = dl + (16 * dt + ln) * kDStride + 4 * lg;
-          const half4 lo = *(const half4*)dr;
-          const half4 hi = *(const half4*)(dr + 16);
-          db = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
-      }
-    }
-    // ---- the next step into the other buffer ----
-    if (more) store(nxt, buf ^ 1);
-    if constexpr (!DK) nxt = ahead;
-    __syncthreads();
-    if (++ch == NQ) {
-      ch = 0;
-      ++ct;
-    }
-  }
-
-  // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
-  float* out = a.dv + (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t key = kw0 + 16 * kt + 4 * lg + e;
-      if (key >= a.T) continue;
       if constexpr (DK) {
         // 1/sqrt(D), then the rotary's transpose at the key's position:
         // dims f and f + 64 (slices dt and dt + 4) are one rotation pair
@@ -769,6 +500,16 @@ void prefill_kv_grad_kernel(ValueGradArgs a) {
         for (int dt = 0; dt < 8; ++dt) out[key * kBD + 16 * dt + ln] = acc[kt][dt][e];
       }
     }
+}
+
+// 168 registers: three workgroups per CU
+__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void prefill_value_grad_kernel(ValueGradArgs a) {
+  kv_grad_walk<false>(a);
+}
+__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_key_grad_kernel(ValueGradArgs a) {
+  kv_grad_walk<true>(a);
 }
 
 // Query gradient of the same attention, and delta = rowsum(dO * O) that the
@@ -1098,12 +839,13 @@ int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t QH, int64_t KV
 
 namespace jkv {
 
-// shared by the value and key gradients: checks, the row runs, the launch and
-// the reduction of the runs' partial slots
+// shared by the value and key gradients: checks, the rotated queries (into
+// the workspace, unless `rotated` says an earlier leg left them there), the
+// row runs, the launch and the reduction of the runs' partial slots
 template <bool DK>
 static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[12], int nstrides,
                           const void* rope_table, float* d_out_buf, void* workspace, int64_t workspace_bytes,
-                          hipStream_t stream) {
+                          hipStream_t stream, bool rotated = false) {
   const int64_t B = a.B, QH = a.QH, KVH = a.KVH, T = a.T;
   JKV_CHECK_ARG(D == kBD, "prefill gradients support head_dim 128, got %lld", (long long)D);
   JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
@@ -1115,16 +857,15 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   JKV_CHECK_ARG(!DK || (a.v && a.delta), "null buffer");
   JKV_CHECK_ARG(a.rope_len >= 1, "rotary table is empty");
   JKV_CHECK_ARG(B < 65536 && QH < 65536, "prefill gradients: batch and query heads must be below 65536");
-  if constexpr (!DK) {
-    // the value kernel's 32-bit offsets: positions, rotary rows, and the
-    // bytes of one (batch row, kv head)'s rotated queries, output gradient
-    // and lse
+  {
+    // the walk's 32-bit offsets: positions, rotary rows, and the bytes of
+    // one (batch row, kv head)'s rotated queries, output gradient and lse
     const int64_t nq1 = NQ - 1, lim = (int64_t)1 << 31;
     JKV_CHECK_ARG(T < ((int64_t)1 << 30) && a.rope_len < ((int64_t)1 << 23),
                   "prefill gradients support at most 2^30 tokens and 2^23 rotary positions");
     JKV_CHECK_ARG(a.dst >= 0 && a.dsh >= 0 && NQ * T * kBD * 2 < lim &&
                       (nq1 * a.dsh + (T - 1) * a.dst + kBD) * 2 < lim && (nq1 * T + kBRows) * 4 < lim,
-                  "prefill value gradient: the query heads of one kv head must span under 2^31 bytes "
+                  "prefill gradients: the query heads of one kv head must span under 2^31 bytes "
                   "of q, d_out and lse");
   }
   for (int i = 0; i < nstrides; ++i)
@@ -1139,16 +880,13 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   a.chunk_tiles = chunk_tiles;
   a.slots = chunks;
   const int64_t n = B * KVH * T * kBD;
-  // workspace: the chunks' partial slots, then (value gradient) the rotated
-  // queries
+  // workspace: the chunks' partial slots, then the rotated queries
   const int64_t slot_bytes = chunks > 1 ? (int64_t)chunks * n * (int64_t)sizeof(float) : 0;
-  const int64_t need = DK ? slot_bytes : value_grad_workspace(B, QH, KVH, T, a.window);
-  if (need > 0) {
-    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                  "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
-                  (long long)need);
-    JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
-  }
+  const int64_t need = value_grad_workspace(B, QH, KVH, T, a.window);
+  JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)need);
+  JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
   if (chunks > 1) {
     a.dv = (float*)workspace;
     a.slot_stride = n;
@@ -1158,15 +896,17 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   }
   const int64_t blocks = ceil_div(T, kBKeys) * KVH * B;
   JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-  if constexpr (DK) {
-    hipLaunchKernelGGL(prefill_kv_grad_kernel<true>, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
-                       stream, a);
-  } else {
-    _Float16* q_rot = (_Float16*)((unsigned char*)workspace + ceil_div(slot_bytes, 256) * 256);
+  _Float16* q_rot = (_Float16*)((unsigned char*)workspace + ceil_div(slot_bytes, 256) * 256);
+  if (!rotated) {
     hipLaunchKernelGGL(rotate_query_rows_kernel, dim3((uint32_t)ceil_div(8 * T, 256), (uint32_t)QH, (uint32_t)B),
                        dim3(256), 0, stream, a.q, a.qsb, a.qsh, a.qst, T, a.start, a.rope, a.rope_len, q_rot);
     JKV_CHECK_LAUNCH();
-    a.q = q_rot;  // contiguous [B,QH,T,128]
+  }
+  a.q = q_rot;  // contiguous [B,QH,T,128]
+  if constexpr (DK) {
+    hipLaunchKernelGGL(prefill_key_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
+                       stream, a);
+  } else {
     hipLaunchKernelGGL(prefill_value_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
                        stream, a);
   }
@@ -1321,12 +1061,15 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
     hipLaunchKernelGGL(prefill_q_grad_kernel, dim3((uint32_t)blocks), dim3(kBThreads), 0, stream, qa);
     JKV_CHECK_LAUNCH();
   }
+  // the key and value legs share the rotated queries: the first writes them
+  // (after the query leg, which may use the slot area)
   if (d_key) {
     const int rc = launch_kv_grad<true>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream);
     if (rc != JKV_OK) return rc;
   }
   if (d_value) {
-    const int rc = launch_kv_grad<false>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream);
+    const int rc = launch_kv_grad<false>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream,
+                                         d_key != nullptr);
     if (rc != JKV_OK) return rc;
   }
   return JKV_OK;

@@ -42,10 +42,6 @@ static const int kBD = 128;            // head dim
 static const int kBKeys = 128;         // keys per workgroup (32 per wave)
 static const int kBRows = 32;          // query rows per step
 static const int kBThreads = 256;      // 4 waves
-static const int kQStride = kBD + 8;   // q tile row stride (halves): 272 B spreads rows over banks
-static const int kDStride = kBRows + 4;  // dOᵀ row stride (halves): 72 B, conflict-free b64 reads
-static const int kQTile = kBRows * kQStride;
-static const int kDTile = kBD * kDStride;
 
 struct ValueGradArgs {
   const _Float16* q;  // pre-RoPE q; for the value kernel the rotated q_rot, contiguous [B,QH,T,128]
@@ -97,17 +93,12 @@ __device__ inline TileRun tile_run(int64_t key0, int64_t T, int64_t window, int6
   return TileRun{hi, hi >= lo ? hi - lo + 1 : 0};
 }
 
-// (a[e], b[e]) as one 32-bit word
-__device__ __forceinline__ uint32_t pair_words(half8 a, half8 b, int e) {
-  const half2v h = {a[e], b[e]};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
-// Rotated queries for the value kernel: q_rot[b,h,t,:] = the reference's fp16
-// rotary of q[b,h,t,:] at position start[b] + t (clamped to the table),
-// contiguous [B,QH,T,128].  One thread per (row, rotary chunk pair p): dims
-// [8p, +8) and their partners [64 + 8p, +8).  Grid (ceil(8T/256), QH, B).
-__global__ __launch_bounds__(256) void rotate_query_rows_kernel(const _Float16* __restrict__ q, int64_t qsb,
+// Rotated rows for the gradient kernels: out[b,h,t,:] = the reference's fp16
+// rotary of q[b,h,t,:] (queries, or keys) at position start[b] + t (clamped
+// to the table), contiguous [B,H,T,128].  One thread per (row, rotary chunk
+// pair p): dims [8p, +8) and their partners [64 + 8p, +8).  Grid
+// (ceil(8T/256), H, B).
+__global__ __launch_bounds__(256) void rotate_rows_kernel(const _Float16* __restrict__ q, int64_t qsb,
                                                                 int64_t qsh, int64_t qst, int64_t T,
                                                                 const int32_t* __restrict__ start,
                                                                 const _Float16* __restrict__ rope,
@@ -140,14 +131,19 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const void __attribute__((address_space(3)))*)p;
 }
 
-// Staged rows (q_rot and dO tiles, 32 rows x 256 bytes) hold their 16-byte
-// chunks XOR-swizzled: chunk j of row r sits in slot j ^ f(r), f(r) =
-// 2 (r & 7) + ((r >> 3) & 1).  An A-operand read takes 16 consecutive rows
-// at one chunk (f is one-to-one on r mod 16); a transposing read takes
-// chunks 2t, 2t + 1 of 8 aligned consecutive rows (f / 2 is one-to-one on r
-// mod 8).  Either way a read's lanes sit on distinct banks.
+// Staged rows (q_rot, dO, K̂_rot and V̂ tiles, 32 rows x 256 bytes) hold their
+// 16-byte chunks XOR-swizzled: chunk j of row r sits in slot j ^ f(r), with f
+// chosen by how the tile is read.  An A-operand read (ds_read_b128) takes 16
+// consecutive rows at one chunk: f = r & 15.  A transposing read
+// (ds_read_b64_tr_b16) takes chunks 2t, 2t + 1 of 8 consecutive rows: f =
+// 2 (r & 7).  A tile read both ways takes f = 2 (r & 7) + ((r >> 3) & 1).
+// Each keeps a read's lanes on distinct banks, or nearly (measured: the
+// both-ways form costs the value kernel ~3 % when used for its tiles).
+enum Swz { kSwzA, kSwzT, kSwzAT };
+template <Swz W>
 __device__ __forceinline__ uint32_t row_slot(int r, int j) {
-  return (uint32_t)(j ^ (((r & 7) << 1) | ((r >> 3) & 1)));
+  const int f = W == kSwzA ? (r & 15) : W == kSwzT ? 2 * (r & 7) : ((r & 7) << 1) | ((r >> 3) & 1);
+  return (uint32_t)(j ^ f);
 }
 
 // The key-block walk of the value gradient (DK = false) and of the key
@@ -165,6 +161,9 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
   __shared__ __align__(1024) _Float16 d_lds[3][kBRows * kBD];
   __shared__ __align__(16) float l_lds[2][kBRows];
   __shared__ __align__(16) float x_lds[DK ? 2 : 1][kBRows];  // delta (DK)
+  // q rows: A operand of S (and, DK, transposed for dK); dO rows: transposed
+  // for dV (DK: A operand of dP)
+  constexpr Swz kQSwz = DK ? kSwzAT : kSwzA, kDSwz = DK ? kSwzA : kSwzT;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the step tests below branch on it
@@ -264,8 +263,8 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
     for (int i = 0; i < 2; ++i) {
       const int r = srow + 4 * i;
       const uint32_t rr = fr0 + r < T32 ? (uint32_t)r : 0u;
-      qo[i] = rr * (2u * kBD) + 16u * row_slot(r, slot);
-      dof[i] = rr * (uint32_t)a.dst * 2u + 16u * row_slot(r, slot);
+      qo[i] = rr * (2u * kBD) + 16u * row_slot<kQSwz>(r, slot);
+      dof[i] = rr * (uint32_t)a.dst * 2u + 16u * row_slot<kDSwz>(r, slot);
     }
   };
   aim();
@@ -343,6 +342,8 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
   const int tr_row = 4 * lg + (ln >> 2);
   const uint32_t tr_off = (uint32_t)tr_row * 256u + 8u * (ln & 1);
   int buf = 0, buf2 = 2;  // buffers of this step and of step + 2
+  // one step; MORE: a step follows, MORE2: two follow (the steady state, with
+  // no tests of its own; the last two steps are peeled)
   for (int32_t step = 0; step < nsteps; ++step) {
     const bool more = step + 1 < nsteps, more2 = step + 2 < nsteps;
     // the lse of step + 1, then step + 2's copies into the buffer that step
@@ -361,7 +362,8 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
       for (int rg = 0; rg < 2; ++rg) {
         half8 qa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qa[c] = *(const half8*)(ql + (16 * rg + ln) * 256 + 16 * row_slot(ln, 4 * c + lg));
+        for (int c = 0; c < 4; ++c)
+          qa[c] = *(const half8*)(ql + (16 * rg + ln) * 256 + 16 * row_slot<kQSwz>(ln, 4 * c + lg));
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -376,7 +378,7 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
           half8 da[4];
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            da[c] = *(const half8*)(dl + (16 * rg + ln) * 256 + 16 * row_slot(ln, 4 * c + lg));
+            da[c] = *(const half8*)(dl + (16 * rg + ln) * 256 + 16 * row_slot<kDSwz>(ln, 4 * c + lg));
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt) {
             dpacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -448,7 +450,7 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
       const uint32_t tl = lds_addr(DK ? (const void*)ql : (const void*)dl) + tr_off;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint32_t at = tl + 16u * row_slot(tr_row, 2 * dt + ((ln & 3) >> 1));
+        const uint32_t at = tl + 16u * row_slot<DK ? kQSwz : kDSwz>(tr_row, 2 * dt + ((ln & 3) >> 1));
         const half4 lo = lds_read_tr16(at);
         const half4 hi = lds_read_tr16(at + 16u * 256u);
         const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -519,12 +521,13 @@ void prefill_key_grad_kernel(ValueGradArgs a) {
 // waves per (batch row, kv head, head group, block of query rows) and run of
 // 32-key tiles; wave w is query head w % HW of the group on rows
 // 32 (w / HW) .. + 31 of the block.  Its rotated q and its dO rows stay in
-// registers as B operands; each key tile's rotated K̂ rows and V̂ rows land in
-// LDS once for the four waves.  Per tile and wave, on v_mfma_f32_16x16x32_f16:
+// registers as B operands; each key tile's rotated K̂ rows (rotated once by
+// the entry point) and V̂ rows go straight into LDS once for the four waves.
+// Per tile and wave, on v_mfma_f32_16x16x32_f16:
 //   Sᵀ[key][row] = K̂ Qᵀ and dPᵀ[key][row] = V̂ dOᵀ   (A = K̂ / V̂ rows from LDS)
 //   dS in A order read straight off the Sᵀ/dPᵀ accumulators (two 16-key
 //   tiles interleaved into the contraction slots)
-//   K̂ in B order from the same K̂ operands by MFMAs against identity columns
+//   K̂ in B order by transposing reads of the staged K̂ rows
 //   dQ[row][dim] += dS K̂
 static const int kQKeys = 32;  // keys per tile
 
@@ -537,10 +540,11 @@ struct QGradArgs {
   int32_t heads_per_wg, row_sets, head_groups;
 };
 
-__global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_) {
-  const ValueGradArgs& a = qa_.g;
-  __shared__ __align__(16) _Float16 k_lds[2][kQKeys * kQStride];
-  __shared__ __align__(16) _Float16 v_lds[2][kQKeys * kQStride];
+__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_q_grad_kernel(QGradArgs qa_) {
+  const ValueGradArgs& a = qa_.g;  // a.k: the rotated K̂_rot, contiguous [B,KVH,T,128]
+  __shared__ __align__(1024) _Float16 k_lds[3][kQKeys * kBD];
+  __shared__ __align__(1024) _Float16 v_lds[3][kQKeys * kBD];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the tile tests below branch on it
   const int ln = lane & 15, lg = lane >> 4;
@@ -604,11 +608,6 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
     l2[rg] = ok ? a.lse[(b * a.QH + head) * a.T + row] * 1.4426950408889634f : 0.f;
     if (ok && lg == 0 && chunk == 0) qa_.delta[(b * a.QH + head) * a.T + row] = dsum;
   }
-  half8 ident[2];
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ident[hf][e] = (_Float16)(8 * lg + e == 16 * hf + ln ? 1.f : 0.f);
   float4v acc[2][8];  // dQ_rot[row 16rg + 4lg + e][dim 16dt + ln]
 #pragma unroll
   for (int rg = 0; rg < 2; ++rg)
@@ -627,67 +626,76 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
   if (ntiles > a.chunk_tiles) ntiles = a.chunk_tiles;
   if (ntiles < 0) ntiles = 0;
 
-  // ---- tile loaders: thread -> key tid/8, rotary chunk pair (p, p+8),
-  // p = tid%8: rotated K̂ and plain V̂ ----
-  const int kr = tid >> 3, kp = tid & 7;
-  const _Float16* kb_ = a.k + b * a.ksb + kvh * a.ksh;
-  const _Float16* vb_ = a.v + b * a.vsb + kvh * a.vsh;
-  // Every load of a tile (the rotary rows too) is unconditional and left
-  // untouched until store(): keys past T read the tile's first key (always in
-  // range; causality masks them for every row).  A select right after a load
-  // would make the wave wait for the whole prefetch where it is issued.
-  struct TileRegs {
-    half8 k0, k1, v0, v1, cs, sn;
+  // ---- tile staging: a tile's K̂_rot rows (rotated by the entry point,
+  // contiguous [B,KVH,T,128]) and V̂ rows go global -> LDS directly, as in
+  // the key-block walk: two tiles ahead into three buffers, wave w filling
+  // key rows 8w..8w+7 of both with two instructions each, chunks swizzled
+  // by row_slot (K̂ rows read both ways, V̂ rows as A operands).  Keys past
+  // T read the tile's first key (always in range; causality masks them for
+  // every row) ----
+  const int srow = 8 * wave + (lane >> 4), slot = lane & 15;
+  const int32_t T32 = (int32_t)a.T;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.k + (b * a.KVH + kvh) * a.T * kBD), (short)0, (int)(a.T * 2 * kBD), 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.v + b * a.vsb + kvh * a.vsh), (short)0, (int)(((a.T - 1) * a.vst + kBD) * 2), 0x00020000);
+  const int32_t key_first = (int32_t)((t_first + tile_lo) * kQKeys);
+  const int32_t nt = (int32_t)ntiles;
+  auto copy = [&](int32_t tile, int buf) {
+    const int32_t first = key_first + tile * kQKeys;
+    char* kd = (char*)k_lds[buf] + 2048 * wave;
+    char* vd = (char*)v_lds[buf] + 2048 * wave;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = srow + 4 * i;
+      const uint32_t rr = first + r < T32 ? (uint32_t)r : 0u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (void __attribute__((address_space(3)))*)(kd + 1024 * i), 16,
+                                               rr * (2u * kBD) + 16u * row_slot<kSwzAT>(r, slot),
+                                               (uint32_t)first * (2u * kBD), 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (void __attribute__((address_space(3)))*)(vd + 1024 * i), 16,
+                                               rr * (uint32_t)a.vst * 2u + 16u * row_slot<kSwzA>(r, slot),
+                                               (uint32_t)first * (uint32_t)a.vst * 2u, 0, 0);
+    }
   };
-  auto fetch = [&](int64_t tile, TileRegs& r) {
-    const int64_t first = (t_first + tile_lo + tile) * kQKeys;
-    const int64_t key = first + kr;
-    const int64_t kk_ = key < a.T ? key : first;
-    const _Float16* kp_ = kb_ + kk_ * a.kst + 8 * kp;
-    const _Float16* vp_ = vb_ + kk_ * a.vst + 8 * kp;
-    r.k0 = *(const half8*)kp_;
-    r.k1 = *(const half8*)(kp_ + 64);
-    r.v0 = *(const half8*)vp_;
-    r.v1 = *(const half8*)(vp_ + 64);
-    load_trig8(rope_row(p0 + kk_), 8 * kp, &r.cs, &r.sn);
-  };
-  auto store = [&](const TileRegs& r, int buf) {
-    half8 r0, r1;
-    rope16(r.k0, r.k1, r.cs, r.sn, &r0, &r1);
-    _Float16* kd = k_lds[buf] + kr * kQStride + 8 * kp;
-    *(half8*)kd = r0;
-    *(half8*)(kd + 64) = r1;
-    _Float16* vd = v_lds[buf] + kr * kQStride + 8 * kp;
-    *(half8*)vd = r.v0;
-    *(half8*)(vd + 64) = r.v1;
-  };
-  if (ntiles > 0) {
-    TileRegs r;
-    fetch(0, r);
-    store(r, 0);
+  // s_waitcnt vmcnt(4), leaving the other counters alone (gfx9 encoding)
+  constexpr int kWaitVm4 = 4 | (7 << 4) | (15 << 8);
+  if (nt > 0) {
+    copy(0, 0);
+    if (nt > 1) {
+      copy(1, 1);
+      __builtin_amdgcn_s_waitcnt(kWaitVm4);  // tile 0 has landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
   }
   __syncthreads();
-  const int win = a.window < 0x40000000 ? (int)a.window : 0x40000000;
+  const int32_t win = a.window < 0x40000000 ? (int32_t)a.window : 0x40000000;
+  const int32_t r32 = (int32_t)row0;
+  // per-lane LDS byte offsets of the transposing reads: key rows 4lg + ln/4
+  // (+16), dims 16dt + 4(ln%4), 8 bytes
+  const int tr_row = 4 * lg + (ln >> 2);
+  const uint32_t tr_off = (uint32_t)tr_row * 256u + 8u * (ln & 1);
 
-  for (int64_t tile = 0; tile < ntiles; ++tile) {
-    const int buf = (int)(tile & 1);
-    const bool more = tile + 1 < ntiles;
-    TileRegs nxt;
-    if (more) fetch(tile + 1, nxt);
-    const int64_t key0 = (t_first + tile_lo + tile) * kQKeys;
-    const bool any = key0 <= row0 + 31 && row0 - (key0 + kQKeys - 1) < a.window;
+  int buf = 0, buf2 = 2;  // buffers of this tile and of tile + 2
+  // one tile; MORE2: two follow (the steady state; the last two are peeled)
+  for (int32_t tile = 0; tile < nt; ++tile) {
+    const bool more2 = tile + 2 < nt;
+    if (more2) copy(tile + 2, buf2);
+    const int32_t key0 = key_first + tile * kQKeys;
+    const bool any = key0 <= r32 + 31 && r32 - (key0 + kQKeys - 1) < win;
     if (any) {
-      const _Float16* kl = k_lds[buf];
-      const _Float16* vl = v_lds[buf];
-      // ---- Sᵀ and dPᵀ [key][row]: 2 key tiles x 2 row tiles ----
+      const char* kl = (const char*)k_lds[buf];
+      const char* vl = (const char*)v_lds[buf];
+      // ---- Sᵀ and dPᵀ [key][row]: 2 key tiles x 2 row tiles; A = the staged
+      // rows (key 16kt + ln, chunk 4c + lg) ----
       float4v st[2][2], dpt[2][2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         half8 ka[4], va[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          ka[c] = *(const half8*)(kl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
-          va[c] = *(const half8*)(vl + (16 * kt + ln) * kQStride + 32 * c + 8 * lg);
+          ka[c] = *(const half8*)(kl + (16 * kt + ln) * 256 + 16 * row_slot<kSwzAT>(ln, 4 * c + lg));
+          va[c] = *(const half8*)(vl + (16 * kt + ln) * 256 + 16 * row_slot<kSwzA>(ln, 4 * c + lg));
         }
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg) {
@@ -702,10 +710,10 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
       }
       // ---- dS, masked: element (kt, rg, e) is key key0 + 16kt + 4lg + e of
       // row row0 + 16rg + ln; dsa[rg] contraction slot 4kt + e (of lane group
-      // lg) <-> key 16kt + 4lg + e ----
-      const bool full = key0 + kQKeys - 1 <= row0 && row0 + 31 - key0 < a.window && row0 + 32 <= a.T;
-      const int base = (int)(row0 - key0) + ln - 4 * lg;  // row - key = base + 16rg - 16kt - e
-      const int rows_left = (int)(a.T - row0 < 32 ? a.T - row0 : 32);
+      // lg) <-> key 16kt + 4lg + e.  Rows past T need no mask: a row's dQ
+      // depends on its own dS only, and those rows are never stored ----
+      const bool full = key0 + kQKeys - 1 <= r32 && r32 + 31 - key0 < win;
+      const int base = r32 - key0 + ln - 4 * lg;  // row - key = base + 16rg - 16kt - e
       half8 dsa[2];
       auto make_ds = [&](auto masked_tag) {
         constexpr bool masked = decltype(masked_tag)::value;
@@ -715,13 +723,19 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
           for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float p = __builtin_amdgcn_exp2f(fmaf(st[kt][rg][e], scale2, -l2[rg]));
+              // hidden elements take exponent -inf (weight exactly 0),
+              // selected before the exponential; visible: 0 <= row - key <
+              // window, one unsigned compare
+              float x = fmaf(st[kt][rg][e], scale2, -l2[rg]);
               if constexpr (masked) {
-                const int diff = base + 16 * rg - 16 * kt - e;
-                const bool vis = diff >= 0 && diff < win && 16 * rg + ln < rows_left;
-                p = vis ? p : 0.f;
+                const uint32_t diff = (uint32_t)(base + 16 * rg - 16 * kt - e);
+                x = diff < (uint32_t)win ? x : -__builtin_inff();
               }
-              dsa[rg][4 * kt + e] = (_Float16)(p * (dpt[kt][rg][e] - dl[rg]));
+              // dS = fp16(fp32(P (dP - delta))) in every element (the empty
+              // asm keeps the product out of the conversion, v_fma_mixlo_f16)
+              float ds = __builtin_amdgcn_exp2f(x) * (dpt[kt][rg][e] - dl[rg]);
+              asm volatile("" : "+v"(ds));
+              dsa[rg][4 * kt + e] = (_Float16)ds;
             }
       };
       // a uniform branch: the tiles away from the diagonal and the ends pay
@@ -732,26 +746,28 @@ __global__ __launch_bounds__(kBThreads) void prefill_q_grad_kernel(QGradArgs qa_
         make_ds(std::true_type{});
       }
       // ---- dQ += dS K̂: B = K̂ in B order (keys {4lg+e, 16+4lg+e} of dim
-      // 16dt + ln) from the identity MFMAs ----
+      // 16dt + ln), two transposing reads of the staged K̂ rows ----
+      const uint32_t tl = lds_addr(kl) + tr_off;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        half8 kbo;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          // the K̂ operand again from LDS (cheaper than keeping all eight live)
-          const half8 kav = *(const half8*)(kl + (16 * kt + ln) * kQStride + 32 * (dt >> 1) + 8 * lg);
-          const float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(kav, ident[dt & 1],
-                                                                 float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) kbo[4 * kt + e] = (_Float16)t[e];
-        }
+        const uint32_t at = tl + 16u * row_slot<kSwzAT>(tr_row, 2 * dt + ((ln & 3) >> 1));
+        const half4 lo = lds_read_tr16(at);
+        const half4 hi = lds_read_tr16(at + 16u * 256u);
+        const half8 kbo = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg)
           acc[rg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dsa[rg], kbo, acc[rg][dt], 0, 0, 0);
       }
     }
-    if (more) store(nxt, buf ^ 1);
+    // tile + 1 has landed (this wave's part; the barrier covers the rest)
+    if (more2) {
+      __builtin_amdgcn_s_waitcnt(kWaitVm4);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
     __syncthreads();
+    buf = buf == 2 ? 0 : buf + 1;
+    buf2 = buf2 == 2 ? 0 : buf2 + 1;
   }
 
   // ---- 1/sqrt(D), the rotary's transpose at the row's position, store:
@@ -898,7 +914,7 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
   _Float16* q_rot = (_Float16*)((unsigned char*)workspace + ceil_div(slot_bytes, 256) * 256);
   if (!rotated) {
-    hipLaunchKernelGGL(rotate_query_rows_kernel, dim3((uint32_t)ceil_div(8 * T, 256), (uint32_t)QH, (uint32_t)B),
+    hipLaunchKernelGGL(rotate_rows_kernel, dim3((uint32_t)ceil_div(8 * T, 256), (uint32_t)QH, (uint32_t)B),
                        dim3(256), 0, stream, a.q, a.qsb, a.qsh, a.qst, T, a.start, a.rope, a.rope_len, q_rot);
     JKV_CHECK_LAUNCH();
   }
@@ -981,11 +997,12 @@ int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH,
   int chunk_tiles, chunks;
   value_grad_chunks(T, window, &chunk_tiles, &chunks);
   const int64_t delta = ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
+  const int64_t k_rot = ceil_div(B * KVH * T * kBD * 2, 256) * 256;
   // the slot area serves the query leg (delta only), the key leg's slots and
   // the value leg's slots and rotated queries in turn
   const int64_t qk = (int64_t)chunks * B * QH * T * kBD * (int64_t)sizeof(float);
   const int64_t v = value_grad_workspace(B, QH, KVH, T, window);
-  return delta + (qk > v ? qk : v);
+  return delta + k_rot + (qk > v ? qk : v);
 }
 
 int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
@@ -1008,8 +1025,10 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
   JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace) % 16 == 0,
                 "prefill backward needs %lld bytes of 16-byte aligned workspace", (long long)need);
   const int64_t NQ = QH / KVH;
+  // workspace: delta, the rotated keys of the query leg, the slot area
   float* delta = (float*)workspace;
-  unsigned char* slots = (unsigned char*)workspace + ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
+  _Float16* k_rot = (_Float16*)((unsigned char*)workspace + ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256);
+  unsigned char* slots = (unsigned char*)k_rot + ceil_div(B * KVH * T * kBD * 2, 256) * 256;
   const int64_t slot_bytes = workspace_bytes - (slots - (unsigned char*)workspace);
   ValueGradArgs g = {};
   g.q = (const _Float16*)q; g.qsb = q_stride_b; g.qsh = q_stride_h; g.qst = q_stride_t;
@@ -1038,8 +1057,18 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
                   "prefill buffers must be 16-byte aligned");
     // four waves: head w % HW on rows 32 (w / HW) of the block
     JKV_CHECK_ARG(NQ < 4 || NQ % 4 == 0, "query heads per kv head must be 1, 2 or a multiple of 4");
+    // the query kernel's 32-bit offsets into one (batch row, kv head)'s K̂_rot and V̂
+    JKV_CHECK_ARG(B < 65536 && KVH < 65536 && T < ((int64_t)1 << 30) && rope_len < ((int64_t)1 << 23) &&
+                      v_stride_t >= 0 && T * kBD * 2 < ((int64_t)1 << 31) &&
+                      ((T - 1) * v_stride_t + kBD) * 2 < ((int64_t)1 << 31),
+                  "prefill backward: one (batch row, kv head) must span under 2^31 bytes of K and V");
+    hipLaunchKernelGGL(rotate_rows_kernel, dim3((uint32_t)ceil_div(8 * T, 256), (uint32_t)KVH, (uint32_t)B),
+                       dim3(256), 0, stream, (const _Float16*)k, k_stride_b, k_stride_h, k_stride_t, T,
+                       start_positions, (const _Float16*)rope_table, rope_len, k_rot);
+    JKV_CHECK_LAUNCH();
     QGradArgs qa = {};
     qa.g = g;
+    qa.g.k = k_rot;  // contiguous [B,KVH,T,128]
     qa.g.rope = (const _Float16*)rope_table;
     qa.g.nq = (int32_t)NQ;
     qa.o = (const _Float16*)out; qa.osb = o_stride_b; qa.osh = o_stride_h; qa.ost = o_stride_t;

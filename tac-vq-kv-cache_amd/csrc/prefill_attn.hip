@@ -88,6 +88,15 @@ __device__ __forceinline__ uint32_t pair16(half8 a, half8 b, int e) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// transposing LDS read of the 8-byte piece at LDS byte address addr: in each
+// 16-lane block, lane 4j + e receives element e of the pieces that the
+// block's lanes j, j+4, j+8, j+12 address (ds_read_b64_tr_b16)
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+__device__ __forceinline__ half4 lds_read_tr16(uint32_t addr) {
+  return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(size_t)addr));
+}
+
 // CS = 0: the chunk's fp16 K̂/V̂ rows.  CS = 1, 2: K̂/V̂ rebuilt from uint8
 // codes while each tile loads (codes -> 16-byte codeword gathers from the
 // L2-resident fp16 tables -> fp16 stage sum, the codec's reconstruction), so
@@ -241,18 +250,30 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   auto word = [&](const _Float16* tab, int g, int st, uint32_t code) -> half8 {
     return *(const half8*)(tab + ((g * NW + st) * kPCodewords + (int)code) * 8);
   };
+  // CS = 0: K̂ rows and rotary rows through buffer loads: a per-thread 32-bit
+  // offset and the tile's uniform one, with int32 row arithmetic (keys past T
+  // read the tile's first key; positions clamp to the table)
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kbase, (short)0, CS == 0 ? (int)(((a.T - 1) * a.kst + kPD) * 2) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t t_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.rope, (short)0, (int)(a.rope_len * kRopeRow * 2), 0x00020000);
+  const int32_t p32 = (int32_t)p0, rlast32 = (int32_t)(a.rope_len - 1), T32 = (int32_t)a.T;
   auto fetch = [&](int64_t tile, const CodeRegs& c, TileRegs& r) {
-    const TileBase t = tile_base(tile);
-    r.cs = *(const half8*)(t.tt + t.to);
-    r.sn = *(const half8*)(t.tt + t.to + 64);
     if constexpr (CS == 0) {
-      const _Float16* kt = kbase + t.first * a.kst + 8 * kpart;
-      const _Float16* vt = vbase + t.first * a.vst + 8 * vdb;
-      r.k[0][0] = *(const half8*)(kt + t.ko);
-      r.k[1][0] = *(const half8*)(kt + t.ko + 64);
-      r.v[0][0] = *(const half8*)(vt + t.vo0);
-      r.v[1][0] = *(const half8*)(vt + t.vo1);
+      const int32_t first = (int32_t)(tile * kPKT);
+      const uint32_t kr = first + kk < T32 ? (uint32_t)kk : 0u;
+      int32_t pos = p32 >= rlast32 ? rlast32 : p32 + first + (int32_t)kr;  // (no int32 overflow)
+      pos = pos < 0 ? 0 : (pos < rlast32 ? pos : rlast32);
+      const uint32_t ko = kr * (uint32_t)a.kst * 2u + 16u * kpart, to = (uint32_t)pos * (2u * kRopeRow) + 16u * kpart;
+      const int ks = (int)((uint32_t)first * (uint32_t)a.kst * 2u);
+      r.k[0][0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, (int)ko, ks, 0));
+      r.k[1][0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, (int)(ko + 128u), ks, 0));
+      r.cs = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(t_rsrc, (int)to, 0, 0));
+      r.sn = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(t_rsrc, (int)(to + 128u), 0, 0));
     } else {
+      const TileBase t = tile_base(tile);
+      r.cs = *(const half8*)(t.tt + t.to);
+      r.sn = *(const half8*)(t.tt + t.to + 64);
 #pragma unroll
       for (int st = 0; st < CS; ++st) {
         r.k[0][st] = word(ktab, kpart, st, (c.kw >> (8 * st)) & 0xffu);
@@ -265,21 +286,51 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   auto store = [&](const TileRegs& r, int buf) {
     // the codec's reconstruction: fp16 of the fp32 stage sum, which one fp16
     // add gives for two stages
-    half8 k0 = r.k[0][0], k1 = r.k[1][0], v0 = r.v[0][0], v1 = r.v[1][0];
+    half8 k0 = r.k[0][0], k1 = r.k[1][0];
     if constexpr (CS == 2) {
       k0 = k0 + r.k[0][1];
       k1 = k1 + r.k[1][1];
-      v0 = v0 + r.v[0][1];
-      v1 = v1 + r.v[1][1];
     }
     half8 r0, r1;
     rope16(k0, k1, r.cs, r.sn, &r0, &r1);
     _Float16* kd = k_lds[buf] + kk * kKStride + 8 * kpart;
     *(half8*)kd = r0;
     *(half8*)(kd + 64) = r1;
-    _Float16* vd = v_lds[buf] + (8 * vdb) * kVStride + 2 * vkp;
+    if constexpr (CS > 0) {
+      half8 v0 = r.v[0][0], v1 = r.v[1][0];
+      if constexpr (CS == 2) {
+        v0 = v0 + r.v[0][1];
+        v1 = v1 + r.v[1][1];
+      }
+      _Float16* vd = v_lds[buf] + (8 * vdb) * kVStride + 2 * vkp;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) *(uint32_t*)(vd + e * kVStride) = pair16(v0, v1, e);
+      for (int e = 0; e < 8; ++e) *(uint32_t*)(vd + e * kVStride) = pair16(v0, v1, e);
+    }
+  };
+  // CS = 0: a tile's V̂ rows go global -> LDS directly (buffer_load_dwordx4
+  // ... lds: lane i of an instruction lands at its LDS base + 16 i), row-major
+  // [key][dim] with 16-byte chunk j of key r in slot j ^ 2 (r & 7), so that
+  // the transposing reads of the product below (32 bytes of 8 keys) hit
+  // distinct banks.  Wave w fills keys 8w..8w+7 with two instructions; keys
+  // past T read the tile's first key (their weights are 0).  Offsets fit 32
+  // bits (host-checked).
+  const int vrow = 8 * wave + (lane >> 4), vslot = lane & 15;
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)vbase, (short)0, CS == 0 ? (int)(((a.T - 1) * a.vst + kPD) * 2) : 0, 0x00020000);
+  auto copy_v = [&](int64_t tile, int buf) {
+    if constexpr (CS == 0) {
+      const int32_t first = (int32_t)(tile * kPKT), T32 = (int32_t)a.T;
+      char* vd = (char*)v_lds[buf] + 2048 * wave;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = vrow + 4 * i;
+        const uint32_t rr = first + r < T32 ? (uint32_t)r : 0u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            v_rsrc, (void __attribute__((address_space(3)))*)(vd + 1024 * i), 16,
+            rr * (uint32_t)a.vst * 2u + 16u * (uint32_t)(vslot ^ (2 * (r & 7))), (uint32_t)first * (uint32_t)a.vst * 2u,
+            0, 0);
+      }
+    }
   };
 
   // codes two tiles ahead, rows (or gathered words) one tile ahead
@@ -289,8 +340,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     load_codes(tile0, c0);
     TileRegs r;
     fetch(tile0, c0, r);
+    copy_v(tile0, 0);
     if (tile0 + 1 < tile1) load_codes(tile0 + 1, cn);
     store(r, 0);
+    if constexpr (CS == 0) __builtin_amdgcn_s_waitcnt(0);  // the V̂ copies have landed
   }
   __syncthreads();
 
@@ -299,7 +352,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     const int64_t key0 = tile * kPKT;
     const bool more = tile + 1 < tile1;
     TileRegs nxt;
-    if (more) fetch(tile + 1, cn, nxt);
+    if (more) {
+      fetch(tile + 1, cn, nxt);
+      copy_v(tile + 1, buf ^ 1);  // (the other buffer was freed by the last barrier)
+    }
     if (tile + 2 < tile1) load_codes(tile + 2, cn);
     const _Float16* kl = k_lds[buf];
     const _Float16* vl = v_lds[buf];
@@ -396,13 +452,25 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       }
     // ---- Oᵀ += V̂ᵀ Pᵀ: contraction slot 8lg+e <-> key 32kp + 4lg + e (e < 4),
     //      32kp + 16 + 4lg + e - 4 (e >= 4) ----
+    // (CS = 0: V̂ᵀ by two transposing reads of the row-major tile, keys
+    // 32kp + 4lg + ln/4 and 16 further, dims 16dt + 4(ln%4))
+    const int tr_row = 4 * lg + (ln >> 2);
+    const uint32_t vtr = (uint32_t)(size_t)(const void __attribute__((address_space(3)))*)vl + (uint32_t)tr_row * 256u +
+                         8u * (ln & 1);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
-        const _Float16* vr = vl + (16 * dt + ln) * kVStride + 32 * kp + 4 * lg;
-        const half4 lo = *(const half4*)vr;
-        const half4 hi = *(const half4*)(vr + 16);
+        half4 lo, hi;
+        if constexpr (CS == 0) {
+          const uint32_t at = vtr + 32u * 256u * kp + 16u * (uint32_t)((2 * dt + ((ln & 3) >> 1)) ^ (2 * (tr_row & 7)));
+          lo = lds_read_tr16(at);
+          hi = lds_read_tr16(at + 16u * 256u);
+        } else {
+          const _Float16* vr = vl + (16 * dt + ln) * kVStride + 32 * kp + 4 * lg;
+          lo = *(const half4*)vr;
+          hi = *(const half4*)(vr + 16);
+        }
         const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[0][kp], o[0][dt], 0, 0, 0);
         o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[1][kp], o[1][dt], 0, 0, 0);
@@ -410,6 +478,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     }
     // ---- the next tile into the other buffer ----
     if (more) store(nxt, buf ^ 1);
+    if constexpr (CS == 0) __builtin_amdgcn_s_waitcnt(0);  // the next tile's V̂ copies have landed
     __syncthreads();
   }
 
@@ -486,10 +555,10 @@ int jkv_prefill_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   JKV_CHECK_ARG((NQ & (NQ - 1)) == 0, "query heads per kv head must be a power of two");
   JKV_CHECK_ARG(window >= 1, "window must be positive");
   JKV_CHECK_ARG(T < ((int64_t)1 << 31), "prefill chunk too long");
-  JKV_CHECK_ARG(T * (k_st > v_st ? k_st : v_st) < ((int64_t)1 << 31), "prefill K/V rows too far apart");
+  JKV_CHECK_ARG(T * (k_st > v_st ? k_st : v_st) < ((int64_t)1 << 30), "prefill K/V rows too far apart");
   if (B == 0 || T == 0) return JKV_OK;
   JKV_CHECK_ARG(q && k && v && out && start_positions && rope_table, "null buffer");
-  JKV_CHECK_ARG(rope_len >= 1, "rotary table is empty");
+  JKV_CHECK_ARG(rope_len >= 1 && rope_len < ((int64_t)1 << 23), "rotary table must have 1 to 2^23 - 1 rows");
   const int64_t strides[9] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st};
   for (int i = 0; i < 9; ++i)
     JKV_CHECK_ARG(strides[i] % 8 == 0, "prefill strides must be multiples of 8 elements");

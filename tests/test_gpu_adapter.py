@@ -139,6 +139,39 @@ def test_key_grad_entry_matches_backward_key_leg(device, batch, qh, kvh, tokens,
     assert err <= 1e-4 * scale + 1e-6
 
 
+@pytest.mark.parametrize("batch,qh,kvh,tokens,starts,window", [
+    (2, 8, 2, 300, (0, 40), 4096),      # GQA 4, ragged tiles, two start positions
+    (1, 32, 8, 200, (0,), 64),          # Mistral heads, window binds
+])
+def test_strided_layouts_equal_contiguous(device, batch, qh, kvh, tokens, starts, window):
+    # q, K, V and dO as [B,T,H,D] tensors viewed as [B,H,T,D] (the layout a
+    # projection leaves): the forward, the value gradient and the full
+    # backward address them by their strides and must give the same bits as
+    # on contiguous copies
+    print(f"strided B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)
+    gen = torch.Generator().manual_seed(4400 + tokens)
+    views = [torch.randn(batch, tokens, h, 128, generator=gen).half().to(device).transpose(1, 2)
+             for h in (qh, kvh, kvh, qh)]
+    q, k, v, d = views
+    assert not q.is_contiguous() and q.stride(2) == qh * 128
+    qc, kc, vc, dc = (t.contiguous() for t in views)
+    st = torch.tensor(starts, dtype=torch.int32, device=device)
+    max_pos = max(starts) + tokens - 1
+    kw = dict(window=window, rope_theta=10000.0, max_position=max_pos)
+    lse_s = torch.empty(batch, qh, tokens, dtype=torch.float32, device=device)
+    lse_c = torch.empty_like(lse_s)
+    out_s = _ops.prefill_attention(q, k, v, st, lse=lse_s, **kw)
+    out_c = _ops.prefill_attention(qc, kc, vc, st, lse=lse_c, **kw)
+    assert torch.equal(out_s, out_c) and torch.equal(lse_s, lse_c)
+    dv_s = _ops.prefill_attention_value_grad(q, k, d, lse_c, st, **kw)
+    dv_c = _ops.prefill_attention_value_grad(qc, kc, dc, lse_c, st, **kw)
+    assert torch.equal(dv_s, dv_c)
+    grads_s = _ops.prefill_attention_backward(q, k, v, out_c, d, lse_c, st, **kw)
+    grads_c = _ops.prefill_attention_backward(qc, kc, vc, out_c, dc, lse_c, st, **kw)
+    for name, a, b in zip(("dq", "dk", "dv"), grads_s, grads_c):
+        assert torch.equal(a, b), name
+
+
 @pytest.mark.parametrize("tokens,stages,whitened", [(96, 2, False), (150, 4, True)])
 def test_closed_loop_attention_value_step(device, tokens, stages, whitened):
     # a small decoder layer (4 query heads, 1 kv head, head_dim 128) with

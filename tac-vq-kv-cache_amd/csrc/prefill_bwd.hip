@@ -537,6 +537,7 @@ struct QGradArgs {
   int64_t osb, osh, ost;
   float* delta;       // [B,QH,T] written
   float* dq;          // [B,QH,T,D] fp32, or the run's partial slot
+  _Float16* q_rot;    // [B,QH,T,D] fp16 contiguous: the rotated queries, written for the key and value legs (or null)
   int32_t heads_per_wg, row_sets, head_groups;
 };
 
@@ -593,6 +594,13 @@ void prefill_q_grad_kernel(QGradArgs qa_) {
       rope16(*(const half8*)(qp + d0), *(const half8*)(qp + d0 + 64), cs, sn, &r0, &r1);
       qop[rg][c] = ok ? r0 : zero8;
       qop[rg][c + 2] = ok ? r1 : zero8;
+      // every (head, row) has one wave (one run per row block): it also
+      // writes the row's q_rot for the key and value legs
+      if (qa_.q_rot != nullptr && ok) {
+        _Float16* qr = qa_.q_rot + ((b * a.QH + head) * a.T + row) * kBD + d0;
+        *(half8*)qr = r0;
+        *(half8*)(qr + 64) = r1;
+      }
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -861,7 +869,7 @@ namespace jkv {
 template <bool DK>
 static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[12], int nstrides,
                           const void* rope_table, float* d_out_buf, void* workspace, int64_t workspace_bytes,
-                          hipStream_t stream, bool rotated = false) {
+                          hipStream_t stream, const _Float16* q_rot_given = nullptr) {
   const int64_t B = a.B, QH = a.QH, KVH = a.KVH, T = a.T;
   JKV_CHECK_ARG(D == kBD, "prefill gradients support head_dim 128, got %lld", (long long)D);
   JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
@@ -896,13 +904,16 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   a.chunk_tiles = chunk_tiles;
   a.slots = chunks;
   const int64_t n = B * KVH * T * kBD;
-  // workspace: the chunks' partial slots, then the rotated queries
+  // workspace: the chunks' partial slots, then the rotated queries (unless
+  // the caller hands them in)
   const int64_t slot_bytes = chunks > 1 ? (int64_t)chunks * n * (int64_t)sizeof(float) : 0;
-  const int64_t need = value_grad_workspace(B, QH, KVH, T, a.window);
-  JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
-                (long long)need);
-  JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  const int64_t need = q_rot_given != nullptr ? slot_bytes : value_grad_workspace(B, QH, KVH, T, a.window);
+  if (need > 0) {
+    JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
+                  (long long)need);
+    JKV_CHECK_ARG(((uintptr_t)workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  }
   if (chunks > 1) {
     a.dv = (float*)workspace;
     a.slot_stride = n;
@@ -912,11 +923,13 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   }
   const int64_t blocks = ceil_div(T, kBKeys) * KVH * B;
   JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
-  _Float16* q_rot = (_Float16*)((unsigned char*)workspace + ceil_div(slot_bytes, 256) * 256);
-  if (!rotated) {
+  const _Float16* q_rot = q_rot_given;
+  if (q_rot == nullptr) {
+    _Float16* qr = (_Float16*)((unsigned char*)workspace + ceil_div(slot_bytes, 256) * 256);
     hipLaunchKernelGGL(rotate_rows_kernel, dim3((uint32_t)ceil_div(8 * T, 256), (uint32_t)QH, (uint32_t)B),
-                       dim3(256), 0, stream, a.q, a.qsb, a.qsh, a.qst, T, a.start, a.rope, a.rope_len, q_rot);
+                       dim3(256), 0, stream, a.q, a.qsb, a.qsh, a.qst, T, a.start, a.rope, a.rope_len, qr);
     JKV_CHECK_LAUNCH();
+    q_rot = qr;
   }
   a.q = q_rot;  // contiguous [B,QH,T,128]
   if constexpr (DK) {
@@ -998,11 +1011,12 @@ int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH,
   value_grad_chunks(T, window, &chunk_tiles, &chunks);
   const int64_t delta = ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
   const int64_t k_rot = ceil_div(B * KVH * T * kBD * 2, 256) * 256;
+  const int64_t q_rot = ceil_div(B * QH * T * kBD * 2, 256) * 256;
   // the slot area serves the query leg (delta only), the key leg's slots and
-  // the value leg's slots and rotated queries in turn
+  // the value leg's slots (and rotated queries, when it runs alone) in turn
   const int64_t qk = (int64_t)chunks * B * QH * T * kBD * (int64_t)sizeof(float);
   const int64_t v = value_grad_workspace(B, QH, KVH, T, window);
-  return delta + k_rot + (qk > v ? qk : v);
+  return delta + k_rot + q_rot + (qk > v ? qk : v);
 }
 
 int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
@@ -1025,10 +1039,12 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
   JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace) % 16 == 0,
                 "prefill backward needs %lld bytes of 16-byte aligned workspace", (long long)need);
   const int64_t NQ = QH / KVH;
-  // workspace: delta, the rotated keys of the query leg, the slot area
+  // workspace: delta, the rotated keys of the query leg, the rotated
+  // queries it writes for the key and value legs, the slot area
   float* delta = (float*)workspace;
   _Float16* k_rot = (_Float16*)((unsigned char*)workspace + ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256);
-  unsigned char* slots = (unsigned char*)k_rot + ceil_div(B * KVH * T * kBD * 2, 256) * 256;
+  _Float16* q_rot = (_Float16*)((unsigned char*)k_rot + ceil_div(B * KVH * T * kBD * 2, 256) * 256);
+  unsigned char* slots = (unsigned char*)q_rot + ceil_div(B * QH * T * kBD * 2, 256) * 256;
   const int64_t slot_bytes = workspace_bytes - (slots - (unsigned char*)workspace);
   ValueGradArgs g = {};
   g.q = (const _Float16*)q; g.qsb = q_stride_b; g.qsh = q_stride_h; g.qst = q_stride_t;
@@ -1073,6 +1089,7 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
     qa.g.nq = (int32_t)NQ;
     qa.o = (const _Float16*)out; qa.osb = o_stride_b; qa.osh = o_stride_h; qa.ost = o_stride_t;
     qa.delta = delta;
+    qa.q_rot = (d_key || d_value) ? q_rot : nullptr;
     qa.heads_per_wg = (int32_t)(NQ < 4 ? NQ : 4);
     qa.row_sets = 4 / qa.heads_per_wg;
     qa.head_groups = (int32_t)(NQ / qa.heads_per_wg);
@@ -1090,15 +1107,16 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
     hipLaunchKernelGGL(prefill_q_grad_kernel, dim3((uint32_t)blocks), dim3(kBThreads), 0, stream, qa);
     JKV_CHECK_LAUNCH();
   }
-  // the key and value legs share the rotated queries: the first writes them
-  // (after the query leg, which may use the slot area)
+  // the key and value legs read the rotated queries the query leg wrote;
+  // without it (d_value alone) the value leg rotates them itself
+  const bool q_leg = d_query || d_key;
   if (d_key) {
-    const int rc = launch_kv_grad<true>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream);
+    const int rc = launch_kv_grad<true>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream, q_rot);
     if (rc != JKV_OK) return rc;
   }
   if (d_value) {
     const int rc = launch_kv_grad<false>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream,
-                                         d_key != nullptr);
+                                         q_leg ? q_rot : nullptr);
     if (rc != JKV_OK) return rc;
   }
   return JKV_OK;

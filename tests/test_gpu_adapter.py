@@ -84,6 +84,8 @@ def test_autograd_value_path(device):
     (1, 16, 2, 96, (0,), 4096),         # GQA 8: two head groups per kv head
     (1, 8, 2, 600, (0,), 4096),         # rows and keys split in runs (workspace + reduce)
     (1, 8, 2, 1500, (0,), 256),         # window binds over many tiles: chunks wrap the slots
+    (1, 4, 1, 1, (9,), 4096),           # one token: one step in every walk
+    (2, 8, 2, 33, (0, 31), 16),         # one row past a tile, window of 16
 ])
 def test_full_backward_matches_oracle(device, batch, qh, kvh, tokens, starts, window):
     print(f"backward B={batch} QH={qh} KVH={kvh} T={tokens} starts={starts} win={window}", flush=True)

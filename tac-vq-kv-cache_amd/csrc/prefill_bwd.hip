@@ -60,6 +60,7 @@ struct ValueGradArgs {
   const _Float16* rope;
   int64_t rope_len;
   float* dv;  // [B,KVH,T,D] fp32 contiguous, or the chunk's partial slot
+  float* dk;  // the same for dK̂ when the walk forms both gradients
   int32_t nq;
   int32_t chunk_tiles;  // query tiles per chunk (the query rows are split in chunks of tiles)
   int64_t slot_stride;  // elements between the chunks' partial slots (0: one chunk)
@@ -77,15 +78,17 @@ struct ValueGradArgs {
 struct TileRun {
   int64_t top, n;
 };
-__host__ __device__ inline void block_tiles(int64_t key0, int64_t T, int64_t window, int64_t* tf, int64_t* tl) {
-  int64_t rend = key0 + kBKeys - 1 + window;
+__host__ __device__ inline void block_tiles(int64_t key0, int64_t T, int64_t window, int keys, int64_t* tf,
+                                            int64_t* tl) {
+  int64_t rend = key0 + keys - 1 + window;
   if (rend > T || rend < 0) rend = T;
   *tf = key0 / kBRows;
   *tl = (rend - 1) / kBRows;
 }
-__device__ inline TileRun tile_run(int64_t key0, int64_t T, int64_t window, int64_t per, int slots, int y) {
+__device__ inline TileRun tile_run(int64_t key0, int64_t T, int64_t window, int keys, int64_t per, int slots,
+                                  int y) {
   int64_t tf, tl;
-  block_tiles(key0, T, window, &tf, &tl);
+  block_tiles(key0, T, window, keys, &tf, &tl);
   const int64_t c_lo = tf / per;
   const int64_t c = c_lo + ((int64_t)y - c_lo % slots + slots) % slots;
   const int64_t lo = tf > c * per ? tf : c * per;
@@ -146,30 +149,39 @@ __device__ __forceinline__ uint32_t row_slot(int r, int j) {
   return (uint32_t)(j ^ f);
 }
 
-// The key-block walk of the value gradient (DK = false) and of the key
-// gradient (DK = true):
-//   DK = false  dV̂ += Pᵀ dO
-//   DK = true   dP = dO V̂ᵀ, dS = P (dP - delta_row), dK̂_rot += dSᵀ Q_rot /
-//               sqrt(D), then the rotary's transpose at the key's position
+// The key-block walk of the value gradient (MODE kWalkV), of the key gradient
+// (kWalkK) and of both at once (kWalkKV):
+//   V   dV̂ += Pᵀ dO
+//   K   dP = dO V̂ᵀ, dS = P (dP - delta_row), dK̂_rot += dSᵀ Q_rot / sqrt(D),
+//       then the rotary's transpose at the key's position
+//   KV  both, from one S and one dP per step
 // (delta = rowsum(dO * O) from the query kernel).  For the key gradient the
 // wave's V̂ rows join its K̂ as B operands, the staged dO rows are the A
 // operand of dP, and Q_rotᵀ for the last product comes off the staged q
 // rows with the same transposing reads that give dOᵀ to the value gradient.
-template <bool DK>
+// Each wave owns KT 16-key tiles (a workgroup 64 KT keys): KT = 2 for one
+// gradient, KT = 1 for both, which keeps both sets of accumulators within
+// three waves per SIMD.
+enum WalkMode { kWalkV, kWalkK, kWalkKV };
+template <int MODE, int KT>
 __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
+  constexpr bool kV = MODE != kWalkK, DK = MODE != kWalkV;  // forms dV̂ / dK̂
+  constexpr int kKeys = 64 * KT;                           // keys per workgroup
+  constexpr int NA = (kV ? 1 : 0) + (DK ? 1 : 0);          // accumulator sets
+  constexpr int iV = 0, iK = kV ? 1 : 0;
   __shared__ __align__(1024) _Float16 q_lds[3][kBRows * kBD];
   __shared__ __align__(1024) _Float16 d_lds[3][kBRows * kBD];
   __shared__ __align__(16) float l_lds[2][kBRows];
   __shared__ __align__(16) float x_lds[DK ? 2 : 1][kBRows];  // delta (DK)
   // q rows: A operand of S (and, DK, transposed for dK); dO rows: transposed
-  // for dV (DK: A operand of dP)
-  constexpr Swz kQSwz = DK ? kSwzAT : kSwzA, kDSwz = DK ? kSwzA : kSwzT;
+  // for dV and (DK) the A operand of dP
+  constexpr Swz kQSwz = DK ? kSwzAT : kSwzA, kDSwz = DK ? (kV ? kSwzAT : kSwzA) : kSwzT;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the step tests below branch on it
   const int ln = lane & 15, lg = lane >> 4;
   const int NQ = a.nq;
-  const int64_t nkb = ceil_div(a.T, kBKeys);
+  const int64_t nkb = ceil_div(a.T, kKeys);
   // key blocks fastest: the blocks of one (batch row, kv head) share its q and
   // dO rows in one XCD's L2
   const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
@@ -177,8 +189,8 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
   const int64_t kb = bid % (uint32_t)nkb;
   const int64_t kvh = (bid / (uint32_t)nkb) % (uint32_t)a.KVH;
   const int64_t b = bid / ((uint32_t)nkb * (uint32_t)a.KVH);
-  const int64_t key0 = kb * kBKeys;
-  const int64_t kw0 = key0 + 32 * wave;  // this wave's first key
+  const int64_t key0 = kb * kKeys;
+  const int64_t kw0 = key0 + 16 * KT * wave;  // this wave's first key
   const int64_t p0 = a.start[b];
   const float scale2 = 1.4426950408889634f / sqrtf((float)kBD);
   const int64_t rope_last = a.rope_len - 1;
@@ -190,9 +202,9 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
   // ---- the wave's rotated keys as B operands: kop[kt][c] = dims
   // [32c + 8lg, +8) of key kw0 + 16kt + ln (chunks c and c+2 are rotary
   // partners); DK: its V̂ rows the same way (no rotary) ----
-  half8 kop[2][4], vop[2][4];
+  half8 kop[KT][4], vop[KT][4];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
+  for (int kt = 0; kt < KT; ++kt) {
     const int64_t key = kw0 + 16 * kt + ln;
     const bool ok = key < a.T;
     const _Float16* kp = a.k + b * a.ksb + kvh * a.ksh + (ok ? key : 0) * a.kst;
@@ -212,14 +224,16 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
       for (int c = 0; c < 4; ++c) vop[kt][c] = ok ? *(const half8*)(vp + 32 * c + 8 * lg) : zero8;
     }
   }
-  float4v acc[2][8];  // d[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
+  float4v acc[NA][KT][8];  // dV̂ (set iV) and dK̂ (set iK)[key kw0 + 16kt + 4lg + e][dim 16dt + ln]
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int i = 0; i < NA; ++i)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[i][kt][dt] = float4v{0.f, 0.f, 0.f, 0.f};
 
   // this workgroup's query tiles, top first (none: no slot to write)
-  const TileRun run = tile_run(key0, a.T, a.window, a.chunk_tiles, a.slots, chunk);
+  const TileRun run = tile_run(key0, a.T, a.window, kKeys, a.chunk_tiles, a.slots, chunk);
   if (run.n == 0) return;
   const int64_t t_top = run.top;
   const int32_t nsteps = (int32_t)run.n * NQ;
@@ -351,13 +365,13 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
     if (more) load_lse();
     if (more2) copy(buf2);
     // does any row of the step see any of this wave's keys?
-    const bool any = r0 + kBRows - 1 >= kw32 && r0 - (kw32 + 31) < win && kw32 < T32;
+    const bool any = r0 + kBRows - 1 >= kw32 && r0 - (kw32 + 16 * KT - 1) < win && kw32 < T32;
     if (any) {
       const char* ql = (const char*)q_lds[buf];
       const char* dl = (const char*)d_lds[buf];
-      // ---- S[row][key] (and DK: dP[row][key] = dO V̂ᵀ): 2 row tiles x 2
+      // ---- S[row][key] (and DK: dP[row][key] = dO V̂ᵀ): 2 row tiles x KT
       // key tiles; A = the staged rows (row 16rg + ln, chunk 4c + lg) ----
-      float4v sacc[2][2], dpacc[2][2];
+      float4v sacc[2][KT], dpacc[2][KT];
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg) {
         half8 qa[4];
@@ -365,7 +379,7 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
         for (int c = 0; c < 4; ++c)
           qa[c] = *(const half8*)(ql + (16 * rg + ln) * 256 + 16 * row_slot<kQSwz>(ln, 4 * c + lg));
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+        for (int kt = 0; kt < KT; ++kt) {
           sacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < 4; ++c)
@@ -380,7 +394,7 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
           for (int c = 0; c < 4; ++c)
             da[c] = *(const half8*)(dl + (16 * rg + ln) * 256 + 16 * row_slot<kDSwz>(ln, 4 * c + lg));
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
+          for (int kt = 0; kt < KT; ++kt) {
             dpacc[rg][kt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 4; ++c)
@@ -391,12 +405,13 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
       // ---- P, masked: element (rg, kt, e) is row r0 + 16rg + 4lg + e, key
       // kw0 + 16kt + ln; pa[kt] contraction slot 4rg + e (of lane group lg)
       // <-> row 16rg + 4lg + e ----
-      const bool full = r0 >= kw32 + 31 && r0 + kBRows - 1 - kw32 < win && r0 + kBRows <= T32;
+      const bool full = r0 >= kw32 + 16 * KT - 1 && r0 + kBRows - 1 - kw32 < win && r0 + kBRows <= T32;
       const int base = r0 - kw32 + 4 * lg - ln;  // row - key = base + 16rg + e - 16kt
       // (rows past T hold the step's first row and lse +inf, keys past T
       // zeros: their scores are finite and their weights 0, rows by the
       // lse and keys by the mask, since a visible key is at most the row)
-      half8 pa[2];
+      // P (for dV̂) and dS (for dK̂) in A order
+      half8 pa[KT], dsa[KT];
       auto make_p = [&](auto masked_tag) {
         constexpr bool masked = decltype(masked_tag)::value;
 #pragma unroll
@@ -412,7 +427,7 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
             x4[3] = d4.w;
           }
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               // hidden elements take exponent -inf (weight exactly 0); the
@@ -424,16 +439,17 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
                 const uint32_t diff = (uint32_t)(base + 16 * rg + e - 16 * kt);
                 x = diff < (uint32_t)win ? x : -__builtin_inff();
               }
-              float p = __builtin_amdgcn_exp2f(x);
-              // DK: dS = P (dP - delta_row) in place of P, rounded to fp32
-              // and then to fp16 in every element (the empty asm keeps the
-              // compiler from fusing the product into the conversion,
-              // v_fma_mixlo_f16, in some elements and not in others)
+              const float p = __builtin_amdgcn_exp2f(x);
+              if constexpr (kV) pa[kt][4 * rg + e] = (_Float16)p;
+              // DK: dS = P (dP - delta_row), rounded to fp32 and then to
+              // fp16 in every element (the empty asm keeps the compiler from
+              // fusing the product into the conversion, v_fma_mixlo_f16, in
+              // some elements and not in others)
               if constexpr (DK) {
-                p *= dpacc[rg][kt][e] - x4[e];
-                asm volatile("" : "+v"(p));
+                float ds = p * (dpacc[rg][kt][e] - x4[e]);
+                asm volatile("" : "+v"(ds));
+                dsa[kt][4 * rg + e] = (_Float16)ds;
               }
-              pa[kt][4 * rg + e] = (_Float16)p;
             }
         }
       };
@@ -444,19 +460,31 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
       } else {
         make_p(std::true_type{});
       }
-      // ---- d += Pᵀ dO (DK: dSᵀ Q_rot): B = the staged rows' dim 16dt + ln
-      // at slots {4lg..4lg+3} = rows 4lg..4lg+3 and {16+4lg..} = rows
-      // 16+4lg.., two transposing reads of dO (DK: q_rot) ----
-      const uint32_t tl = lds_addr(DK ? (const void*)ql : (const void*)dl) + tr_off;
+      // ---- dV̂ += Pᵀ dO and dK̂ += dSᵀ Q_rot: B = the staged rows' dim
+      // 16dt + ln at slots {4lg..4lg+3} = rows 4lg..4lg+3 and {16+4lg..} =
+      // rows 16+4lg.., two transposing reads of dO (for dV̂) or q_rot (dK̂) ----
+      const uint32_t tld = lds_addr(dl) + tr_off, tlq = lds_addr(ql) + tr_off;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint32_t at = tl + 16u * row_slot<DK ? kQSwz : kDSwz>(tr_row, 2 * dt + ((ln & 3) >> 1));
-        const half4 lo = lds_read_tr16(at);
-        const half4 hi = lds_read_tr16(at + 16u * 256u);
-        const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const int ch2 = 2 * dt + ((ln & 3) >> 1);
+        if constexpr (kV) {
+          const uint32_t at = tld + 16u * row_slot<kDSwz>(tr_row, ch2);
+          const half4 lo = lds_read_tr16(at);
+          const half4 hi = lds_read_tr16(at + 16u * 256u);
+          const half8 db = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-          acc[kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[kt][dt], 0, 0, 0);
+          for (int kt = 0; kt < KT; ++kt)
+            acc[iV][kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kt], db, acc[iV][kt][dt], 0, 0, 0);
+        }
+        if constexpr (DK) {
+          const uint32_t at = tlq + 16u * row_slot<kQSwz>(tr_row, ch2);
+          const half4 lo = lds_read_tr16(at);
+          const half4 hi = lds_read_tr16(at + 16u * 256u);
+          const half8 qb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt)
+            acc[iK][kt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dsa[kt], qb, acc[iK][kt][dt], 0, 0, 0);
+        }
       }
     }
     if (++ch == NQ) {
@@ -476,30 +504,34 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
     buf2 = buf2 == 2 ? 0 : buf2 + 1;
   }
 
-  // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt + 4lg + e ----
-  float* out = a.dv + (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
+  // ---- store the wave's keys: lane holds dims 16dt + ln of keys kw0 + 16kt
+  // + 4lg + e.  dV̂ goes to a.dv; dK̂ (1/sqrt(D), then the rotary's transpose
+  // at the key's position: dims f and f + 64, slices dt and dt + 4, are one
+  // rotation pair) to a.dv when it is the only gradient, else to a.dk ----
+  const int64_t orow = (int64_t)chunk * a.slot_stride + ((b * a.KVH + kvh) * a.T) * kBD;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t key = kw0 + 16 * kt + 4 * lg + e;
       if (key >= a.T) continue;
+      if constexpr (kV) {
+        float* out = a.dv + orow;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) out[key * kBD + 16 * dt + ln] = acc[iV][kt][dt][e];
+      }
       if constexpr (DK) {
-        // 1/sqrt(D), then the rotary's transpose at the key's position:
-        // dims f and f + 64 (slices dt and dt + 4) are one rotation pair
+        float* out = (kV ? a.dk : a.dv) + orow;
         const _Float16* tr = rope_row(p0 + key);
         const float inv = 1.0f / sqrtf((float)kBD);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           const int f = 16 * dt + ln;
           const float c = (float)tr[f], sn = (float)tr[64 + f];
-          const float lo = acc[kt][dt][e] * inv, hi = acc[kt][dt + 4][e] * inv;
+          const float lo = acc[iK][kt][dt][e] * inv, hi = acc[iK][kt][dt + 4][e] * inv;
           out[key * kBD + f] = lo * c + hi * sn;
           out[key * kBD + 64 + f] = hi * c - lo * sn;
         }
-      } else {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) out[key * kBD + 16 * dt + ln] = acc[kt][dt][e];
       }
     }
 }
@@ -507,11 +539,15 @@ __device__ __forceinline__ void kv_grad_walk(const ValueGradArgs& a) {
 // 168 registers: three workgroups per CU
 __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void prefill_value_grad_kernel(ValueGradArgs a) {
-  kv_grad_walk<false>(a);
+  kv_grad_walk<kWalkV, 2>(a);
 }
 __global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_key_grad_kernel(ValueGradArgs a) {
-  kv_grad_walk<true>(a);
+  kv_grad_walk<kWalkK, 2>(a);
+}
+__global__ __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void prefill_kv_grad_kernel(ValueGradArgs a) {
+  kv_grad_walk<kWalkKV, 1>(a);
 }
 
 // Query gradient of the same attention, and delta = rowsum(dO * O) that the
@@ -805,12 +841,12 @@ void prefill_q_grad_kernel(QGradArgs qa_) {
 __global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dv, int64_t n4,
                                                                 int64_t slot4, int slots, int64_t T,
-                                                                int64_t window, int64_t per) {
+                                                                int64_t window, int keys, int64_t per) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
   const int64_t key = (i / (kBD / 4)) % T;
   int64_t tf, tl;
-  block_tiles(key - key % kBKeys, T, window, &tf, &tl);
+  block_tiles(key - key % keys, T, window, keys, &tf, &tl);
   const int64_t c_lo = tf / per, c_hi = tl / per;
   float4 acc = ((const float4*)part)[i + (c_lo % slots) * slot4];
   for (int64_t c = c_lo + 1; c <= c_hi; ++c) {
@@ -823,23 +859,23 @@ __global__ __launch_bounds__(256) void value_grad_reduce_kernel(const float* __r
   ((float4*)dv)[i] = acc;
 }
 
-// Tiles per chunk and partial slots of the key-block kernels: chunks of 16
-// tiles, or of an eighth of the longest block's rows when that is more; the
-// slots are the most chunks one block meets.
-static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* slots);
+// Tiles per chunk and partial slots of the key-block kernels (blocks of
+// `keys` keys): chunks of 16 tiles, or of an eighth of the longest block's
+// rows when that is more; the slots are the most chunks one block meets.
+static void value_grad_chunks(int64_t T, int64_t window, int keys, int* chunk_tiles, int* slots);
 
 // bytes of the value gradient's workspace: the chunks' partial slots (when
 // there are several), then the rotated queries [B,QH,T,128] fp16 at a
 // 256-byte boundary
 static int64_t value_grad_workspace(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window) {
   int chunk_tiles, chunks;
-  value_grad_chunks(T, window, &chunk_tiles, &chunks);
+  value_grad_chunks(T, window, kBKeys, &chunk_tiles, &chunks);
   const int64_t slots = chunks > 1 ? (int64_t)chunks * B * KVH * T * kBD * (int64_t)sizeof(float) : 0;
   return ceil_div(slots, 256) * 256 + B * QH * T * kBD * 2;
 }
 
-static void value_grad_chunks(int64_t T, int64_t window, int* chunk_tiles, int* slots) {
-  int64_t rows = (int64_t)kBKeys - 1 + window;
+static void value_grad_chunks(int64_t T, int64_t window, int keys, int* chunk_tiles, int* slots) {
+  int64_t rows = (int64_t)keys - 1 + window;
   if (rows > T || rows < 0) rows = T;
   const int64_t span = ceil_div(rows, kBRows);  // tiles of the longest block (blocks start on a tile)
   int64_t per = 16;
@@ -863,13 +899,18 @@ int64_t jkv_prefill_value_grad_workspace_bytes(int64_t B, int64_t QH, int64_t KV
 
 namespace jkv {
 
-// shared by the value and key gradients: checks, the rotated queries (into
-// the workspace, unless `rotated` says an earlier leg left them there), the
-// row runs, the launch and the reduction of the runs' partial slots
-template <bool DK>
+// shared by the value and key gradients and the walk that forms both:
+// checks, the rotated queries (into the workspace, unless the caller hands
+// them in), the row runs, the launch and the reduction of the runs' partial
+// slots.  d_out_buf is dV̂ (kWalkV, kWalkKV) or dK̂ (kWalkK); d_key_buf dK̂
+// for kWalkKV.
+template <int MODE>
 static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[12], int nstrides,
                           const void* rope_table, float* d_out_buf, void* workspace, int64_t workspace_bytes,
-                          hipStream_t stream, const _Float16* q_rot_given = nullptr) {
+                          hipStream_t stream, const _Float16* q_rot_given = nullptr, float* d_key_buf = nullptr) {
+  constexpr bool DK = MODE != kWalkV;
+  constexpr int keys = MODE == kWalkKV ? 64 : kBKeys;
+  constexpr int nout = MODE == kWalkKV ? 2 : 1;
   const int64_t B = a.B, QH = a.QH, KVH = a.KVH, T = a.T;
   JKV_CHECK_ARG(D == kBD, "prefill gradients support head_dim 128, got %lld", (long long)D);
   JKV_CHECK_ARG(B >= 0 && QH > 0 && KVH > 0 && T >= 0 && QH % KVH == 0, "invalid prefill geometry");
@@ -879,6 +920,8 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   if (B == 0 || T == 0) return JKV_OK;
   JKV_CHECK_ARG(a.q && a.k && a.dout && a.lse && d_out_buf && a.start && rope_table, "null buffer");
   JKV_CHECK_ARG(!DK || (a.v && a.delta), "null buffer");
+  JKV_CHECK_ARG(MODE != kWalkKV || (d_key_buf && q_rot_given && (uintptr_t)d_key_buf % 16 == 0),
+                "null or misaligned buffer");
   JKV_CHECK_ARG(a.rope_len >= 1, "rotary table is empty");
   JKV_CHECK_ARG(B < 65536 && QH < 65536, "prefill gradients: batch and query heads must be below 65536");
   {
@@ -900,14 +943,15 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   a.rope = (const _Float16*)rope_table;
   a.nq = (int32_t)NQ;
   int chunk_tiles, chunks;
-  value_grad_chunks(T, a.window, &chunk_tiles, &chunks);
+  value_grad_chunks(T, a.window, keys, &chunk_tiles, &chunks);
   a.chunk_tiles = chunk_tiles;
   a.slots = chunks;
   const int64_t n = B * KVH * T * kBD;
-  // workspace: the chunks' partial slots, then the rotated queries (unless
-  // the caller hands them in)
+  // workspace: the chunks' partial slots (of each output), then the rotated
+  // queries (unless the caller hands them in)
   const int64_t slot_bytes = chunks > 1 ? (int64_t)chunks * n * (int64_t)sizeof(float) : 0;
-  const int64_t need = q_rot_given != nullptr ? slot_bytes : value_grad_workspace(B, QH, KVH, T, a.window);
+  const int64_t need =
+      q_rot_given != nullptr ? nout * slot_bytes : value_grad_workspace(B, QH, KVH, T, a.window);
   if (need > 0) {
     JKV_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                   "prefill gradient workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
@@ -916,12 +960,14 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   }
   if (chunks > 1) {
     a.dv = (float*)workspace;
+    a.dk = (float*)((unsigned char*)workspace + slot_bytes);
     a.slot_stride = n;
   } else {
     a.dv = d_out_buf;
+    a.dk = d_key_buf;
     a.slot_stride = 0;
   }
-  const int64_t blocks = ceil_div(T, kBKeys) * KVH * B;
+  const int64_t blocks = ceil_div(T, keys) * KVH * B;
   JKV_CHECK_ARG(blocks < ((int64_t)1 << 31), "prefill grid too large");
   const _Float16* q_rot = q_rot_given;
   if (q_rot == nullptr) {
@@ -932,8 +978,11 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
     q_rot = qr;
   }
   a.q = q_rot;  // contiguous [B,QH,T,128]
-  if constexpr (DK) {
+  if constexpr (MODE == kWalkK) {
     hipLaunchKernelGGL(prefill_key_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
+                       stream, a);
+  } else if constexpr (MODE == kWalkKV) {
+    hipLaunchKernelGGL(prefill_kv_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
                        stream, a);
   } else {
     hipLaunchKernelGGL(prefill_value_grad_kernel, dim3((uint32_t)blocks, (uint32_t)chunks), dim3(kBThreads), 0,
@@ -942,9 +991,12 @@ static int launch_kv_grad(ValueGradArgs a, int64_t D, const int64_t (&strides)[1
   JKV_CHECK_LAUNCH();
   if (chunks > 1) {
     const int64_t n4 = n / 4;
-    hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
-                       (const float*)workspace, d_out_buf, n4, n4, chunks, T, a.window, (int64_t)chunk_tiles);
-    JKV_CHECK_LAUNCH();
+    for (int o = 0; o < nout; ++o) {
+      hipLaunchKernelGGL(value_grad_reduce_kernel, dim3((uint32_t)ceil_div(n4, 256)), dim3(256), 0, stream,
+                         (const float*)((unsigned char*)workspace + o * slot_bytes), o == 0 ? d_out_buf : d_key_buf,
+                         n4, n4, chunks, T, a.window, keys, (int64_t)chunk_tiles);
+      JKV_CHECK_LAUNCH();
+    }
   }
   return JKV_OK;
 }
@@ -973,8 +1025,8 @@ int jkv_prefill_attention_value_grad(const void* q, int64_t q_stride_b, int64_t 
   a.rope_len = rope_len;
   const int64_t strides[12] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h, k_stride_t,
                                d_stride_b, d_stride_h, d_stride_t, 0, 0, 0};
-  return launch_kv_grad<false>(a, D, strides, 9, rope_table, d_value, workspace, workspace_bytes,
-                               (hipStream_t)stream_);
+  return launch_kv_grad<kWalkV>(a, D, strides, 9, rope_table, d_value, workspace, workspace_bytes,
+                                (hipStream_t)stream_);
 }
 
 int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
@@ -1000,23 +1052,27 @@ int jkv_prefill_attention_key_grad(const void* q, int64_t q_stride_b, int64_t q_
   a.rope_len = rope_len;
   const int64_t strides[12] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h, k_stride_t,
                                v_stride_b, v_stride_h, v_stride_t, d_stride_b, d_stride_h, d_stride_t};
-  return launch_kv_grad<true>(a, D, strides, 12, rope_table, d_key, workspace, workspace_bytes,
-                              (hipStream_t)stream_);
+  return launch_kv_grad<kWalkK>(a, D, strides, 12, rope_table, d_key, workspace, workspace_bytes,
+                                (hipStream_t)stream_);
 }
 
 int64_t jkv_prefill_backward_workspace_bytes(int64_t B, int64_t QH, int64_t KVH, int64_t T, int64_t window) {
   using namespace jkv;
   if (B <= 0 || QH <= 0 || KVH <= 0 || T <= 0 || window < 1) return 0;
-  int chunk_tiles, chunks;
-  value_grad_chunks(T, window, &chunk_tiles, &chunks);
+  int chunk_tiles, chunks, chunks64;
+  value_grad_chunks(T, window, kBKeys, &chunk_tiles, &chunks);
+  value_grad_chunks(T, window, 64, &chunk_tiles, &chunks64);
   const int64_t delta = ceil_div(B * QH * T * (int64_t)sizeof(float), 256) * 256;
   const int64_t k_rot = ceil_div(B * KVH * T * kBD * 2, 256) * 256;
   const int64_t q_rot = ceil_div(B * QH * T * kBD * 2, 256) * 256;
-  // the slot area serves the query leg (delta only), the key leg's slots and
-  // the value leg's slots (and rotated queries, when it runs alone) in turn
+  // the slot area serves the query leg (delta only), then the key leg's
+  // slots, the value leg's slots (and rotated queries, when it runs alone) or
+  // the slots of both from the walk that forms both
   const int64_t qk = (int64_t)chunks * B * QH * T * kBD * (int64_t)sizeof(float);
   const int64_t v = value_grad_workspace(B, QH, KVH, T, window);
-  return delta + k_rot + q_rot + (qk > v ? qk : v);
+  const int64_t kv = chunks64 > 1 ? 2 * (int64_t)chunks64 * B * KVH * T * kBD * (int64_t)sizeof(float) : 0;
+  const int64_t area = qk > v ? (qk > kv ? qk : kv) : (v > kv ? v : kv);
+  return delta + k_rot + q_rot + area;
 }
 
 int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
@@ -1108,15 +1164,19 @@ int jkv_prefill_attention_backward(const void* q, int64_t q_stride_b, int64_t q_
     JKV_CHECK_LAUNCH();
   }
   // the key and value legs read the rotated queries the query leg wrote;
-  // without it (d_value alone) the value leg rotates them itself
+  // without it (d_value alone) the value leg rotates them itself.  Both
+  // gradients come from one walk (one S and one dP per step)
   const bool q_leg = d_query || d_key;
-  if (d_key) {
-    const int rc = launch_kv_grad<true>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream, q_rot);
+  if (d_key && d_value) {
+    const int rc = launch_kv_grad<kWalkKV>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream,
+                                           q_rot, d_key);
     if (rc != JKV_OK) return rc;
-  }
-  if (d_value) {
-    const int rc = launch_kv_grad<false>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream,
-                                         q_leg ? q_rot : nullptr);
+  } else if (d_key) {
+    const int rc = launch_kv_grad<kWalkK>(g, D, strides, 12, rope_table, d_key, slots, slot_bytes, stream, q_rot);
+    if (rc != JKV_OK) return rc;
+  } else if (d_value) {
+    const int rc = launch_kv_grad<kWalkV>(g, D, strides, 12, rope_table, d_value, slots, slot_bytes, stream,
+                                          q_leg ? q_rot : nullptr);
     if (rc != JKV_OK) return rc;
   }
   return JKV_OK;

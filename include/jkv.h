@@ -100,6 +100,29 @@ int jkv_rvq_encode_kv(const void* key_states, const void* value_states, int32_t 
                       int64_t workspace_bytes, jkv_stream_t stream);
 
 /*
+ * n_jobs encodes of one geometry in one call: a whole cache's layers and
+ * their K and V, as the codec forward encodes them one layer at a time
+ * (src/jointkv/uniform_depth_tac.py:69-101 called per layer).  Job j is
+ * jkv_rvq_encode(states[j], ..., tables[j], ..., codes[j], ...,
+ * recon + j * n_exits, ...) without a whitener; all jobs share B/H/T/G/d/S/K,
+ * the state strides, the code strides and the exit depths, and each output
+ * is what that call writes, bit for bit.  With fp16 states, d in {4, 8},
+ * K = 256 and S <= 2, up to 64 jobs run in one launch (the first workgroups
+ * of one job overlap the last of the one before, and each workgroup
+ * encodes a longer row range); other geometries run the jobs in turn,
+ * sharing `workspace`.  recon is [n_jobs][n_exits] (NULL: no
+ * reconstructions).
+ */
+int jkv_rvq_encode_many(int32_t n_jobs, const void* const* states, int32_t states_dtype,
+                        int64_t B, int64_t H, int64_t T, int64_t G, int64_t d,
+                        int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                        const float* const* tables, int64_t S, int64_t K,
+                        uint8_t* const* codes, int64_t code_stride_b,
+                        int64_t code_stride_h, int64_t code_stride_t, int32_t n_exits,
+                        const int32_t* exit_depths, void* const* recon, void* workspace,
+                        int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
  * Codes-to-vector reconstruction with given (frozen) codes:
  * out = dtype( sum_{s<depth} fp32(fp16(tables[h*G+g, s, code])) ).
  * Replaces frozen_assignment_u16_reconstruction

@@ -968,4 +968,61 @@ int jkv_rvq_encode_kv(const void* key_states, const void* value_states, int32_t 
                         n_exits, exit_depths, value_recon, workspace, workspace_bytes, stream_);
 }
 
+int jkv_rvq_encode_many(int32_t n_jobs, const void* const* states, int32_t states_dtype, int64_t B,
+                        int64_t H, int64_t T, int64_t G, int64_t d, int64_t stride_b, int64_t stride_h,
+                        int64_t stride_t, const float* const* tables, int64_t S, int64_t K,
+                        uint8_t* const* codes, int64_t code_stride_b, int64_t code_stride_h,
+                        int64_t code_stride_t, int32_t n_exits, const int32_t* exit_depths,
+                        void* const* recon, void* workspace, int64_t workspace_bytes,
+                        jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(n_jobs >= 0, "negative job count");
+  JKV_CHECK_ARG(B >= 0 && H > 0 && T >= 0 && G > 0 && d > 0 && S > 0 && K > 0, "invalid geometry");
+  JKV_CHECK_ARG(n_exits >= 0 && n_exits <= JKV_MAX_EXITS, "at most %d exits", JKV_MAX_EXITS);
+  if (n_jobs == 0 || B * T == 0) return JKV_OK;
+  JKV_CHECK_ARG(states && tables && codes, "null job array");
+  EncodeArgs batch[kMaxManyJobs];
+  for (int32_t j0 = 0; j0 < n_jobs; j0 += kMaxManyJobs) {
+    const int n = (int)std::min<int64_t>(kMaxManyJobs, n_jobs - j0);
+    bool grouped = true;
+    for (int i = 0; i < n; ++i) {
+      const int32_t j = j0 + i;
+      JKV_CHECK_ARG(states[j] && tables[j] && codes[j], "null buffer in job %d", j);
+      EncodeArgs& a = batch[i];
+      a = EncodeArgs{};
+      a.states = states[j];
+      a.sb = stride_b; a.sh = stride_h; a.st = stride_t;
+      a.B = B; a.H = H; a.T = T; a.G = G; a.d = d; a.S = S; a.K = K;
+      a.tables = tables[j];
+      a.codes = codes[j];
+      a.cb = code_stride_b; a.ch = code_stride_h; a.ct = code_stride_t;
+      a.n_exits = n_exits;
+      for (int e = 0; e < n_exits; ++e) {
+        JKV_CHECK_ARG(exit_depths[e] >= 1 && exit_depths[e] <= S, "exit depth outside the ladder");
+        a.exit_depth[e] = exit_depths[e];
+        a.recon[e] = recon ? recon[(int64_t)j * n_exits + e] : nullptr;
+      }
+      if (!mfma_eligible(a, states_dtype)) grouped = false;
+    }
+    if (grouped) {
+      const int rc = launch_grouped_many(batch, n, stream);
+      if (rc != JKV_OK) return rc;
+      continue;
+    }
+    // other geometries: the encodes one after the other on the stream
+    // (they may share the workspace: each starts after the one before)
+    for (int i = 0; i < n; ++i) {
+      const int32_t j = j0 + i;
+      const int rc = jkv_rvq_encode(states[j], states_dtype, B, H, T, G, d, stride_b, stride_h, stride_t,
+                                    tables[j], S, K, nullptr, codes[j], code_stride_b, code_stride_h,
+                                    code_stride_t, n_exits, exit_depths,
+                                    recon ? recon + (int64_t)j * n_exits : nullptr, workspace,
+                                    workspace_bytes, stream_);
+      if (rc != JKV_OK) return rc;
+    }
+  }
+  return JKV_OK;
+}
+
 }  // extern "C"

@@ -40,10 +40,30 @@ struct MfmaArgs {
   int64_t split;
 };
 
+// Many jobs of one geometry in one launch (every layer's K and V of a
+// cache): the geometry once, then each job's buffers.  Job j takes logical
+// workgroups [j * per_job, (j + 1) * per_job).
+static const int kMaxManyJobs = 64;
+struct MfmaJobBuffers {
+  const void* states;
+  const float* tables;
+  uint8_t* codes;
+  void* recon_depth[2];
+};
+struct MfmaManyArgs {
+  MfmaJob shape;  // geometry, strides and row chunks (its buffers unused)
+  int64_t per_job;
+  int32_t n_jobs;
+  MfmaJobBuffers buf[kMaxManyJobs];
+};
+
 // Rows a workgroup encodes per iteration (4 waves x 64 rows).
 static const int kGroupedRowsPerIter = 256;
 
 // Unwhitened grouped encode (encode_grouped.hip); e2 = second job or null.
 int launch_grouped(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t stream);
+// The same for n <= kMaxManyJobs jobs that share everything but their
+// buffers (states, tables, codes, reconstructions).
+int launch_grouped_many(const EncodeArgs* jobs, int n, hipStream_t stream);
 
 }  // namespace jkv

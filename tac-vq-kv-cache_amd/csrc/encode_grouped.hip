@@ -99,17 +99,58 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
 }
 
 static const int kRowsPerWave = 64;
+// largest row range per workgroup
+static const int64_t kMaxRowsPerWg = 4096;
 
 }  // namespace
 
-template <int D, int S, bool PAIR>
+// launch forms: one job, a pair of jobs (a token's K and V), or many jobs of
+// one geometry (the layers of a cache)
+enum GroupedMode { kOneJob = 0, kPairJobs = 1, kManyJobs = 2 };
+template <int MODE> struct GroupedArgsOf { using type = MfmaArgs; };
+template <> struct GroupedArgsOf<kManyJobs> { using type = MfmaManyArgs; };
+
+template <int D, int S, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
-void rvq_encode_grouped(MfmaArgs m) {
+void rvq_encode_grouped(typename GroupedArgsOf<MODE>::type m) {
   static_assert(D == 4 || D == 8, "group dimension 4 or 8");
   static_assert(S == 1 || S == 2, "one or two stages");
   const uint32_t L0 = xcd_remap(blockIdx.x, gridDim.x);
-  const int jb = PAIR && (int64_t)L0 >= m.split ? 1 : 0;
-  const MfmaJob& mj = m.job[jb];
+  // this block's job: its geometry, its logical block L within the job and
+  // its buffers (all wave-uniform)
+  uint32_t L;
+  const MfmaJob* mjp;
+  const void* states_v;
+  const float* tables;
+  uint8_t* codes_out;
+  void* recon1;
+  void* recon2;
+  if constexpr (MODE == kManyJobs) {
+    const uint32_t per = (uint32_t)m.per_job;
+    uint32_t jb = L0 / per;
+    L = L0 - jb * per;
+    if (jb >= (uint32_t)m.n_jobs) {  // grid padding: stages the last job's tables, then leaves
+      jb = (uint32_t)m.n_jobs - 1u;
+      L = 0xFFFFFFFFu;
+    }
+    mjp = &m.shape;
+    const MfmaJobBuffers& bf = m.buf[jb];
+    states_v = bf.states;
+    tables = bf.tables;
+    codes_out = bf.codes;
+    recon1 = bf.recon_depth[0];
+    recon2 = bf.recon_depth[1];
+  } else {
+    const int jb = MODE == kPairJobs && (int64_t)L0 >= m.split ? 1 : 0;
+    L = jb ? L0 - (uint32_t)m.split : L0;
+    mjp = &m.job[jb];
+    states_v = mjp->e.states;
+    tables = mjp->e.tables;
+    codes_out = mjp->e.codes;
+    recon1 = mjp->recon_depth[0];
+    recon2 = mjp->recon_depth[1];
+  }
+  const MfmaJob& mj = *mjp;
   const EncodeArgs& a = mj.e;
 
   __shared__ half8 tab_lo[S][256];  // codeword planes, MFMA order (d=4: [c, c])
@@ -126,7 +167,6 @@ void rvq_encode_grouped(MfmaArgs m) {
   // groups of one row range share its 256-byte rows and the blocks of one
   // head (its tables and rows) sit on one XCD
   // (block counts, problems and chunks fit 32 bits: host-checked)
-  const uint32_t L = jb ? L0 - (uint32_t)m.split : L0;
   const uint32_t G32 = (uint32_t)a.G, nch = (uint32_t)mj.n_chunks;
   const bool active = L < (uint32_t)(a.H * a.G) * nch;
   const uint32_t Lg = active ? L / G32 : 0u;
@@ -140,7 +180,7 @@ void rvq_encode_grouped(MfmaArgs m) {
   const uint32_t rows = (uint32_t)(a.B * a.T);
   const uint32_t r_begin = chunk * (uint32_t)mj.rows_per_wg;
   const uint32_t r_end = min(r_begin + (uint32_t)mj.rows_per_wg, rows);
-  const _Float16* states = (const _Float16*)a.states;
+  const _Float16* states = (const _Float16*)states_v;
   const uint32_t Dfull = G32 * D;
   const uint32_t T32 = (uint32_t)a.T;
   const uint32_t head_x = h * (uint32_t)a.sh + g * D;
@@ -336,7 +376,7 @@ void rvq_encode_grouped(MfmaArgs m) {
     const int slot = mfma_slot(tid);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const float* src = a.tables + ((p * S + s) * 256 + tid) * D;
+      const float* src = tables + ((p * S + s) * 256 + tid) * D;
       half_t cw[D];
       const float4 v0 = ((const float4*)src)[0];
       cw[0] = (half_t)v0.x; cw[1] = (half_t)v0.y; cw[2] = (half_t)v0.z; cw[3] = (half_t)v0.w;
@@ -404,8 +444,8 @@ void rvq_encode_grouped(MfmaArgs m) {
     half8 c1;
     const uint32_t win1 = rescore(0, key1, xs, half8{}, false, beta1, &code1, &c1);
     uint32_t code = (uint32_t)code1;
-    if (mj.recon_depth[0] != nullptr && valid) {
-      _Float16* op = (_Float16*)mj.recon_depth[0] + oo;
+    if (recon1 != nullptr && valid) {
+      _Float16* op = (_Float16*)recon1 + oo;
       if constexpr (D == 8) {
         *(half8*)op = c1;
       } else {
@@ -448,9 +488,9 @@ void rvq_encode_grouped(MfmaArgs m) {
       // depth-2 reconstruction fp16(fp32(c1) + fp32(c2)): the sum of two fp16
       // words is exact in fp32 or, when it is not, too small to move the fp16
       // rounding, so one fp16 add gives the same bits
-      if (mj.recon_depth[1] != nullptr && valid) {
+      if (recon2 != nullptr && valid) {
         const half8 dec = c1 + c2;
-        _Float16* op = (_Float16*)mj.recon_depth[1] + oo;
+        _Float16* op = (_Float16*)recon2 + oo;
         if constexpr (D == 8) {
           *(half8*)op = dec;
         } else {
@@ -459,7 +499,7 @@ void rvq_encode_grouped(MfmaArgs m) {
       }
     }
     if (valid) {
-      uint8_t* cp = a.codes + co;
+      uint8_t* cp = codes_out + co;
       if constexpr (S == 1) {
         cp[0] = (uint8_t)code;
       } else {
@@ -471,15 +511,16 @@ void rvq_encode_grouped(MfmaArgs m) {
 }
 
 // ---------------------------------------------------------------------------
-static MfmaJob grouped_job(const EncodeArgs& e) {
+// rows per workgroup: amortise the codebook staging while the launch still
+// has `min_blocks` workgroups
+static MfmaJob grouped_job(const EncodeArgs& e, int64_t min_blocks) {
   MfmaJob j = {};
   j.e = e;
   for (int i = 0; i < e.n_exits; ++i) j.recon_depth[e.exit_depth[i] - 1] = e.recon[i];
   const int64_t rows = e.B * e.T;
   const int64_t P = e.H * e.G;
-  // rows per workgroup: amortise the codebook staging, fill 256 CUs x 4 WGs
-  int64_t rpw = 4096;
-  while (rpw > kGroupedRowsPerIter && P * ceil_div(rows, rpw) < 256 * 4) rpw >>= 1;
+  int64_t rpw = kMaxRowsPerWg;
+  while (rpw > kGroupedRowsPerIter && P * ceil_div(rows, rpw) < min_blocks) rpw >>= 1;
   j.rows_per_wg = rpw;
   j.n_chunks = ceil_div(rows, rpw);
   return j;
@@ -488,12 +529,13 @@ static MfmaJob grouped_job(const EncodeArgs& e) {
 template <int D, int S>
 static int launch_grouped_t(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t stream) {
   MfmaArgs m = {};
-  m.job[0] = grouped_job(e);
+  // one job fills 256 CUs x 4 workgroups by itself
+  m.job[0] = grouped_job(e, 256 * 4);
   const int64_t per_job = e.H * e.G * m.job[0].n_chunks;
   int64_t nblocks = per_job;
   m.split = per_job;
   if (e2 != nullptr) {
-    m.job[1] = grouped_job(*e2);
+    m.job[1] = grouped_job(*e2, 256 * 4);
     nblocks += per_job;
   } else {
     m.job[1] = m.job[0];
@@ -502,10 +544,34 @@ static int launch_grouped_t(const EncodeArgs& e, const EncodeArgs* e2, hipStream
   JKV_CHECK_ARG(nblocks < (int64_t)1 << 31, "grid too large");
   if (e2 == nullptr) {
     m.split = nblocks;
-    hipLaunchKernelGGL((rvq_encode_grouped<D, S, false>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+    hipLaunchKernelGGL((rvq_encode_grouped<D, S, kOneJob>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
   } else {
-    hipLaunchKernelGGL((rvq_encode_grouped<D, S, true>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
+    hipLaunchKernelGGL((rvq_encode_grouped<D, S, kPairJobs>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
   }
+  JKV_CHECK_LAUNCH();
+  return JKV_OK;
+}
+
+template <int D, int S>
+static int launch_grouped_many_t(const EncodeArgs* jobs, int n, hipStream_t stream) {
+  MfmaManyArgs m = {};
+  // the jobs together fill the chip: rows per workgroup only need to leave
+  // every CU several workgroups' worth
+  m.shape = grouped_job(jobs[0], (256 * 4 * 4 + n - 1) / n);
+  m.n_jobs = n;
+  m.per_job = jobs[0].H * jobs[0].G * m.shape.n_chunks;
+  for (int j = 0; j < n; ++j) {
+    const MfmaJob one = grouped_job(jobs[j], (256 * 4 * 4 + n - 1) / n);
+    m.buf[j].states = jobs[j].states;
+    m.buf[j].tables = jobs[j].tables;
+    m.buf[j].codes = jobs[j].codes;
+    m.buf[j].recon_depth[0] = one.recon_depth[0];
+    m.buf[j].recon_depth[1] = one.recon_depth[1];
+  }
+  int64_t nblocks = m.per_job * n;
+  if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
+  JKV_CHECK_ARG(nblocks < (int64_t)1 << 31, "grid too large");
+  hipLaunchKernelGGL((rvq_encode_grouped<D, S, kManyJobs>), dim3((uint32_t)nblocks), dim3(256), 0, stream, m);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }
@@ -513,6 +579,13 @@ static int launch_grouped_t(const EncodeArgs& e, const EncodeArgs* e2, hipStream
 int launch_grouped(const EncodeArgs& e, const EncodeArgs* e2, hipStream_t stream) {
   if (e.d == 8) return e.S == 1 ? launch_grouped_t<8, 1>(e, e2, stream) : launch_grouped_t<8, 2>(e, e2, stream);
   return e.S == 1 ? launch_grouped_t<4, 1>(e, e2, stream) : launch_grouped_t<4, 2>(e, e2, stream);
+}
+
+int launch_grouped_many(const EncodeArgs* jobs, int n, hipStream_t stream) {
+  JKV_CHECK_ARG(n >= 1 && n <= kMaxManyJobs, "1 to %d jobs per launch", kMaxManyJobs);
+  const EncodeArgs& e = jobs[0];
+  if (e.d == 8) return e.S == 1 ? launch_grouped_many_t<8, 1>(jobs, n, stream) : launch_grouped_many_t<8, 2>(jobs, n, stream);
+  return e.S == 1 ? launch_grouped_many_t<4, 1>(jobs, n, stream) : launch_grouped_many_t<4, 2>(jobs, n, stream);
 }
 
 }  // namespace jkv

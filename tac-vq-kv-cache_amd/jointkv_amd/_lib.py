@@ -43,6 +43,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp,
          _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _vp],
     ),
+    "jkv_rvq_encode_many": (
+        ctypes.c_int,
+        [_i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp,
+         _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i64, _vp],
+    ),
     "jkv_nearest_f32": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "jkv_nearest_topk_f32": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
     "jkv_gain_shape_sums": (

@@ -139,6 +139,62 @@ def rvq_encode_kv(
     return recon_k, codes[0], recon_v, codes[1]
 
 
+def rvq_encode_many(
+    states: Sequence[torch.Tensor],
+    tables: Sequence[torch.Tensor],
+    *,
+    groups: int,
+    group_dim: int,
+    exits: Sequence[int],
+) -> list[tuple[list[torch.Tensor], torch.Tensor]]:
+    """:func:`rvq_encode` of every ``states[j]`` with ``tables[j]`` (one
+    geometry, no whitener) in one call: the layers of a cache and their K and
+    V.  On the grouped MFMA path up to 64 encodes share one launch.  Returns
+    ``[(reconstructions in exits order, codes), ...]`` in job order, each
+    what :func:`rvq_encode` returns for that job."""
+
+    if len(states) != len(tables):
+        raise ValueError("one table set per states tensor")
+    if not states:
+        return []
+    device = _lib.require_device(*states, *tables)
+    first = states[0]
+    batch, heads, tokens, dim = map(int, first.shape)
+    problems, stages, clusters, d = map(int, tables[0].shape)
+    if dim != groups * group_dim or d != group_dim or problems != heads * groups:
+        raise ValueError("state and table geometry differs")
+    for x, t in zip(states, tables):
+        if x.shape != first.shape or x.dtype != first.dtype or t.shape != tables[0].shape:
+            raise ValueError("every job must share the first job's geometry")
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("encode tables must be contiguous fp32 masters")
+    if len(exits) > _lib.MAX_EXITS:
+        raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
+    prepared = [_encode_states_strides(x) for x in states]
+    strides = prepared[0][1]
+    if any(st != strides for _, st in prepared):
+        prepared = [_encode_states_strides(x.contiguous()) for x in states]
+        strides = prepared[0][1]
+    xs = [x for x, _ in prepared]
+    codes = [torch.empty((batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device) for _ in xs]
+    recon = [[torch.empty((batch, heads, tokens, dim), dtype=first.dtype, device=device) for _ in exits]
+             for _ in xs]
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_rvq_encode_workspace_bytes(heads, groups, stages, clusters, d, 0))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
+    code = lib.jkv_rvq_encode_many(
+        len(xs), _lib.ptr_array(ctypes.c_void_p, [x.data_ptr() for x in xs]), _lib.dtype_code(first.dtype),
+        batch, heads, tokens, groups, d, *strides,
+        _lib.ptr_array(ctypes.c_void_p, [t.data_ptr() for t in tables]), stages, clusters,
+        _lib.ptr_array(ctypes.c_void_p, [c.data_ptr() for c in codes]), *codes[0].stride()[:3],
+        len(exits), _lib.ptr_array(ctypes.c_int32, [int(e) for e in exits]),
+        _lib.ptr_array(ctypes.c_void_p, [r.data_ptr() for rs in recon for r in rs]),
+        _lib.ptr(workspace), ws_bytes, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return [(rs, c) for rs, c in zip(recon, codes)]
+
+
 def nearest_f32(states: torch.Tensor, tables: torch.Tensor) -> torch.Tensor:
     """Nearest fp32 codeword per row: ``states[H,N,D]``, ``tables[H,K,D]``
     (fp32, D <= 128) -> int64 ``[H,N]`` (nested_vq.py:178-215 without

@@ -283,6 +283,44 @@ def test_encode_kv_equals_two_encodes(device, batch, tokens, groups, dim, stages
         assert torch.equal(a, b)
 
 
+# (heads, batch, tokens, groups, dim, stages, dtype, exits, jobs)
+@pytest.mark.parametrize("heads,batch,tokens,groups,dim,stages,dtype,exits,jobs", [
+    (8, 2, 300, 16, 8, 2, torch.float16, (1, 2), 5),    # G2, one launch, ragged rows
+    # 70 jobs: a 64-job launch whose workgroups take 4,096-row ranges (16
+    # iterations per wave, a ragged second chunk), then a 6-job launch
+    (2, 1, 4500, 16, 8, 2, torch.float16, (2,), 70),
+    (8, 16, 1, 32, 4, 1, torch.float16, (1,), 4),       # cq2, one token per sequence
+    (8, 1, 70, 16, 8, 2, torch.float32, (2,), 3),       # fp32 states: the encodes in turn
+    (8, 1, 40, 1, 128, 4, torch.float16, (2, 4), 2),    # full-vector tables: in turn, shared workspace
+])
+def test_encode_many_equals_per_job_encodes(device, heads, batch, tokens, groups, dim, stages, dtype, exits, jobs):
+    from jointkv_amd import _ops
+
+    print(f"encode_many jobs={jobs} H={heads} B={batch} T={tokens} G={groups} d={dim} S={stages} {dtype}",
+          flush=True)
+    gen = _gen(5150 + tokens + jobs)
+    sig = tuple(0.5 ** s for s in range(stages))
+    states_cpu = [ref.synthetic_states(gen, batch, heads, tokens, groups * dim) for _ in range(jobs)]
+    tables_cpu = [ref.synthetic_tables(gen, (heads * groups, stages, 256, dim), sig, stage_axis=1)
+                  for _ in range(jobs)]
+    states = [x.to(dtype).to(device) for x in states_cpu]
+    tables = [t.to(device) for t in tables_cpu]
+    out = _ops.rvq_encode_many(states, tables, groups=groups, group_dim=dim, exits=exits)
+    assert len(out) == jobs
+    for j, (recon, codes) in enumerate(out):
+        e_recon, e_codes = _ops.rvq_encode(states[j], tables[j], groups=groups, group_dim=dim, exits=exits)
+        assert torch.equal(codes, e_codes), f"job {j}: codes differ from its own encode"
+        for a, b in zip(recon, e_recon):
+            assert torch.equal(a, b), f"job {j}: reconstructions differ from its own encode"
+    if dtype == torch.float16 and dim == 8 and stages == 2 and batch * tokens <= 600:
+        # the last job against the oracle as well
+        st = states_cpu[-1].half()
+        r_exits, r_codes, d1, d2 = ref.grouped_residual_vq(
+            st, tables_cpu[-1].reshape(heads, groups, stages, 256, dim), prefixes=(1, 2), return_margins=True)
+        assert_codes(out[-1][1], r_codes, d1, d2)
+    assert _ops.rvq_encode_many([], [], groups=groups, group_dim=dim, exits=exits) == []
+
+
 @pytest.mark.parametrize("dim,batch,tokens,seed", [(4, 2, 300, 51), (4, 4, 2048, 52), (4, 16, 1, 53),
                                                     (8, 2, 300, 54), (8, 1, 2048, 55), (8, 16, 1, 56)])
 def test_whitened_grouped_cq_on_mfma(device, dim, batch, tokens, seed):

@@ -416,9 +416,11 @@ def vstep_workload(args, device):
         # the 32 layers' V states are given, so their encodes share one launch
         encoded = _ops.rvq_encode_many(values, [p.detach() for p in masters], groups=GROUPS,
                                        group_dim=GROUP_DIM, exits=(STAGES,))
-        for (_recon, codes), p, g in zip(encoded, masters, upstream):
-            grad = torch.zeros_like(p)
-            _ops.rvq_scatter_grad([g], [STAGES], codes, grad, group_dim=GROUP_DIM)
+        # and their table gradients one scatter launch, stored into fresh
+        # tables (no zero fill)
+        grads = _ops.rvq_scatter_grad_many([[g] for g in upstream], [STAGES], [c for _, c in encoded],
+                                           group_dim=GROUP_DIM, table_shape=masters[0].shape)
+        for p, grad in zip(masters, grads):
             p.grad = grad
         jkv.clip_codebook_gradients(Codec, maximum_norm=1.0, mode="global")
         jkv.sgd_step(masters, lr=0.001)

@@ -172,6 +172,30 @@ int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads,
                          int64_t workspace_bytes, jkv_stream_t stream);
 
 /*
+ * n_jobs straight-through scatters of one geometry in one call: the value
+ * tables of every layer in a calibration step, whose backward runs
+ * closed_loop_vq.py:376-381 once per layer.  Job j is
+ * jkv_rvq_scatter_grad(n_exits, grads + j * n_exits, ..., codes[j], ...,
+ * grad_tables[j], ...): all jobs share B/H/T/G/d/S/K, the code strides and
+ * the exit depths.  accumulate != 0 adds into grad_tables[j] as that call
+ * does; accumulate == 0 stores the sums (a fresh gradient: grad_tables[j]
+ * need not be initialised, and codewords no row picks get 0).  fp16
+ * gradients with one exit, aligned to the 8- (or 4-) element slice, run up
+ * to 64 jobs per launch on the exact fixed-point bins (one block per
+ * job, head, group, stage and slice over every row), bit-identical to the
+ * one-job call; other jobs run one call each, sharing `workspace` (sized by
+ * jkv_rvq_scatter_workspace_bytes for one job).
+ */
+int jkv_rvq_scatter_grad_many(int32_t n_jobs, int32_t n_exits, const void* const* grads,
+                              int32_t grad_dtype, const int32_t* exit_depths,
+                              const uint8_t* const* codes, int64_t code_stride_b,
+                              int64_t code_stride_h, int64_t code_stride_t, int64_t B,
+                              int64_t H, int64_t T, int64_t G, int64_t d, int64_t S,
+                              int64_t K, float* const* grad_tables, int32_t accumulate,
+                              int32_t deterministic, void* workspace,
+                              int64_t workspace_bytes, jkv_stream_t stream);
+
+/*
  * Squared L2 norm of each of n fp32 buffers, accumulated in fp64, written to
  * out_sumsq[n] (device).  Replaces the per-table torch.linalg.vector_norm of
  * clip_codebook_gradients

@@ -34,6 +34,28 @@ struct ScatterArgs {
   void* partials;            // per-chunk partial bins (workspace)
 };
 
+// Many scatters of one geometry in one launch (every layer's value tables):
+// the geometry and exits once, then each job's buffers.  One row chunk per
+// job, so no partial bins.  Job j takes logical blocks [j * per_job,
+// (j + 1) * per_job).  overwrite != 0 stores the sums instead of adding them
+// (the gradient tables need not be initialised).
+static const int kMaxScatterJobs = 64;
+static const int kMaxScatterJobExits = 1;
+struct ScatterJobBuffers {
+  const void* grads[kMaxScatterJobExits];
+  const uint8_t* codes;
+  float* grad_tables;
+};
+struct ScatterManyArgs {
+  ScatterArgs shape;  // geometry, strides, exits (its buffers unused)
+  int64_t per_job;
+  int32_t n_jobs;
+  int32_t overwrite;
+  ScatterJobBuffers buf[kMaxScatterJobs];
+};
+template <bool MANY> struct ScatterArgsOf { using type = ScatterArgs; };
+template <> struct ScatterArgsOf<true> { using type = ScatterManyArgs; };
+
 template <int DT>
 __device__ __forceinline__ float grad_sum(const ScatterArgs& a, int s, int64_t off) {
   float acc = 0.f;
@@ -110,8 +132,12 @@ __device__ __forceinline__ void lds_add(float* p, float v) { atomicAdd(p, v); }
 // Fixed-point mode (fp16): if a slice holds inf or nan the block discards its
 // bins and adds every slice of its chunk with global fp32 atomics instead,
 // which gives the IEEE inf/nan outcome of a floating-point sum.
-template <int DT, int D>
-__global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
+//
+// MANY: one launch for many jobs of one geometry (ScatterManyArgs), one row
+// chunk each; with `overwrite` the block stores its bins (zeros for a stage
+// no exit reaches) instead of adding them.
+template <int DT, int D, bool MANY>
+__global__ __launch_bounds__(1024) void scatter_bins_kernel(typename ScatterArgsOf<MANY>::type m) {
   constexpr bool kFixed = DT == JKV_F16;
   constexpr int U = 4;  // rows per thread with their loads in flight together
   typedef typename std::conditional<kFixed, long long, float>::type Acc;
@@ -119,16 +145,44 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
   Acc* bins = (Acc*)lds_raw;
   __shared__ uint32_t nonfinite;
 
+  uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const ScatterArgs* ap;
+  const void* grad0 = nullptr;  // a many-job launch's one exit gradient
+  const uint8_t* codes;
+  float* grad_tables;
+  bool overwrite = false;
+  if constexpr (MANY) {
+    const uint32_t per = (uint32_t)m.per_job;
+    const uint32_t job = bid / per;
+    if (job >= (uint32_t)m.n_jobs) return;  // grid padding (before any barrier)
+    bid -= job * per;
+    ap = &m.shape;
+    grad0 = m.buf[job].grads[0];
+    codes = m.buf[job].codes;
+    grad_tables = m.buf[job].grad_tables;
+    overwrite = m.overwrite != 0;
+  } else {
+    ap = &m;
+    codes = m.codes;
+    grad_tables = m.grad_tables;
+  }
+  const ScatterArgs& a = *ap;
+  auto grads = [&](int e) -> const void* {
+    if constexpr (MANY) {
+      return grad0;
+    } else {
+      return a.grads[e];
+    }
+  };
   const int S = (int)a.S, K = (int)a.K, d = (int)a.d;
   const uint32_t n_slices = (uint32_t)(d / D);
-  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t j = bid % n_slices;
   const uint32_t s = (bid / n_slices) % (uint32_t)S;
   const uint32_t p = (bid / (n_slices * S)) % (uint32_t)(a.H * a.G);
   const uint32_t chunk = bid / (n_slices * S * (uint32_t)(a.H * a.G));
   const uint32_t h = p / (uint32_t)a.G, g = p % (uint32_t)a.G;
   const int per_out = K * D;
-  float* const out_base = a.grad_tables + (((int64_t)p * S + s) * K) * d + (int64_t)j * D;
+  float* const out_base = grad_tables + (((int64_t)p * S + s) * K) * d + (int64_t)j * D;
   Acc* const part_base =
       (Acc*)a.partials + ((((int64_t)chunk * a.H * a.G + p) * S + s) * K) * d + (int64_t)j * D;
 
@@ -138,6 +192,8 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
     if (a.n_chunks > 1)
       for (int i = threadIdx.x; i < per_out; i += blockDim.x)
         part_base[(int64_t)(i / D) * d + i % D] = (Acc)0;
+    if (overwrite)
+      for (int i = threadIdx.x; i < per_out; i += blockDim.x) out_base[(int64_t)(i / D) * d + i % D] = 0.f;
     return;
   }
   for (int i = threadIdx.x; i < K * (D + 1); i += blockDim.x) bins[i] = (Acc)0;
@@ -166,8 +222,8 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
         const uint32_t rw = (uint32_t)(ok[u] ? row : r0);
         const uint32_t b = rw / T32, t = rw - b * T32;
         offs[u] = (((int64_t)b * a.H + h) * a.T + t) * Dfull + col;
-        cv[u] = a.codes[(int64_t)b * a.cb + (int64_t)h * a.ch + (int64_t)t * a.ct +
-                        (int64_t)g * S + s];
+        cv[u] = codes[(int64_t)b * a.cb + (int64_t)h * a.ch + (int64_t)t * a.ct +
+                      (int64_t)g * S + s];
       }
       row_fn(offs, cv, ok);
     }
@@ -175,9 +231,9 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
 
   for_rows([&](const int64_t(&offs)[U], const uint32_t(&cv)[U], const bool(&ok)[U]) {
     Acc v[U][D];
-    if (a.n_exits == 1) {
+    if (MANY || a.n_exits == 1) {  // a many-job launch takes one exit
 #pragma unroll
-      for (int u = 0; u < U; ++u) load_slice<DT, D>(a.grads[0], offs[u], v[u], bad);
+      for (int u = 0; u < U; ++u) load_slice<DT, D>(grads(0), offs[u], v[u], bad);
     } else {
       // stage s takes the sum of the exits deeper than s
 #pragma unroll
@@ -189,7 +245,7 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           Acc x[D];
-          load_slice<DT, D>(a.grads[e], offs[u], x, bad);
+          load_slice<DT, D>(grads(e), offs[u], x, bad);
 #pragma unroll
           for (int i = 0; i < D; ++i) v[u][i] += x[i];
         }
@@ -210,6 +266,13 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
 
   if (kFixed && nonfinite) {
     // fp32 sums with global atomics (exit sums in exit order, as grad_sum)
+    if (overwrite) {
+      // this block owns its part of the table: clear it, and make the stores
+      // reach memory before any atomic adds to it
+      for (int i = threadIdx.x; i < per_out; i += blockDim.x) out_base[(int64_t)(i / D) * d + i % D] = 0.f;
+      __threadfence();
+      __syncthreads();
+    }
     for_rows([&](const int64_t(&offs)[U], const uint32_t(&cv)[U], const bool(&ok)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -219,7 +282,7 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
         for (int i = 0; i < D; ++i) {
           float acc = 0.f;
           for (int e = 0; e < a.n_exits; ++e)
-            if (a.exit_depth[e] > (int)s) acc += Elem<DT>::load(a.grads[e], offs[u] + i);
+            if (a.exit_depth[e] > (int)s) acc += Elem<DT>::load(grads(e), offs[u] + i);
           if (acc != 0.f || acc != acc) atomicAdd(&dst[i], acc);
         }
       }
@@ -233,10 +296,16 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(ScatterArgs a) {
     const int k = i / D, c = i - k * D;
     const Acc v = bins[k * (D + 1) + c];
     if (a.n_chunks == 1) {
+      float x;
       if constexpr (kFixed) {
-        out_base[(int64_t)k * d + c] += fixed_to_float(v);
+        x = fixed_to_float(v);
       } else {
-        out_base[(int64_t)k * d + c] += v;
+        x = v;
+      }
+      if (overwrite) {
+        out_base[(int64_t)k * d + c] = x;
+      } else {
+        out_base[(int64_t)k * d + c] += x;
       }
     } else {
       part_base[(int64_t)k * d + c] = v;
@@ -565,9 +634,9 @@ static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) 
     a.rows_per_chunk = ceil_div(rows, plan.chunks);
     const dim3 grid((uint32_t)(P * a.S * (a.d / plan.slice) * plan.chunks));
     if (plan.slice == 8) {
-      hipLaunchKernelGGL((scatter_bins_kernel<DT, 8>), grid, dim3(1024), plan.lds, stream, a);
+      hipLaunchKernelGGL((scatter_bins_kernel<DT, 8, false>), grid, dim3(1024), plan.lds, stream, a);
     } else {
-      hipLaunchKernelGGL((scatter_bins_kernel<DT, 4>), grid, dim3(1024), plan.lds, stream, a);
+      hipLaunchKernelGGL((scatter_bins_kernel<DT, 4, false>), grid, dim3(1024), plan.lds, stream, a);
     }
     JKV_CHECK_LAUNCH();
     if (a.n_chunks > 1) {
@@ -590,6 +659,44 @@ static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) 
                      stream, a);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
+}
+
+// Many fp16 scatters in one launch (scatter_bins_kernel<F16, D, true>): up to
+// kMaxScatterJobs jobs of one geometry, one row chunk each.  Returns
+// JKV_ENOTSUP when the geometry or the buffers do not fit that path.
+static int launch_scatter_many(const ScatterArgs& shape, const ScatterJobBuffers* buf, int n,
+                               bool overwrite, hipStream_t stream) {
+  const BinsPlan plan = bins_plan(shape.B, shape.T, shape.H, shape.G, shape.d, shape.S, shape.K, JKV_F16);
+  if (!plan.ok || !plan.fixed || shape.n_exits > kMaxScatterJobExits) return JKV_ENOTSUP;
+  const uintptr_t align = (uintptr_t)(plan.slice * sizeof(uint16_t));
+  for (int j = 0; j < n; ++j)
+    for (int e = 0; e < shape.n_exits; ++e)
+      if ((uintptr_t)buf[j].grads[e] % align != 0) return JKV_ENOTSUP;
+  ScatterManyArgs m = {};
+  m.shape = shape;
+  m.shape.n_chunks = 1;
+  m.shape.rows_per_chunk = shape.B * shape.T;
+  m.shape.partials = nullptr;
+  m.per_job = shape.H * shape.G * shape.S * (shape.d / plan.slice);
+  m.n_jobs = n;
+  m.overwrite = overwrite ? 1 : 0;
+  for (int j = 0; j < n; ++j) m.buf[j] = buf[j];
+  int64_t nblocks = m.per_job * n;
+  if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
+  JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
+  const size_t lds = (size_t)(shape.K * (plan.slice + 1) * 8);
+  if (plan.slice == 8) {
+    hipLaunchKernelGGL((scatter_bins_kernel<JKV_F16, 8, true>), dim3((uint32_t)nblocks), dim3(1024), lds, stream, m);
+  } else {
+    hipLaunchKernelGGL((scatter_bins_kernel<JKV_F16, 4, true>), dim3((uint32_t)nblocks), dim3(1024), lds, stream, m);
+  }
+  JKV_CHECK_LAUNCH();
+  return JKV_OK;
+}
+
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = 0.f;
 }
 
 }  // namespace jkv
@@ -640,6 +747,80 @@ int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads, int32_t grad
     case JKV_BF16: return launch_scatter<JKV_BF16>(a, deterministic, stream);
     default: return launch_scatter<JKV_F32>(a, deterministic, stream);
   }
+}
+
+int jkv_rvq_scatter_grad_many(int32_t n_jobs, int32_t n_exits, const void* const* grads,
+                              int32_t grad_dtype, const int32_t* exit_depths,
+                              const uint8_t* const* codes, int64_t code_stride_b,
+                              int64_t code_stride_h, int64_t code_stride_t, int64_t B, int64_t H,
+                              int64_t T, int64_t G, int64_t d, int64_t S, int64_t K,
+                              float* const* grad_tables, int32_t accumulate, int32_t deterministic,
+                              void* workspace, int64_t workspace_bytes, jkv_stream_t stream_) {
+  using namespace jkv;
+  hipStream_t stream = (hipStream_t)stream_;
+  JKV_CHECK_ARG(n_jobs >= 0, "negative job count");
+  JKV_CHECK_ARG(n_exits >= 1 && n_exits <= JKV_MAX_EXITS, "1..%d exits", JKV_MAX_EXITS);
+  JKV_CHECK_ARG(B >= 0 && H > 0 && T >= 0 && G > 0 && d > 0 && S > 0 && K > 0 && K <= 256,
+                "invalid scatter geometry");
+  JKV_CHECK_ARG(grad_dtype == JKV_F16 || grad_dtype == JKV_BF16 || grad_dtype == JKV_F32,
+                "unknown gradient dtype %d", grad_dtype);
+  if (n_jobs == 0) return JKV_OK;
+  JKV_CHECK_ARG(grads && codes && grad_tables && exit_depths, "null job array");
+  for (int32_t j = 0; j < n_jobs; ++j) {
+    JKV_CHECK_ARG(codes[j] && grad_tables[j], "null buffer in job %d", j);
+    for (int e = 0; e < n_exits; ++e)
+      JKV_CHECK_ARG(grads[(int64_t)j * n_exits + e] != nullptr, "null exit gradient in job %d", j);
+  }
+  for (int e = 0; e < n_exits; ++e)
+    JKV_CHECK_ARG(exit_depths[e] >= 1 && exit_depths[e] <= S, "exit depth outside the ladder");
+  const int64_t table_elems = H * G * S * K * d;
+  if (B * T == 0) {
+    if (!accumulate)
+      for (int32_t j = 0; j < n_jobs; ++j) {
+        hipLaunchKernelGGL(zero_f32_kernel, dim3((uint32_t)ceil_div(table_elems, 256)), dim3(256), 0, stream,
+                           grad_tables[j], table_elems);
+        JKV_CHECK_LAUNCH();
+      }
+    return JKV_OK;
+  }
+  // fp16 gradients: up to kMaxScatterJobs jobs per launch; jobs that path
+  // does not take (other dtypes, more exits, misaligned gradients) run one
+  // scatter each
+  int32_t first_single = 0;
+  if (grad_dtype == JKV_F16 && n_exits <= kMaxScatterJobExits) {
+    ScatterArgs shape = {};
+    shape.n_exits = n_exits;
+    for (int e = 0; e < n_exits; ++e) shape.exit_depth[e] = exit_depths[e];
+    shape.cb = code_stride_b; shape.ch = code_stride_h; shape.ct = code_stride_t;
+    shape.B = B; shape.H = H; shape.T = T; shape.G = G; shape.d = d; shape.S = S; shape.K = K;
+    ScatterJobBuffers buf[kMaxScatterJobs];
+    for (int32_t j0 = 0; j0 < n_jobs; j0 += kMaxScatterJobs) {
+      const int n = (int)std::min<int64_t>(kMaxScatterJobs, n_jobs - j0);
+      for (int i = 0; i < n; ++i) {
+        const int64_t j = j0 + i;
+        buf[i] = ScatterJobBuffers{};
+        for (int e = 0; e < n_exits; ++e) buf[i].grads[e] = grads[j * n_exits + e];
+        buf[i].codes = codes[j];
+        buf[i].grad_tables = grad_tables[j];
+      }
+      const int rc = launch_scatter_many(shape, buf, n, !accumulate, stream);
+      if (rc == JKV_ENOTSUP) break;
+      if (rc != JKV_OK) return rc;
+      first_single = j0 + n;
+    }
+  }
+  for (int32_t j = first_single; j < n_jobs; ++j) {
+    if (!accumulate) {
+      hipLaunchKernelGGL(zero_f32_kernel, dim3((uint32_t)ceil_div(table_elems, 256)), dim3(256), 0, stream,
+                         grad_tables[j], table_elems);
+      JKV_CHECK_LAUNCH();
+    }
+    const int rc = jkv_rvq_scatter_grad(n_exits, grads + (int64_t)j * n_exits, grad_dtype, exit_depths, codes[j],
+                                        code_stride_b, code_stride_h, code_stride_t, B, H, T, G, d, S, K,
+                                        grad_tables[j], deterministic, workspace, workspace_bytes, stream_);
+    if (rc != JKV_OK) return rc;
+  }
+  return JKV_OK;
 }
 
 }  // extern "C"

@@ -65,6 +65,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_i32, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _vp, _i32, _vp, _i64, _vp],
     ),
+    "jkv_rvq_scatter_grad_many": (
+        ctypes.c_int,
+        [_i32, _i32, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _vp, _i32, _i32, _vp, _i64, _vp],
+    ),
     "jkv_pair_block_select": (
         ctypes.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp,

@@ -353,6 +353,85 @@ def rvq_scatter_grad(
     _lib.check(code)
 
 
+def rvq_scatter_grad_many(
+    grads: Sequence[Sequence[torch.Tensor]],
+    exits: Sequence[int],
+    codes: Sequence[torch.Tensor],
+    grad_tables: Sequence[torch.Tensor] | None = None,
+    *,
+    group_dim: int,
+    table_shape: Sequence[int] | None = None,
+    accumulate: bool | None = None,
+    deterministic: bool = False,
+) -> list[torch.Tensor]:
+    """:func:`rvq_scatter_grad` for every job ``j`` (``grads[j]`` per exit,
+    ``codes[j]``) of one geometry in one call.  Given ``grad_tables``, the
+    sums are added into them (``accumulate`` True, the default) or stored
+    over whatever they hold (``accumulate=False``); without, fresh fp32
+    tables of ``table_shape`` are returned holding the sums alone (no zero
+    fill).  fp16 gradients with one exit run up to 64 jobs per launch."""
+
+    if len(grads) != len(codes) or (grad_tables is not None and len(grad_tables) != len(codes)):
+        raise ValueError("one gradient list, code tensor and table per job")
+    if not codes:
+        return []
+    device = _lib.require_device(*codes, *(g for gs in grads for g in gs),
+                                 *(grad_tables if grad_tables is not None else ()))
+    batch, heads, tokens, groups, stages = map(int, codes[0].shape)
+    n_exits = len(exits)
+    if any(len(gs) != n_exits for gs in grads):
+        raise ValueError("every job needs one gradient per exit")
+    if grad_tables is None:
+        if accumulate:
+            raise ValueError("accumulating needs grad_tables")
+        accumulate = False
+    elif accumulate is None:
+        accumulate = True
+    if grad_tables is not None:
+        shape = tuple(map(int, grad_tables[0].shape))
+    else:
+        if table_shape is None:
+            raise ValueError("fresh gradient tables need table_shape")
+        shape = tuple(int(v) for v in table_shape)
+    problems, t_stages, clusters, d = shape
+    if problems != heads * groups or t_stages != stages or d != group_dim:
+        raise ValueError("code and gradient-table geometry differs")
+    if grad_tables is not None:
+        for t in grad_tables:
+            if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shape:
+                raise ValueError("gradient tables must be contiguous fp32 of one shape")
+        tables = list(grad_tables)
+    else:
+        tables = [torch.empty(shape, dtype=torch.float32, device=device) for _ in codes]
+    strides = codes[0].stride()[:3]
+    for c in codes:
+        if tuple(c.shape) != (batch, heads, tokens, groups, stages) or c.dtype != torch.uint8:
+            raise ValueError("every job's codes must share the first job's geometry")
+        if c.stride()[:3] != strides or c.stride(-1) != 1 or c.stride(-2) != stages:
+            raise ValueError("every job's codes must share the first job's strides")
+    dtype = grads[0][0].dtype
+    align = (8 if d % 8 == 0 else 4) * torch.tensor([], dtype=dtype).element_size()
+    flat = []
+    for gs in grads:
+        for g in gs:
+            g = g.to(dtype).contiguous()
+            flat.append(g if g.data_ptr() % align == 0 else g.clone())
+    lib = _lib.load()
+    ws_bytes = int(lib.jkv_rvq_scatter_workspace_bytes(
+        batch, heads, tokens, groups, d, stages, clusters, _lib.dtype_code(dtype), int(deterministic)))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    code = lib.jkv_rvq_scatter_grad_many(
+        len(codes), n_exits, _lib.ptr_array(ctypes.c_void_p, [g.data_ptr() for g in flat]),
+        _lib.dtype_code(dtype), _lib.ptr_array(ctypes.c_int32, [int(e) for e in exits]),
+        _lib.ptr_array(ctypes.c_void_p, [c.data_ptr() for c in codes]), *strides,
+        batch, heads, tokens, groups, d, stages, clusters,
+        _lib.ptr_array(ctypes.c_void_p, [t.data_ptr() for t in tables]), int(accumulate),
+        int(deterministic), _lib.ptr(workspace), ws_bytes, _lib.stream_handle(device),
+    )
+    _lib.check(code)
+    return tables
+
+
 def sumsq(tensors: Sequence[torch.Tensor]) -> torch.Tensor:
     """fp64 squared L2 norms of fp32 device tensors, as one device tensor."""
 

@@ -219,3 +219,85 @@ def test_scatter_misaligned_gradient_view(device):
         got = torch.zeros(32, 2, 256, 8, device=device)
         _ops.rvq_scatter_grad([view], (2,), codes.to(device), got, group_dim=8, deterministic=deterministic)
         assert torch.equal(got.cpu(), expect)
+
+
+MANY_CASES = [
+    # (jobs, B, H, T, G, d, S, exits, dtype)
+    (5, 4, 8, 200, 16, 8, 2, (2,), torch.float16),     # one launch
+    (70, 1, 2, 300, 16, 8, 2, (2,), torch.float16),    # 64 + 6 jobs: two launches
+    (3, 2, 2, 100, 32, 4, 1, (1,), torch.float16),     # 4-dim slices
+    (3, 2, 8, 100, 16, 8, 2, (1,), torch.float16),     # stage 2 reached by no exit: zeros stored
+    (3, 2, 8, 100, 16, 8, 2, (1, 2), torch.float16),   # two exits: one scatter per job
+    (3, 2, 4, 300, 32, 4, 1, (1,), torch.bfloat16),    # bf16: one scatter per job
+]
+
+
+@pytest.mark.parametrize("case", MANY_CASES)
+def test_scatter_many_equals_per_job_scatters(device, case):
+    # every job of the many-job call against its exact sum (fp16: the
+    # correctly rounded fp64 sum, bit for bit) and against its own one-job
+    # call; fresh tables hold the sums alone, given tables get them added
+    from jointkv_amd import _ops
+
+    jobs, batch, heads, tokens, groups, d, stages, exits, dtype = case
+    print(f"scatter_many jobs={jobs} B={batch} H={heads} T={tokens} G={groups} d={d} S={stages} "
+          f"exits={exits} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(8700 + jobs + tokens + d)
+    shape = (heads * groups, stages, 256, d)
+    cases = [_random_scatter_case(gen, batch, heads, tokens, groups, d, stages, len(exits), dtype)
+             for _ in range(jobs)]
+    codes = [c.to(device) for c, _ in cases]
+    grads = [[g.to(device) for g in gs] for _, gs in cases]
+    fresh = _ops.rvq_scatter_grad_many(grads, exits, codes, group_dim=d, table_shape=shape)
+    base = [torch.randn(shape, generator=gen) for _ in range(jobs)]
+    added = _ops.rvq_scatter_grad_many(grads, exits, codes, [b.to(device) for b in base], group_dim=d)
+    exact = dtype == torch.float16
+    for j in range(jobs):
+        c, gs = cases[j]
+        if exact:
+            expect = ref.table_gradient(gs, exits, c, shape, accumulate=torch.float64).float()
+            assert torch.equal(fresh[j].cpu(), expect), f"job {j}"
+            assert torch.equal(added[j].cpu(), base[j] + expect), f"job {j}"
+            one = torch.zeros(shape, device=device)
+            _ops.rvq_scatter_grad(grads[j], exits, codes[j], one, group_dim=d)
+            assert torch.equal(one, fresh[j]), f"job {j}"
+        else:
+            expect = ref.table_gradient(gs, exits, c, shape)
+            assert _rel(fresh[j], expect) <= GRAD_RTOL, f"job {j}"
+            assert _rel(added[j].cpu() - base[j], expect) <= GRAD_RTOL, f"job {j}"
+
+
+def test_scatter_many_overwrite_clears_tables_and_handles_nonfinite(device):
+    # stored sums replace whatever the tables held (NaN here): codewords no
+    # row picks come back 0, and a job with inf/nan slices gets the IEEE
+    # outcome of a floating-point sum (its blocks clear their part first)
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(8711)
+    jobs, heads = 4, 8
+    shape = (heads * 16, 2, 256, 8)
+    cases = [_random_scatter_case(gen, 1, heads, 3000, 16, 8, 2, 1, torch.float16) for _ in range(jobs)]
+    g = cases[2][1][0]
+    g[0, 0, 5, 3] = float("inf")
+    g[0, 1, 2999, 17] = float("-inf")
+    g[0, 1, 100, 40] = float("nan")
+    codes = [c.to(device) for c, _ in cases]
+    # codewords 200..255 of stage 1 unused in job 0
+    codes[0][..., 0] = codes[0][..., 0] % 200
+    grads = [[x.to(device) for x in gs] for _, gs in cases]
+    tables = [torch.full(shape, float("nan"), device=device) for _ in range(jobs)]
+    out = _ops.rvq_scatter_grad_many(grads, (2,), codes, tables, group_dim=8, accumulate=False)
+    for j in range(jobs):
+        c, gs = cases[j]
+        c = codes[j].cpu()
+        expect = ref.table_gradient(gs, (2,), c, shape, accumulate=torch.float64).float()
+        got = out[j].cpu()
+        if j != 2:
+            assert torch.equal(got, expect), f"job {j}"
+            continue
+        assert torch.equal(torch.isnan(got), torch.isnan(expect))
+        assert torch.equal(torch.isinf(got), torch.isinf(expect))
+        assert torch.equal(got[torch.isinf(got)], expect[torch.isinf(expect)])
+        finite = torch.isfinite(expect)
+        torch.testing.assert_close(got[finite], expect[finite], rtol=1e-5, atol=1e-6)
+    assert bool((out[0].cpu()[:, 0, 200:] == 0).all())

@@ -88,6 +88,10 @@ def timed(fn, steps, warmup):
         fn()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # a spin kernel ahead of the start event keeps the stream busy while the
+    # host enqueues the first step, so the events time the steps themselves
+    # (back to back) and not the host's enqueue of the first one
+    torch.cuda._sleep(20_000_000)
     start.record()
     for _ in range(steps):
         fn()

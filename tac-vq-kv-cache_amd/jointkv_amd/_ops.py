@@ -157,42 +157,53 @@ def rvq_encode_many(
         raise ValueError("one table set per states tensor")
     if not states:
         return []
-    device = _lib.require_device(*states, *tables)
+    # one pass of checks and one allocation per output kind: a cache's 64
+    # tensors are enqueued in well under the launch's own GPU time
     first = states[0]
+    device = _lib.require_device(first, tables[0])
     batch, heads, tokens, dim = map(int, first.shape)
     problems, stages, clusters, d = map(int, tables[0].shape)
     if dim != groups * group_dim or d != group_dim or problems != heads * groups:
         raise ValueError("state and table geometry differs")
-    for x, t in zip(states, tables):
-        if x.shape != first.shape or x.dtype != first.dtype or t.shape != tables[0].shape:
+    if len(exits) > _lib.MAX_EXITS:
+        raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
+    xshape, xdtype, tshape = first.shape, first.dtype, tables[0].shape
+    strides = first.stride()
+    xs = list(states)
+    for j, (x, t) in enumerate(zip(states, tables)):
+        if x.shape != xshape or x.dtype != xdtype or t.shape != tshape:
             raise ValueError("every job must share the first job's geometry")
         if t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError("encode tables must be contiguous fp32 masters")
-    if len(exits) > _lib.MAX_EXITS:
-        raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
-    prepared = [_encode_states_strides(x) for x in states]
-    strides = prepared[0][1]
-    if any(st != strides for _, st in prepared):
-        prepared = [_encode_states_strides(x.contiguous()) for x in states]
-        strides = prepared[0][1]
-    xs = [x for x, _ in prepared]
-    codes = [torch.empty((batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device) for _ in xs]
-    recon = [[torch.empty((batch, heads, tokens, dim), dtype=first.dtype, device=device) for _ in exits]
-             for _ in xs]
+        if x.device != device or t.device != device:
+            raise ValueError("tensors live on different devices")
+        if x.stride() != strides or strides[-1] != 1:
+            xs[j] = x = x.contiguous()
+    if any(x.stride() != xs[0].stride() for x in xs):
+        xs = [x.contiguous() for x in xs]
+    sb, sh, st = xs[0].stride()[:3]
+    n = len(xs)
+    codes_all = torch.empty((n, batch, heads, tokens, groups, stages), dtype=torch.uint8, device=device)
+    recon_all = torch.empty((n, len(exits), batch, heads, tokens, dim), dtype=xdtype, device=device)
+    c0, cstep = codes_all.data_ptr(), codes_all.stride(0)
+    r0, rstep, estep = recon_all.data_ptr(), recon_all.stride(0) * recon_all.element_size(), \
+        recon_all.stride(1) * recon_all.element_size()
     lib = _lib.load()
     ws_bytes = int(lib.jkv_rvq_encode_workspace_bytes(heads, groups, stages, clusters, d, 0))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
     code = lib.jkv_rvq_encode_many(
-        len(xs), _lib.ptr_array(ctypes.c_void_p, [x.data_ptr() for x in xs]), _lib.dtype_code(first.dtype),
-        batch, heads, tokens, groups, d, *strides,
+        n, _lib.ptr_array(ctypes.c_void_p, [x.data_ptr() for x in xs]), _lib.dtype_code(xdtype),
+        batch, heads, tokens, groups, d, sb, sh, st,
         _lib.ptr_array(ctypes.c_void_p, [t.data_ptr() for t in tables]), stages, clusters,
-        _lib.ptr_array(ctypes.c_void_p, [c.data_ptr() for c in codes]), *codes[0].stride()[:3],
+        _lib.ptr_array(ctypes.c_void_p, [c0 + j * cstep for j in range(n)]), *codes_all.stride()[1:4],
         len(exits), _lib.ptr_array(ctypes.c_int32, [int(e) for e in exits]),
-        _lib.ptr_array(ctypes.c_void_p, [r.data_ptr() for rs in recon for r in rs]),
+        _lib.ptr_array(ctypes.c_void_p, [r0 + j * rstep + e * estep for j in range(n) for e in range(len(exits))]),
         _lib.ptr(workspace), ws_bytes, _lib.stream_handle(device),
     )
     _lib.check(code)
-    return [(rs, c) for rs, c in zip(recon, codes)]
+    codes = codes_all.unbind(0)
+    recon = recon_all.unbind(0)
+    return [(list(r.unbind(0)), c) for r, c in zip(recon, codes)]
 
 
 def nearest_f32(states: torch.Tensor, tables: torch.Tensor) -> torch.Tensor:
@@ -402,7 +413,7 @@ def rvq_scatter_grad_many(
                 raise ValueError("gradient tables must be contiguous fp32 of one shape")
         tables = list(grad_tables)
     else:
-        tables = [torch.empty(shape, dtype=torch.float32, device=device) for _ in codes]
+        tables = list(torch.empty((len(codes), *shape), dtype=torch.float32, device=device).unbind(0))
     strides = codes[0].stride()[:3]
     for c in codes:
         if tuple(c.shape) != (batch, heads, tokens, groups, stages) or c.dtype != torch.uint8:
@@ -414,7 +425,8 @@ def rvq_scatter_grad_many(
     flat = []
     for gs in grads:
         for g in gs:
-            g = g.to(dtype).contiguous()
+            if g.dtype != dtype or not g.is_contiguous():
+                g = g.to(dtype).contiguous()
             flat.append(g if g.data_ptr() % align == 0 else g.clone())
     lib = _lib.load()
     ws_bytes = int(lib.jkv_rvq_scatter_workspace_bytes(

@@ -164,3 +164,59 @@ def test_nearest_rejects_rows_beyond_the_grid_before_touching_the_device():
         args += extra + [dummy, ctypes.c_void_p(0)]
         assert fn(*args) == _lib.JKV_EINVAL
         assert b"rows per head" in lib.jkv_last_error()
+
+
+def test_many_job_entry_points_validate_before_touching_the_device():
+    # argument errors and empty calls return before any HIP call
+    lib = _lib.load()
+    p = (ctypes.c_void_p * 1)(16)
+    depth = (ctypes.c_int32 * 1)(1)
+    bad_depth = (ctypes.c_int32 * 1)(3)
+    enc = dict(n=1, states=p, dtype=0, B=1, H=1, T=4, G=1, d=8, sb=32, sh=32, st=8, tables=p, S=1, K=256,
+               codes=p, cb=4, ch=4, ct=1, n_exits=1, exits=depth, recon=None, ws=None, ws_bytes=0, stream=None)
+
+    def encode_many(**kw):
+        a = dict(enc)
+        a.update(kw)
+        return lib.jkv_rvq_encode_many(*a.values())
+
+    assert encode_many(n=-1) == _lib.JKV_EINVAL
+    assert encode_many(K=0) == _lib.JKV_EINVAL
+    assert encode_many(n_exits=99) == _lib.JKV_EINVAL
+    assert encode_many(n=0) == _lib.JKV_OK
+    assert encode_many(T=0) == _lib.JKV_OK
+    assert encode_many(states=None) == _lib.JKV_EINVAL
+    assert encode_many(exits=bad_depth) == _lib.JKV_EINVAL
+    assert b"ladder" in lib.jkv_last_error()
+
+    sc = dict(n=1, n_exits=1, grads=p, dtype=0, exits=depth, codes=p, cb=4, ch=4, ct=2, B=1, H=1, T=4, G=1,
+              d=8, S=2, K=256, tables=p, accumulate=1, deterministic=0, ws=None, ws_bytes=0, stream=None)
+
+    def scatter_many(**kw):
+        a = dict(sc)
+        a.update(kw)
+        return lib.jkv_rvq_scatter_grad_many(*a.values())
+
+    assert scatter_many(n=-1) == _lib.JKV_EINVAL
+    assert scatter_many(K=300) == _lib.JKV_EINVAL
+    assert scatter_many(dtype=7) == _lib.JKV_EINVAL
+    assert scatter_many(n_exits=0) == _lib.JKV_EINVAL
+    assert scatter_many(n=0) == _lib.JKV_OK
+    assert scatter_many(codes=None) == _lib.JKV_EINVAL
+    assert scatter_many(exits=bad_depth) == _lib.JKV_EINVAL
+    # an empty problem that accumulates is a no-op
+    assert scatter_many(T=0) == _lib.JKV_OK
+
+
+def test_many_job_wrappers_reject_host_tensors_and_accept_empty_lists():
+    from jointkv_amd import _ops
+
+    assert _ops.rvq_encode_many([], [], groups=1, group_dim=8, exits=(1,)) == []
+    assert _ops.rvq_scatter_grad_many([], (1,), [], group_dim=8) == []
+    with pytest.raises(ValueError, match="HIP"):
+        _ops.rvq_encode_many([torch.randn(1, 2, 4, 8).half()], [torch.randn(2, 1, 256, 8)], groups=1,
+                             group_dim=8, exits=(1,))
+    with pytest.raises(ValueError, match="HIP"):
+        _ops.rvq_scatter_grad_many([[torch.randn(1, 2, 4, 8).half()]], (1,),
+                                   [torch.zeros(1, 2, 4, 1, 1, dtype=torch.uint8)], group_dim=8,
+                                   table_shape=(2, 1, 256, 8))

@@ -181,9 +181,9 @@ int jkv_rvq_scatter_grad(int32_t n_exits, const void* const* grads,
  * does; accumulate == 0 stores the sums (a fresh gradient: grad_tables[j]
  * need not be initialised, and codewords no row picks get 0).  fp16
  * gradients with one exit, aligned to the 8- (or 4-) element slice, run up
- * to 64 jobs per launch on the exact fixed-point bins (one block per
- * job, head, group, stage and slice over every row), bit-identical to the
- * one-job call; other jobs run one call each, sharing `workspace` (sized by
+ * to 64 jobs per launch on the exact fixed-point bins over every row (one
+ * block per job, head and group taking all stages when d = 8, else per
+ * stage and slice), bit-identical to the one-job call; other jobs run one call each, sharing `workspace` (sized by
  * jkv_rvq_scatter_workspace_bytes for one job).
  */
 int jkv_rvq_scatter_grad_many(int32_t n_jobs, int32_t n_exits, const void* const* grads,

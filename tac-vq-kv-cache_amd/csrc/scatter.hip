@@ -320,15 +320,47 @@ __global__ __launch_bounds__(1024) void scatter_bins_kernel(typename ScatterArgs
 // addresses advance by the block stride without a division per row.
 // Logical blocks run group, chunk, head from fastest to slowest: the groups
 // of one row range share its 256-byte rows in one XCD's L2.
-template <int S>
-__global__ __launch_bounds__(1024) void scatter_group8_kernel(ScatterArgs a) {
+//
+// MANY: one launch for many jobs of one geometry and one exit
+// (ScatterManyArgs), one row chunk each; with `overwrite` the block stores
+// its bins instead of adding them.
+template <int S, bool MANY>
+__global__ __launch_bounds__(1024) void scatter_group8_kernel(typename ScatterArgsOf<MANY>::type m) {
   constexpr int D = 8, U = 4, kPad = D + 1;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   long long* bins = (long long*)lds_raw;  // [S][K][kPad]
   __shared__ uint32_t nonfinite;
+  uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
+  const ScatterArgs* ap;
+  const void* grad0 = nullptr;
+  const uint8_t* codes;
+  float* grad_tables;
+  bool overwrite = false;
+  if constexpr (MANY) {
+    const uint32_t per = (uint32_t)m.per_job;
+    const uint32_t job = bid / per;
+    if (job >= (uint32_t)m.n_jobs) return;  // grid padding (before any barrier)
+    bid -= job * per;
+    ap = &m.shape;
+    grad0 = m.buf[job].grads[0];
+    codes = m.buf[job].codes;
+    grad_tables = m.buf[job].grad_tables;
+    overwrite = m.overwrite != 0;
+  } else {
+    ap = &m;
+    codes = m.codes;
+    grad_tables = m.grad_tables;
+  }
+  const ScatterArgs& a = *ap;
+  auto grads = [&](int e) -> const void* {
+    if constexpr (MANY) {
+      return grad0;
+    } else {
+      return a.grads[e];
+    }
+  };
   const int K = (int)a.K;
   const uint32_t G = (uint32_t)a.G;
-  const uint32_t bid = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t g = bid % G;
   const uint32_t chunk = (bid / G) % (uint32_t)a.n_chunks;
   const uint32_t h = bid / (G * (uint32_t)a.n_chunks);
@@ -375,13 +407,14 @@ __global__ __launch_bounds__(1024) void scatter_group8_kernel(ScatterArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int s = 0; s < S; ++s) code[u][s] = a.codes[coff[u] + s];
+      for (int s = 0; s < S; ++s) code[u][s] = codes[coff[u] + s];
     // each exit's slice goes straight into the bins of the stages it covers
     // (exact integer sums, so the order of the additions does not matter)
-    for (int e = 0; e < a.n_exits; ++e) {
+    const int n_exits = MANY ? 1 : a.n_exits;
+    for (int e = 0; e < n_exits; ++e) {
       long long x[U][D];
 #pragma unroll
-      for (int u = 0; u < U; ++u) load_slice<JKV_F16, D>(a.grads[e], goff[u], x[u], bad);
+      for (int u = 0; u < U; ++u) load_slice<JKV_F16, D>(grads(e), goff[u], x[u], bad);
       const int depth = a.exit_depth[e];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -403,16 +436,24 @@ __global__ __launch_bounds__(1024) void scatter_group8_kernel(ScatterArgs a) {
   if (nonfinite) {
     // a slice holds inf or nan: fp32 sums with global atomics give the IEEE
     // outcome (exit sums in exit order, as grad_sum)
+    if (overwrite) {
+      // this block owns its (head, group) of the table: clear it, and make
+      // the stores reach memory before any atomic adds to it
+      float* own = grad_tables + (int64_t)p * S * K * d;
+      for (int i = threadIdx.x; i < S * K * D; i += blockDim.x) own[i] = 0.f;
+      __threadfence();
+      __syncthreads();
+    }
     for (uint32_t rr = r0 + threadIdx.x; rr < r1; rr += step) {
       const uint32_t bb = rr / T32, tt = rr - bb * T32;
       const int64_t off = (int64_t)bb * gstride_b + gbase + (int64_t)tt * gstride_t;
       const int64_t co = (int64_t)bb * a.cb + cbase + (int64_t)tt * a.ct;
       for (int s = 0; s < S; ++s) {
-        float* dst = a.grad_tables + (((int64_t)p * S + s) * K + a.codes[co + s]) * d;
+        float* dst = grad_tables + (((int64_t)p * S + s) * K + codes[co + s]) * d;
         for (int i = 0; i < D; ++i) {
           float acc = 0.f;
           for (int e = 0; e < a.n_exits; ++e)
-            if (a.exit_depth[e] > s) acc += Elem<JKV_F16>::load(a.grads[e], off + i);
+            if (a.exit_depth[e] > s) acc += Elem<JKV_F16>::load(grads(e), off + i);
           if (acc != 0.f || acc != acc) atomicAdd(&dst[i], acc);
         }
       }
@@ -433,7 +474,11 @@ __global__ __launch_bounds__(1024) void scatter_group8_kernel(ScatterArgs a) {
       const long long v = bins[(s * K + (i >> 3)) * kPad + (i & 7)];
       const int64_t o = (int64_t)s * K * D + i;
       if (a.n_chunks == 1) {
-        a.grad_tables[pbase + o] += fixed_to_float(v);
+        if (overwrite) {
+          grad_tables[pbase + o] = fixed_to_float(v);
+        } else {
+          grad_tables[pbase + o] += fixed_to_float(v);
+        }
       } else {
         part[o] = v;
       }
@@ -615,10 +660,10 @@ static int launch_scatter(ScatterArgs a, int deterministic, hipStream_t stream) 
     int64_t nblocks = P * plan.chunks;
     const dim3 grid((uint32_t)nblocks);
     switch (a.S) {
-      case 1: hipLaunchKernelGGL(scatter_group8_kernel<1>, grid, dim3(1024), plan.lds, stream, a); break;
-      case 2: hipLaunchKernelGGL(scatter_group8_kernel<2>, grid, dim3(1024), plan.lds, stream, a); break;
-      case 3: hipLaunchKernelGGL(scatter_group8_kernel<3>, grid, dim3(1024), plan.lds, stream, a); break;
-      default: hipLaunchKernelGGL(scatter_group8_kernel<4>, grid, dim3(1024), plan.lds, stream, a); break;
+      case 1: hipLaunchKernelGGL((scatter_group8_kernel<1, false>), grid, dim3(1024), plan.lds, stream, a); break;
+      case 2: hipLaunchKernelGGL((scatter_group8_kernel<2, false>), grid, dim3(1024), plan.lds, stream, a); break;
+      case 3: hipLaunchKernelGGL((scatter_group8_kernel<3, false>), grid, dim3(1024), plan.lds, stream, a); break;
+      default: hipLaunchKernelGGL((scatter_group8_kernel<4, false>), grid, dim3(1024), plan.lds, stream, a); break;
     }
     JKV_CHECK_LAUNCH();
     if (a.n_chunks > 1) {
@@ -677,13 +722,30 @@ static int launch_scatter_many(const ScatterArgs& shape, const ScatterJobBuffers
   m.shape.n_chunks = 1;
   m.shape.rows_per_chunk = shape.B * shape.T;
   m.shape.partials = nullptr;
-  m.per_job = shape.H * shape.G * shape.S * (shape.d / plan.slice);
   m.n_jobs = n;
   m.overwrite = overwrite ? 1 : 0;
   for (int j = 0; j < n; ++j) m.buf[j] = buf[j];
+  // 8-dim groups: one block per (job, head, group) takes every stage, so
+  // each row's 16-byte slice is read once (the jobs fill the chip without
+  // row chunks)
+  const bool group8 = shape.d == 8 && shape.S <= 4 && shape.K <= 256 &&
+                      shape.B * shape.H * shape.T * shape.G * shape.d < ((int64_t)1 << 31);
+  m.per_job = group8 ? shape.H * shape.G : shape.H * shape.G * shape.S * (shape.d / plan.slice);
   int64_t nblocks = m.per_job * n;
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
+  if (group8) {
+    const size_t lds8 = (size_t)(shape.S * shape.K * 9 * 8);
+    const dim3 grid((uint32_t)nblocks);
+    switch (shape.S) {
+      case 1: hipLaunchKernelGGL((scatter_group8_kernel<1, true>), grid, dim3(1024), lds8, stream, m); break;
+      case 2: hipLaunchKernelGGL((scatter_group8_kernel<2, true>), grid, dim3(1024), lds8, stream, m); break;
+      case 3: hipLaunchKernelGGL((scatter_group8_kernel<3, true>), grid, dim3(1024), lds8, stream, m); break;
+      default: hipLaunchKernelGGL((scatter_group8_kernel<4, true>), grid, dim3(1024), lds8, stream, m); break;
+    }
+    JKV_CHECK_LAUNCH();
+    return JKV_OK;
+  }
   const size_t lds = (size_t)(shape.K * (plan.slice + 1) * 8);
   if (plan.slice == 8) {
     hipLaunchKernelGGL((scatter_bins_kernel<JKV_F16, 8, true>), dim3((uint32_t)nblocks), dim3(1024), lds, stream, m);

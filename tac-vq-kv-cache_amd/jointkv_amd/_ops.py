@@ -169,17 +169,20 @@ def rvq_encode_many(
         raise ValueError(f"at most {_lib.MAX_EXITS} exits per call")
     xshape, xdtype, tshape = first.shape, first.dtype, tables[0].shape
     strides = first.stride()
+    index = first.get_device()
     xs = list(states)
+    copied = False
     for j, (x, t) in enumerate(zip(states, tables)):
         if x.shape != xshape or x.dtype != xdtype or t.shape != tshape:
             raise ValueError("every job must share the first job's geometry")
         if t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError("encode tables must be contiguous fp32 masters")
-        if x.device != device or t.device != device:
+        if x.get_device() != index or t.get_device() != index:
             raise ValueError("tensors live on different devices")
         if x.stride() != strides or strides[-1] != 1:
-            xs[j] = x = x.contiguous()
-    if any(x.stride() != xs[0].stride() for x in xs):
+            xs[j] = x.contiguous()
+            copied = True
+    if copied and any(x.stride() != xs[0].stride() for x in xs):
         xs = [x.contiguous() for x in xs]
     sb, sh, st = xs[0].stride()[:3]
     n = len(xs)
@@ -202,8 +205,8 @@ def rvq_encode_many(
     )
     _lib.check(code)
     codes = codes_all.unbind(0)
-    recon = recon_all.unbind(0)
-    return [(list(r.unbind(0)), c) for r, c in zip(recon, codes)]
+    per_exit = [recon_all[:, e].unbind(0) for e in range(len(exits))]
+    return [([pe[j] for pe in per_exit], codes[j]) for j in range(n)]
 
 
 def nearest_f32(states: torch.Tensor, tables: torch.Tensor) -> torch.Tensor:

@@ -301,3 +301,20 @@ def test_scatter_many_overwrite_clears_tables_and_handles_nonfinite(device):
         finite = torch.isfinite(expect)
         torch.testing.assert_close(got[finite], expect[finite], rtol=1e-5, atol=1e-6)
     assert bool((out[0].cpu()[:, 0, 200:] == 0).all())
+
+
+def test_scatter_many_config5_equals_per_layer_scatters(device):
+    # the V-only step's 32 value-table scatters at config 5's shape in one
+    # launch, against each layer's own scatter (exact sums: bit for bit)
+    from jointkv_amd import _ops
+
+    print("scatter_many config 5 (32 x [4,8,2048,128])", flush=True)
+    gen = torch.Generator(device=device).manual_seed(8607)
+    codes = [torch.randint(0, 256, (4, 8, 2048, 16, 2), generator=gen, device=device, dtype=torch.int32)
+             .to(torch.uint8) for _ in range(32)]
+    grads = [[(torch.randn(4, 8, 2048, 128, generator=gen, device=device) * 1e-3 ** 0.5).half()] for _ in range(32)]
+    fresh = _ops.rvq_scatter_grad_many(grads, (2,), codes, group_dim=8, table_shape=(128, 2, 256, 8))
+    for layer in range(32):
+        one = torch.zeros(128, 2, 256, 8, device=device)
+        _ops.rvq_scatter_grad(grads[layer], (2,), codes[layer], one, group_dim=8)
+        assert torch.equal(one, fresh[layer]), f"layer {layer}"

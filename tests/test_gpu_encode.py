@@ -338,3 +338,24 @@ def test_whitened_grouped_cq_on_mfma(device, dim, batch, tokens, seed):
     rows = res["prefix_ok"].all(-1)
     same = (codes.cpu() == r_codes).all(-1)
     assert torch.equal(out.cpu()[same], r_out.detach()[same])
+
+
+def test_encode_many_full_cache_equals_per_layer_launches(device):
+    # the bench's headline workload at full size: the 64 tensors of a
+    # 32-layer [1,8,8192,128] G2 cache in one call, against each layer's
+    # K/V launch (itself checked against the oracle above), bit for bit
+    from jointkv_amd import _ops
+
+    print("encode_many full config-2 cache (64 x [1,8,8192,128])", flush=True)
+    gen = torch.Generator(device=device).manual_seed(8601)
+    states = [(torch.randn(1, 8, 8192, 128, generator=gen, device=device)).half() for _ in range(64)]
+    tables = [(torch.randn(128, 2, 256, 8, generator=gen, device=device)
+               * torch.tensor([1.0, 0.5], device=device)[None, :, None, None]).half().float() for _ in range(64)]
+    out = _ops.rvq_encode_many(states, tables, groups=16, group_dim=8, exits=(1, 2))
+    for layer in range(32):
+        k, v = 2 * layer, 2 * layer + 1
+        rk, ck, rv, cv = _ops.rvq_encode_kv(states[k], states[v], tables[k], tables[v], groups=16, group_dim=8,
+                                            exits=(1, 2))
+        assert torch.equal(out[k][1], ck) and torch.equal(out[v][1], cv), f"layer {layer}: codes"
+        for a, b in zip(out[k][0] + out[v][0], rk + rv):
+            assert torch.equal(a, b), f"layer {layer}: reconstructions"

@@ -21,7 +21,8 @@ Extra measurements in the same JSON line:
            tokens), forward + backward through the stack, per_layer_kv clip,
            SGD; steps/s
   vstep    config 5: V-only STE calibration step over 32 layers at
-           [4,8,2048,128] (encode fwd, scatter bwd, global clip, SGD), steps/s
+           [4,8,2048,128] (encode fwd, scatter bwd, global clip, SGD), steps/s,
+           with the layers' encodes and scatters batched (and per layer)
   cq2      config 3: reference cq2 grouped-CQ encode ([8,32,256,4]) of
            32 layers x {K,V} x [4,8,2048,128] in one call (and per layer),
            tokens/s
@@ -429,8 +430,24 @@ def vstep_workload(args, device):
         jkv.clip_codebook_gradients(Codec, maximum_norm=1.0, mode="global")
         jkv.sgd_step(masters, lr=0.001)
 
+    # the same step with a launch per layer for each encode and each scatter
+    # (and a zero-filled gradient per table), as a codec forward and its
+    # autograd backward issue them inside a model
+    def step_per_layer():
+        for p in masters:
+            p.grad = None
+        for x, p, g in zip(values, masters, upstream):
+            _recon, codes = _ops.rvq_encode(x, p.detach(), groups=GROUPS, group_dim=GROUP_DIM, exits=(STAGES,))
+            grad = torch.zeros_like(p)
+            _ops.rvq_scatter_grad([g], [STAGES], codes, grad, group_dim=GROUP_DIM)
+            p.grad = grad
+        jkv.clip_codebook_gradients(Codec, maximum_norm=1.0, mode="global")
+        jkv.sgd_step(masters, lr=0.001)
+
     ms = timed(step, max(1, args.steps // 2), 1)
-    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms}
+    ms_per_layer = timed(step_per_layer, max(1, args.steps // 2), 1)
+    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms,
+            "per_layer_launches": {"ms_per_step": ms_per_layer, "steps_per_s": 1e3 / ms_per_layer}}
 
 
 def adapter_workload(args, device):

@@ -359,3 +359,23 @@ def test_encode_many_full_cache_equals_per_layer_launches(device):
         assert torch.equal(out[k][1], ck) and torch.equal(out[v][1], cv), f"layer {layer}: codes"
         for a, b in zip(out[k][0] + out[v][0], rk + rv):
             assert torch.equal(a, b), f"layer {layer}: reconstructions"
+
+
+def test_encode_many_strided_views_and_geometry_errors(device):
+    # states given as [B,T,H,D] storage viewed as [B,H,T,D] (the layout a
+    # projection produces), mixed with contiguous ones: each job's output
+    # equals its own encode; mismatched geometry is refused
+    from jointkv_amd import _ops
+
+    gen = torch.Generator(device=device).manual_seed(5161)
+    base = [torch.randn(2, 300, 8, 128, generator=gen, device=device).half() for _ in range(3)]
+    states = [base[0].transpose(1, 2), base[1].transpose(1, 2).contiguous(), base[2].transpose(1, 2)]
+    tables = [(torch.randn(128, 2, 256, 8, generator=gen, device=device)).half().float() for _ in range(3)]
+    out = _ops.rvq_encode_many(states, tables, groups=16, group_dim=8, exits=(2,))
+    for j in range(3):
+        recon, codes = _ops.rvq_encode(states[j], tables[j], groups=16, group_dim=8, exits=(2,))
+        assert torch.equal(out[j][1], codes) and torch.equal(out[j][0][0], recon[0]), f"job {j}"
+    with pytest.raises(ValueError, match="geometry"):
+        _ops.rvq_encode_many([states[0], states[1][:, :, :200]], tables[:2], groups=16, group_dim=8, exits=(2,))
+    with pytest.raises(ValueError):
+        _ops.rvq_encode_many(states[:2], tables[:1], groups=16, group_dim=8, exits=(2,))

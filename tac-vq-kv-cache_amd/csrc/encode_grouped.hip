@@ -32,6 +32,11 @@
 // codeword taken, ties to the lowest index.  Keys keep 27 bits of the
 // distance (2^-18 relative); the re-scored distances are full fp32.
 //
+// Launch forms: one encode, a token's K and V, or up to 64 encodes of one
+// geometry (a whole cache) whose workgroups run back to back in one grid,
+// so the table staging of one job's first workgroups overlaps the last
+// workgroups of the job before.
+//
 // delta = 2^-8 (|r|^2 + max|c|^2) keeps every D negative despite fp32
 // rounding; it is common to all codewords of a row, so it never changes
 // their order.  Stage 2's |x - c1|^2 is read off stage 1's re-scored

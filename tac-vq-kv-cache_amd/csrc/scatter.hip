@@ -15,6 +15,10 @@
 //                          a multiple of 4).
 //   scatter_det_*          fixed-order fp32 sums for bf16/fp32 gradients when
 //                          a deterministic result is asked for.
+// scatter_group8_kernel (below) serves fp16 8-dim groups with every stage's
+// bins in one block.  The bins and group8 kernels also run many scatters of
+// one geometry (a calibration step's layers) in one launch, one job per
+// range of blocks, storing or adding their sums.
 #include <type_traits>
 
 #include "jkv_common.h"

@@ -204,6 +204,7 @@ struct FullArgs {
   const float* mc;          // whitened: M c per codeword [P][S][256][128]
   const _Float16* mperm;    // whitened: M's permuted rows, hi and lo planes [P][256][128]
   int64_t row_blocks;  // row blocks per problem
+  int64_t blocks_per_wg;  // consecutive row blocks of one problem per workgroup (1 when whitened)
 };
 
 __device__ __forceinline__ uint32_t umin3_f(uint32_t a, uint32_t b, uint32_t c) {
@@ -306,21 +307,39 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   constexpr int nw = NW;  // 4 or 8 waves
   const int lg = lane >> 4, j = lane & 15;
 
-  // logical block: row blocks of one problem are consecutive (one table set
-  // per XCD's L2)
+  // logical workgroup: a run of consecutive row blocks of one problem (one
+  // table set per XCD's L2); with S <= 2 both stage tables stay in LDS for
+  // the whole run
   const uint32_t L = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t P = a.H * a.G;
-  if ((int64_t)L >= P * f.row_blocks) return;
-  const int64_t p = (int64_t)L / f.row_blocks;
-  const int64_t blk = (int64_t)L % f.row_blocks;
+  const int64_t wgs_per_p = (f.row_blocks + f.blocks_per_wg - 1) / f.blocks_per_wg;
+  if ((int64_t)L >= P * wgs_per_p) return;
+  const int64_t p = (int64_t)L / wgs_per_p;
+  const int64_t blk0 = ((int64_t)L % wgs_per_p) * f.blocks_per_wg;
+  const int64_t nblk = min(f.blocks_per_wg, f.row_blocks - blk0);
   const int64_t h = p / a.G, g = p % a.G;
   const int S = (int)a.S;
+  const bool resident = !WH && S <= 2;  // both tables loaded once per run
   const int64_t rows = a.B * a.T;
-  const int64_t row = blk * (16 * nw) + wave * 16 + j;
-  const bool valid = row < rows;
-  const int64_t rw = valid ? row : 0;
-  const int64_t b = rw / a.T, t = rw - (rw / a.T) * a.T;
-  const _Float16* xrow = (const _Float16*)a.states + b * a.sb + h * a.sh + t * a.st + g * kFullD;
+  // this lane's row of block blk0 + bi (rows past the end read row 0)
+  struct RowAt {
+    bool valid;
+    int64_t b, t;
+  };
+  auto row_at = [&](int64_t bi) {
+    const int64_t row = (blk0 + bi) * (16 * nw) + wave * 16 + j;
+    RowAt r;
+    r.valid = row < rows;
+    const int64_t rw = r.valid ? row : 0;
+    r.b = rw / a.T;
+    r.t = rw - r.b * a.T;
+    return r;
+  };
+  auto load_x = [&](const RowAt& r, half8 (&x)[4]) {
+    const _Float16* xrow = (const _Float16*)a.states + r.b * a.sb + h * a.sh + r.t * a.st + g * kFullD;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) x[kk] = *(const half8*)(xrow + 32 * kk + 8 * lg);
+  };
 
   // stage tables: 64 direct buffer->LDS loads of 1 KiB (4 codeword rows) plus
   // one of the -|c|^2/2 plane.  Wave w issues loads k = w + nw*i, i < 64/nw;
@@ -377,15 +396,9 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
     for (int i = 0; i < 16; ++i) m = fmaxf(m, part[i]);
     ncm_s[tid] = m;
   }
+  RowAt ra = row_at(0);
   half8 x[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) x[kk] = *(const half8*)(xrow + 32 * kk + 8 * lg);
-  float dec[4][8];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dec[kk][e] = 0.f;
-  uint8_t* const code_row = a.codes + b * a.cb + h * a.ch + t * a.ct + g * S;
+  load_x(ra, x);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -397,6 +410,16 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   float one = 1.0f;
   asm volatile("" : "+v"(one));
   const int64_t Dfull = a.G * kFullD;
+
+  for (int64_t bi = 0; bi < nblk; ++bi) {
+  const bool valid = ra.valid;
+  const int64_t b = ra.b, t = ra.t;
+  float dec[4][8];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dec[kk][e] = 0.f;
+  uint8_t* const code_row = a.codes + b * a.cb + h * a.ch + t * a.ct + g * S;
   const int64_t out_off = ((b * a.H + h) * a.T + t) * Dfull + g * kFullD;
 
   // whitened state: u in the B-operand layout (dims 32kk + 8lg + e) and |r'|^2
@@ -430,10 +453,18 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   }
 
   for (int s = 0; s < S; ++s) {
-    const int buf = s & 1;
-    const bool next = s + 1 < S;
+    // streamed tables alternate buffers over the whole run (stage s of block
+    // bi is the run's (bi S + s)-th table); resident ones sit in buffer s
+    const int buf = resident ? s : (int)((bi * S + s) & 1);
+    // the table this stage's search loads into the other buffer: the next
+    // stage's, or the next block's first when the run goes on; resident
+    // tables load only during the run's first block
+    const bool next_stage = s + 1 < S && (!resident || bi == 0);
+    const bool next_block = !resident && s + 1 == S && bi + 1 < nblk;
+    const bool next = next_stage || next_block;
+    const int next_s = next_stage ? s + 1 : 0;
     auto dma = [&](int t) {
-      if (next) dma_step(s + 1, buf ^ 1, t);
+      if (next) dma_step(next_s, buf ^ 1, t);
     };
     const half8* tabA = (const half8*)(lds + buf * kFullBufBytes);
     const float* nhA = (const float*)(lds + buf * kFullBufBytes + kFullTabBytes);
@@ -490,6 +521,12 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
     const float M = __uint_as_float((__float_as_uint(A) & 0x7F800000u) + (2u << 23));
     const float bm = 1.5f * M;
 
+    // x is spent for this block: the next block's rows load during the
+    // last stage's search
+    if (s + 1 == S && bi + 1 < nblk) {
+      ra = row_at(bi + 1);
+      load_x(ra, x);
+    }
     const uint32_t best = (s == 0 && !WH) ? full_search<false>(tabA, nhA, bh, bl, bm, lg, j, dma)
                                           : full_search<true>(tabA, nhA, bh, bl, bm, lg, j, dma);
     // the row's winner over the four lane groups (lanes j + 16 lg hold row j)
@@ -542,10 +579,14 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
         }
       }
     }
-    // stage s+1's table has landed and every wave is done with stage s's
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // the table loaded during this stage has landed and every wave is done
+    // with this stage's (the next stage's load goes into its buffer)
+    if (next) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
   }
+  }  // row blocks of the run
 }
 
 int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
@@ -589,7 +630,12 @@ int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
   while (nw > 4 && P * ceil_div(rows, 16 * nw) < 256) nw >>= 1;  // nw in {4, 8}
   if (wh) nw = 4;  // the whitened state (u) needs the registers of one wave per SIMD
   f.row_blocks = ceil_div(rows, 16 * nw);
-  int64_t nblocks = P * f.row_blocks;
+  // runs of row blocks per workgroup: one workgroup per CU's worth of the
+  // problem's blocks (tables loaded once per run; the whitened state keeps
+  // one block per workgroup)
+  f.blocks_per_wg = wh ? 1 : std::max<int64_t>(1, (P * f.row_blocks) / 256);
+  const int64_t wgs_per_p = ceil_div(f.row_blocks, f.blocks_per_wg);
+  int64_t nblocks = P * wgs_per_p;
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
   if (wh)

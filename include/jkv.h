@@ -109,10 +109,20 @@ int jkv_rvq_encode_kv(const void* key_states, const void* value_states, int32_t 
  * is what that call writes, bit for bit.  With fp16 states, d in {4, 8},
  * K = 256 and S <= 2, up to 64 jobs run in one launch (the first workgroups
  * of one job overlap the last of the one before, and each workgroup
- * encodes a longer row range); other geometries run the jobs in turn,
- * sharing `workspace`.  recon is [n_jobs][n_exits] (NULL: no
+ * encodes a longer row range).  Full-vector codebooks (fp16, d = 128,
+ * K = 256, S <= 32, at most two exits) with
+ * jkv_rvq_encode_many_workspace_bytes() of workspace run up to 64 jobs in
+ * one table launch and one search launch.  Other geometries run the jobs in
+ * turn, sharing `workspace`.  recon is [n_jobs][n_exits] (NULL: no
  * reconstructions).
  */
+/* Bytes of workspace jkv_rvq_encode_many needs for n_jobs encodes of this
+ * geometry (no whitener): for full-vector codebooks (d = 128, K = 256,
+ * S <= 32) one table region per job of a launch (up to 64), so that every
+ * job runs in one launch; otherwise what one jkv_rvq_encode needs. */
+int64_t jkv_rvq_encode_many_workspace_bytes(int32_t n_jobs, int64_t H, int64_t G,
+                                            int64_t S, int64_t K, int64_t d);
+
 int jkv_rvq_encode_many(int32_t n_jobs, const void* const* states, int32_t states_dtype,
                         int64_t B, int64_t H, int64_t T, int64_t G, int64_t d,
                         int64_t stride_b, int64_t stride_h, int64_t stride_t,

@@ -835,6 +835,13 @@ int64_t jkv_rvq_encode_workspace_bytes(int64_t H, int64_t G, int64_t S, int64_t 
   return 0;
 }
 
+int64_t jkv_rvq_encode_many_workspace_bytes(int32_t n_jobs, int64_t H, int64_t G, int64_t S, int64_t K,
+                                            int64_t d) {
+  const bool full = d == 128 && K == 256 && S >= 1 && S <= 32;
+  if (full && n_jobs > 1) return std::min<int64_t>(n_jobs, jkv::kMaxManyJobs) * jkv::full_workspace_bytes(H * G, S);
+  return jkv_rvq_encode_workspace_bytes(H, G, S, K, d, 0);
+}
+
 int jkv_rvq_encode(const void* states, int32_t states_dtype, int64_t B, int64_t H,
                    int64_t T, int64_t G, int64_t d, int64_t stride_b, int64_t stride_h,
                    int64_t stride_t, const float* tables, int64_t S, int64_t K,
@@ -1007,6 +1014,22 @@ int jkv_rvq_encode_many(int32_t n_jobs, const void* const* states, int32_t state
     }
     if (grouped) {
       const int rc = launch_grouped_many(batch, n, stream);
+      if (rc != JKV_OK) return rc;
+      continue;
+    }
+    // full-vector codebooks with a workspace region per job: every job's
+    // tables in one launch, every job's search in another
+    bool full = n > 1 && states_dtype == JKV_F16 && d == 128 && K == 256 && S <= 32 && n_exits <= 2 &&
+                workspace != nullptr && ((uintptr_t)workspace) % 16 == 0 &&
+                workspace_bytes >= n * full_workspace_bytes(H * G, S) && stride_b % 8 == 0 && stride_h % 8 == 0 &&
+                stride_t % 8 == 0 && !(n_exits == 2 && exit_depths[0] == exit_depths[1]);
+    for (int i = 0; i < n && full; ++i) {
+      if (((uintptr_t)batch[i].states) % 16 != 0) full = false;
+      for (int e = 0; e < n_exits; ++e)
+        if (batch[i].recon[e] && ((uintptr_t)batch[i].recon[e]) % 16 != 0) full = false;
+    }
+    if (full) {
+      const int rc = launch_full_many(batch, n, workspace, stream);
       if (rc != JKV_OK) return rc;
       continue;
     }

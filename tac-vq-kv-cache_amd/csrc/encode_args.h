@@ -25,6 +25,10 @@ struct EncodeArgs {
 int64_t full_workspace_bytes(int64_t P, int64_t S);
 int64_t full_wh_workspace_bytes(int64_t P, int64_t S);  // with an assignment whitener
 int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream);
+// The same for n <= 64 jobs of one geometry (no whitener, at most two
+// exits) in one table launch and one search launch; `workspace` holds n
+// regions of full_workspace_bytes(P, S).
+int launch_full_many(const EncodeArgs* jobs, int n, void* workspace, hipStream_t stream);
 
 // Grouped encode on MFMA (d in {4, 8}, K = 256, S <= 2, fp16 states): one job
 // is one encode call; a launch runs one or two jobs of the same geometry (a

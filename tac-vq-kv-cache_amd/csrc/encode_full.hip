@@ -64,12 +64,11 @@ int64_t full_wh_workspace_bytes(int64_t P, int64_t S) {
 // converts 8 dims, the 16 lanes of a codeword sum its norm, and the block
 // writes the largest |c|^2 of its 16 codewords (the main kernel folds the 16
 // partial maxima of a stage).
-__global__ __launch_bounds__(256) void full_tables_kernel(const float* __restrict__ masters,
-                                                          _Float16* __restrict__ tab16,
-                                                          float* __restrict__ nhalf,
-                                                          float* __restrict__ ncmax_part) {
-  const int64_t ps = blockIdx.x >> 4;  // (problem, stage)
-  const int part = blockIdx.x & 15;
+__device__ __forceinline__ void full_tables_block(const float* __restrict__ masters, _Float16* __restrict__ tab16,
+                                                  float* __restrict__ nhalf, float* __restrict__ ncmax_part,
+                                                  uint32_t bid) {
+  const int64_t ps = bid >> 4;  // (problem, stage)
+  const int part = bid & 15;
   const int tid = threadIdx.x;
   const int k = part * 16 + (tid >> 4), q = tid & 15;
   const int64_t row = (ps * kFullK + k) * kFullD + 8 * q;
@@ -91,6 +90,44 @@ __global__ __launch_bounds__(256) void full_tables_kernel(const float* __restric
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   if (tid == 0) ncmax_part[ps * 16 + part] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void full_tables_kernel(const float* __restrict__ masters,
+                                                          _Float16* __restrict__ tab16,
+                                                          float* __restrict__ nhalf,
+                                                          float* __restrict__ ncmax_part) {
+  full_tables_block(masters, tab16, nhalf, ncmax_part, blockIdx.x);
+}
+
+// Many encodes of one geometry: job j's tables land in workspace region j
+// (full_workspace_bytes(P, S) each); its blocks are [j P S 16, (j + 1) P S 16).
+static const int kFullMaxJobs = 64;
+struct FullPrepMany {
+  const float* masters[kFullMaxJobs];
+  unsigned char* ws;
+  int64_t ws_stride;
+  int64_t P, S;
+};
+
+// the workspace regions of one job: fp16 tables, -|c|^2/2, partial maxima
+struct FullTables {
+  _Float16* tab16;
+  float* nhalf;
+  float* ncmax;
+};
+__host__ __device__ __forceinline__ FullTables full_tables_at(unsigned char* ws, int64_t P, int64_t S) {
+  FullTables t;
+  t.tab16 = (_Float16*)ws;
+  t.nhalf = (float*)(ws + P * S * (int64_t)kFullTabBytes);
+  t.ncmax = (float*)(ws + P * S * ((int64_t)kFullTabBytes + kFullK * 4));
+  return t;
+}
+
+__global__ __launch_bounds__(256) void full_tables_many_kernel(FullPrepMany m) {
+  const uint32_t per = (uint32_t)(m.P * m.S * 16);
+  const uint32_t job = blockIdx.x / per;
+  const FullTables t = full_tables_at(m.ws + (int64_t)job * m.ws_stride, m.P, m.S);
+  full_tables_block(m.masters[job], t.tab16, t.nhalf, t.ncmax, blockIdx.x - job * per);
 }
 
 // M = W^T W per problem, and M's rows as hi/lo fp16 planes in the order the
@@ -296,9 +333,68 @@ __device__ __forceinline__ uint32_t full_search(const half8* __restrict__ tabA, 
 //   u starts at M x, and each stage subtracts M c of its winner;
 //   |r'|^2 starts at x . u and each stage subtracts 2 c . u and adds |c'|^2
 //   (this only sets the row's binade, never the order within the row).
-template <int NW, bool WH>
-__global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
+// MANY: up to kFullMaxJobs encodes of one geometry (no whitener, at most two
+// exits) in one launch: job j takes logical workgroups [j W, (j + 1) W) and
+// its tables from workspace region j.
+struct FullJobBuffers {
+  const void* states;
+  uint8_t* codes;
+  void* recon[2];  // exits 0 and 1 of the shared exit list
+};
+struct FullManyArgs {
+  FullArgs shape;  // geometry, exits, row blocks and runs (buffers unused)
+  int64_t wgs_per_job;
+  int32_t n_jobs;
+  unsigned char* ws;
+  int64_t ws_stride;
+  FullJobBuffers buf[kFullMaxJobs];
+};
+template <bool MANY> struct FullArgsOf { using type = FullArgs; };
+template <> struct FullArgsOf<true> { using type = FullManyArgs; };
+
+template <int NW, bool WH, bool MANY>
+__global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(typename FullArgsOf<MANY>::type m) {
+  static_assert(!(WH && MANY), "many-job launches carry no whitener");
+  uint32_t L = xcd_remap(blockIdx.x, gridDim.x);
+  const FullArgs* fp;
+  const void* states_v;
+  uint8_t* codes_p;
+  const _Float16* tab16_p;
+  const float* nhalf_p;
+  const float* ncmax_p;
+  void* rec01[2] = {nullptr, nullptr};
+  if constexpr (MANY) {
+    const uint32_t per = (uint32_t)m.wgs_per_job;
+    const uint32_t job = L / per;
+    if (job >= (uint32_t)m.n_jobs) return;  // grid padding (before any barrier)
+    L -= job * per;
+    fp = &m.shape;
+    states_v = m.buf[job].states;
+    codes_p = m.buf[job].codes;
+    rec01[0] = m.buf[job].recon[0];
+    rec01[1] = m.buf[job].recon[1];
+    const FullTables tb = full_tables_at(m.ws + (int64_t)job * m.ws_stride, m.shape.e.H * m.shape.e.G,
+                                         m.shape.e.S);
+    tab16_p = tb.tab16;
+    nhalf_p = tb.nhalf;
+    ncmax_p = tb.ncmax;
+  } else {
+    fp = &m;
+    states_v = m.e.states;
+    codes_p = m.e.codes;
+    tab16_p = m.tab16;
+    nhalf_p = m.nhalf;
+    ncmax_p = m.ncmax;
+  }
+  const FullArgs& f = *fp;
   const EncodeArgs& a = f.e;
+  auto recon_of = [&](int ex) -> void* {
+    if constexpr (MANY) {
+      return ex == 0 ? rec01[0] : rec01[1];
+    } else {
+      return a.recon[ex];
+    }
+  };
   extern __shared__ __align__(16) unsigned char lds[];  // 2 x (table + -|c|^2/2 plane)
   __shared__ float ncm_s[kFullMaxS];
   const int tid = threadIdx.x;
@@ -310,7 +406,6 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   // logical workgroup: a run of consecutive row blocks of one problem (one
   // table set per XCD's L2); with S <= 2 both stage tables stay in LDS for
   // the whole run
-  const uint32_t L = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t P = a.H * a.G;
   const int64_t wgs_per_p = (f.row_blocks + f.blocks_per_wg - 1) / f.blocks_per_wg;
   if ((int64_t)L >= P * wgs_per_p) return;
@@ -336,7 +431,7 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
     return r;
   };
   auto load_x = [&](const RowAt& r, half8 (&x)[4]) {
-    const _Float16* xrow = (const _Float16*)a.states + r.b * a.sb + h * a.sh + r.t * a.st + g * kFullD;
+    const _Float16* xrow = (const _Float16*)states_v + r.b * a.sb + h * a.sh + r.t * a.st + g * kFullD;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) x[kk] = *(const half8*)(xrow + 32 * kk + 8 * lg);
   };
@@ -353,9 +448,9 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   const int rlane = 4 * wave + lg;  // row 4k + lg for i = 0
   const uint32_t lane_off = (uint32_t)(rlane * kFullD + 8 * ((lane & 15) ^ (rlane & 15))) * 2u;
   const __amdgpu_buffer_rsrc_t tab_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(f.tab16 + (int64_t)p * S * kFullTabHalves), (short)0, S * kFullTabBytes, 0x00020000);
+      (void*)(tab16_p + (int64_t)p * S * kFullTabHalves), (short)0, S * kFullTabBytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t plane_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(f.nhalf + (int64_t)p * S * kFullK), (short)0, S * kFullK * 4, 0x00020000);
+      (void*)(nhalf_p + (int64_t)p * S * kFullK), (short)0, S * kFullK * 4, 0x00020000);
   auto dma_load = [&](int s, int buf, int i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         tab_rsrc, (__attribute__((address_space(3))) void*)(lds + buf * kFullBufBytes + (wave + nw * i) * 1024), 16,
@@ -390,7 +485,7 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
           lane_off, (uint32_t)(i * nw * 1024), 0, 0);
   }
   if (tid < S) {
-    const float* part = f.ncmax + ((int64_t)p * S + tid) * 16;
+    const float* part = ncmax_p + ((int64_t)p * S + tid) * 16;
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) m = fmaxf(m, part[i]);
@@ -419,7 +514,7 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
   for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
     for (int e = 0; e < 8; ++e) dec[kk][e] = 0.f;
-  uint8_t* const code_row = a.codes + b * a.cb + h * a.ch + t * a.ct + g * S;
+  uint8_t* const code_row = codes_p + b * a.cb + h * a.ch + t * a.ct + g * S;
   const int64_t out_off = ((b * a.H + h) * a.T + t) * Dfull + g * kFullD;
 
   // whitened state: u in the B-operand layout (dims 32kk + 8lg + e) and |r'|^2
@@ -568,8 +663,8 @@ __global__ __launch_bounds__(64 * NW) void rvq_encode_full_kernel(FullArgs f) {
     }
     if (valid) {
       for (int ex = 0; ex < a.n_exits; ++ex) {
-        if (a.exit_depth[ex] != s + 1 || a.recon[ex] == nullptr) continue;
-        _Float16* op = (_Float16*)a.recon[ex] + out_off;
+        if (a.exit_depth[ex] != s + 1 || recon_of(ex) == nullptr) continue;
+        _Float16* op = (_Float16*)recon_of(ex) + out_off;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           half8 o;
@@ -639,14 +734,67 @@ int launch_full(const EncodeArgs& a, void* workspace, hipStream_t stream) {
   if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
   JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
   if (wh)
-    hipLaunchKernelGGL((rvq_encode_full_kernel<4, true>), dim3((uint32_t)nblocks), dim3(64 * 4),
+    hipLaunchKernelGGL((rvq_encode_full_kernel<4, true, false>), dim3((uint32_t)nblocks), dim3(64 * 4),
                        2 * kFullBufBytes, stream, f);
   else if (nw == 8)
-    hipLaunchKernelGGL((rvq_encode_full_kernel<8, false>), dim3((uint32_t)nblocks), dim3(64 * 8),
+    hipLaunchKernelGGL((rvq_encode_full_kernel<8, false, false>), dim3((uint32_t)nblocks), dim3(64 * 8),
                        2 * kFullBufBytes, stream, f);
   else
-    hipLaunchKernelGGL((rvq_encode_full_kernel<4, false>), dim3((uint32_t)nblocks), dim3(64 * 4),
+    hipLaunchKernelGGL((rvq_encode_full_kernel<4, false, false>), dim3((uint32_t)nblocks), dim3(64 * 4),
                        2 * kFullBufBytes, stream, f);
+  JKV_CHECK_LAUNCH();
+  return JKV_OK;
+}
+
+// Many full-vector encodes of one geometry in two launches (every job's
+// tables, then every job's search): jobs share everything but their
+// buffers; no whitener; at most two exits; `workspace` holds n regions of
+// full_workspace_bytes(P, S).
+int launch_full_many(const EncodeArgs* jobs, int n, void* workspace, hipStream_t stream) {
+  JKV_CHECK_ARG(n >= 1 && n <= kFullMaxJobs, "1 to %d jobs per launch", kFullMaxJobs);
+  const EncodeArgs& a = jobs[0];
+  JKV_CHECK_ARG(a.n_exits <= 2 && a.whiteners == nullptr, "many-job full-vector launches take at most two exits");
+  const int64_t P = a.H * a.G;
+  const int64_t S = a.S;
+  const int64_t stride = full_workspace_bytes(P, S);
+  unsigned char* ws = (unsigned char*)workspace;
+  FullPrepMany pm = {};
+  for (int j = 0; j < n; ++j) pm.masters[j] = jobs[j].tables;
+  pm.ws = ws;
+  pm.ws_stride = stride;
+  pm.P = P;
+  pm.S = S;
+  JKV_CHECK_ARG(n * P * S * 16 < ((int64_t)1 << 31), "too many (problem, stage) tables");
+  hipLaunchKernelGGL(full_tables_many_kernel, dim3((uint32_t)(n * P * S * 16)), dim3(256), 0, stream, pm);
+  JKV_CHECK_LAUNCH();
+
+  FullManyArgs m = {};
+  m.shape.e = a;
+  const int64_t rows = a.B * a.T;
+  int nw = kFullMaxWaves;
+  while (nw > 4 && n * P * ceil_div(rows, 16 * nw) < 256) nw >>= 1;  // nw in {4, 8}
+  m.shape.row_blocks = ceil_div(rows, 16 * nw);
+  // runs as long as the jobs leave two rounds of workgroups, within a problem
+  m.shape.blocks_per_wg =
+      std::min<int64_t>(m.shape.row_blocks, std::max<int64_t>(1, (n * P * m.shape.row_blocks) / 512));
+  m.wgs_per_job = P * ceil_div(m.shape.row_blocks, m.shape.blocks_per_wg);
+  m.n_jobs = n;
+  m.ws = ws;
+  m.ws_stride = stride;
+  for (int j = 0; j < n; ++j) {
+    m.buf[j].states = jobs[j].states;
+    m.buf[j].codes = jobs[j].codes;
+    for (int e = 0; e < a.n_exits; ++e) m.buf[j].recon[e] = jobs[j].recon[e];
+  }
+  int64_t nblocks = n * m.wgs_per_job;
+  if (nblocks > 8) nblocks = ceil_div(nblocks, 8) * 8;  // xcd_remap needs a multiple of 8
+  JKV_CHECK_ARG(nblocks < ((int64_t)1 << 31), "grid too large");
+  if (nw == 8)
+    hipLaunchKernelGGL((rvq_encode_full_kernel<8, false, true>), dim3((uint32_t)nblocks), dim3(64 * 8),
+                       2 * kFullBufBytes, stream, m);
+  else
+    hipLaunchKernelGGL((rvq_encode_full_kernel<4, false, true>), dim3((uint32_t)nblocks), dim3(64 * 4),
+                       2 * kFullBufBytes, stream, m);
   JKV_CHECK_LAUNCH();
   return JKV_OK;
 }

@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp,
          _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _vp],
     ),
+    "jkv_rvq_encode_many_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64]),
     "jkv_rvq_encode_many": (
         ctypes.c_int,
         [_i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp,

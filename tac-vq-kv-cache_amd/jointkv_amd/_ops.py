@@ -192,7 +192,7 @@ def rvq_encode_many(
     r0, rstep, estep = recon_all.data_ptr(), recon_all.stride(0) * recon_all.element_size(), \
         recon_all.stride(1) * recon_all.element_size()
     lib = _lib.load()
-    ws_bytes = int(lib.jkv_rvq_encode_workspace_bytes(heads, groups, stages, clusters, d, 0))
+    ws_bytes = int(lib.jkv_rvq_encode_many_workspace_bytes(n, heads, groups, stages, clusters, d))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
     code = lib.jkv_rvq_encode_many(
         n, _lib.ptr_array(ctypes.c_void_p, [x.data_ptr() for x in xs]), _lib.dtype_code(xdtype),

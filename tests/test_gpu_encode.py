@@ -291,7 +291,10 @@ def test_encode_kv_equals_two_encodes(device, batch, tokens, groups, dim, stages
     (2, 1, 4500, 16, 8, 2, torch.float16, (2,), 70),
     (8, 16, 1, 32, 4, 1, torch.float16, (1,), 4),       # cq2, one token per sequence
     (8, 1, 70, 16, 8, 2, torch.float32, (2,), 3),       # fp32 states: the encodes in turn
-    (8, 1, 40, 1, 128, 4, torch.float16, (2, 4), 2),    # full-vector tables: in turn, shared workspace
+    (8, 1, 40, 1, 128, 4, torch.float16, (2, 4), 2),    # full-vector tables: one table launch, one search launch
+    (8, 2, 300, 1, 128, 2, torch.float16, (1, 2), 5),    # full-vector, config-3-like: both tables kept for a run
+    (8, 1, 700, 1, 128, 16, torch.float16, (8, 16), 3),  # full-vector, 16 stages streamed through a run
+    (8, 1, 50, 1, 128, 4, torch.float16, (1, 2, 4), 2),  # full-vector with three exits: one encode per job
 ])
 def test_encode_many_equals_per_job_encodes(device, heads, batch, tokens, groups, dim, stages, dtype, exits, jobs):
     from jointkv_amd import _ops
@@ -379,3 +382,20 @@ def test_encode_many_strided_views_and_geometry_errors(device):
         _ops.rvq_encode_many([states[0], states[1][:, :, :200]], tables[:2], groups=16, group_dim=8, exits=(2,))
     with pytest.raises(ValueError):
         _ops.rvq_encode_many(states[:2], tables[:1], groups=16, group_dim=8, exits=(2,))
+
+
+def test_encode_many_full_vector_config3_literal_equals_per_tensor(device):
+    # config 3 read as two full-vector stages at full size: 64 tensors
+    # [4,8,2048,128] with tables [8,2,256,128] in one call, against each
+    # tensor's own encode (itself checked against the oracle), bit for bit
+    from jointkv_amd import _ops
+
+    print("encode_many full-vector config 3 (64 x [4,8,2048,128], S = 2)", flush=True)
+    gen = torch.Generator(device=device).manual_seed(8602)
+    states = [torch.randn(4, 8, 2048, 128, generator=gen, device=device).half() for _ in range(64)]
+    tables = [(torch.randn(8, 2, 256, 128, generator=gen, device=device)
+               * torch.tensor([1.0, 0.5], device=device)[None, :, None, None]).half().float() for _ in range(64)]
+    out = _ops.rvq_encode_many(states, tables, groups=1, group_dim=128, exits=(2,))
+    for j in range(64):
+        recon, codes = _ops.rvq_encode(states[j], tables[j], groups=1, group_dim=128, exits=(2,))
+        assert torch.equal(out[j][1], codes) and torch.equal(out[j][0][0], recon[0]), f"tensor {j}"

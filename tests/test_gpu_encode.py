@@ -295,6 +295,7 @@ def test_encode_kv_equals_two_encodes(device, batch, tokens, groups, dim, stages
     (8, 2, 300, 1, 128, 2, torch.float16, (1, 2), 5),    # full-vector, config-3-like: both tables kept for a run
     (8, 1, 700, 1, 128, 16, torch.float16, (8, 16), 3),  # full-vector, 16 stages streamed through a run
     (8, 1, 50, 1, 128, 4, torch.float16, (1, 2, 4), 2),  # full-vector with three exits: one encode per job
+    (2, 1, 40, 1, 128, 2, torch.float16, (2,), 66),     # full-vector, 64 + 2 jobs: the workspace regions reused
 ])
 def test_encode_many_equals_per_job_encodes(device, heads, batch, tokens, groups, dim, stages, dtype, exits, jobs):
     from jointkv_amd import _ops

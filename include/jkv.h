@@ -146,6 +146,17 @@ int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b,
                    const float* tables, int64_t S, int64_t K, int32_t depth,
                    void* out, int32_t out_dtype, jkv_stream_t stream);
 
+/* jkv_rvq_decode with the tables given as their fp16 deployed words
+ * (fp16(masters), [H*G,S,K,d], e.g. jkv_f32_to_f16 output or a codec's
+ * deployed tables): out = dtype( sum_{s<depth} fp32(tables16[h*G+g, s,
+ * code]) ), the same bits as jkv_rvq_decode on the masters, reading half the
+ * table bytes. */
+int jkv_rvq_decode_f16(const uint8_t* codes, int64_t code_stride_b,
+                       int64_t code_stride_h, int64_t code_stride_t, int64_t B,
+                       int64_t H, int64_t T, int64_t G, int64_t d,
+                       const void* tables16, int64_t S, int64_t K, int32_t depth,
+                       void* out, int32_t out_dtype, jkv_stream_t stream);
+
 /* Bytes of device workspace jkv_rvq_scatter_grad needs for this geometry,
  * gradient dtype and determinism request. */
 int64_t jkv_rvq_scatter_workspace_bytes(int64_t B, int64_t H, int64_t T,

@@ -8,7 +8,7 @@ struct RvqDecodeArgs {
   int64_t cb, ch, ct;  // code byte strides (b, h, t); the (G,S) block contiguous
   int64_t BH, H;
   int32_t T, G, d, S, K, depth;
-  const float* tables;  // [H*G][S][K][d] fp32 masters
+  const void* tables;   // [H*G][S][K][d]: fp32 masters, or their fp16 deployed words
   void* out;            // [B,H,T,G*d] contiguous
 };
 
@@ -38,8 +38,9 @@ __device__ __forceinline__ void store_chunk(void* out, int64_t i, const float* v
 // order and stored as CW consecutive outputs:
 //   out[b,h,t,g*d+i] = dtype( sum_{s<depth} fp32(fp16(C[h*G+g, s, code_s, i])) ).
 // Grid: x over the (row, group) items of one (batch, head) slice, y over the
-// slices.
-template <int DT, int CW>
+// slices.  F16: the tables are already the fp16 deployed words (half the
+// bytes per codeword read; the same sums).
+template <int DT, int CW, bool F16>
 __global__ __launch_bounds__(256) void rvq_decode_kernel(RvqDecodeArgs a) {
   const uint32_t item = blockIdx.x * 256u + threadIdx.x;
   const uint32_t n = (uint32_t)a.T * (uint32_t)a.G;
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(256) void rvq_decode_kernel(RvqDecodeArgs a) {
   for (int64_t bh = blockIdx.y; bh < a.BH; bh += gridDim.y) {
     const int64_t b = bh / a.H, h = bh % a.H;
     const uint8_t* cp = a.codes + b * a.cb + h * a.ch + t * a.ct + g * a.S;
-    const float* tab = a.tables + (h * a.G + g) * (int64_t)a.S * a.K * a.d;
+    const int64_t tab0 = (h * a.G + g) * (int64_t)a.S * a.K * a.d;
     const int64_t o = (bh * a.T + t) * D + (int64_t)g * a.d;
     const int depth = a.depth;
     for (int i = 0; i < a.d; i += CW) {
@@ -57,7 +58,15 @@ __global__ __launch_bounds__(256) void rvq_decode_kernel(RvqDecodeArgs a) {
 #pragma unroll
       for (int e = 0; e < CW; ++e) acc[e] = 0.f;
       for (int s = 0; s < depth; ++s) {
-        const float* w = tab + ((int64_t)s * a.K + cp[s]) * a.d + i;
+        const int64_t wo = tab0 + ((int64_t)s * a.K + cp[s]) * a.d + i;
+        if constexpr (F16) {
+          typedef _Float16 hv __attribute__((ext_vector_type(CW)));
+          const hv w = *((const hv*)((const _Float16*)a.tables + wo));
+#pragma unroll
+          for (int e = 0; e < CW; ++e) acc[e] += (float)w[e];
+          continue;
+        }
+        const float* w = (const float*)a.tables + wo;
         if constexpr (CW == 1) {
           acc[0] += deploy16(w[0]);
         } else {
@@ -76,23 +85,21 @@ __global__ __launch_bounds__(256) void rvq_decode_kernel(RvqDecodeArgs a) {
   }
 }
 
-template <int DT>
+template <int DT, bool F16>
 static void launch_decode(const RvqDecodeArgs& a, int cw, dim3 grid, hipStream_t stream) {
   if (cw == 8) {
-    hipLaunchKernelGGL((rvq_decode_kernel<DT, 8>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((rvq_decode_kernel<DT, 8, F16>), grid, dim3(256), 0, stream, a);
   } else if (cw == 4) {
-    hipLaunchKernelGGL((rvq_decode_kernel<DT, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((rvq_decode_kernel<DT, 4, F16>), grid, dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((rvq_decode_kernel<DT, 1>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((rvq_decode_kernel<DT, 1, F16>), grid, dim3(256), 0, stream, a);
   }
 }
 
-}  // namespace jkv
-
-extern "C" int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b, int64_t code_stride_h,
-                              int64_t code_stride_t, int64_t B, int64_t H, int64_t T, int64_t G,
-                              int64_t d, const float* tables, int64_t S, int64_t K, int32_t depth,
-                              void* out, int32_t out_dtype, jkv_stream_t stream_) {
+static int rvq_decode_impl(const uint8_t* codes, int64_t code_stride_b, int64_t code_stride_h,
+                           int64_t code_stride_t, int64_t B, int64_t H, int64_t T, int64_t G, int64_t d,
+                           const void* tables, bool tables_f16, int64_t S, int64_t K, int32_t depth, void* out,
+                           int32_t out_dtype, jkv_stream_t stream_) {
   using namespace jkv;
   hipStream_t stream = (hipStream_t)stream_;
   JKV_CHECK_ARG(B >= 0 && H > 0 && T >= 0 && G > 0 && d > 0 && S > 0 && K > 0 && K <= 256,
@@ -114,16 +121,41 @@ extern "C" int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b, int64
   // (fp32 rows) and the output chunk is aligned to its own width
   const size_t esize = out_dtype == JKV_F32 ? 4 : 2;
   auto aligned = [&](int cw) {
-    return d % cw == 0 && (uintptr_t)tables % 16 == 0 && (uintptr_t)out % (cw * esize) == 0;
+    const uintptr_t tab_align = tables_f16 ? (uintptr_t)(cw * 2) : 16u;
+    return d % cw == 0 && (uintptr_t)tables % tab_align == 0 && (uintptr_t)out % (cw * esize) == 0;
   };
   const int cw = aligned(8) ? 8 : aligned(4) ? 4 : 1;
   const int64_t slices = B * H;
   const dim3 grid((uint32_t)ceil_div(T * G, 256), (uint32_t)(slices < 65535 ? slices : 65535));
   switch (out_dtype) {
-    case JKV_F16: launch_decode<JKV_F16>(a, cw, grid, stream); break;
-    case JKV_BF16: launch_decode<JKV_BF16>(a, cw, grid, stream); break;
-    default: launch_decode<JKV_F32>(a, cw, grid, stream); break;
+    case JKV_F16:
+      tables_f16 ? launch_decode<JKV_F16, true>(a, cw, grid, stream) : launch_decode<JKV_F16, false>(a, cw, grid, stream);
+      break;
+    case JKV_BF16:
+      tables_f16 ? launch_decode<JKV_BF16, true>(a, cw, grid, stream) : launch_decode<JKV_BF16, false>(a, cw, grid, stream);
+      break;
+    default:
+      tables_f16 ? launch_decode<JKV_F32, true>(a, cw, grid, stream) : launch_decode<JKV_F32, false>(a, cw, grid, stream);
+      break;
   }
   JKV_CHECK_LAUNCH();
   return JKV_OK;
+}
+
+}  // namespace jkv
+
+extern "C" int jkv_rvq_decode(const uint8_t* codes, int64_t code_stride_b, int64_t code_stride_h,
+                              int64_t code_stride_t, int64_t B, int64_t H, int64_t T, int64_t G,
+                              int64_t d, const float* tables, int64_t S, int64_t K, int32_t depth,
+                              void* out, int32_t out_dtype, jkv_stream_t stream) {
+  return jkv::rvq_decode_impl(codes, code_stride_b, code_stride_h, code_stride_t, B, H, T, G, d, tables, false, S,
+                              K, depth, out, out_dtype, stream);
+}
+
+extern "C" int jkv_rvq_decode_f16(const uint8_t* codes, int64_t code_stride_b, int64_t code_stride_h,
+                                  int64_t code_stride_t, int64_t B, int64_t H, int64_t T, int64_t G,
+                                  int64_t d, const void* tables16, int64_t S, int64_t K, int32_t depth,
+                                  void* out, int32_t out_dtype, jkv_stream_t stream) {
+  return jkv::rvq_decode_impl(codes, code_stride_b, code_stride_h, code_stride_t, B, H, T, G, d, tables16, true,
+                              S, K, depth, out, out_dtype, stream);
 }

@@ -60,6 +60,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i32,
          _vp],
     ),
+    "jkv_rvq_decode_f16": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i32,
+         _vp],
+    ),
     "jkv_rvq_scatter_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32]),
     "jkv_rvq_scatter_grad": (
         ctypes.c_int,

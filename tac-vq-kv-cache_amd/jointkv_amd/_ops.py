@@ -307,7 +307,9 @@ def rvq_decode(
     depth: int,
     dtype: torch.dtype,
 ) -> torch.Tensor:
-    """``codes[B,H,T,G,S]`` + fp32 masters ``tables[H*G,S,K,d]`` -> ``[B,H,T,G*d]``."""
+    """``codes[B,H,T,G,S]`` + fp32 masters ``tables[H*G,S,K,d]`` -> ``[B,H,T,G*d]``.
+    fp16 ``tables`` are taken as the deployed words (``fp16(masters)``): the
+    same result, half the table bytes read."""
 
     device = _lib.require_device(codes, tables)
     batch, heads, tokens, groups, stages = map(int, codes.shape)
@@ -317,10 +319,15 @@ def rvq_decode(
     if codes.dtype != torch.uint8 or codes.stride(-1) != 1 or codes.stride(-2) != stages:
         raise ValueError("codes must be uint8 with a contiguous (G,S) block")
     tables = tables.detach()
-    if tables.dtype != torch.float32 or not tables.is_contiguous():
+    lib = _lib.load()
+    entry = lib.jkv_rvq_decode
+    if tables.dtype == torch.float16:
+        entry = lib.jkv_rvq_decode_f16
+        tables = tables.contiguous()
+    elif tables.dtype != torch.float32 or not tables.is_contiguous():
         tables = tables.float().contiguous()
     out = torch.empty((batch, heads, tokens, groups * d), dtype=dtype, device=device)
-    code = _lib.load().jkv_rvq_decode(
+    code = entry(
         codes.data_ptr(), codes.stride(0), codes.stride(1), codes.stride(2),
         batch, heads, tokens, groups, d, tables.data_ptr(), stages, clusters, int(depth),
         out.data_ptr(), _lib.dtype_code(dtype), _lib.stream_handle(device),

@@ -233,8 +233,8 @@ def prefill_attention_from_codes(
         return _ops.prefill_attention_codes(query, key_codes, value_codes, key_tables16, value_tables16, starts,
                                             window=window, rope_theta=rope_theta, max_position=top)
     stages = int(key_codes.shape[-1])
-    khat = _ops.rvq_decode(key_codes, key_tables16.float(), depth=stages, dtype=torch.float16)
-    vhat = _ops.rvq_decode(value_codes, value_tables16.float(), depth=stages, dtype=torch.float16)
+    khat = _ops.rvq_decode(key_codes, key_tables16, depth=stages, dtype=torch.float16)
+    vhat = _ops.rvq_decode(value_codes, value_tables16, depth=stages, dtype=torch.float16)
     return prefill_attention(query, khat, vhat, start_positions, window=window, rope_theta=rope_theta)
 
 

@@ -400,3 +400,23 @@ def test_encode_many_full_vector_config3_literal_equals_per_tensor(device):
     for j in range(64):
         recon, codes = _ops.rvq_encode(states[j], tables[j], groups=1, group_dim=128, exits=(2,))
         assert torch.equal(out[j][1], codes) and torch.equal(out[j][0][0], recon[0]), f"tensor {j}"
+
+
+@pytest.mark.parametrize("groups,d,stages,depth,dtype", [
+    (16, 8, 2, 2, torch.float16),     # the GSRQ-2 cache geometry (8-element chunks)
+    (32, 4, 1, 1, torch.float16),     # grouped CQ (4-element chunks)
+    (1, 128, 4, 3, torch.float32),    # full-vector, fp32 out
+    (4, 6, 2, 2, torch.bfloat16),     # d = 6: element-wise
+])
+def test_rvq_decode_from_fp16_tables_equals_masters(device, groups, d, stages, depth, dtype):
+    # the deployed fp16 words give the same reconstruction as the fp32 masters
+    # (which the kernel rounds to fp16 itself), bit for bit
+    from jointkv_amd import _ops
+
+    gen = torch.Generator(device=device).manual_seed(3300 + groups + d)
+    codes = torch.randint(0, 256, (2, 8, 77, groups, stages), generator=gen, device=device,
+                          dtype=torch.int32).to(torch.uint8)
+    masters = torch.randn(8 * groups, stages, 256, d, generator=gen, device=device)
+    a = _ops.rvq_decode(codes, masters, depth=depth, dtype=dtype)
+    b = _ops.rvq_decode(codes, masters.half(), depth=depth, dtype=dtype)
+    assert torch.equal(a, b)

@@ -420,3 +420,22 @@ def test_rvq_decode_from_fp16_tables_equals_masters(device, groups, d, stages, d
     a = _ops.rvq_decode(codes, masters, depth=depth, dtype=dtype)
     b = _ops.rvq_decode(codes, masters.half(), depth=depth, dtype=dtype)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("groups,stages,depth,tables_f16,dtype", [
+    (16, 2, 2, False, torch.float16),   # GSRQ-2 masters: two 512-token runs and a ragged third
+    (16, 2, 1, True, torch.float32),    # deployed fp16 words, first stage only
+    (32, 1, 1, True, torch.bfloat16),   # grouped CQ's 32 x 8 cell (G S = 32)
+])
+def test_rvq_decode_lds_runs_match_oracle(device, groups, stages, depth, tables_f16, dtype):
+    # 8-dim groups rebuild from tables staged in LDS, 512 tokens per
+    # workgroup: bit for bit against the oracle over several runs per head
+    gen = _gen(6161 + groups + stages)
+    batch, heads, tokens = 2, 3, 1100
+    tables = ref.synthetic_tables(gen, (heads * groups, stages, 256, 8), (1.0, 0.5)[:stages], stage_axis=1)
+    tables = tables + 1e-3 * torch.randn(tables.shape, generator=gen)
+    codes = torch.randint(0, 256, (batch, heads, tokens, groups, stages), generator=gen, dtype=torch.uint8)
+    given = tables.half() if tables_f16 else tables
+    got = jkv.closed_loop_vq._ops.rvq_decode(codes.to(device), given.to(device), depth=depth, dtype=dtype)
+    want = ref.frozen_decode(codes, tables, depth, dtype)
+    assert torch.equal(got.cpu(), want)

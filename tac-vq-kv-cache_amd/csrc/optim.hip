@@ -5,6 +5,9 @@
 namespace jkv {
 
 static const int kMaxTensors = 64;
+#ifndef JKV_SUMSQ_EPT
+#define JKV_SUMSQ_EPT 64
+#endif
 
 struct SumsqArgs {
   const float* buf[kMaxTensors];
@@ -19,12 +22,31 @@ __global__ __launch_bounds__(256) void sumsq_kernel(SumsqArgs a) {
   const int part = blockIdx.x % a.blocks_per_tensor;
   const float* __restrict__ x = a.buf[tensor];
   const int64_t n = a.numel[tensor];
-  double acc = 0.0;
-  for (int64_t i = (int64_t)part * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)a.blocks_per_tensor * blockDim.x) {
-    const double v = x[i];
-    acc = fma(v, v, acc);
+  const int64_t stride = (int64_t)a.blocks_per_tensor * blockDim.x;
+  // 16-byte loads over the aligned body, four in flight per thread, two fp64
+  // chains; the tail one by one
+  const int64_t n4 = ((uintptr_t)x % 16 == 0) ? n / 4 : 0;
+  double acc0 = 0.0, acc1 = 0.0;
+  for (int64_t i = (int64_t)part * blockDim.x + threadIdx.x; i < n4; i += 4 * stride) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = i + u * stride;
+      v[u] = j < n4 ? ((const float4*)x)[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc0 = fma((double)v[u].x, (double)v[u].x, acc0);
+      acc1 = fma((double)v[u].y, (double)v[u].y, acc1);
+      acc0 = fma((double)v[u].z, (double)v[u].z, acc0);
+      acc1 = fma((double)v[u].w, (double)v[u].w, acc1);
+    }
   }
+  for (int64_t i = 4 * n4 + (int64_t)part * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const double v = x[i];
+    acc0 = fma(v, v, acc0);
+  }
+  double acc = acc0 + acc1;
   // block reduction
   __shared__ double red[4];
 #pragma unroll
@@ -39,7 +61,7 @@ __global__ __launch_bounds__(256) void sumsq_kernel(SumsqArgs a) {
 }
 
 __global__ void zero_f64_kernel(double* out, int n) {
-  int i = threadIdx.x;
+  const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) out[i] = 0.0;
 }
 
@@ -59,8 +81,27 @@ __global__ __launch_bounds__(256) void scale_sgd_kernel(ScaleSgdArgs a) {
   float* __restrict__ p = a.param[tensor];
   const float sc = a.scale[tensor];
   const int64_t n = a.numel[tensor];
-  for (int64_t i = (int64_t)part * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)a.blocks_per_tensor * blockDim.x) {
+  const int64_t stride = (int64_t)a.blocks_per_tensor * blockDim.x;
+  // 16-byte accesses over the aligned body (the same per-element arithmetic)
+  const bool vec = (uintptr_t)g % 16 == 0 && (a.lr == 0.f || (uintptr_t)p % 16 == 0);
+  const int64_t n4 = vec ? n / 4 : 0;
+  for (int64_t i = (int64_t)part * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 gv = ((const float4*)g)[i];
+    gv.x *= sc;
+    gv.y *= sc;
+    gv.z *= sc;
+    gv.w *= sc;
+    ((float4*)g)[i] = gv;
+    if (a.lr != 0.f) {
+      float4 pv = ((const float4*)p)[i];
+      pv.x = pv.x + (-a.lr) * gv.x;
+      pv.y = pv.y + (-a.lr) * gv.y;
+      pv.z = pv.z + (-a.lr) * gv.z;
+      pv.w = pv.w + (-a.lr) * gv.w;
+      ((float4*)p)[i] = pv;
+    }
+  }
+  for (int64_t i = 4 * n4 + (int64_t)part * blockDim.x + threadIdx.x; i < n; i += stride) {
     const float gv = g[i] * sc;
     g[i] = gv;
     if (a.lr != 0.f) p[i] = p[i] + (-a.lr) * gv;
@@ -78,7 +119,7 @@ int jkv_sumsq(int32_t n, const float* const* buffers, const int64_t* numels, dou
   JKV_CHECK_ARG(n >= 0, "negative tensor count");
   if (n == 0) return JKV_OK;
   JKV_CHECK_ARG(out_sumsq != nullptr && buffers != nullptr && numels != nullptr, "null buffer");
-  hipLaunchKernelGGL(zero_f64_kernel, dim3(1), dim3(256), 0, stream, out_sumsq, n);
+  hipLaunchKernelGGL(zero_f64_kernel, dim3((uint32_t)ceil_div(n, 256)), dim3(256), 0, stream, out_sumsq, n);
   JKV_CHECK_LAUNCH();
   for (int32_t base = 0; base < n; base += kMaxTensors) {
     SumsqArgs a = {};
@@ -92,7 +133,7 @@ int jkv_sumsq(int32_t n, const float* const* buffers, const int64_t* numels, dou
       if (a.numel[i] > maxn) maxn = a.numel[i];
     }
     a.out = out_sumsq + base;
-    int64_t bpt = ceil_div(maxn, 256 * 16);
+    int64_t bpt = ceil_div(maxn, 256 * JKV_SUMSQ_EPT);  // elements per thread
     if (bpt < 1) bpt = 1;
     if (bpt > 256) bpt = 256;
     a.blocks_per_tensor = (int32_t)bpt;

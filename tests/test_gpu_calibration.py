@@ -107,6 +107,35 @@ def test_sgd_step_matches_torch_sgd(device):
         torch.testing.assert_close(p.detach(), q.detach(), rtol=1e-6, atol=1e-7)
 
 
+def test_norms_and_scaled_sgd_on_many_ragged_tensors(device):
+    """Over 256 tensors (more than one launch's table), sizes 0 to a few
+    thousand that are not multiples of 4, and views 4 bytes off a 16-byte
+    boundary: the vector bodies, the scalar tails and the zeroing of every
+    output slot."""
+    from jointkv_amd import _ops
+
+    gen = torch.Generator().manual_seed(77)
+    sizes = [0, 1, 3, 4, 5, 7, 4099, 70001] + [int(torch.randint(0, 3000, (1,), generator=gen)) for _ in range(292)]
+    grads, params, cpu_g, cpu_p = [], [], [], []
+    for i, n in enumerate(sizes):
+        off = i % 2
+        g = torch.randn(n + off, generator=gen)
+        q = torch.randn(n + off, generator=gen)
+        grads.append(g.to(device)[off:])
+        params.append(q.to(device)[off:])
+        cpu_g.append(g[off:].double())
+        cpu_p.append(q[off:])
+    norms = _ops.sumsq(grads).cpu()
+    expect = torch.stack([(g * g).sum() for g in cpu_g])
+    torch.testing.assert_close(norms, expect, rtol=1e-12, atol=1e-12)
+    scales = [0.5 + 0.001 * i for i in range(len(sizes))]
+    _ops.scale_sgd(grads, scales, params=params, lr=0.01)
+    for g, q, g0, q0, sc in zip(grads, params, cpu_g, cpu_p, scales):
+        gs = g0.float() * sc
+        torch.testing.assert_close(g.cpu(), gs, rtol=0, atol=0)
+        torch.testing.assert_close(q.cpu(), q0 - 0.01 * gs, rtol=1e-6, atol=1e-7)
+
+
 def test_uniform_codec_equals_direct_call_and_v_only_step(device):
     # tests/test_pure_uniform16_closed_loop_vq.py:308-336 relation, on the
     # grouped G2 geometry, then one V-only calibration step (config 5 order:

@@ -1066,18 +1066,38 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return min(min(r0, r1), min(r2, r3));
 }
 
-// Greedy residual search of one raw fp16 head vector over the kv head's
-// fp16 tables in LDS ([16][S][256][8], 4 KiB per (group, stage)): wave w
-// takes groups 2w and 2w + 1, lane l codewords l, l + 64, l + 128, l + 192.
+// What lane l of wave w needs to encode the appended token x: its groups
+// 2w and 2w + 1 of x and their codewords l, l + 64, l + 128, l + 192 of
+// every stage, from the kv head's fp16 tables ([16][S][256][8], 4 KiB per
+// (group, stage)) in global memory or LDS.  The K search reads them from
+// global memory before the tables' direct-to-LDS copy is issued, so that it
+// runs while the copy is in flight (a load issued after the copy would wait
+// for all of it).
+template <int S>
+__device__ __forceinline__ void fetch_new_token_words(const unsigned char* gtab, const _Float16* x, int wave,
+                                                      int lane, half8 (&xv)[2], half8 (&cw)[S][2][4]) {
+  xv[0] = *(const half8*)(x + 16 * wave);
+  xv[1] = *(const half8*)(x + 16 * wave + 8);
+#pragma unroll
+  for (int st = 0; st < S; ++st)
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        cw[st][gi][j] = *(const half8*)(gtab + ((2 * wave + gi) * S + st) * kG8Plane + (lane + 64 * j) * 16);
+}
+
+// Greedy residual search of one raw fp16 head vector over those codewords.
 // Stage s scores ||c||^2 - 2 r.c, the reference's expanded distance
 // ||r||^2 + ||c||^2 - 2 r.c less the row's constant ||r||^2, with r the
 // residual x - c_1 - ... taken in its exact split x.c - c_1.c - ...: every
 // product is fp16 x fp16 into an fp32 v_dot2 sum.  Keys keep the score's
 // order-preserving bits with the index in the low byte, so the lowest score
-// wins and, within 2^-16 of it, the lowest index.  The code record [16][S]
-// goes to rec (LDS) and out (global).
+// wins and, within 2^-16 of it, the lowest index.  The chosen codeword of a
+// stage comes from the lane that holds it.  The code record [16][S] goes to
+// rec (LDS) and out (global).
 template <int S>
-__device__ __forceinline__ void encode_new_token(const unsigned char* tab, const _Float16* x, uint8_t* rec,
+__device__ __forceinline__ void encode_new_token(const half8 (&xv)[2], const half8 (&cw)[S][2][4], uint8_t* rec,
                                                  uint8_t* out, int wave, int lane) {
   auto dot8 = [](half8 p, half8 q, float acc) {
 #pragma unroll
@@ -1087,7 +1107,6 @@ __device__ __forceinline__ void encode_new_token(const unsigned char* tab, const
     }
     return acc;
   };
-  const half8 xv[2] = {*(const half8*)(x + 16 * wave), *(const half8*)(x + 16 * wave + 8)};
   half8 negc[2][S];  // negated words of the stages chosen so far
 #pragma unroll
   for (int st = 0; st < S; ++st) {
@@ -1097,8 +1116,7 @@ __device__ __forceinline__ void encode_new_token(const unsigned char* tab, const
       const int k = lane + 64 * j;
 #pragma unroll
       for (int gi = 0; gi < 2; ++gi) {
-        const int g = 2 * wave + gi;
-        const half8 c = *(const half8*)(tab + (g * S + st) * kG8Plane + k * 16);
+        const half8 c = cw[st][gi][j];
         float rc = dot8(xv[gi], c, 0.f);
 #pragma unroll
         for (int p = 0; p < st; ++p) rc = dot8(negc[gi][p], c, rc);
@@ -1114,10 +1132,24 @@ __device__ __forceinline__ void encode_new_token(const unsigned char* tab, const
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       const int g = 2 * wave + gi;
-      const int code = (int)(best[gi] & 0xffu);
-      const uint4 w = *(const uint4*)(tab + (g * S + st) * kG8Plane + code * 16);
-      negc[gi][st] = __builtin_bit_cast(half8, uint4{w.x ^ 0x80008000u, w.y ^ 0x80008000u, w.z ^ 0x80008000u,
-                                                     w.w ^ 0x80008000u});
+      const int code = (int)(best[gi] & 0xffu);  // wave-uniform
+      if (st + 1 < S) {
+        // codeword `code` is slot code >> 6 of lane code & 63: read every
+        // slot of that lane, then pick (register arrays stay static-indexed)
+        const int jj = code >> 6, src = code & 63;
+        uint4 w = uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 m = __builtin_bit_cast(uint4, cw[st][gi][j]);
+          const uint4 r = uint4{(uint32_t)__builtin_amdgcn_readlane((int)m.x, src),
+                                (uint32_t)__builtin_amdgcn_readlane((int)m.y, src),
+                                (uint32_t)__builtin_amdgcn_readlane((int)m.z, src),
+                                (uint32_t)__builtin_amdgcn_readlane((int)m.w, src)};
+          if (jj == j) w = r;
+        }
+        negc[gi][st] = __builtin_bit_cast(half8, uint4{w.x ^ 0x80008000u, w.y ^ 0x80008000u, w.z ^ 0x80008000u,
+                                                       w.w ^ 0x80008000u});
+      }
       if (lane == 0) {
         rec[g * S + st] = (uint8_t)code;
         out[g * S + st] = (uint8_t)code;
@@ -1223,7 +1255,20 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
 
   // ---- K tables into LDS; the first chunk's records and rotary rows load
   // beside them ----
-  load_tables(a.kt);
+  if constexpr (APPEND) {
+    if (owner) {
+      half8 xv[2], cw[S][2][4];
+      fetch_new_token_words<S>((const unsigned char*)a.kt + kvh * (int64_t)tab_bytes, a.knew + b * a.nsb + kvh * a.nsh,
+                               wave, lane, xv, cw);
+      __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the copy
+      load_tables(a.kt);
+      encode_new_token<S>(xv, cw, newrec, a.kc_out + new_slot, wave, lane);
+    } else {
+      load_tables(a.kt);
+    }
+  } else {
+    load_tables(a.kt);
+  }
   uint32_t rk[2][kCw];  // the records of the wave's two tiles in the current chunk
 #pragma unroll
   for (int tl = 0; tl < 2; ++tl) load_rec(a.kc, 32 * wave + 16 * tl + ln, rk[tl]);
@@ -1252,13 +1297,7 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   half8 trig[4];
   fetch_trig(0, 0, trig);
   __builtin_amdgcn_s_waitcnt(0);  // the tables' direct-to-LDS loads have landed
-  __syncthreads();
-  if constexpr (APPEND) {
-    if (owner) {
-      encode_new_token<S>(tab, a.knew + b * a.nsb + kvh * a.nsh, newrec, a.kc_out + new_slot, wave, lane);
-      __syncthreads();
-    }
-  }
+  __syncthreads();                 // (and the appended K record is in LDS)
 
   // ---- K phase, no barriers: each wave streams its own keys' records.
   // Lane (key ln of a 16-key tile, lane group lg) owns 8-dim chunks 4q+lg
@@ -1394,8 +1433,12 @@ __global__ __launch_bounds__(kG8Threads) void decode_g8_kernel(DecodeArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if constexpr (APPEND) {
+    // the V search reads the landed tables (the softmax above already
+    // covers the copy's flight time)
     if (owner) {
-      encode_new_token<S>(tab, a.vnew + b * a.nsb + kvh * a.nsh, newrec, a.vc_out + new_slot, wave, lane);
+      half8 xv[2], cw[S][2][4];
+      fetch_new_token_words<S>(tab, a.vnew + b * a.nsb + kvh * a.nsh, wave, lane, xv, cw);
+      encode_new_token<S>(xv, cw, newrec, a.vc_out + new_slot, wave, lane);
       __syncthreads();
     }
   }
